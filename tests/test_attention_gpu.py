@@ -1,0 +1,140 @@
+"""GPU parity of split-KV flash-decoding (configs 2 and 3b) against the float64
+textbook oracle, ragged-batch exactness, edge cases and the reference-ABI kernels."""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from oracle.attention import attention_ref
+from tests._dev import down, empty, up
+from tests.conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+NQ, NKV, D = 12, 2, 128
+SCALE = 1.0 / math.sqrt(D)
+
+
+def _run(hip, K, q, kc, vc, offsets, split, dtype="f32"):
+    """q [B,NQ,D]; caches [B,max_seq,NKV,D] fp16; offsets [B] (position of last token)."""
+    B, max_seq = kc.shape[0], kc.shape[1]
+    max_splits = (max_seq + split - 1) // split
+    part_m = empty(hip, (B, NQ, max_splits), np.float32)
+    part_l = empty(hip, (B, NQ, max_splits), np.float32)
+    part_o = empty(hip, (B, NQ, max_splits, D), np.float32)
+    out = empty(hip, (B, NQ, D), np.float32 if dtype == "f32" else np.float16)
+    K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), part_m, part_l, part_o, out, B, NQ, NKV, D, SCALE,
+                    up(hip, np.asarray(offsets, np.int32)), max_seq * NKV * D, split, max_splits, dtype=dtype,
+                    stream=hip.stream)
+    return down(out)
+
+
+def _inputs(rng, B, max_seq):
+    q = rng.standard_normal((B, NQ, D)).astype(np.float32)
+    kc = (0.5 * rng.standard_normal((B, max_seq, NKV, D))).astype(np.float16)
+    vc = (0.5 * rng.standard_normal((B, max_seq, NKV, D))).astype(np.float16)
+    return q, kc, vc
+
+
+@pytest.mark.parametrize("ctx", [512, 4096, 32768])
+@pytest.mark.parametrize("split", [256, 512, 1024])
+def test_config2_single_sequence(hip, K, ctx, split):
+    rng = np.random.default_rng(ctx + split)
+    q, kc, vc = _inputs(rng, 1, ctx)
+    got = _run(hip, K, q, kc, vc, [ctx - 1], split)
+    ref = attention_ref(q[0], kc[0], vc[0], ctx, SCALE)
+    assert rel_l2(got[0], ref) <= TOL
+
+
+@pytest.mark.parametrize("B", [8, 16, 32])
+def test_config3b_ragged_matches_batch1_exactly(hip, K, B):
+    rng = np.random.default_rng(1000 + B)
+    lens = rng.integers(128, 8193, B)
+    max_seq = 8192
+    q, kc, vc = _inputs(rng, B, max_seq)
+    split = 512
+    got = _run(hip, K, q, kc, vc, lens - 1, split)
+    for b in range(B):
+        one = _run(hip, K, q[b:b + 1], kc[b:b + 1], vc[b:b + 1], [lens[b] - 1], split)
+        assert np.array_equal(one[0].view(np.uint32), got[b].view(np.uint32)), b
+        if b < 4:
+            assert rel_l2(got[b], attention_ref(q[b], kc[b], vc[b], int(lens[b]), SCALE)) <= TOL
+
+
+@pytest.mark.parametrize("ctx", [1, 2, 31, 33, 255, 257])
+def test_short_and_ragged_tails(hip, K, ctx):
+    rng = np.random.default_rng(ctx)
+    q, kc, vc = _inputs(rng, 1, 512)
+    got = _run(hip, K, q, kc, vc, [ctx - 1], 256)
+    assert rel_l2(got[0], attention_ref(q[0], kc[0], vc[0], ctx, SCALE)) <= TOL
+    if ctx == 1:  # a single position returns v0 exactly
+        for h in range(NQ):
+            assert np.array_equal(got[0, h], vc[0, 0, h // 6].astype(np.float32))
+
+
+def test_identical_keys_give_mean_v(hip, K):
+    rng = np.random.default_rng(5)
+    q, kc, vc = _inputs(rng, 1, 1024)
+    kc[:] = kc[:, :1]
+    got = _run(hip, K, q, kc, vc, [999], 256)
+    for h in range(NQ):
+        assert np.allclose(got[0, h], vc[0, :1000, h // 6].astype(np.float64).mean(0), atol=2e-4)
+
+
+def test_f16_io(hip, K):
+    rng = np.random.default_rng(6)
+    q, kc, vc = _inputs(rng, 2, 2048)
+    got = _run(hip, K, q.astype(np.float16), kc, vc, [2047, 700], 256, dtype="f16")
+    for b, L in enumerate([2048, 701]):
+        ref = attention_ref(q[b].astype(np.float16).astype(np.float32), kc[b], vc[b], L, SCALE)
+        assert rel_l2(got[b], ref) <= TOL
+
+
+def test_kv_append(hip, K):
+    rng = np.random.default_rng(8)
+    B, max_seq = 3, 64
+    kc = np.zeros((B, max_seq, NKV, D), np.float16)
+    vc = np.zeros_like(kc)
+    k = rng.standard_normal((B, NKV, D)).astype(np.float16)
+    v = rng.standard_normal((B, NKV, D)).astype(np.float16)
+    offs = np.array([0, 17, 63], np.int32)
+    dk, dv = up(hip, kc), up(hip, vc)
+    K.kv_append(up(hip, k), up(hip, v), dk, dv, B, NKV, D, up(hip, offs), max_seq * NKV * D, stream=hip.stream)
+    gk, gv = down(dk), down(dv)
+    ek, ev = kc.copy(), vc.copy()
+    for b in range(B):
+        ek[b, offs[b]] = k[b]
+        ev[b, offs[b]] = v[b]
+    assert np.array_equal(gk, ek) and np.array_equal(gv, ev)
+
+
+def test_reference_abi_split_kv_kernels(hip):
+    """Drop-in: the reference-named partial + reduce kernels from the code object,
+    reference launch geometry, chunk size 32 (the compiled constant)."""
+    from vte_amd.kernels import HSACO_PATH
+    _, fp = hip.load_kernel(str(HSACO_PATH), "flash_attention_split_kv_partial_kernel")
+    _, fr = hip.load_kernel(str(HSACO_PATH), "flash_attention_split_kv_reduce_kernel")
+    rng = np.random.default_rng(10)
+    B, max_seq, chunk = 2, 256, 32
+    q, kc, vc = _inputs(rng, B, max_seq)
+    q16 = q.astype(np.float16)
+    offs = np.array([255, 100], np.int32)
+    max_chunks = max_seq // chunk
+    pm = empty(hip, (B, NQ, max_chunks), np.float32)
+    pl = empty(hip, (B, NQ, max_chunks), np.float32)
+    po = empty(hip, (B, NQ, max_chunks, D), np.float32)
+    out = empty(hip, (B, NQ, D), np.float16)
+    dq_, dk, dv, do = up(hip, q16), up(hip, kc), up(hip, vc), up(hip, offs)
+    P = ctypes.c_void_p
+    hip.launch_kernel(fp, (B, NQ, max_chunks), (D, 1, 1),
+                      [P(dq_.ptr), P(dk.ptr), P(dv.ptr), P(pm.ptr), P(pl.ptr), P(po.ptr), ctypes.c_int(NQ),
+                       ctypes.c_int(NKV), ctypes.c_int(D), ctypes.c_float(SCALE), P(do.ptr),
+                       ctypes.c_int(max_seq * NKV * D), ctypes.c_int(max_chunks)], expected_args=13)
+    hip.launch_kernel(fr, (B, NQ, 1), (D, 1, 1),
+                      [P(pm.ptr), P(pl.ptr), P(po.ptr), P(out.ptr), ctypes.c_int(NQ), ctypes.c_int(D),
+                       ctypes.c_int(max_chunks)], shared_mem=max_chunks * 4, expected_args=7)
+    got = down(out).astype(np.float32)
+    for b in range(B):
+        ref = attention_ref(q16[b].astype(np.float32), kc[b], vc[b], int(offs[b]) + 1, SCALE)
+        assert rel_l2(got[b], ref) <= TOL

@@ -1,0 +1,146 @@
+"""GPU parity of the dequantisers, the VALU GEMV, the MFMA batched GEMM and the
+reference-named code-object kernels, against the CPU oracle (configs 0, 1, 3a)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import dequant as dq
+from tests._dev import down, empty, up
+from tests.conftest import rel_l2
+from vte_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3  # rel-L2 <= 1e-3 with fp32 accumulation
+
+
+def _mat(fmt, n, k, seed):
+    return syn.random_matrix(fmt, np.random.default_rng(seed), n, k)
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q4_k", 64, 1536), ("q6_k", 64, 8960), ("q8_0", 64, 2048),
+                                     ("q4_k", 3, 8960), ("q6_k", 5, 256)])
+def test_dequant_bit_exact(hip, K, fmt, n, k):
+    raw = _mat(fmt, n, k, 11)
+    dw = up(hip, raw)
+    out = empty(hip, n * k, np.float32)
+    K.dequantize(fmt, dw, out, n * k, stream=hip.stream)
+    got = down(out)
+    ref = dq.dequantize_matrix(fmt, raw, n, k).reshape(-1)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_known_answer_block(hip, K):
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(np.array([1.0], np.float16).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.array([0.5], np.float16).tobytes(), np.uint8)
+    blk[4], blk[8], blk[16] = 2, 3, 10
+    out = empty(hip, 256, np.float32)
+    K.dequantize("q4_k", up(hip, blk), out, 256, stream=hip.stream)
+    assert down(out)[0] == 18.5
+
+
+@pytest.mark.parametrize("fmt,n,k,seed", [
+    ("q4_k", 8960, 1536, 42),    # config 0
+    ("q6_k", 1536, 8960, 42),    # config 1, FFN down
+    ("q8_0", 2048, 2048, 42),    # config 1, Q8_0
+    ("q4_k", 1536, 8960, 7),
+    ("q6_k", 256, 1536, 7),
+])
+def test_gemv_f32_configs(hip, K, fmt, n, k, seed):
+    rng = np.random.default_rng(seed)
+    raw = syn.random_matrix(fmt, rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    y = empty(hip, n, np.float32)
+    K.gemv(fmt, up(hip, x), up(hip, raw), y, 1, k, n, stream=hip.stream)
+    assert rel_l2(down(y), dq.gemv(fmt, raw, n, k, x)) <= TOL
+
+
+def test_gemv_lm_head_rows(hip, K):
+    """Config 1 LM head 151936x1536 Q6_K: full kernel run, oracle on 4096 sampled rows
+    plus the one-hot column property on the full output."""
+    n, k = 151936, 1536
+    rng = np.random.default_rng(42)
+    raw = syn.random_q6_k(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    dw = up(hip, raw)
+    y = empty(hip, n, np.float32)
+    K.gemv("q6_k", up(hip, x), dw, y, 1, k, n, stream=hip.stream)
+    got = down(y)
+    rows = np.sort(rng.choice(n, 4096, replace=False))
+    rb = raw.reshape(n, -1)[rows].reshape(-1)
+    assert rel_l2(got[rows], dq.gemv("q6_k", rb, len(rows), k, x)) <= TOL
+    # one-hot activation returns a dequantised column (exact up to fp32 rounding of d*sc*q)
+    e = np.zeros(k, np.float32); e[777] = 1.0
+    K.gemv("q6_k", up(hip, e), dw, y, 1, k, n, stream=hip.stream)
+    col = down(y)
+    wc = dq.dequantize_q6_k(raw.reshape(n, -1)[rows].reshape(-1), len(rows) * k).reshape(len(rows), k)[:, 777]
+    assert np.allclose(col[rows], wc, rtol=1e-6, atol=1e-9)
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q8_0"])
+@pytest.mark.parametrize("M", [1, 2, 3, 5])
+def test_gemv_f16_epilogue_batched(hip, K, fmt, M):
+    """fp16 I/O with bias, residual_scale and residual (the reference's 10-arg contract)."""
+    n, k = 384, 512
+    rng = np.random.default_rng(100 + M)
+    raw = syn.random_matrix(fmt, rng, n, k)
+    x = rng.standard_normal((M, k)).astype(np.float16)
+    bias = (0.1 * rng.standard_normal(n)).astype(np.float16)
+    res = rng.standard_normal((M, n)).astype(np.float16)
+    y = empty(hip, (M, n), np.float16)
+    K.gemv(fmt, up(hip, x), up(hip, raw), y, M, k, n, bias=up(hip, bias), residual=up(hip, res),
+           residual_scale=0.5, in_dtype="f16", out_dtype="f16", stream=hip.stream)
+    ref = dq.gemv_epilogue(dq.gemv(fmt, raw, n, k, x.astype(np.float32)), bias, res, 0.5)
+    got = down(y).astype(np.float64)
+    assert rel_l2(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q4_k", 8960, 1536), ("q6_k", 1536, 8960), ("q4_k", 1536, 1536),
+                                     ("q6_k", 4096, 1536)])
+@pytest.mark.parametrize("M", [1, 8, 16, 32, 5, 20])
+def test_gemm_mfma_configs(hip, K, fmt, n, k, M):
+    """Config 3a (and Q6_K twins): MFMA fp16-dequant path, fp32 activations."""
+    rng = np.random.default_rng(300 + M)
+    raw = syn.random_matrix(fmt, rng, n, k)
+    x = rng.standard_normal((M, k)).astype(np.float32)
+    y = empty(hip, (M, n), np.float32)
+    K.gemm_mfma(fmt, up(hip, x), up(hip, raw), y, M, k, n, stream=hip.stream)
+    assert rel_l2(down(y), dq.gemv(fmt, raw, n, k, x)) <= TOL
+
+
+def test_gemm_mfma_f16_epilogue(hip, K):
+    n, k, M = 512, 1536, 16
+    rng = np.random.default_rng(5)
+    raw = syn.random_q4_k(rng, n, k)
+    x = rng.standard_normal((M, k)).astype(np.float16)
+    bias = (0.1 * rng.standard_normal(n)).astype(np.float16)
+    res = rng.standard_normal((M, n)).astype(np.float16)
+    y = empty(hip, (M, n), np.float16)
+    K.gemm_mfma("q4_k", up(hip, x), up(hip, raw), y, M, k, n, bias=up(hip, bias), residual=up(hip, res),
+                residual_scale=1.0, in_dtype="f16", out_dtype="f16", stream=hip.stream)
+    ref = dq.gemv_epilogue(dq.gemv("q4_k", raw, n, k, x.astype(np.float32)), bias, res, 1.0)
+    assert rel_l2(down(y), ref) <= TOL
+
+
+@pytest.mark.parametrize("name,fmt", [("gemv_q4k_kernel", "q4_k"), ("gemv_q6k_kernel", "q6_k"),
+                                      ("gemv_q8_0_kernel", "q8_0")])
+def test_reference_abi_code_object(hip, name, fmt):
+    """Drop-in path: load the code object by kernel name and launch it with the
+    reference's 10-argument ABI and geometry (grid (N, B*S), block 64)."""
+    from vte_amd.kernels import HSACO_PATH
+    _, fn = hip.load_kernel(str(HSACO_PATH), name)
+    n, k, B = 300, 2048, 2
+    rng = np.random.default_rng(9)
+    raw = syn.random_matrix(fmt, rng, n, k)
+    x = rng.standard_normal((B, k)).astype(np.float16)
+    bias = (0.1 * rng.standard_normal(n)).astype(np.float16)
+    res = rng.standard_normal((B, n)).astype(np.float16)
+    dx, dw, db, dr = up(hip, x), up(hip, raw), up(hip, bias), up(hip, res)
+    y = empty(hip, (B, n), np.float16)
+    args = [ctypes.c_void_p(dx.ptr), ctypes.c_void_p(dw.ptr), ctypes.c_void_p(y.ptr), ctypes.c_int(B),
+            ctypes.c_int(1), ctypes.c_int(k), ctypes.c_int(n), ctypes.c_void_p(db.ptr), ctypes.c_void_p(dr.ptr),
+            ctypes.c_float(1.0)]
+    hip.launch_kernel(fn, (n, B, 1), (64, 1, 1), args, expected_args=10)
+    ref = dq.gemv_epilogue(dq.gemv(fmt, raw, n, k, x.astype(np.float32)), bias, res, 1.0)
+    assert rel_l2(down(y), ref) <= TOL

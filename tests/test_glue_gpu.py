@@ -1,0 +1,85 @@
+"""GPU parity of the decode-step glue kernels and the top-k selector."""
+import numpy as np
+import pytest
+
+from oracle import step as st
+from tests._dev import down, empty, up
+from vte_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulp_close(a, b, ulps=1):
+    """fp16 results within `ulps` units in the last place (fp32 math, one rounding)."""
+    a = a.astype(np.float16).view(np.int16).astype(np.int32)
+    b = b.astype(np.float16).view(np.int16).astype(np.int32)
+    return np.max(np.abs(a - b)) <= ulps
+
+
+def test_rmsnorm(hip, K):
+    rng = np.random.default_rng(1)
+    rows, H = 16, 1536
+    x = rng.standard_normal((rows, H)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+    out = empty(hip, (rows, H), np.float16)
+    K.rmsnorm(up(hip, x), up(hip, w), out, rows, H, 1e-6, stream=hip.stream)
+    assert _ulp_close(down(out), st.rmsnorm(x, w, 1e-6), 2)
+
+
+def test_swiglu_and_add(hip, K):
+    rng = np.random.default_rng(2)
+    n = 8960 * 3
+    g = (3 * rng.standard_normal(n)).astype(np.float16)
+    u = rng.standard_normal(n).astype(np.float16)
+    out = empty(hip, n, np.float16)
+    K.swiglu(up(hip, g), up(hip, u), out, n, stream=hip.stream)
+    assert _ulp_close(down(out), st.swiglu(g, u), 1)
+    r = rng.standard_normal(n).astype(np.float16)
+    K.add(up(hip, r), up(hip, u), out, n, 0.25, stream=hip.stream)
+    assert _ulp_close(down(out), (r.astype(np.float32) + 0.25 * u.astype(np.float32)), 1)
+
+
+def test_rope_neox_batched(hip, K):
+    rng = np.random.default_rng(3)
+    B, nq, nkv, hd = 4, 12, 2, 128
+    cos_c, sin_c = st.rope_cache(4096, hd, 1e6)
+    q = rng.standard_normal((B, nq, hd)).astype(np.float16)
+    k = rng.standard_normal((B, nkv, hd)).astype(np.float16)
+    offs = np.array([0, 1, 777, 4095], np.int32)
+    dq_, dk = up(hip, q), up(hip, k)
+    K.rope(dq_, dk, up(hip, cos_c), up(hip, sin_c), B, 1, nq, nkv, hd, up(hip, offs), 0, 0, stream=hip.stream)
+    gq, gk = down(dq_), down(dk)
+    for b in range(B):
+        assert _ulp_close(gq[b], st.rope_neox(q[b], int(offs[b]), cos_c, sin_c), 1)
+        assert _ulp_close(gk[b], st.rope_neox(k[b], int(offs[b]), cos_c, sin_c), 1)
+    # position 0 is the identity; a rotation keeps each (i, i+64) pair's norm
+    assert np.array_equal(gq[0], q[0])
+
+
+def test_embedding_q6k_bit_exact(hip, K):
+    rng = np.random.default_rng(4)
+    vocab, H = 1000, 1536
+    table = syn.random_q6_k(rng, vocab, H)
+    toks = np.array([0, 5, 999, 5, 123], np.int32)
+    out = empty(hip, (len(toks), H), np.float16)
+    K.embedding_q6k(up(hip, toks), up(hip, table), out, len(toks), H, stream=hip.stream)
+    got = down(out)
+    for i, t in enumerate(toks):
+        assert np.array_equal(got[i], st.embedding_q6k(table, int(t), H))
+
+
+@pytest.mark.parametrize("k", [1, 40, 64])
+def test_topk_exact(hip, K, k):
+    rng = np.random.default_rng(5)
+    rows, vocab = 4, 151936
+    logits = rng.standard_normal((rows, vocab)).astype(np.float32)
+    logits[1, :] = -3.0          # heavy ties: lowest indices must win
+    logits[1, 70000] = 5.0
+    logits[2, 1000:1100] = 9.0    # a tied block above everything else
+    vals, idx = empty(hip, (rows, k), np.float32), empty(hip, (rows, k), np.int32)
+    K.topk(up(hip, logits), rows, vocab, k, vals, idx, stream=hip.stream)
+    gv, gi = down(vals), down(idx)
+    for r in range(rows):
+        order = np.lexsort((np.arange(vocab), -logits[r]))[:k]  # value desc, index asc
+        assert np.array_equal(gi[r], order), r
+        assert np.array_equal(gv[r], logits[r, order])

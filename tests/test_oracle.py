@@ -1,0 +1,180 @@
+"""Pins for the CPU oracle (no GPU): known answers, closed forms, inverse
+encoders written from the GGUF block description, and float64 invariants.
+Each check is built so that a plausible decoding mistake (swapped nibbles,
+wrong scale byte, j-4 vs j for the min high bits, wrong qh shift, sign of the
+-32 offset) fails it."""
+import numpy as np
+import pytest
+
+from oracle import dequant as dq
+from oracle.attention import attention_ref, split_kv_ref
+from vte_amd import synthetic as syn
+
+
+def f16b(x):
+    return np.array([x], np.float16).tobytes()
+
+
+# ---------------------------------------------------------------- Q4_K
+def test_q4k_reference_known_answer_block():
+    """Reference test block (tests/integration/test_kernels_numerical.py:63-77):
+    d=1, dmin=0.5, scales[0]=2, scales[4]=3, qs[0]=10.  Under dequantizer.py
+    semantics w[0] = (1*2)*10 - 0.5*3 = 18.5 (the reference test's 2.5 comes
+    from a different, wrong formula in math_refs and is not used)."""
+    blk = bytearray(144)
+    blk[0:2] = f16b(1.0)
+    blk[2:4] = f16b(0.5)
+    blk[4] = 2
+    blk[8] = 3
+    blk[16] = 10
+    w = dq.dequantize_q4_k(bytes(blk), 256)
+    assert w[0] == 18.5
+    # same byte's high nibble (0) belongs to sub-block 1 (scale byte 5 = 0)
+    assert w[32] == 0.0
+    # other low nibbles of group 0 are zero -> -dmin*m = -1.5
+    assert np.all(w[1:32] == -1.5)
+
+
+def _encode_q4k(d, dmin, sc, mn, q):
+    """Independent encoder: 256 4-bit values q (element order of the format)."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(f16b(d), np.uint8)
+    blk[2:4] = np.frombuffer(f16b(dmin), np.uint8)
+    blk[4:16] = syn.pack_q4k_scales(np.array(sc)[None], np.array(mn)[None])[0]
+    for e in range(256):
+        grp, r = divmod(e, 64)
+        hi, i = divmod(r, 32)
+        byte = 16 + 32 * grp + i
+        blk[byte] |= (q[e] & 15) << (4 * hi)
+    return blk
+
+
+def test_q4k_scale_min_all_subblocks_distinct():
+    """Distinct 6-bit scales/mins with high bits set in every sub-block: each
+    output must use its own (sc_j, m_j); catches the j-4 / j high-bit mixup."""
+    sc = [33, 47, 18, 63, 49, 34, 61, 52]
+    mn = [62, 17, 44, 35, 58, 39, 21, 48]
+    q = np.full(256, 1, np.int64)
+    blk = _encode_q4k(1.0, 1.0, sc, mn, q)
+    w = dq.dequantize_q4_k(blk.tobytes(), 256)
+    for e in range(256):
+        j = 2 * (e // 64) + (e % 64) // 32
+        assert w[e] == np.float32(sc[j]) - np.float32(mn[j]), e
+
+
+def test_q4k_unit_scales_give_raw_nibbles():
+    rng = np.random.default_rng(1)
+    q = rng.integers(0, 16, 256)
+    blk = _encode_q4k(1.0, 0.0, [1] * 8, [0] * 8, q)
+    w = dq.dequantize_q4_k(blk.tobytes(), 256)
+    assert np.array_equal(w, q.astype(np.float32))
+
+
+def test_q4k_scale_packing_roundtrip():
+    rng = np.random.default_rng(2)
+    sc = rng.integers(0, 64, (500, 8))
+    mn = rng.integers(0, 64, (500, 8))
+    packed = syn.pack_q4k_scales(sc, mn).astype(np.int32)
+    for j in range(8):
+        s, m = dq.q4k_scale_min(packed, j)
+        assert np.array_equal(s, sc[:, j].astype(np.float32))
+        assert np.array_equal(m, mn[:, j].astype(np.float32))
+
+
+# ---------------------------------------------------------------- Q6_K
+def _encode_q6k(d, scales, u):
+    """Independent encoder: 256 unsigned 6-bit values u (q = u - 32)."""
+    blk = np.zeros(210, np.uint8)
+    for e in range(256):
+        half, r = divmod(e, 128)
+        g, l = divmod(r, 32)
+        ql_byte = 64 * half + l + (32 if g in (1, 3) else 0)
+        blk[ql_byte] |= (u[e] & 15) << (4 if g >= 2 else 0)
+        blk[128 + 32 * half + l] |= ((u[e] >> 4) & 3) << (2 * g)
+    blk[192:208] = np.array(scales, np.int8).view(np.uint8)
+    blk[208:210] = np.frombuffer(f16b(d), np.uint8)
+    return blk
+
+
+def test_q6k_roundtrip_positions_and_scales():
+    rng = np.random.default_rng(3)
+    u = rng.integers(0, 64, 256)
+    scales = [1] * 16
+    blk = _encode_q6k(1.0, scales, u)
+    w = dq.dequantize_q6_k(blk.tobytes(), 256)
+    assert np.array_equal(w, (u - 32).astype(np.float32))
+    # each 16-element run uses its own scale index 8*half + l//16 + 2*g
+    scales = [2, -3, 5, -7, 11, -13, 17, -19, 23, -29, 31, -31, 3, -5, 7, -1]
+    u = np.full(256, 33)  # q = 1 everywhere
+    w = dq.dequantize_q6_k(_encode_q6k(1.0, scales, u).tobytes(), 256)
+    for e in range(256):
+        half, r = divmod(e, 128)
+        g, l = divmod(r, 32)
+        assert w[e] == scales[8 * half + l // 16 + 2 * g], e
+
+
+def test_q6k_zero_quants():
+    blk = _encode_q6k(0.5, [4] * 16, np.zeros(256, np.int64))
+    w = dq.dequantize_q6_k(blk.tobytes(), 256)
+    assert np.all(w == np.float32(-32 * 0.5 * 4))
+
+
+# ---------------------------------------------------------------- Q8_0
+def test_q80_closed_form():
+    rng = np.random.default_rng(4)
+    q = rng.integers(-127, 128, 32)
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.frombuffer(f16b(1.0), np.uint8)
+    blk[2:] = q.astype(np.int8).view(np.uint8)
+    assert np.array_equal(dq.dequantize_q8_0(blk.tobytes(), 32), q.astype(np.float32))
+    blk[0:2] = np.frombuffer(f16b(0.25), np.uint8)
+    assert np.array_equal(dq.dequantize_q8_0(blk.tobytes(), 32), (0.25 * q).astype(np.float32))
+
+
+# ---------------------------------------------------------------- generators
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q8_0"])
+def test_synthetic_header_ranges(fmt):
+    rng = np.random.default_rng(5)
+    raw = syn.random_matrix(fmt, rng, 8, 512)
+    assert raw.nbytes == syn.matrix_bytes(fmt, 8, 512)
+    bb = syn.BLOCK_BYTES[fmt]
+    blocks = raw.reshape(-1, bb)
+    d_off = {"q4_k": 0, "q6_k": 208, "q8_0": 0}[fmt]
+    d = blocks[:, d_off:d_off + 2].copy().view(np.float16).astype(np.float32)
+    assert np.all((d >= 9.9e-4) & (d <= 1.001e-2))
+    w = dq.dequantize_matrix(fmt, raw, 8, 512)
+    assert np.all(np.isfinite(w))
+
+
+def test_gemv_oracle_linearity_and_onehot():
+    rng = np.random.default_rng(6)
+    raw = syn.random_q4_k(rng, 16, 512)
+    x1, x2 = rng.standard_normal(512), rng.standard_normal(512)
+    y = dq.gemv("q4_k", raw, 16, 512, np.stack([x1, x2, 2 * x1 - 3 * x2]))
+    assert np.allclose(y[2], 2 * y[0] - 3 * y[1], rtol=1e-12, atol=1e-12)
+    e = np.zeros(512); e[300] = 1.0
+    col = dq.gemv("q4_k", raw, 16, 512, e)
+    assert np.array_equal(col, dq.dequantize_matrix("q4_k", raw, 16, 512)[:, 300].astype(np.float64))
+
+
+# ---------------------------------------------------------------- attention
+def test_attention_oracle_invariants():
+    rng = np.random.default_rng(7)
+    n_q, n_kv, d, ctx = 12, 2, 128, 300
+    q = rng.standard_normal((n_q, d)).astype(np.float32)
+    k = (0.5 * rng.standard_normal((ctx, n_kv, d))).astype(np.float16)
+    v = (0.5 * rng.standard_normal((ctx, n_kv, d))).astype(np.float16)
+    # ctx = 1 -> v0
+    o1 = attention_ref(q, k, v, 1, 1 / np.sqrt(d))
+    for h in range(n_q):
+        assert np.array_equal(o1[h], v[0, h // 6].astype(np.float64))
+    # identical keys -> mean of V
+    kk = np.repeat(k[:1], ctx, axis=0)
+    o2 = attention_ref(q, kk, v, ctx, 1 / np.sqrt(d))
+    for h in range(n_q):
+        assert np.allclose(o2[h], v[:, h // 6].astype(np.float64).mean(0), atol=1e-12)
+    # split-KV restatement agrees with the textbook form
+    full = attention_ref(q, k, v, ctx, 1 / np.sqrt(d))
+    for chunk in (32, 64, 300):
+        sp = split_kv_ref(q, k, v, ctx, 1 / np.sqrt(d), chunk)
+        assert np.linalg.norm(sp - full) / np.linalg.norm(full) < 1e-5

@@ -1,0 +1,382 @@
+"""ctypes bridge to the HIP runtime (libamdhip64.so) with VTE's HIPRuntime API.
+
+Mirrors the public surface of the reference bridge
+(vte/bridge/hip_runtime.py:155-1089) so the engine code above it reads the
+same: ``initialize``, ``safe_malloc`` / ``safe_free``,
+``safe_memcpy_host_to_device`` / ``safe_memcpy_device_to_host`` /
+``safe_memset``, ``load_kernel``, ``launch_kernel`` /
+``launch_kernel_recorded``, ``synchronize``, stream capture and graph calls,
+events, ``get_num_cus``, ``get_gpu_architecture`` and ``cleanup``.  Errors
+keep the reference's classes: ``HIPRuntimeError`` for a nonzero HIP return,
+``HIPSafetyError`` for a rejected call, ``MemoryGuardianOOMError`` for an
+allocation refused by the VRAM ceiling.
+
+Differences, by design for a Linux MI355X server: no Windows DLL discovery,
+watchdog, duty-cycle throttle or desktop telemetry (the reference's
+desktop-GPU protections); device properties come from
+``vte_device_info`` in libvte_amd.so instead of a hand-maintained
+``hipDeviceProp_t`` mirror.
+"""
+from __future__ import annotations
+
+import ctypes
+import ctypes.util
+import os
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+hipMemcpyHostToDevice = 1
+hipMemcpyDeviceToHost = 2
+hipMemcpyDeviceToDevice = 3
+HIP_STREAM_CAPTURE_MODE_GLOBAL = 0
+hipErrorOutOfMemory = 2
+
+# Same allocation guards as the reference (vte/config.py); the VRAM ceiling is
+# the fraction of device memory this process may reserve.
+VRAM_USAGE_LIMIT = 0.95
+MAX_ALLOCATION_SIZE = 64 * 1024 ** 3
+MAX_GRID_DIMENSIONS = 2 ** 31 - 1
+
+
+class HIPRuntimeError(RuntimeError):
+    """A HIP API call returned an error code."""
+
+
+class HIPSafetyError(RuntimeError):
+    """A call was refused by the bridge's own validation."""
+
+
+class MemoryGuardianOOMError(HIPSafetyError):
+    """An allocation would exceed the VRAM ceiling or failed with OOM."""
+
+
+def find_hip_library() -> Optional[str]:
+    """Locate libamdhip64.so (ROCM_PATH, HIP_PATH, /opt/rocm, then the loader path)."""
+    roots = [os.environ.get("ROCM_PATH"), os.environ.get("HIP_PATH"), "/opt/rocm"]
+    for root in roots:
+        if root:
+            for name in ("libamdhip64.so", "libamdhip64.so.7"):
+                p = Path(root) / "lib" / name
+                if p.exists():
+                    return str(p)
+    return ctypes.util.find_library("amdhip64")
+
+
+class HIPRuntime:
+    """Thin, validated wrapper over libamdhip64 (one device, one stream)."""
+
+    _process_wide_allocated_bytes: int = 0
+
+    def __init__(self, library_path: Optional[str] = None):
+        path = library_path or find_hip_library()
+        if path is None:
+            raise HIPRuntimeError("libamdhip64.so not found: install ROCm and set ROCM_PATH")
+        try:
+            self._lib = ctypes.CDLL(path)
+        except OSError as e:  # pragma: no cover - depends on the image
+            raise HIPRuntimeError(f"failed to load {path}: {e}") from e
+        self.library_path = path
+        self._initialized = False
+        self._active_allocations: dict[int, tuple[int, str]] = {}
+        self._prevent_host_copies = True
+        self._vram_total = 0
+        self._num_cus = 0
+        self._arch = ""
+        self._device_index = 0
+        self._stream = ctypes.c_void_p(0)
+        self._modules: list[ctypes.c_void_p] = []
+        self._map_hip_functions()
+
+    # ------------------------------------------------------------------ setup
+    def _map_hip_functions(self) -> None:
+        L = self._lib
+        vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        sig = {
+            "hipInit": ([ctypes.c_uint], i),
+            "hipSetDevice": ([i], i),
+            "hipGetDeviceCount": ([ctypes.POINTER(i)], i),
+            "hipMalloc": ([ctypes.POINTER(vp), sz], i),
+            "hipFree": ([vp], i),
+            "hipMemcpy": ([vp, vp, sz, i], i),
+            "hipMemcpyAsync": ([vp, vp, sz, i, vp], i),
+            "hipMemset": ([vp, i, sz], i),
+            "hipMemsetAsync": ([vp, i, sz, vp], i),
+            "hipMemGetInfo": ([ctypes.POINTER(sz), ctypes.POINTER(sz)], i),
+            "hipDeviceSynchronize": ([], i),
+            "hipStreamCreate": ([ctypes.POINTER(vp)], i),
+            "hipStreamDestroy": ([vp], i),
+            "hipStreamSynchronize": ([vp], i),
+            "hipModuleLoad": ([ctypes.POINTER(vp), ctypes.c_char_p], i),
+            "hipModuleUnload": ([vp], i),
+            "hipModuleGetFunction": ([ctypes.POINTER(vp), vp, ctypes.c_char_p], i),
+            "hipModuleLaunchKernel": ([vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
+                                       ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp,
+                                       ctypes.POINTER(vp), ctypes.POINTER(vp)], i),
+            "hipStreamBeginCapture": ([vp, i], i),
+            "hipStreamEndCapture": ([vp, ctypes.POINTER(vp)], i),
+            "hipGraphInstantiate": ([ctypes.POINTER(vp), vp, vp, vp, sz], i),
+            "hipGraphLaunch": ([vp, vp], i),
+            "hipGraphDestroy": ([vp], i),
+            "hipGraphExecDestroy": ([vp], i),
+            "hipEventCreate": ([ctypes.POINTER(vp)], i),
+            "hipEventRecord": ([vp, vp], i),
+            "hipEventSynchronize": ([vp], i),
+            "hipEventElapsedTime": ([ctypes.POINTER(ctypes.c_float), vp, vp], i),
+            "hipEventDestroy": ([vp], i),
+            "hipGetErrorString": ([i], ctypes.c_char_p),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+
+    def _check_error(self, err: int, context: str) -> None:
+        if err != 0:
+            msg = self._lib.hipGetErrorString(err)
+            raise HIPRuntimeError(f"HIP error: {context} returned {err} ({msg.decode() if msg else '?'})")
+
+    def device_count(self) -> int:
+        n = ctypes.c_int(0)
+        err = self._lib.hipGetDeviceCount(ctypes.byref(n))
+        return n.value if err == 0 else 0
+
+    def initialize(self) -> bool:
+        """hipInit, select the device (VTE_DEVICE_INDEX, default 0), create the stream."""
+        if self._initialized:
+            return True
+        if self._lib.hipInit(0) != 0:
+            return False
+        self._device_index = int(os.environ.get("VTE_DEVICE_INDEX", "0"))
+        if self._lib.hipSetDevice(self._device_index) != 0:
+            return False
+        from ..kernels import kernels  # device properties without a struct mirror
+        info = kernels().device_info(self._device_index)
+        self._num_cus = info["num_cus"]
+        self._vram_total = info["total_mem"]
+        self._arch = info["arch"]
+        self._check_error(self._lib.hipStreamCreate(ctypes.byref(self._stream)), "hipStreamCreate")
+        self._initialized = True
+        return True
+
+    @property
+    def stream(self) -> ctypes.c_void_p:
+        return self._stream
+
+    def get_num_cus(self) -> int:
+        env = os.environ.get("VTE_NUM_CUS")
+        return int(env) if env else self._num_cus
+
+    def get_gpu_architecture(self) -> str:
+        return self._arch.split(":")[0] if self._arch else ""
+
+    def get_real_mem_info(self) -> tuple[int, int]:
+        free, total = ctypes.c_size_t(0), ctypes.c_size_t(0)
+        self._check_error(self._lib.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)), "hipMemGetInfo")
+        return free.value, total.value
+
+    # ----------------------------------------------------------------- memory
+    def _require_init(self) -> None:
+        if not self._initialized:
+            raise HIPSafetyError("HIP operation requires initialize()")
+
+    def safe_malloc(self, size_bytes: int, tag: str = "unnamed") -> ctypes.c_void_p:
+        """hipMalloc with the reference's guards (size > 0, below the per-allocation
+        maximum and the process-wide VRAM ceiling)."""
+        self._require_init()
+        if size_bytes <= 0:
+            raise HIPSafetyError(f"invalid allocation size {size_bytes} [{tag}]")
+        if size_bytes > MAX_ALLOCATION_SIZE:
+            raise HIPSafetyError(f"allocation {size_bytes} above maximum {MAX_ALLOCATION_SIZE} [{tag}]")
+        if HIPRuntime._process_wide_allocated_bytes + size_bytes > self._vram_total * VRAM_USAGE_LIMIT:
+            raise MemoryGuardianOOMError(f"allocating {size_bytes} bytes [{tag}] would exceed "
+                                         f"{VRAM_USAGE_LIMIT:.0%} of {self._vram_total} bytes")
+        ptr = ctypes.c_void_p()
+        err = self._lib.hipMalloc(ctypes.byref(ptr), size_bytes)
+        if err == hipErrorOutOfMemory:
+            raise MemoryGuardianOOMError(f"hipMalloc out of memory ({size_bytes} bytes) [{tag}]")
+        self._check_error(err, "hipMalloc")
+        if not ptr.value:
+            raise HIPSafetyError("hipMalloc returned a null pointer with status 0")
+        self._active_allocations[ptr.value] = (size_bytes, tag)
+        HIPRuntime._process_wide_allocated_bytes += size_bytes
+        return ptr
+
+    def safe_free(self, ptr: ctypes.c_void_p, tag: str = "unnamed") -> bool:
+        val = ptr.value if isinstance(ptr, ctypes.c_void_p) else int(ptr)
+        if val not in self._active_allocations:
+            raise HIPSafetyError(f"free of untracked pointer 0x{(val or 0):016X} [{tag}]")
+        size, _ = self._active_allocations.pop(val)
+        self._check_error(self._lib.hipFree(ctypes.c_void_p(val)), "hipFree")
+        HIPRuntime._process_wide_allocated_bytes = max(0, HIPRuntime._process_wide_allocated_bytes - size)
+        return True
+
+    def _owning_allocation(self, addr: int, length: int, what: str, tag: str) -> None:
+        for base, (size, _) in self._active_allocations.items():
+            if base <= addr < base + size:
+                if addr + length > base + size:
+                    raise HIPSafetyError(f"{what} overflow: {length} bytes cross the allocation end [{tag}]")
+                return
+        raise HIPSafetyError(f"{what}: untracked device pointer 0x{addr:016X} [{tag}]")
+
+    @staticmethod
+    def _addr(p) -> int:
+        if isinstance(p, ctypes.c_void_p):
+            return p.value or 0
+        return int(p)
+
+    def safe_memcpy_host_to_device(self, dst, src, tag: str = "unnamed") -> bool:
+        self._require_init()
+        buf = np.ascontiguousarray(np.frombuffer(src, dtype=np.uint8) if isinstance(src, (bytes, bytearray))
+                                   else src).view(np.uint8).reshape(-1)
+        d = self._addr(dst)
+        self._owning_allocation(d, buf.nbytes, "memcpy_h2d", tag)
+        self._check_error(self._lib.hipMemcpy(ctypes.c_void_p(d), buf.ctypes.data_as(ctypes.c_void_p),
+                                              buf.nbytes, hipMemcpyHostToDevice), "hipMemcpy (H2D)")
+        return True
+
+    def safe_memset(self, dst, size_bytes: int, tag: str = "unnamed", value: int = 0) -> bool:
+        self._require_init()
+        d = self._addr(dst)
+        self._owning_allocation(d, size_bytes, "memset", tag)
+        self._check_error(self._lib.hipMemset(ctypes.c_void_p(d), value, size_bytes), "hipMemset")
+        return True
+
+    def safe_memcpy_device_to_host(self, dst, src, tag: str = "unnamed") -> bool:
+        """D2H copy into a writable buffer (bytearray or numpy array).  As in the
+        reference, copies are allow-listed by tag ('logits', 'output', 'sampler')
+        unless ``_prevent_host_copies`` is cleared."""
+        self._require_init()
+        if self._prevent_host_copies and not any(t in tag.lower() for t in ("logits", "output", "sampler")):
+            raise HIPSafetyError(f"data isolation: device->host copy refused for tag '{tag}'")
+        out = np.frombuffer(dst, dtype=np.uint8) if isinstance(dst, bytearray) else dst.view(np.uint8).reshape(-1)
+        s = self._addr(src)
+        self._owning_allocation(s, out.nbytes, "memcpy_d2h", tag)
+        self._check_error(self._lib.hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(s), out.nbytes,
+                                              hipMemcpyDeviceToHost), "hipMemcpy (D2H)")
+        return True
+
+    def memcpy_device_to_device(self, dst, src, nbytes: int) -> None:
+        self._check_error(self._lib.hipMemcpyAsync(ctypes.c_void_p(self._addr(dst)), ctypes.c_void_p(self._addr(src)),
+                                                   nbytes, hipMemcpyDeviceToDevice, self._stream), "hipMemcpyAsync")
+
+    # ---------------------------------------------------------------- kernels
+    def load_kernel(self, hsaco_path: str, kernel_name: str) -> tuple[ctypes.c_void_p, ctypes.c_void_p]:
+        module = ctypes.c_void_p()
+        self._check_error(self._lib.hipModuleLoad(ctypes.byref(module), str(hsaco_path).encode()), "hipModuleLoad")
+        self._modules.append(module)
+        fn = ctypes.c_void_p()
+        self._check_error(self._lib.hipModuleGetFunction(ctypes.byref(fn), module, kernel_name.encode()),
+                          "hipModuleGetFunction")
+        return module, fn
+
+    def _launch(self, function, grid, block, args, shared_mem, context) -> bool:
+        if len(grid) != 3 or any(g <= 0 for g in grid):
+            raise HIPSafetyError(f"invalid grid dims {grid}")
+        if len(block) != 3 or any(b <= 0 for b in block):
+            raise HIPSafetyError(f"invalid block dims {block}")
+        if grid[0] * grid[1] * grid[2] > MAX_GRID_DIMENSIONS:
+            raise HIPSafetyError(f"grid of {grid[0] * grid[1] * grid[2]} blocks exceeds the limit")
+        if block[0] * block[1] * block[2] > 1024:
+            raise HIPSafetyError(f"block size {block} exceeds 1024 threads")
+        if shared_mem > 160 * 1024:
+            raise HIPSafetyError(f"shared memory {shared_mem} exceeds the 160 KiB LDS of a CU")
+        keep = []
+        c_args = (ctypes.c_void_p * len(args))()
+        for k, a in enumerate(args):
+            if isinstance(a, int) and not isinstance(a, bool):
+                a = ctypes.c_uint64(a)
+            keep.append(a)
+            c_args[k] = ctypes.cast(ctypes.byref(a), ctypes.c_void_p)
+        err = self._lib.hipModuleLaunchKernel(function, grid[0], grid[1], grid[2], block[0], block[1], block[2],
+                                              shared_mem, self._stream, c_args, None)
+        self._check_error(err, context)
+        return True
+
+    def launch_kernel(self, function, grid: tuple, block: tuple, args: list, shared_mem: int = 0,
+                      expected_args: Optional[int] = None) -> bool:
+        """hipModuleLaunchKernel with ABI-count and geometry validation
+        (vte/bridge/hip_runtime.py:805-867)."""
+        if expected_args is not None and len(args) != expected_args:
+            raise HIPSafetyError(f"ABI mismatch: kernel expects {expected_args} args, got {len(args)}")
+        return self._launch(function, grid, block, args, shared_mem, "hipModuleLaunchKernel")
+
+    def launch_kernel_recorded(self, function, args: list, grid: tuple, block: tuple, shared_mem: int = 0) -> bool:
+        """Same launch while the stream is being captured (recorded into the graph)."""
+        return self._launch(function, grid, block, args, shared_mem, "hipModuleLaunchKernel (recorded)")
+
+    def synchronize(self) -> bool:
+        self._check_error(self._lib.hipDeviceSynchronize(), "hipDeviceSynchronize")
+        return True
+
+    def stream_synchronize(self) -> None:
+        self._check_error(self._lib.hipStreamSynchronize(self._stream), "hipStreamSynchronize")
+
+    # ------------------------------------------------------------ graphs/events
+    def stream_begin_capture(self) -> None:
+        self._check_error(self._lib.hipStreamBeginCapture(self._stream, HIP_STREAM_CAPTURE_MODE_GLOBAL),
+                          "hipStreamBeginCapture")
+
+    def stream_end_capture(self) -> ctypes.c_void_p:
+        g = ctypes.c_void_p()
+        self._check_error(self._lib.hipStreamEndCapture(self._stream, ctypes.byref(g)), "hipStreamEndCapture")
+        return g
+
+    def graph_instantiate(self, graph) -> ctypes.c_void_p:
+        ge = ctypes.c_void_p()
+        self._check_error(self._lib.hipGraphInstantiate(ctypes.byref(ge), graph, None, None, 0), "hipGraphInstantiate")
+        return ge
+
+    def graph_launch(self, graph_exec) -> None:
+        self._check_error(self._lib.hipGraphLaunch(graph_exec, self._stream), "hipGraphLaunch")
+
+    def graph_destroy(self, graph) -> None:
+        self._check_error(self._lib.hipGraphDestroy(graph), "hipGraphDestroy")
+
+    def graph_exec_destroy(self, graph_exec) -> None:
+        self._check_error(self._lib.hipGraphExecDestroy(graph_exec), "hipGraphExecDestroy")
+
+    def event_create(self) -> ctypes.c_void_p:
+        ev = ctypes.c_void_p()
+        self._check_error(self._lib.hipEventCreate(ctypes.byref(ev)), "hipEventCreate")
+        return ev
+
+    def event_record(self, event) -> None:
+        self._check_error(self._lib.hipEventRecord(event, self._stream), "hipEventRecord")
+
+    def event_elapsed_ms(self, start, stop) -> float:
+        self._check_error(self._lib.hipEventSynchronize(stop), "hipEventSynchronize")
+        ms = ctypes.c_float(0.0)
+        self._check_error(self._lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+        return float(ms.value)
+
+    def event_destroy(self, event) -> None:
+        self._lib.hipEventDestroy(event)
+
+    # ---------------------------------------------------------------- cleanup
+    def cleanup(self) -> None:
+        if not self._initialized:
+            return
+        try:
+            self._lib.hipDeviceSynchronize()
+        finally:
+            for base in list(self._active_allocations):
+                size, _ = self._active_allocations.pop(base)
+                self._lib.hipFree(ctypes.c_void_p(base))
+                HIPRuntime._process_wide_allocated_bytes = max(0, HIPRuntime._process_wide_allocated_bytes - size)
+            for m in self._modules:
+                self._lib.hipModuleUnload(m)
+            self._modules.clear()
+            if self._stream.value:
+                self._lib.hipStreamDestroy(self._stream)
+                self._stream = ctypes.c_void_p(0)
+            self._initialized = False
+
+    def __enter__(self):
+        if not self.initialize():
+            raise HIPRuntimeError("HIP initialisation failed (no GPU visible?)")
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        self.cleanup()

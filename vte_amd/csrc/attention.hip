@@ -1,0 +1,337 @@
+// Split-KV flash-decoding attention over an fp16 KV cache, gfx950.
+//
+// Reference algorithm: vte/compiler/templates/rdna/kv_cache_append.hip.template:13-39,
+// flash_attention_split_kv_partial.hip.template:31-120 (online softmax per chunk,
+// partial m / l / o) and flash_attention_split_kv_reduce.hip.template:14-67
+// (log-sum-exp combine).  KV layout is the reference's:
+//   cache[b * kv_batch_stride + (pos * n_kv + kv_head) * head_dim + d]   (fp16)
+// and the current position of sequence b is kv_offset[b] (positions 0..kv_offset
+// are valid), read from device memory so one captured graph serves every step.
+//
+// MI355X design of the partial pass (one 256-thread block per (split, kv head, b)):
+//  * GQA-aware: the block serves all G = n_q / n_kv query heads of its KV head,
+//    so every K/V byte is read from HBM once (the reference reads it G times).
+//  * Scores S^T[token][head] = K . Q^T come from MFMA 16x16x32 f16: K rows are
+//    loaded straight into the A operand (16-byte loads), Q^T (padded to 16 heads)
+//    is a per-block constant B operand.  fp32 accumulation.
+//  * Online softmax on the MFMA C registers (one head per lane column), P staged
+//    through LDS, P.V accumulated in fp32 on the VALU with coalesced V row reads.
+//  * Ragged batches: per-sequence split count ceil((kv_offset[b]+1) / split);
+//    blocks past a sequence's last split exit at once, and the combine reads
+//    only that sequence's splits, so each sequence's result is independent of
+//    the batch it sits in.
+#include "vte_common.h"
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+#define ATT_D 128
+#define ATT_WAVES 4
+#define ATT_TILE 32  // tokens per wave step (two 16-token MFMA tiles)
+#define ATT_MAXG 8   // query heads per KV head served by one block
+
+// ---------------------------------------------------------------------------
+// KV append (reference ABI, vte/compiler/templates/rdna/kv_cache_append.hip.template:13-39)
+// grid (batch, n_kv), block (head_dim)
+// ---------------------------------------------------------------------------
+extern "C" __global__ void kv_cache_append_kernel(const __half* __restrict__ k, const __half* __restrict__ v,
+                                                  __half* __restrict__ k_cache, __half* __restrict__ v_cache,
+                                                  int num_kv_heads, int head_dim,
+                                                  const int* __restrict__ kv_cache_offset_ptr,
+                                                  int kv_batch_stride) {
+    const int b = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+    if (t >= head_dim) return;
+    const int pos = kv_cache_offset_ptr[b];
+    const size_t src = ((size_t)b * num_kv_heads + h) * head_dim + t;
+    const size_t dst = (size_t)b * kv_batch_stride + ((size_t)pos * num_kv_heads + h) * head_dim + t;
+    k_cache[dst] = k[src];
+    v_cache[dst] = v[src];
+}
+
+// ---------------------------------------------------------------------------
+// Native partial pass
+// ---------------------------------------------------------------------------
+template <typename TQ>
+__global__ __launch_bounds__(256) void attn_partial_gqa(
+    const TQ* __restrict__ q,            // [B][n_q][D]
+    const __half* __restrict__ k_cache, const __half* __restrict__ v_cache,
+    float* __restrict__ part_m, float* __restrict__ part_l, float* __restrict__ part_o,
+    int n_q, int n_kv, float scale, const int* __restrict__ kv_offset, int kv_batch_stride,
+    int split, int max_splits) {
+    const int sp = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int len = kv_offset[b] + 1;
+    const int t_begin = sp * split;
+    if (t_begin >= len) return;  // past this sequence's last split
+    const int t_end = min(t_begin + split, len);
+    const int G = n_q / n_kv;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int col = lane & 15;   // head (MFMA N index) / token row (A operand)
+    const int grp = lane >> 4;   // 0..3
+
+    __shared__ float p_sh[ATT_WAVES][ATT_TILE][17];   // P tile per wave, [token][head]
+    __shared__ float corr_sh[ATT_WAVES][16];
+    __shared__ float m_sh[ATT_WAVES][16], l_sh[ATT_WAVES][16];
+    __shared__ float o_sh[ATT_WAVES][ATT_MAXG][ATT_D + 4];
+
+    // B operand: Q^T for this KV head's G query heads, fp16, zero-padded to 16.
+    half8_t qb[ATT_D / 32];
+    {
+        const int qh = kvh * G + col;
+        const TQ* qp = q + ((size_t)b * n_q + qh) * ATT_D;
+#pragma unroll
+        for (int s = 0; s < ATT_D / 32; ++s) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float v = (col < G) ? ld_act<TQ>(qp + 32 * s + 8 * grp + j) : 0.f;
+                qb[s][j] = (_Float16)v;
+            }
+        }
+    }
+
+    const size_t row_stride = (size_t)n_kv * ATT_D;  // elements between consecutive positions
+    const __half* kb = k_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
+    const __half* vb = v_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
+
+    float m_run = -1e30f;  // running max of head `col` (identical across grp)
+    float l_run = 0.f;     // per-lane partial denominator of head `col`
+    float o_acc[ATT_MAXG][2];  // O[h][2*lane .. 2*lane+1], h < G
+#pragma unroll
+    for (int h = 0; h < ATT_MAXG; ++h) { o_acc[h][0] = 0.f; o_acc[h][1] = 0.f; }
+
+    for (int t0 = t_begin + wv * ATT_TILE; t0 < t_end; t0 += ATT_WAVES * ATT_TILE) {
+        // ---- scores for 32 tokens: two 16x16 S^T tiles ----
+        floatx4_t acc[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            acc[tt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+            const int tok = t0 + 16 * tt + col;
+            const bool valid = tok < t_end;
+            const __half* kr = kb + (size_t)(valid ? tok : t_begin) * row_stride;
+#pragma unroll
+            for (int s = 0; s < ATT_D / 32; ++s) {
+                half8_t a = *reinterpret_cast<const half8_t*>(kr + 32 * s + 8 * grp);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[s], acc[tt], 0, 0, 0);
+            }
+        }
+        // lane holds S^T[token = t0 + 16*tt + 4*grp + i][head = col]
+        float sc[2][4];
+        float tmax = -1e30f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tok = t0 + 16 * tt + 4 * grp + i;
+                float s = acc[tt][i] * scale;
+                s = (tok < t_end) ? s : -INFINITY;
+                sc[tt][i] = s;
+                tmax = fmaxf(tmax, s);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run, tmax);
+        const float corr = __expf(m_run - m_new);
+        float psum = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = __expf(sc[tt][i] - m_new);
+                psum += p;
+                p_sh[wv][16 * tt + 4 * grp + i][col] = p;
+            }
+        l_run = l_run * corr + psum;
+        m_run = m_new;
+        if (grp == 0) corr_sh[wv][col] = corr;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+
+        // ---- O = O * corr + P . V  (lane owns dims 2*lane, 2*lane+1) ----
+#pragma unroll
+        for (int h = 0; h < ATT_MAXG; ++h) {
+            if (h < G) {
+                const float c = corr_sh[wv][h];
+                o_acc[h][0] *= c;
+                o_acc[h][1] *= c;
+            }
+        }
+        const int nt = min(ATT_TILE, t_end - t0);
+        for (int t = 0; t < nt; ++t) {
+            const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vb + (size_t)(t0 + t) * row_stride + 2 * lane);
+            const float v0 = h2f_bits(v2), v1 = h2f_bits(v2 >> 16);
+#pragma unroll
+            for (int h = 0; h < ATT_MAXG; ++h) {
+                if (h < G) {
+                    const float p = p_sh[wv][t][h];
+                    o_acc[h][0] = fmaf(p, v0, o_acc[h][0]);
+                    o_acc[h][1] = fmaf(p, v1, o_acc[h][1]);
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // ---- combine the four waves of this block ----
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (grp == 0) { m_sh[wv][col] = m_run; l_sh[wv][col] = l_run; }
+#pragma unroll
+    for (int h = 0; h < ATT_MAXG; ++h) {
+        if (h < G) {
+            o_sh[wv][h][2 * lane] = o_acc[h][0];
+            o_sh[wv][h][2 * lane + 1] = o_acc[h][1];
+        }
+    }
+    __syncthreads();
+    // thread -> (head h, dim pair): 256 threads cover 2 heads x 128 dims per pass
+    for (int idx = threadIdx.x; idx < G * ATT_D; idx += 256) {
+        const int h = idx / ATT_D, d = idx % ATT_D;
+        float M = -1e30f;
+#pragma unroll
+        for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, m_sh[w][h]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < ATT_WAVES; ++w) {
+            const float c = __expf(m_sh[w][h] - M);
+            L = fmaf(l_sh[w][h], c, L);
+            O = fmaf(o_sh[w][h][d], c, O);
+        }
+        const int qh = kvh * G + h;
+        const size_t st = ((size_t)b * n_q + qh) * max_splits + sp;
+        part_o[st * ATT_D + d] = O;
+        if (d == 0) { part_m[st] = M; part_l[st] = L; }
+    }
+}
+
+// LSE combine: grid (n_q, B), block 128 (one thread per dim).
+template <typename TO>
+__global__ __launch_bounds__(128) void attn_combine(const float* __restrict__ part_m,
+                                                    const float* __restrict__ part_l,
+                                                    const float* __restrict__ part_o, TO* __restrict__ out,
+                                                    int n_q, const int* __restrict__ kv_offset, int split,
+                                                    int max_splits) {
+    const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int len = kv_offset[b] + 1;
+    const int ns = (len + split - 1) / split;
+    const size_t base = ((size_t)b * n_q + qh) * max_splits;
+    float M = -1e30f;
+    for (int c = 0; c < ns; ++c) M = fmaxf(M, part_m[base + c]);
+    float L = 0.f, O = 0.f;
+    for (int c = 0; c < ns; ++c) {
+        const float w = __expf(part_m[base + c] - M);
+        L = fmaf(part_l[base + c], w, L);
+        O = fmaf(part_o[(base + c) * ATT_D + d], w, O);
+    }
+    st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(L, 1e-20f));
+}
+
+// ---------------------------------------------------------------------------
+// Reference-ABI split-KV kernels (hipModuleGetFunction drop-in).
+// Chunk size is a compile-time constant as in the reference template
+// (flash_attention_split_kv_partial.hip.template:29).
+// ---------------------------------------------------------------------------
+#ifndef SPLIT_KV_CHUNK_SIZE
+#define SPLIT_KV_CHUNK_SIZE 32
+#endif
+
+// grid (batch, n_q, max_chunks), block (head_dim <= 256); one lane per dim,
+// scores reduced with a wave butterfly plus a 4-entry LDS exchange.
+extern "C" __global__ __launch_bounds__(256) void flash_attention_split_kv_partial_kernel(
+    const __half* __restrict__ q, const __half* __restrict__ k_cache, const __half* __restrict__ v_cache,
+    float* __restrict__ partial_m, float* __restrict__ partial_l, float* __restrict__ partial_o,
+    int num_q_heads, int num_kv_heads, int head_dim, float scale, const int* __restrict__ kv_cache_offset_ptr,
+    int kv_batch_stride, int max_chunks) {
+    __shared__ float red[4];
+    const int b = blockIdx.x, qh = blockIdx.y, chunk = blockIdx.z, tid = threadIdx.x;
+    const int total = kv_cache_offset_ptr[b] + 1;
+    const int st = (b * num_q_heads + qh) * max_chunks + chunk;
+    const int start = chunk * SPLIT_KV_CHUNK_SIZE;
+    if (start >= total) {
+        if (tid == 0) { partial_m[st] = -1e30f; partial_l[st] = 0.f; }
+        if (tid < head_dim) partial_o[(size_t)st * head_dim + tid] = 0.f;
+        return;
+    }
+    const int end = min(start + SPLIT_KV_CHUNK_SIZE, total);
+    const int kvh = qh / (num_q_heads / num_kv_heads);
+    const bool act = tid < head_dim;
+    const float qv = act ? __half2float(q[((size_t)b * num_q_heads + qh) * head_dim + tid]) : 0.f;
+    const __half* kc = k_cache + (size_t)b * kv_batch_stride;
+    const __half* vc = v_cache + (size_t)b * kv_batch_stride;
+    const int nw = (blockDim.x + 63) >> 6;
+    float m = -1e30f, l = 0.f, o = 0.f;
+    for (int j = start; j < end; ++j) {
+        const size_t base = ((size_t)j * num_kv_heads + kvh) * head_dim;
+        float part = act ? qv * __half2float(kc[base + tid]) : 0.f;
+        part = wave_sum(part);
+        if ((tid & 63) == 0) red[tid >> 6] = part;
+        __syncthreads();
+        float s = 0.f;
+        for (int w = 0; w < nw; ++w) s += red[w];
+        __syncthreads();
+        s *= scale;
+        const float mn = fmaxf(m, s);
+        const float c = __expf(m - mn);
+        const float p = __expf(s - mn);
+        l = l * c + p;
+        o = o * c + p * (act ? __half2float(vc[base + tid]) : 0.f);
+        m = mn;
+    }
+    if (tid == 0) { partial_m[st] = m; partial_l[st] = l; }
+    if (act) partial_o[(size_t)st * head_dim + tid] = o;
+}
+
+// grid (batch, n_q), block (head_dim); dynamic LDS unused (kept for ABI parity).
+extern "C" __global__ __launch_bounds__(256) void flash_attention_split_kv_reduce_kernel(
+    const float* __restrict__ partial_m, const float* __restrict__ partial_l,
+    const float* __restrict__ partial_o, __half* __restrict__ output, int num_q_heads, int head_dim,
+    int max_chunks) {
+    const int b = blockIdx.x, qh = blockIdx.y, tid = threadIdx.x;
+    const int base = (b * num_q_heads + qh) * max_chunks;
+    float M = -1e30f;
+    for (int c = 0; c < max_chunks; ++c) M = fmaxf(M, partial_m[base + c]);
+    float L = 0.f, O = 0.f;
+    for (int c = 0; c < max_chunks; ++c) {
+        const float w = __expf(partial_m[base + c] - M);
+        L += partial_l[base + c] * w;
+        if (tid < head_dim) O += partial_o[((size_t)base + c) * head_dim + tid] * w;
+    }
+    if (tid < head_dim) output[((size_t)b * num_q_heads + qh) * head_dim + tid] = __float2half(O / fmaxf(L, 1e-20f));
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+namespace vte {
+
+template <typename TQ, typename TO>
+hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache, float* part_m, float* part_l,
+                         float* part_o, void* out, int B, int n_q, int n_kv, float scale, const int* kv_offset,
+                         int kv_batch_stride, int split, int max_splits, hipStream_t st) {
+    dim3 g1(max_splits, n_kv, B), b1(256);
+    hipLaunchKernelGGL((attn_partial_gqa<TQ>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,
+                       (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset,
+                       kv_batch_stride, split, max_splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    dim3 g2(n_q, B), b2(ATT_D);
+    hipLaunchKernelGGL((attn_combine<TO>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q, kv_offset, split,
+                       max_splits);
+    return hipGetLastError();
+}
+
+template hipError_t attn_split_kv<float, float>(const void*, const void*, const void*, float*, float*, float*,
+                                                void*, int, int, int, float, const int*, int, int, int,
+                                                hipStream_t);
+template hipError_t attn_split_kv<__half, __half>(const void*, const void*, const void*, float*, float*, float*,
+                                                  void*, int, int, int, float, const int*, int, int, int,
+                                                  hipStream_t);
+
+hipError_t kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int B, int n_kv, int head_dim,
+                     const int* kv_offset, int kv_batch_stride, hipStream_t st) {
+    hipLaunchKernelGGL(kv_cache_append_kernel, dim3(B, n_kv), dim3(head_dim), 0, st, (const __half*)k,
+                       (const __half*)v, (__half*)k_cache, (__half*)v_cache, n_kv, head_dim, kv_offset,
+                       kv_batch_stride);
+    return hipGetLastError();
+}
+
+}  // namespace vte

@@ -1,0 +1,212 @@
+// C ABI of libvte_amd.so: plain pointers, sizes and a hipStream_t passed as
+// void*.  Every entry point validates shapes on the host before launching, so
+// a kernel never runs with a geometry it does not support.  Return value: 0 on
+// success, VTE_EINVAL (-1) for a rejected argument, otherwise the hipError_t
+// of the failed launch; vte_last_error() gives the message.  Declarations and
+// reference citations: include/vte_amd.h.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "vte_common.h"
+
+#define VTE_EINVAL (-1)
+#define VTE_F32 0
+#define VTE_F16 1
+
+namespace vte {
+template <typename TI, typename TO>
+hipError_t gemv_valu(int fmt, const void* x, const void* w, void* y, int M, int K, int N, const void* bias,
+                     const void* residual, float rs, hipStream_t st);
+hipError_t gemm_mfma(int fmt, int in_dt, int out_dt, const void* x, const void* w, void* y, int M, int K, int N,
+                     const void* bias, const void* residual, float rs, hipStream_t st);
+hipError_t dequantize(int fmt, const void* src, float* dst, long long n_elements, hipStream_t st);
+template <typename TQ, typename TO>
+hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache, float* part_m, float* part_l,
+                         float* part_o, void* out, int B, int n_q, int n_kv, float scale, const int* kv_offset,
+                         int kv_batch_stride, int split, int max_splits, hipStream_t st);
+hipError_t kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int B, int n_kv, int head_dim,
+                     const int* kv_offset, int kv_batch_stride, hipStream_t st);
+hipError_t rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps, hipStream_t st);
+hipError_t rope(void* q, void* k, const void* cosc, const void* sinc, int B, int seq_len, int n_q, int n_kv,
+                int head_dim, const int* kv_offset, int rope_type, int rotary_dim, hipStream_t st);
+hipError_t swiglu(const void* g, const void* u, void* out, int n, hipStream_t st);
+hipError_t add(const void* r, const void* in, void* out, int n, float scale, hipStream_t st);
+hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
+                         hipStream_t st);
+hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, hipStream_t st);
+}  // namespace vte
+
+static thread_local char g_err[512] = "";
+
+static int fail(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return VTE_EINVAL;
+}
+
+static int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return 0;
+    snprintf(g_err, sizeof(g_err), "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+    return (int)e;
+}
+
+#define REQUIRE(cond, ...) \
+    do {                   \
+        if (!(cond)) return fail(__VA_ARGS__); \
+    } while (0)
+
+static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+static int check_gemv(int fmt, int in_dt, int out_dt, const void* x, const void* w, void* y, int M, int K, int N) {
+    REQUIRE(fmt == 4 || fmt == 6 || fmt == 8, "gemv: unknown format %d (4=Q4_K, 6=Q6_K, 8=Q8_0)", fmt);
+    REQUIRE(in_dt == VTE_F32 || in_dt == VTE_F16, "gemv: in_dtype must be 0 (f32) or 1 (f16)");
+    REQUIRE(out_dt == VTE_F32 || out_dt == VTE_F16, "gemv: out_dtype must be 0 (f32) or 1 (f16)");
+    REQUIRE(x && w && y, "gemv: null input/weight/output pointer");
+    REQUIRE(M >= 1 && N >= 1 && K >= 1, "gemv: empty shape M=%d K=%d N=%d", M, K, N);
+    REQUIRE(K % ((fmt == 8) ? 32 : 256) == 0, "gemv: in_features %d not a multiple of the block size", K);
+    REQUIRE(K <= 65536, "gemv: in_features %d exceeds 65536", K);
+    REQUIRE(aligned(x, 16), "gemv: input must be 16-byte aligned");
+    REQUIRE(aligned(w, 16), "gemv: weight must be 16-byte aligned");
+    return 0;
+}
+
+extern "C" {
+
+const char* vte_last_error(void) { return g_err; }
+
+int vte_abi_version(void) { return 1; }
+
+int vte_device_info(int device, int* n_cu, long long* total_mem, char* arch, int arch_len) {
+    REQUIRE(n_cu && total_mem && arch && arch_len > 0, "device_info: null pointer");
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, device);
+    if (e != hipSuccess) return hip_status(e, "hipGetDeviceProperties");
+    *n_cu = p.multiProcessorCount;
+    *total_mem = (long long)p.totalGlobalMem;
+    snprintf(arch, (size_t)arch_len, "%s", p.gcnArchName);
+    return 0;
+}
+
+int vte_gemv(int fmt, int in_dtype, int out_dtype, const void* x, const void* w, void* y, int M, int K, int N,
+             const void* bias, const void* residual, float residual_scale, void* stream) {
+    int rc = check_gemv(fmt, in_dtype, out_dtype, x, w, y, M, K, N);
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e;
+    if (in_dtype == VTE_F32 && out_dtype == VTE_F32)
+        e = vte::gemv_valu<float, float>(fmt, x, w, y, M, K, N, bias, residual, residual_scale, st);
+    else if (in_dtype == VTE_F16 && out_dtype == VTE_F16)
+        e = vte::gemv_valu<__half, __half>(fmt, x, w, y, M, K, N, bias, residual, residual_scale, st);
+    else if (in_dtype == VTE_F16 && out_dtype == VTE_F32)
+        e = vte::gemv_valu<__half, float>(fmt, x, w, y, M, K, N, bias, residual, residual_scale, st);
+    else
+        return fail("gemv: f32 input with f16 output is not provided");
+    return hip_status(e, "vte_gemv launch");
+}
+
+int vte_gemm_mfma(int fmt, int in_dtype, int out_dtype, const void* x, const void* w, void* y, int M, int K,
+                  int N, const void* bias, const void* residual, float residual_scale, void* stream) {
+    int rc = check_gemv(fmt, in_dtype, out_dtype, x, w, y, M, K, N);
+    if (rc) return rc;
+    REQUIRE(fmt == 4 || fmt == 6, "gemm_mfma: Q4_K and Q6_K only");
+    REQUIRE(!(in_dtype == VTE_F32 && out_dtype == VTE_F16), "gemm_mfma: f32 input with f16 output is not provided");
+    return hip_status(vte::gemm_mfma(fmt, in_dtype, out_dtype, x, w, y, M, K, N, bias, residual, residual_scale,
+                                     (hipStream_t)stream),
+                      "vte_gemm_mfma launch");
+}
+
+int vte_dequantize(int fmt, const void* src, float* dst, long long n_elements, void* stream) {
+    REQUIRE(fmt == 4 || fmt == 6 || fmt == 8, "dequantize: unknown format %d", fmt);
+    REQUIRE(src && dst, "dequantize: null pointer");
+    REQUIRE(n_elements > 0 && n_elements % ((fmt == 8) ? 32 : 256) == 0,
+            "dequantize: n_elements %lld not a positive multiple of the block size", n_elements);
+    REQUIRE(n_elements / 256 < (1LL << 31), "dequantize: too many elements");
+    return hip_status(vte::dequantize(fmt, src, dst, n_elements, (hipStream_t)stream), "vte_dequantize launch");
+}
+
+long long vte_attn_scratch_floats(int batch, int n_q, int max_splits) {
+    // part_m + part_l + part_o
+    return (long long)batch * n_q * max_splits * (2 + 128);
+}
+
+int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void* v_cache, float* part_m,
+                      float* part_l, float* part_o, void* out, int batch, int n_q, int n_kv, int head_dim,
+                      float scale, const int* kv_offset, int kv_batch_stride, int split, int max_splits,
+                      void* stream) {
+    REQUIRE(dtype == VTE_F32 || dtype == VTE_F16, "attn: dtype must be 0 (f32) or 1 (f16)");
+    REQUIRE(q && k_cache && v_cache && part_m && part_l && part_o && out && kv_offset, "attn: null pointer");
+    REQUIRE(head_dim == 128, "attn: head_dim %d unsupported (128 only)", head_dim);
+    REQUIRE(batch >= 1 && n_kv >= 1 && n_q >= n_kv && n_q % n_kv == 0, "attn: bad head counts %d/%d", n_q, n_kv);
+    REQUIRE(n_q / n_kv <= 8, "attn: GQA group %d > 8 unsupported", n_q / n_kv);
+    REQUIRE(split >= 32 && split % 32 == 0, "attn: split %d must be a positive multiple of 32", split);
+    REQUIRE(max_splits >= 1 && max_splits <= 65535, "attn: max_splits %d out of range", max_splits);
+    REQUIRE(aligned(k_cache, 16) && aligned(v_cache, 16), "attn: KV cache must be 16-byte aligned");
+    REQUIRE(kv_batch_stride % 8 == 0, "attn: kv_batch_stride must keep rows 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = (dtype == VTE_F32)
+                       ? vte::attn_split_kv<float, float>(q, k_cache, v_cache, part_m, part_l, part_o, out, batch,
+                                                          n_q, n_kv, scale, kv_offset, kv_batch_stride, split,
+                                                          max_splits, st)
+                       : vte::attn_split_kv<__half, __half>(q, k_cache, v_cache, part_m, part_l, part_o, out,
+                                                            batch, n_q, n_kv, scale, kv_offset, kv_batch_stride,
+                                                            split, max_splits, st);
+    return hip_status(e, "vte_attn_split_kv launch");
+}
+
+int vte_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int batch, int n_kv, int head_dim,
+                  const int* kv_offset, int kv_batch_stride, void* stream) {
+    REQUIRE(k && v && k_cache && v_cache && kv_offset, "kv_append: null pointer");
+    REQUIRE(batch >= 1 && n_kv >= 1 && head_dim >= 1 && head_dim <= 1024, "kv_append: bad shape");
+    return hip_status(vte::kv_append(k, v, k_cache, v_cache, batch, n_kv, head_dim, kv_offset, kv_batch_stride,
+                                     (hipStream_t)stream),
+                      "vte_kv_append launch");
+}
+
+int vte_rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps, void* stream) {
+    REQUIRE(x && w && out, "rmsnorm: null pointer");
+    REQUIRE(rows >= 1 && hidden >= 1, "rmsnorm: empty shape");
+    REQUIRE(hidden % 8 != 0 || (aligned(x, 16) && aligned(w, 16) && aligned(out, 16)),
+            "rmsnorm: 16-byte alignment required");
+    return hip_status(vte::rmsnorm(x, w, out, rows, hidden, eps, (hipStream_t)stream), "vte_rmsnorm launch");
+}
+
+int vte_rope(void* q, void* k, const void* cos_cache, const void* sin_cache, int batch, int seq_len, int n_q,
+             int n_kv, int head_dim, const int* kv_offset, int rope_type, int rotary_dim, void* stream) {
+    REQUIRE(q && k && cos_cache && sin_cache && kv_offset, "rope: null pointer");
+    REQUIRE(batch >= 1 && seq_len >= 1 && n_q >= n_kv && n_kv >= 1 && head_dim % 2 == 0, "rope: bad shape");
+    REQUIRE(rope_type >= 0 && rope_type <= 2, "rope: rope_type %d unknown", rope_type);
+    REQUIRE(rope_type != 2 || (rotary_dim > 0 && rotary_dim <= head_dim && rotary_dim % 2 == 0),
+            "rope: bad rotary_dim %d", rotary_dim);
+    return hip_status(vte::rope(q, k, cos_cache, sin_cache, batch, seq_len, n_q, n_kv, head_dim, kv_offset,
+                                rope_type, rotary_dim, (hipStream_t)stream),
+                      "vte_rope launch");
+}
+
+int vte_swiglu(const void* gate, const void* up, void* out, int n, void* stream) {
+    REQUIRE(gate && up && out && n >= 1, "swiglu: bad arguments");
+    return hip_status(vte::swiglu(gate, up, out, n, (hipStream_t)stream), "vte_swiglu launch");
+}
+
+int vte_add(const void* residual, const void* input, void* out, int n, float scale, void* stream) {
+    REQUIRE(residual && input && out && n >= 1, "add: bad arguments");
+    return hip_status(vte::add(residual, input, out, n, scale, (hipStream_t)stream), "vte_add launch");
+}
+
+int vte_embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
+                      void* stream) {
+    REQUIRE(tokens && table && out && n_tokens >= 1, "embedding: bad arguments");
+    REQUIRE(hidden % 256 == 0, "embedding: hidden %d not a multiple of 256", hidden);
+    return hip_status(vte::embedding_q6k(tokens, table, out, n_tokens, hidden, scale, (hipStream_t)stream),
+                      "vte_embedding_q6k launch");
+}
+
+int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* stream) {
+    REQUIRE(logits && out_val && out_idx, "topk: null pointer");
+    REQUIRE(rows >= 1 && k >= 1 && k <= 64 && vocab >= k, "topk: need 1 <= k <= min(64, vocab)");
+    return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, (hipStream_t)stream), "vte_topk launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,280 @@
+// Batched decode GEMM over raw Q4_K / Q6_K super-blocks on MFMA, gfx950.
+//
+//   Y[m, r] = ((sum_k dequant(W[r, k]) * X[m, k] + bias[r]) * rs) + residual[m, r]
+//
+// Same contract as the GEMV (vte/compiler/templates/rdna/gemv_q4k.hip.template:56-168);
+// the reference re-reads W once per batch row (grid.y = batch), this kernel
+// reads it once per 32-column batch tile.
+//
+// Design:
+//  * v_mfma_f32_16x16x32_f16: M = 16 weight rows, N = 16 batch columns,
+//    K = 32.  A block of 8 waves owns RT x 16 rows; each wave takes a
+//    contiguous range of super-blocks (split-K inside the block) and the
+//    partial C tiles are summed through LDS before the epilogue.
+//  * Weights are dequantised in registers to fp16 with packed fp16 math
+//    (nibble -> 0x64xx magic -> exact subtract -> v_pk_fma_f16), so only the
+//    final weight carries an fp16 rounding; activations go to fp16; the MFMA
+//    accumulates in fp32.
+//  * K-slot permutation: MFMA pairs A and B by (lane group, slot), so any
+//    bijection of super-block elements to (k-step, group, slot) is valid as
+//    long as A and B use the same one.  The map is chosen so each lane's 8
+//    slots are 8 contiguous elements sharing one sub-block scale:
+//      Q4_K step t, group g: qs chunk c = g + 4*(t>>2), nibble (t>>1)&1, half t&1
+//      Q6_K step t, group g: half h = t>>2, quarter q = t&3, l = 8g .. 8g+7
+//  * Q4_K rows are 16-byte aligned and load straight from HBM; Q6_K tiles are
+//    staged through LDS with aligned 16-byte loads (blocks are 2-byte aligned).
+#include "quant.h"
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+union H8 {
+    half8_t v;
+    uint32_t u[4];
+    half2_t h2[4];
+};
+
+#define MF_WAVES 8
+#define Q6_SLOT 224  // LDS bytes per staged Q6_K block row (14 aligned chunks)
+
+// bytes b0..b3 of `u` (each < 256, here 6-bit values) -> two fp16 pairs 1024+b.
+__device__ __forceinline__ void bytes_to_f16magic(uint32_t u, uint32_t& lo, uint32_t& hi) {
+    lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+}
+
+// 8 nibble/6-bit values in the bytes of (u0, u1) -> 8 fp16 weights (q - bias) * d - m.
+__device__ __forceinline__ half8_t deq8(uint32_t u0, uint32_t u1, _Float16 sub, half2_t d2, half2_t m2) {
+    H8 r;
+    bytes_to_f16magic(u0, r.u[0], r.u[1]);
+    bytes_to_f16magic(u1, r.u[2], r.u[3]);
+    const half2_t off = {(_Float16)(1024.0f) + sub, (_Float16)(1024.0f) + sub};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.h2[i] = (r.h2[i] - off) * d2 - m2;
+    return r.v;
+}
+
+template <typename TI>
+__device__ __forceinline__ half8_t load_x8(const TI* p, bool valid);
+template <>
+__device__ __forceinline__ half8_t load_x8<__half>(const __half* p, bool valid) {
+    if (!valid) return half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    return *reinterpret_cast<const half8_t*>(p);
+}
+template <>
+__device__ __forceinline__ half8_t load_x8<float>(const float* p, bool valid) {
+    half8_t r = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (!valid) return r;
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    r[0] = (_Float16)a.x; r[1] = (_Float16)a.y; r[2] = (_Float16)a.z; r[3] = (_Float16)a.w;
+    r[4] = (_Float16)b.x; r[5] = (_Float16)b.y; r[6] = (_Float16)b.z; r[7] = (_Float16)b.w;
+    return r;
+}
+
+// Element offset (within a super-block) of step t, group g.
+template <int FMT>
+__device__ __forceinline__ int kslot_base(int t, int g) {
+    if (FMT == 4) {
+        const int c = g + 4 * (t >> 2);
+        return 64 * (c >> 1) + 16 * (c & 1) + 32 * ((t >> 1) & 1) + 8 * (t & 1);
+    } else {
+        return 128 * (t >> 2) + 32 * (t & 3) + 8 * g;
+    }
+}
+
+template <typename TI, typename TO, int FMT, int RT, int NT>
+__global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
+                                                        TO* __restrict__ y, int M, int K, int N,
+                                                        const TO* __restrict__ bias, const TO* __restrict__ residual,
+                                                        float rs) {
+    __shared__ float red[MF_WAVES][RT][NT][4][64];
+    __shared__ uint4 stage_u4[(FMT == 6) ? MF_WAVES * RT * 16 * Q6_SLOT / 16 : 1];
+
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int n_sb = K / QK_K;
+    const int bpr = (FMT == 4) ? Q4K_BYTES : Q6K_BYTES;
+    const size_t row_bytes = (size_t)n_sb * bpr;
+    const int row0 = blockIdx.x * (16 * RT);
+    // contiguous super-block range of this wave
+    const int sb0 = (n_sb * wv) / MF_WAVES, sb1 = (n_sb * (wv + 1)) / MF_WAVES;
+
+    floatx4_t acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    uint8_t* stage = reinterpret_cast<uint8_t*>(stage_u4) + (size_t)wv * RT * 16 * Q6_SLOT;
+
+    for (int sb = sb0; sb < sb1; ++sb) {
+        // ---- B operand (activations) for the 8 k-steps ----
+        half8_t bx[8][NT];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int kb = sb * QK_K + kslot_base<FMT>(t, grp);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int m = nt * 16 + col;
+                bx[t][nt] = load_x8<TI>(x + (size_t)(m < M ? m : 0) * K + kb, m < M);
+            }
+        }
+        if (FMT == 4) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int r = min(row0 + rt * 16 + col, N - 1);
+                const uint8_t* blk = w + (size_t)r * row_bytes + (size_t)sb * Q4K_BYTES;
+                const uint4 h = *reinterpret_cast<const uint4*>(blk);
+                uint4 qc[2];
+                qc[0] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * grp);
+                qc[1] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (grp + 4));
+                Q4KLaneScale s[2];
+                s[0] = q4k_lane_scale(h, grp >> 1);
+                s[1] = q4k_lane_scale(h, 2 + (grp >> 1));
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int ci = t >> 2, part = (t >> 1) & 1, e = t & 1;
+                    const uint32_t wa = (e == 0) ? ((ci == 0) ? qc[0].x : qc[1].x) : ((ci == 0) ? qc[0].z : qc[1].z);
+                    const uint32_t wb = (e == 0) ? ((ci == 0) ? qc[0].y : qc[1].y) : ((ci == 0) ? qc[0].w : qc[1].w);
+                    const uint32_t u0 = part ? ((wa >> 4) & 0x0F0F0F0Fu) : (wa & 0x0F0F0F0Fu);
+                    const uint32_t u1 = part ? ((wb >> 4) & 0x0F0F0F0Fu) : (wb & 0x0F0F0F0Fu);
+                    const float dd = part ? s[ci].d_hi : s[ci].d_lo;
+                    const float mm = part ? s[ci].m_hi : s[ci].m_lo;
+                    const half2_t d2 = {(_Float16)dd, (_Float16)dd};
+                    const half2_t m2 = {(_Float16)mm, (_Float16)mm};
+                    const half8_t a = deq8(u0, u1, (_Float16)0.0f, d2, m2);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx[t][nt], acc[rt][nt], 0, 0, 0);
+                }
+            }
+        } else {
+            // ---- stage RT*16 Q6_K blocks (row r, super-block sb) into LDS ----
+            const int nchunk = RT * 16 * (Q6_SLOT / 16);
+            for (int i = lane; i < nchunk; i += 64) {
+                const int rr = i / (Q6_SLOT / 16), ch = i % (Q6_SLOT / 16);
+                const int r = min(row0 + rr, N - 1);
+                const uintptr_t a = reinterpret_cast<uintptr_t>(w + (size_t)r * row_bytes + (size_t)sb * Q6K_BYTES);
+                const uint4* g = reinterpret_cast<const uint4*>(a & ~(uintptr_t)15);
+                reinterpret_cast<uint4*>(stage + rr * Q6_SLOT)[ch] = g[ch];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int rr = rt * 16 + col;
+                const int r = min(row0 + rr, N - 1);
+                const uintptr_t a = reinterpret_cast<uintptr_t>(w + (size_t)r * row_bytes + (size_t)sb * Q6K_BYTES);
+                const uint8_t* blk = stage + rr * Q6_SLOT + (a & 15);
+                const float d = h2f_bits(lds_u16(blk + 208));
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint8_t* ql = blk + 64 * hh + 8 * grp;
+                    const uint32_t qa0 = lds_u32_a2(ql), qa1 = lds_u32_a2(ql + 4);
+                    const uint32_t qb0 = lds_u32_a2(ql + 32), qb1 = lds_u32_a2(ql + 36);
+                    const uint8_t* qhp = blk + 128 + 32 * hh + 8 * grp;
+                    const uint32_t qh0 = lds_u32_a2(qhp), qh1 = lds_u32_a2(qhp + 4);
+                    const uint8_t* scp = blk + 192 + 8 * hh + (grp >> 1);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        uint32_t u0, u1;
+                        if (q == 0) {
+                            u0 = (qa0 & 0x0F0F0F0Fu) | ((qh0 << 4) & 0x30303030u);
+                            u1 = (qa1 & 0x0F0F0F0Fu) | ((qh1 << 4) & 0x30303030u);
+                        } else if (q == 1) {
+                            u0 = (qb0 & 0x0F0F0F0Fu) | ((qh0 << 2) & 0x30303030u);
+                            u1 = (qb1 & 0x0F0F0F0Fu) | ((qh1 << 2) & 0x30303030u);
+                        } else if (q == 2) {
+                            u0 = ((qa0 >> 4) & 0x0F0F0F0Fu) | (qh0 & 0x30303030u);
+                            u1 = ((qa1 >> 4) & 0x0F0F0F0Fu) | (qh1 & 0x30303030u);
+                        } else {
+                            u0 = ((qb0 >> 4) & 0x0F0F0F0Fu) | ((qh0 >> 2) & 0x30303030u);
+                            u1 = ((qb1 >> 4) & 0x0F0F0F0Fu) | ((qh1 >> 2) & 0x30303030u);
+                        }
+                        const float dsc = d * (float)(int8_t)scp[2 * q];
+                        const half2_t d2 = {(_Float16)dsc, (_Float16)dsc};
+                        const half2_t z2 = {(_Float16)0.0f, (_Float16)0.0f};
+                        const half8_t av = deq8(u0, u1, (_Float16)32.0f, d2, z2);
+                        const int t = 4 * hh + q;
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt)
+                            acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bx[t][nt], acc[rt][nt], 0, 0, 0);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+
+    // ---- split-K reduction across the 8 waves, then the epilogue ----
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wv][rt][nt][i][lane] = acc[rt][nt][i];
+    __syncthreads();
+    // C layout: lane (col, grp) holds rows 4*grp+i of the tile, batch column col.
+    for (int o = threadIdx.x; o < RT * 16 * NT * 16; o += blockDim.x) {
+        const int rr = o / (NT * 16), mc = o % (NT * 16);
+        const int rt = rr >> 4, rw = rr & 15, nt = mc >> 4, cc = mc & 15;
+        const int ln = cc + 16 * (rw >> 2), i = rw & 3;
+        float s = 0.f;
+#pragma unroll
+        for (int wq = 0; wq < MF_WAVES; ++wq) s += red[wq][rt][nt][i][ln];
+        const int row = row0 + rr;
+        if (row < N && mc < M) gemv_store<TO>(y, bias, residual, rs, row, mc, N, s);
+    }
+}
+
+namespace vte {
+
+template <typename TI, typename TO, int FMT, int RT, int NT>
+static void launch_tile(const TI* x, const void* w, TO* y, int M, int K, int N, const void* bias,
+                        const TO* residual, float rs, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<TI, TO, FMT, RT, NT>), dim3((N + 16 * RT - 1) / (16 * RT)),
+                       dim3(64 * MF_WAVES), 0, st, x, (const uint8_t*)w, y, M, K, N, (const TO*)bias, residual, rs);
+}
+
+// Batch columns are processed in chunks of 32 (two 16-wide MFMA N tiles).
+// Q4_K uses 32-row tiles on tall matrices; Q6_K keeps 16-row tiles so its
+// LDS staging stays small enough for several blocks per CU.
+template <typename TI, typename TO, int FMT>
+static hipError_t launch_mfma(const void* x, const void* w, void* y, int M, int K, int N, const void* bias,
+                              const void* residual, float rs, hipStream_t st) {
+    const bool tall = (FMT == 4) && N >= 4096;
+    for (int m0 = 0; m0 < M; m0 += 32) {
+        const int mc = (M - m0 < 32) ? (M - m0) : 32;
+        const TI* xs = (const TI*)x + (size_t)m0 * K;
+        TO* ys = (TO*)y + (size_t)m0 * N;
+        const TO* rp = residual ? (const TO*)residual + (size_t)m0 * N : nullptr;
+        if (mc > 16) {
+            if (tall) launch_tile<TI, TO, FMT, 2, 2>(xs, w, ys, mc, K, N, bias, rp, rs, st);
+            else launch_tile<TI, TO, FMT, 1, 2>(xs, w, ys, mc, K, N, bias, rp, rs, st);
+        } else {
+            if (tall) launch_tile<TI, TO, FMT, 2, 1>(xs, w, ys, mc, K, N, bias, rp, rs, st);
+            else launch_tile<TI, TO, FMT, 1, 1>(xs, w, ys, mc, K, N, bias, rp, rs, st);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t gemm_mfma(int fmt, int in_dt, int out_dt, const void* x, const void* w, void* y, int M, int K, int N,
+                     const void* bias, const void* residual, float rs, hipStream_t st) {
+    // dtype codes: 0 = f32, 1 = f16
+    if (fmt == 4) {
+        if (in_dt == 0) return launch_mfma<float, float, 4>(x, w, y, M, K, N, bias, residual, rs, st);
+        if (out_dt == 1) return launch_mfma<__half, __half, 4>(x, w, y, M, K, N, bias, residual, rs, st);
+        return launch_mfma<__half, float, 4>(x, w, y, M, K, N, bias, residual, rs, st);
+    }
+    if (in_dt == 0) return launch_mfma<float, float, 6>(x, w, y, M, K, N, bias, residual, rs, st);
+    if (out_dt == 1) return launch_mfma<__half, __half, 6>(x, w, y, M, K, N, bias, residual, rs, st);
+    return launch_mfma<__half, float, 6>(x, w, y, M, K, N, bias, residual, rs, st);
+}
+
+}  // namespace vte

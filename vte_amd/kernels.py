@@ -1,0 +1,147 @@
+"""ctypes binding of libvte_amd.so (the C ABI declared in include/vte_amd.h).
+
+The library is built in-tree by ``vte_amd.build``.  There is no fallback: if
+the shared object is missing or lacks a symbol, loading raises, so no caller
+can silently run anything but the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+from .bridge.hip_runtime import HIPRuntimeError, HIPSafetyError
+
+LIB_PATH = Path(__file__).resolve().parent / "libvte_amd.so"
+HSACO_PATH = Path(__file__).resolve().parent / "vte_kernels_gfx950.hsaco"
+
+FMT = {"q4_k": 4, "q6_k": 6, "q8_0": 8}
+DT = {"f32": 0, "f16": 1}
+
+_vp, _i, _f, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
+_IP = ctypes.POINTER(ctypes.c_int)
+_FP = ctypes.POINTER(ctypes.c_float)
+
+# name -> argtypes (every entry returns int status except where noted)
+SIGNATURES = {
+    "vte_abi_version": [],
+    "vte_device_info": [_i, _IP, ctypes.POINTER(_ll), ctypes.c_char_p, _i],
+    "vte_gemv": [_i, _i, _i, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _f, _vp],
+    "vte_gemm_mfma": [_i, _i, _i, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _f, _vp],
+    "vte_dequantize": [_i, _vp, _vp, _ll, _vp],
+    "vte_attn_scratch_floats": [_i, _i, _i],
+    "vte_attn_split_kv": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _i, _i, _i, _vp],
+    "vte_kv_append": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp],
+    "vte_rmsnorm": [_vp, _vp, _vp, _i, _i, _f, _vp],
+    "vte_rope": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i, _i, _vp],
+    "vte_swiglu": [_vp, _vp, _vp, _i, _vp],
+    "vte_add": [_vp, _vp, _vp, _i, _f, _vp],
+    "vte_embedding_q6k": [_vp, _vp, _vp, _i, _i, _f, _vp],
+    "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp],
+    "vte_last_error": [],
+}
+RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll}
+
+
+def _p(x) -> Optional[int]:
+    """Device pointer argument: int, c_void_p, an object with ``.ptr`` or None."""
+    if x is None:
+        return None
+    if isinstance(x, ctypes.c_void_p):
+        return x.value
+    if hasattr(x, "ptr"):
+        return int(x.ptr)
+    return int(x)
+
+
+class VTEKernels:
+    """Loaded libvte_amd.so with checked wrappers."""
+
+    def __init__(self, path: Path = LIB_PATH):
+        if not Path(path).exists():
+            raise HIPRuntimeError(f"{path} is not built: run `python -m vte_amd.build` (hipcc, gfx950)")
+        self.lib = ctypes.CDLL(str(path))
+        for name, args in SIGNATURES.items():
+            fn = getattr(self.lib, name)  # AttributeError if the symbol is missing
+            fn.argtypes = args
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
+
+    def _check(self, rc: int, what: str) -> None:
+        if rc != 0:
+            msg = self.lib.vte_last_error().decode()
+            if rc == -1:
+                raise HIPSafetyError(f"{what}: {msg}")
+            raise HIPRuntimeError(f"{what}: {msg}")
+
+    @staticmethod
+    def _st(stream) -> Optional[int]:
+        return _p(stream)
+
+    def device_info(self, device: int = 0) -> dict:
+        n_cu, mem = ctypes.c_int(0), ctypes.c_longlong(0)
+        arch = ctypes.create_string_buffer(64)
+        self._check(self.lib.vte_device_info(device, ctypes.byref(n_cu), ctypes.byref(mem), arch, 64), "device_info")
+        return {"num_cus": n_cu.value, "total_mem": mem.value, "arch": arch.value.decode()}
+
+    def gemv(self, fmt: str, x, w, y, M: int, K: int, N: int, bias=None, residual=None, residual_scale=1.0,
+             in_dtype="f32", out_dtype="f32", stream=None) -> None:
+        """y[M,N] = dequant(W[N,K]) @ x[M,K] (+ epilogue) on the VALU GEMV kernels."""
+        self._check(self.lib.vte_gemv(FMT[fmt], DT[in_dtype], DT[out_dtype], _p(x), _p(w), _p(y), M, K, N, _p(bias),
+                                      _p(residual), residual_scale, self._st(stream)), "vte_gemv")
+
+    def gemm_mfma(self, fmt: str, x, w, y, M: int, K: int, N: int, bias=None, residual=None, residual_scale=1.0,
+                  in_dtype="f32", out_dtype="f32", stream=None) -> None:
+        """Same contract on the MFMA dequant-to-fp16 kernels (Q4_K / Q6_K)."""
+        self._check(self.lib.vte_gemm_mfma(FMT[fmt], DT[in_dtype], DT[out_dtype], _p(x), _p(w), _p(y), M, K, N,
+                                           _p(bias), _p(residual), residual_scale, self._st(stream)), "vte_gemm_mfma")
+
+    def dequantize(self, fmt: str, src, dst, n_elements: int, stream=None) -> None:
+        self._check(self.lib.vte_dequantize(FMT[fmt], _p(src), _p(dst), n_elements, self._st(stream)),
+                    "vte_dequantize")
+
+    def attn_scratch_floats(self, batch: int, n_q: int, max_splits: int) -> int:
+        return int(self.lib.vte_attn_scratch_floats(batch, n_q, max_splits))
+
+    def attn_split_kv(self, q, k_cache, v_cache, part_m, part_l, part_o, out, batch, n_q, n_kv, head_dim, scale,
+                      kv_offset, kv_batch_stride, split, max_splits, dtype="f32", stream=None) -> None:
+        self._check(self.lib.vte_attn_split_kv(DT[dtype], _p(q), _p(k_cache), _p(v_cache), _p(part_m), _p(part_l),
+                                               _p(part_o), _p(out), batch, n_q, n_kv, head_dim, scale, _p(kv_offset),
+                                               kv_batch_stride, split, max_splits, self._st(stream)),
+                    "vte_attn_split_kv")
+
+    def kv_append(self, k, v, k_cache, v_cache, batch, n_kv, head_dim, kv_offset, kv_batch_stride, stream=None):
+        self._check(self.lib.vte_kv_append(_p(k), _p(v), _p(k_cache), _p(v_cache), batch, n_kv, head_dim,
+                                           _p(kv_offset), kv_batch_stride, self._st(stream)), "vte_kv_append")
+
+    def rmsnorm(self, x, w, out, rows, hidden, eps, stream=None):
+        self._check(self.lib.vte_rmsnorm(_p(x), _p(w), _p(out), rows, hidden, eps, self._st(stream)), "vte_rmsnorm")
+
+    def rope(self, q, k, cos_cache, sin_cache, batch, seq_len, n_q, n_kv, head_dim, kv_offset, rope_type=0,
+             rotary_dim=0, stream=None):
+        self._check(self.lib.vte_rope(_p(q), _p(k), _p(cos_cache), _p(sin_cache), batch, seq_len, n_q, n_kv,
+                                      head_dim, _p(kv_offset), rope_type, rotary_dim, self._st(stream)), "vte_rope")
+
+    def swiglu(self, gate, up, out, n, stream=None):
+        self._check(self.lib.vte_swiglu(_p(gate), _p(up), _p(out), n, self._st(stream)), "vte_swiglu")
+
+    def add(self, residual, inp, out, n, scale=1.0, stream=None):
+        self._check(self.lib.vte_add(_p(residual), _p(inp), _p(out), n, scale, self._st(stream)), "vte_add")
+
+    def embedding_q6k(self, tokens, table, out, n_tokens, hidden, scale=1.0, stream=None):
+        self._check(self.lib.vte_embedding_q6k(_p(tokens), _p(table), _p(out), n_tokens, hidden, scale,
+                                               self._st(stream)), "vte_embedding_q6k")
+
+    def topk(self, logits, rows, vocab, k, out_val, out_idx, stream=None):
+        self._check(self.lib.vte_topk(_p(logits), rows, vocab, k, _p(out_val), _p(out_idx), self._st(stream)),
+                    "vte_topk")
+
+
+_KERNELS: Optional[VTEKernels] = None
+
+
+def kernels() -> VTEKernels:
+    """Process-wide loaded library (raises if it is not built)."""
+    global _KERNELS
+    if _KERNELS is None:
+        _KERNELS = VTEKernels()
+    return _KERNELS
