@@ -1,0 +1,212 @@
+"""Benchmark of the MI355X decode hot path (one GPU).
+
+Workload: one decode step of a random-init Qwen2.5-1.5B
+shaped model (28 layers, Q4_K_M-style weights, tied Q6_K LM head, 2048-token
+fp16 KV prefix, on-device top-k 40) captured as one hipGraph.  A "step" is one
+replay of that graph; ``value`` is batch-1 decode tokens/s with every input
+resident in HBM.  The same line carries the batch-16 step, the quant-GEMV
+bandwidth of configs 0/1 on a cold (> 256 MB MALL) rotating weight pool, the
+roofline of the dominant kernel and a CPU baseline (the NumPy oracle on the
+host cores, bounded sample).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "quant GEMV HBM GB/s (% peak); decode tok/s 1.5B-shape at batch 1/16"
+HBM_PEAK_GBPS = 8000.0
+
+
+def _events(hip):
+    return hip.event_create(), hip.event_create()
+
+
+def time_graph(hip, ex, steps, warmup):
+    ex.build_decode_graph()
+    ex.replay(warmup)
+    hip.synchronize()
+    e0, e1 = _events(hip)
+    t0 = time.perf_counter()
+    hip.event_record(e0)
+    ex.replay(steps)
+    hip.event_record(e1)
+    ms = hip.event_elapsed_ms(e0, e1)
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    return ms / steps, wall
+
+
+def time_e2e(hip, ex, steps, start_pos):
+    """Per-token loop as a caller runs it: stage token/offset, replay, read top-k, sample."""
+    from vte_amd.core.sampler import Sampler
+    rng = np.random.default_rng(0)
+    toks = [1] * ex.B
+    t0 = time.perf_counter()
+    for s in range(steps):
+        ex.execute_decode_batch(toks, [start_pos + s] * ex.B)
+        vals, idx = ex.read_topk()
+        toks = [Sampler.sample_candidates(vals[b], idx[b], 0.7, 0.9, rng) for b in range(ex.B)]
+    return (time.perf_counter() - t0) / steps
+
+
+def gemv_bench(hip, K, fmt, n, k, launches=200, pool_bytes=768 << 20, mfma_batch=0):
+    """Average kernel time over a rotating cold pool; returns dict with GB/s."""
+    from vte_amd import synthetic as syn
+    from vte_amd.bridge import DeviceArray
+    raw = syn.random_matrix(fmt, np.random.default_rng(42), n, k)
+    copies = max(2, int(np.ceil(pool_bytes / raw.nbytes)))
+    pool = DeviceArray(hip, copies * raw.nbytes + 256, np.uint8, f"pool_{fmt}")
+    first = DeviceArray.from_numpy(hip, raw, "w0")
+    stride = raw.nbytes
+    for c in range(copies):
+        hip.memcpy_device_to_device(pool.ptr + c * stride, first.ptr, stride)
+    M = max(1, mfma_batch)
+    x = DeviceArray.from_numpy(hip, np.random.default_rng(1).standard_normal((M, k)).astype(np.float32), "x")
+    y = DeviceArray(hip, (M, n), np.float32, "y")
+    run = (lambda w: K.gemm_mfma(fmt, x, w, y, M, k, n, stream=hip.stream)) if mfma_batch else \
+          (lambda w: K.gemv(fmt, x, w, y, M, k, n, stream=hip.stream))
+    for c in range(min(copies, 20)):
+        run(pool.ptr + c * stride)
+    hip.synchronize()
+    e0, e1 = _events(hip)
+    hip.event_record(e0)
+    for i in range(launches):
+        run(pool.ptr + (i % copies) * stride)
+    hip.event_record(e1)
+    ms = hip.event_elapsed_ms(e0, e1) / launches
+    algo = raw.nbytes + M * k * 4 + M * n * 4
+    for d in (pool, first, x, y):
+        d.free()
+    return {"shape": f"{n}x{k}", "fmt": fmt, "batch": M, "us": round(ms * 1e3, 3),
+            "algo_bytes": int(algo), "GBps": round(algo / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def cpu_baseline(seconds_budget=20.0):
+    """NumPy restatement of the decode step on the host cores: 2 of 28 layers
+    (one Q6_K-down, one Q4_K-down) plus the LM head, dequantised weights cached
+    outside the timed region, per-layer time scaled to 28 layers."""
+    from oracle import step as ost
+    from vte_amd.core.model_config import QWEN25_1P5B
+    from vte_amd.core.weights import SyntheticQwen2
+    cfg = QWEN25_1P5B.with_(n_layers=2, max_seq=2304)
+    model = SyntheticQwen2(cfg, seed=0)
+    rng = np.random.default_rng(0)
+    ks = [(0.5 * rng.standard_normal((1, 2304, 2, 128))).astype(np.float16) for _ in range(2)]
+    vs = [(0.5 * rng.standard_normal((1, 2304, 2, 128))).astype(np.float16) for _ in range(2)]
+    cache = {}
+    ost.decode_step(model, [1], [2048], ks, vs, cache)  # warm: dequantise once
+    t_all, n = 0.0, 0
+    t0 = time.perf_counter()
+    while n < 3 or (time.perf_counter() - t0 < seconds_budget and n < 20):
+        s = time.perf_counter()
+        ost.decode_step(model, [1], [2048], ks, vs, cache)
+        t_all += time.perf_counter() - s
+        n += 1
+    step2 = t_all / n
+    # split: LM head alone
+    hn = np.ones(cfg.hidden, np.float16)
+    s = time.perf_counter()
+    for _ in range(3):
+        cache["lm"] @ hn.astype(np.float32)
+    lm = (time.perf_counter() - s) / 3
+    per_layer = max(step2 - lm, 1e-9) / 2
+    est = per_layer * 28 + lm
+    threads = os.environ.get("OMP_NUM_THREADS") or str(os.cpu_count())
+    return {"value": round(1.0 / est, 3), "unit": "tok/s", "cores": int(threads), "kind": "port",
+            "sample": f"NumPy oracle decode step, batch 1, 2 of 28 layers + LM head at position 2048 "
+                      f"(dequant cached), {n} trials, per-layer time x28 + LM head"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="skip the batch-16 step and GEMV sweep")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+
+    from vte_amd.bridge import HIPRuntime
+    from vte_amd.core.hip_graph_executor import HIPGraphExecutor
+    from vte_amd.core.model_config import QWEN25_1P5B
+    from vte_amd.core.weights import SyntheticQwen2
+    from vte_amd.kernels import kernels
+
+    hip = HIPRuntime()
+    if not hip.initialize():
+        print(json.dumps({"error": "HIP initialisation failed"}))
+        sys.exit(1)
+    K = kernels()
+    t_gen = time.perf_counter()
+    model = SyntheticQwen2(QWEN25_1P5B, seed=0)
+    t_gen = time.perf_counter() - t_gen
+    wbytes = model.weight_bytes()
+    prefix = 2048
+    result = {}
+    for B in ([1] if args.quick else [1, 16]):
+        ex = HIPGraphExecutor(hip, model, batch_size=B, max_seq=prefix + 256)
+        ex.fill_kv_prefix(seed=B)
+        ex._update_staging_buffers([1] * B, [prefix] * B)
+        ms, wall = time_graph(hip, ex, args.steps, args.warmup)
+        e2e = time_e2e(hip, ex, 20, prefix)
+        kv_read = QWEN25_1P5B.n_layers * (prefix + 1) * QWEN25_1P5B.n_kv * QWEN25_1P5B.head_dim * 2 * 2 * B
+        step_bytes = wbytes + kv_read
+        result[B] = {"ms_per_step": ms, "tok_s": B / (ms * 1e-3), "wall_s": wall, "e2e_ms_per_step": e2e * 1e3,
+                     "step_bytes": step_bytes, "step_GBps": step_bytes / (ms * 1e-3) / 1e9}
+        ex.close()
+
+    gemv = []
+    if not args.quick:
+        gemv.append(gemv_bench(hip, K, "q4_k", 8960, 1536))
+        gemv.append(gemv_bench(hip, K, "q6_k", 1536, 8960))
+        gemv.append(gemv_bench(hip, K, "q6_k", 151936, 1536, launches=50, pool_bytes=600 << 20))
+        gemv.append(gemv_bench(hip, K, "q8_0", 2048, 2048))
+        gemv.append(gemv_bench(hip, K, "q4_k", 8960, 1536, mfma_batch=16))
+    dom = gemv[0] if gemv else None
+    cpu = None if args.no_cpu else cpu_baseline()
+    r1 = result[1]
+    line = {
+        "metric": METRIC, "value": round(r1["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(r1["ms_per_step"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_k/q6_k weights, f16 activations, f32 accumulate",
+        "data": "synthetic (random-init Q4_K_M-style weights, random fp16 KV prefix)",
+        "config": {"workload": "config4: Qwen2.5-1.5B-shape decode step as one hipGraph, batch 1, "
+                               "2048-token fp16 KV prefix, on-device top-k 40",
+                   "layers": 28, "hidden": 1536, "ffn": 8960, "heads": "12q/2kv x128", "vocab": 151936,
+                   "kv_prefix": prefix, "batch": 1},
+        "step_GBps_b1": round(r1["step_GBps"], 1),
+        "step_frac_hbm_b1": round(r1["step_GBps"] / HBM_PEAK_GBPS, 4),
+        "e2e_tok_s_b1": round(1e3 / r1["e2e_ms_per_step"], 2),
+        "weight_gen_s": round(t_gen, 1),
+    }
+    if 16 in result:
+        r16 = result[16]
+        line.update({"tok_s_b16": round(r16["tok_s"], 2), "ms_per_step_b16": round(r16["ms_per_step"], 4),
+                     "step_GBps_b16": round(r16["step_GBps"], 1),
+                     "e2e_tok_s_b16": round(16e3 / r16["e2e_ms_per_step"], 2)})
+    if gemv:
+        line["gemv"] = gemv
+    if dom:
+        line["roofline"] = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                            "frac": dom["frac_hbm_peak"], "traffic": None,
+                            "kernel": "gemv_q4k_rows (config 0: Q4_K 8960x1536, batch 1, cold pool)"}
+    if cpu:
+        line["cpu_baseline"] = cpu
+    print(json.dumps(line))
+    hip.cleanup()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,232 @@
+"""Decode-step executor: the whole Qwen2.5 decode step captured as one hipGraph.
+
+Host API mirrors the reference executors (vte/core/hip_graph_executor.py:740-819,
+vte/core/batched_hip_graph_executor.py:272-292): ``build_decode_graph``,
+``execute_decode(token_id, kv_offset)`` for batch 1 and
+``execute_decode_batch(tokens, kv_offsets)`` for a batch; dynamic per-step
+values live in fixed device staging buffers updated by H2D copies before
+``hipGraphLaunch``.  Node order per layer follows vte/compiler/qwen_compute.py:100-282.
+
+MI355X-specific structure:
+* every tensor lives in one slab (fixed addresses for capture), KV cache per
+  layer [B][max_seq][n_kv][hd] fp16 as in vte/compiler/qwen_mapper.py:300-351;
+* projections run the VALU quant GEMV below ``gemm_min_batch`` sequences and
+  the MFMA dequant-to-fp16 GEMM at or above it;
+* attention is the GQA split-KV pair (partial + combine) with per-sequence
+  lengths read from ``kv_offset`` on the device, so ragged batches share a graph;
+* the LM head writes fp32 logits and an on-device top-k (default 40) leaves
+  only k candidates per sequence to copy back for sampling;
+* residual adds are fused into the o/down GEMV epilogues with ping-pong
+  hidden buffers (the output never aliases the residual input).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import numpy as np
+
+from ..bridge.hip_runtime import HIPRuntime, HIPSafetyError
+from ..bridge.memory import DeviceArray, MemoryRegion, SlabAllocator
+from ..kernels import kernels
+from .model_config import Qwen2Config
+from .rope_cache import build_rope_cache
+from .split_kv_attention import SplitKVAttentionDispatcher
+from .weights import PROJ, SyntheticQwen2, proj_shape
+
+
+class GraphCaptureError(RuntimeError):
+    pass
+
+
+class HIPGraphExecutor:
+    def __init__(self, hip: HIPRuntime, model: SyntheticQwen2, batch_size: int = 1, max_seq: Optional[int] = None,
+                 top_k: int = 40, gemm_min_batch: int = 8, split: Optional[int] = None):
+        self.hip = hip
+        self.cfg: Qwen2Config = model.cfg
+        cfg = self.cfg
+        self.B = batch_size
+        self.max_seq = max_seq or cfg.max_seq
+        self.top_k = top_k
+        self.gemm_min_batch = gemm_min_batch
+        self.K = kernels()
+        self.graph = None
+        self.graph_exec = None
+
+        B, H = batch_size, cfg.hidden
+        kv_elems = B * self.max_seq * cfg.n_kv * cfg.head_dim
+        act_bytes = 4 * (B * (2 * H + cfg.q_dim * 2 + cfg.kv_dim * 2 + 3 * cfg.ffn) * 2 + B * cfg.vocab * 4)
+        need = model.weight_bytes() + 2 * cfg.n_layers * kv_elems * 2 + act_bytes + (64 << 20)
+        need += (cfg.n_layers * len(PROJ) + 16) * 1024  # alignment and slack per tensor
+        self.slab = SlabAllocator(hip, 0, requested_pool_size=need + (256 << 20))
+        self.slab.initialize()
+        A = lambda shape, dt, tag, reg=MemoryRegion.ACTIVATIONS: DeviceArray(hip, shape, dt, tag, self.slab, reg)
+        W = lambda arr, tag: DeviceArray.from_numpy(hip, arr, tag, self.slab, MemoryRegion.WEIGHTS)
+
+        # ---- weights ----
+        self.token_embd = W(model.token_embd, "token_embd")
+        self.output_norm = W(model.output_norm, "output_norm")
+        self.layers = []
+        for L, lw in enumerate(model.layers):
+            d = {}
+            for p in PROJ:
+                d[p] = W(lw[p], f"blk.{L}.{p}")
+                d[p + "_fmt"] = lw[p + "_fmt"]
+            for name in ("q_bias", "k_bias", "v_bias", "attn_norm", "ffn_norm"):
+                d[name] = W(lw[name], f"blk.{L}.{name}")
+            self.layers.append(d)
+        # ---- KV cache ----
+        self.kv_batch_stride = self.max_seq * cfg.n_kv * cfg.head_dim
+        kv_shape = (B, self.max_seq, cfg.n_kv, cfg.head_dim)
+        self.k_cache = [A(kv_shape, np.float16, f"blk.{L}.k_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
+        self.v_cache = [A(kv_shape, np.float16, f"blk.{L}.v_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
+        # ---- activations (fp16 between nodes, fp32 logits) ----
+        self.h = [A((B, H), np.float16, "hidden0"), A((B, H), np.float16, "hidden1")]
+        self.xn = A((B, H), np.float16, "normed")
+        self.q = A((B, cfg.q_dim), np.float16, "q")
+        self.k = A((B, cfg.kv_dim), np.float16, "k")
+        self.v = A((B, cfg.kv_dim), np.float16, "v")
+        self.att = A((B, cfg.q_dim), np.float16, "attn_out")
+        self.g = A((B, cfg.ffn), np.float16, "gate")
+        self.u = A((B, cfg.ffn), np.float16, "up")
+        self.a = A((B, cfg.ffn), np.float16, "swiglu")
+        self.logits = A((B, cfg.vocab), np.float32, "logits")
+        self.topk_val = A((B, max(top_k, 1)), np.float32, "topk_val")
+        self.topk_idx = A((B, max(top_k, 1)), np.int32, "topk_idx")
+        self.staging_input = A(B, np.int32, "staging_tokens")
+        self.staging_kv_offset = A(B, np.int32, "staging_kv_offset")
+        cos_c, sin_c = build_rope_cache(self.max_seq, cfg.head_dim, cfg.rope_theta)
+        self.rope_cos = W(cos_c, "rope_cos")
+        self.rope_sin = W(sin_c, "rope_sin")
+        self.attn = SplitKVAttentionDispatcher(hip, cfg.n_q, cfg.n_kv, cfg.head_dim, self.max_seq, B, split,
+                                               allocator=self.slab)
+        self.h_final = 0  # index of the hidden buffer holding the layer output
+
+    # ------------------------------------------------------------------ kernels
+    def _linear(self, fmt, x, w, y, K_in, N, bias=None, residual=None, out_dtype="f16"):
+        st = self.hip.stream
+        if self.B >= self.gemm_min_batch and fmt in ("q4_k", "q6_k"):
+            self.K.gemm_mfma(fmt, x, w, y, self.B, K_in, N, bias=bias, residual=residual, in_dtype="f16",
+                             out_dtype=out_dtype, stream=st)
+        else:
+            self.K.gemv(fmt, x, w, y, self.B, K_in, N, bias=bias, residual=residual, in_dtype="f16",
+                        out_dtype=out_dtype, stream=st)
+
+    def enqueue_step(self) -> None:
+        """Issue every kernel of one decode step on the runtime stream."""
+        cfg, K, st, B = self.cfg, self.K, self.hip.stream, self.B
+        H = cfg.hidden
+        offs = self.staging_kv_offset
+        cur = 0
+        K.embedding_q6k(self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
+        for L, lw in enumerate(self.layers):
+            K.rmsnorm(self.h[cur], lw["attn_norm"], self.xn, B, H, cfg.eps, stream=st)
+            self._linear(lw["q_fmt"], self.xn, lw["q"], self.q, H, cfg.q_dim, bias=lw["q_bias"])
+            self._linear(lw["k_fmt"], self.xn, lw["k"], self.k, H, cfg.kv_dim, bias=lw["k_bias"])
+            self._linear(lw["v_fmt"], self.xn, lw["v"], self.v, H, cfg.kv_dim, bias=lw["v_bias"])
+            K.rope(self.q, self.k, self.rope_cos, self.rope_sin, B, 1, cfg.n_q, cfg.n_kv, cfg.head_dim, offs, 0, 0,
+                   stream=st)
+            K.kv_append(self.k, self.v, self.k_cache[L], self.v_cache[L], B, cfg.n_kv, cfg.head_dim, offs,
+                        self.kv_batch_stride, stream=st)
+            self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], self.att, offs, self.kv_batch_stride,
+                             dtype="f16", batch=B, stream=st)
+            self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
+            cur = 1 - cur
+            K.rmsnorm(self.h[cur], lw["ffn_norm"], self.xn, B, H, cfg.eps, stream=st)
+            self._linear(lw["gate_fmt"], self.xn, lw["gate"], self.g, H, cfg.ffn)
+            self._linear(lw["up_fmt"], self.xn, lw["up"], self.u, H, cfg.ffn)
+            K.swiglu(self.g, self.u, self.a, B * cfg.ffn, stream=st)
+            self._linear(lw["down_fmt"], self.a, lw["down"], self.h[1 - cur], cfg.ffn, H, residual=self.h[cur])
+            cur = 1 - cur
+        self.h_final = cur
+        K.rmsnorm(self.h[cur], self.output_norm, self.xn, B, H, cfg.eps, stream=st)
+        self._linear("q6_k", self.xn, self.token_embd, self.logits, H, cfg.vocab, out_dtype="f32")
+        if self.top_k > 0:
+            K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, stream=st)
+
+    # -------------------------------------------------------------------- graph
+    def build_decode_graph(self) -> None:
+        if self.graph_exec is not None:
+            return
+        self.hip.stream_synchronize()
+        self.hip.stream_begin_capture()
+        try:
+            self.enqueue_step()
+        except Exception as e:
+            try:
+                g = self.hip.stream_end_capture()
+                self.hip.graph_destroy(g)
+            except Exception:
+                pass
+            raise GraphCaptureError(f"decode-step capture failed: {e}") from e
+        self.graph = self.hip.stream_end_capture()
+        self.graph_exec = self.hip.graph_instantiate(self.graph)
+
+    def _update_staging_buffers(self, tokens: Sequence[int], kv_offsets: Sequence[int]) -> None:
+        if len(tokens) != self.B or len(kv_offsets) != self.B:
+            raise HIPSafetyError(f"expected {self.B} tokens and offsets, got {len(tokens)}/{len(kv_offsets)}")
+        offs = np.asarray(kv_offsets, np.int32)
+        if offs.min() < 0 or offs.max() >= self.max_seq:
+            raise HIPSafetyError(f"kv_offset outside [0, {self.max_seq})")
+        toks = np.asarray(tokens, np.int32)
+        if toks.min() < 0 or toks.max() >= self.cfg.vocab:
+            raise HIPSafetyError("token id outside the vocabulary")
+        self.staging_input.upload(toks)
+        self.staging_kv_offset.upload(offs)
+
+    def execute_decode_batch(self, tokens: Sequence[int], kv_offsets: Sequence[int], use_graph: bool = True,
+                             sync: bool = True) -> None:
+        """One token per sequence, sequence b at position kv_offsets[b]."""
+        self._update_staging_buffers(tokens, kv_offsets)
+        if use_graph:
+            self.build_decode_graph()
+            self.hip.graph_launch(self.graph_exec)
+        else:
+            self.enqueue_step()
+        if sync:
+            self.hip.synchronize()
+
+    def execute_decode(self, token_id: int, kv_offset: int, use_graph: bool = True) -> None:
+        if self.B != 1:
+            raise HIPSafetyError("execute_decode is the batch-1 entry point; use execute_decode_batch")
+        self.execute_decode_batch([token_id], [kv_offset], use_graph)
+
+    def replay(self, n: int) -> None:
+        """Launch the captured graph n times back to back (staging unchanged)."""
+        self.build_decode_graph()
+        for _ in range(n):
+            self.hip.graph_launch(self.graph_exec)
+
+    # ------------------------------------------------------------------ outputs
+    def read_logits(self) -> np.ndarray:
+        self.hip.synchronize()
+        out = np.empty((self.B, self.cfg.vocab), np.float32)
+        self.hip.safe_memcpy_device_to_host(out, ctypes.c_void_p(self.logits.ptr), "logits")
+        return out
+
+    def read_topk(self) -> tuple[np.ndarray, np.ndarray]:
+        self.hip.synchronize()
+        v = np.empty((self.B, self.top_k), np.float32)
+        i = np.empty((self.B, self.top_k), np.int32)
+        self.hip.safe_memcpy_device_to_host(v, ctypes.c_void_p(self.topk_val.ptr), "sampler_topk_val")
+        self.hip.safe_memcpy_device_to_host(i, ctypes.c_void_p(self.topk_idx.ptr), "sampler_topk_idx")
+        return v, i
+
+    def fill_kv_prefix(self, seed: int = 0, scale: float = 0.5) -> None:
+        """Fill every KV cache with scale * N(0,1) fp16 on the device (synthetic prefix)."""
+        n = self.B * self.max_seq * self.cfg.n_kv * self.cfg.head_dim
+        for L in range(self.cfg.n_layers):
+            self.K.fill_normal_f16(self.k_cache[L], n, seed * 1000 + 2 * L, scale, stream=self.hip.stream)
+            self.K.fill_normal_f16(self.v_cache[L], n, seed * 1000 + 2 * L + 1, scale, stream=self.hip.stream)
+        self.hip.synchronize()
+
+    def upload_kv(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
+        self.k_cache[layer].upload(k)
+        self.v_cache[layer].upload(v)
+
+    def close(self) -> None:
+        if self.graph_exec is not None:
+            self.hip.graph_exec_destroy(self.graph_exec)
+            self.hip.graph_destroy(self.graph)
+            self.graph_exec = self.graph = None
+        self.slab.cleanup()

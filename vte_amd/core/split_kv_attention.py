@@ -1,0 +1,61 @@
+"""Split-KV flash-decoding dispatcher (host side).
+
+Mirrors the reference's SplitKVAttentionDispatcher
+(vte/core/split_kv_attention.py:52-229): it owns the split size, sizes the
+partial-result scratchpad once (shared by every layer, since layers run in
+sequence) and issues the launches of one layer.  MI355X choices:
+
+* one launch pair per layer (GQA-aware partial kernel + LSE combine) instead
+  of append/partial/reduce with one block per query head; the KV append is a
+  separate tiny launch as in the reference;
+* the split is a token count per block (multiple of 32, at least 128 so each
+  of the block's four waves has a full 32-token MFMA step), chosen so
+  batch x kv_heads x splits covers the GPU about twice at the longest context
+  (the reference's 1024/num_cus rule gives 4-token chunks on 256 CUs);
+* the per-sequence split count is derived on the device from kv_offset[b],
+  so ragged batches inside one captured graph only touch their own splits.
+"""
+from __future__ import annotations
+
+import math
+
+from ..kernels import kernels
+
+
+def choose_split(max_context: int, batch: int, n_kv: int, num_cus: int) -> int:
+    """Tokens per split block: power of two in [128, 1024]."""
+    target_blocks = 2 * max(num_cus, 1)
+    want = max_context * batch * n_kv / target_blocks
+    split = 128
+    while split < want and split < 1024:
+        split *= 2
+    return split
+
+
+class SplitKVAttentionDispatcher:
+    def __init__(self, hip, n_q: int, n_kv: int, head_dim: int, max_context: int, batch_size: int = 1,
+                 split: int | None = None, allocator=None):
+        self.hip = hip
+        self.n_q, self.n_kv, self.head_dim = n_q, n_kv, head_dim
+        self.batch = batch_size
+        self.max_context = max_context
+        self.split = split or choose_split(max_context, batch_size, n_kv, hip.get_num_cus() if hip else 256)
+        self.max_splits = math.ceil(max_context / self.split)
+        self.scale = 1.0 / math.sqrt(head_dim)
+        self.K = kernels()
+        from ..bridge.memory import DeviceArray, MemoryRegion
+        import numpy as np
+        nstat = batch_size * n_q * self.max_splits
+        self.part_m = DeviceArray(hip, nstat, np.float32, "attn_part_m", allocator, MemoryRegion.SCRATCH)
+        self.part_l = DeviceArray(hip, nstat, np.float32, "attn_part_l", allocator, MemoryRegion.SCRATCH)
+        self.part_o = DeviceArray(hip, nstat * head_dim, np.float32, "attn_part_o", allocator, MemoryRegion.SCRATCH)
+
+    def scratch_bytes(self) -> int:
+        return self.part_m.nbytes + self.part_l.nbytes + self.part_o.nbytes
+
+    def launch(self, q, k_cache, v_cache, out, kv_offset, kv_batch_stride: int, dtype: str = "f16",
+               batch: int | None = None, stream=None) -> None:
+        """Partial + combine for one layer.  q [B, n_q, hd]; out [B, n_q, hd]."""
+        self.K.attn_split_kv(q, k_cache, v_cache, self.part_m, self.part_l, self.part_o, out, batch or self.batch,
+                             self.n_q, self.n_kv, self.head_dim, self.scale, kv_offset, kv_batch_stride, self.split,
+                             self.max_splits, dtype=dtype, stream=stream if stream is not None else self.hip.stream)

@@ -35,6 +35,7 @@ hipError_t add(const void* r, const void* in, void* out, int n, float scale, hip
 hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
                          hipStream_t st);
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, hipStream_t st);
+hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, hipStream_t st);
 }  // namespace vte
 
 static thread_local char g_err[512] = "";
@@ -207,6 +208,11 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
     REQUIRE(logits && out_val && out_idx, "topk: null pointer");
     REQUIRE(rows >= 1 && k >= 1 && k <= 64 && vocab >= k, "topk: need 1 <= k <= min(64, vocab)");
     return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, (hipStream_t)stream), "vte_topk launch");
+}
+
+int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, void* stream) {
+    REQUIRE(dst && n >= 1 && n / 256 < (1LL << 31), "fill_normal_f16: bad arguments");
+    return hip_status(vte::fill_normal_f16(dst, n, seed, scale, (hipStream_t)stream), "vte_fill_normal_f16 launch");
 }
 
 }  // extern "C"

@@ -268,9 +268,38 @@ __global__ __launch_bounds__(1024) void topk_rows_kernel(const float* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// Seeded device-side fill of fp16 memory with scale * N(0,1) (counter-based
+// splitmix64 hash + Box-Muller).  Used to lay down synthetic KV prefixes of
+// up to gigabytes without a host round trip; not part of any parity path.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void fill_normal_f16_kernel(__half* __restrict__ dst, long long n,
+                                                              unsigned long long seed, float scale) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t h = splitmix64(seed * 0x2545F4914F6CDD1Dull + (uint64_t)i);
+    const float u1 = ((float)((h >> 40) & 0xFFFFFF) + 1.0f) * (1.0f / 16777217.0f);
+    const float u2 = (float)((h >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
+    const float r = sqrtf(-2.0f * logf(u1));
+    dst[i] = __float2half(scale * r * cosf(6.28318530718f * u2));
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 namespace vte {
+
+hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, hipStream_t st) {
+    hipLaunchKernelGGL(fill_normal_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (__half*)dst, n,
+                       seed, scale);
+    return hipGetLastError();
+}
 
 hipError_t rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps, hipStream_t st) {
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, (const __half*)x, (const __half*)w,

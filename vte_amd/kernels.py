@@ -38,6 +38,7 @@ SIGNATURES = {
     "vte_add": [_vp, _vp, _vp, _i, _f, _vp],
     "vte_embedding_q6k": [_vp, _vp, _vp, _i, _i, _f, _vp],
     "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp],
+    "vte_fill_normal_f16": [_vp, _ll, ctypes.c_ulonglong, _f, _vp],
     "vte_last_error": [],
 }
 RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll}
@@ -134,6 +135,9 @@ class VTEKernels:
     def topk(self, logits, rows, vocab, k, out_val, out_idx, stream=None):
         self._check(self.lib.vte_topk(_p(logits), rows, vocab, k, _p(out_val), _p(out_idx), self._st(stream)),
                     "vte_topk")
+
+    def fill_normal_f16(self, dst, n, seed, scale=1.0, stream=None):
+        self._check(self.lib.vte_fill_normal_f16(_p(dst), n, seed, scale, self._st(stream)), "vte_fill_normal_f16")
 
 
 _KERNELS: Optional[VTEKernels] = None

@@ -14,6 +14,14 @@ chosen so dequantised weights have realistic magnitudes:
 
 All generators take a ``numpy.random.Generator`` so fixtures are
 reproducible from a seed.
+
+``balanced=True`` (used for whole-model decode steps) keeps the formats and
+the random quants/scales but rescales the super-block factors so weights are
+zero-mean with std ~ 1/sqrt(K): Q4_K d ~ U(0.5,1.5)/(200 sqrt K), dmin = 7.5 d;
+Q6_K d ~ U(0.5,1.5)/(340 sqrt K).  With the literal ranges above, Q4_K
+weights average about +1.2 and a 28-layer fp16 residual stream overflows
+after the first FFN; the byte stream, and therefore the memory traffic, is
+unchanged by the rescaling.
 """
 from __future__ import annotations
 
@@ -46,35 +54,44 @@ def _f16_bytes(values: np.ndarray) -> np.ndarray:
     return values.astype(np.float16).view(np.uint8).reshape(values.shape + (2,))
 
 
-def random_q4_k(rng: np.random.Generator, n_rows: int, n_cols: int) -> np.ndarray:
+def random_q4_k(rng: np.random.Generator, n_rows: int, n_cols: int, balanced: bool = False) -> np.ndarray:
     """Row-major Q4_K matrix [n_rows, n_cols] as raw bytes (uint8 array)."""
     assert n_cols % QK_K == 0
     nb = n_rows * (n_cols // QK_K)
     blk = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
-    blk[:, 0:2] = _f16_bytes(rng.uniform(1e-3, 1e-2, nb))
-    blk[:, 2:4] = _f16_bytes(rng.uniform(0.0, 5e-3, nb))
+    if balanced:
+        d = rng.uniform(0.5, 1.5, nb) / (200.0 * np.sqrt(n_cols))
+        blk[:, 0:2] = _f16_bytes(d)
+        blk[:, 2:4] = _f16_bytes(7.5 * d)
+    else:
+        blk[:, 0:2] = _f16_bytes(rng.uniform(1e-3, 1e-2, nb))
+        blk[:, 2:4] = _f16_bytes(rng.uniform(0.0, 5e-3, nb))
     sc = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
     mn = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
     blk[:, 4:16] = pack_q4k_scales(sc, mn)
     return blk.reshape(-1)
 
 
-def random_q6_k(rng: np.random.Generator, n_rows: int, n_cols: int) -> np.ndarray:
+def random_q6_k(rng: np.random.Generator, n_rows: int, n_cols: int, balanced: bool = False) -> np.ndarray:
     """Row-major Q6_K matrix [n_rows, n_cols] as raw bytes (uint8 array)."""
     assert n_cols % QK_K == 0
     nb = n_rows * (n_cols // QK_K)
     blk = rng.integers(0, 256, size=(nb, 210), dtype=np.uint8)
     blk[:, 192:208] = rng.integers(-32, 32, size=(nb, 16), dtype=np.int8).view(np.uint8)
-    blk[:, 208:210] = _f16_bytes(rng.uniform(1e-3, 1e-2, nb))
+    if balanced:
+        blk[:, 208:210] = _f16_bytes(rng.uniform(0.5, 1.5, nb) / (340.0 * np.sqrt(n_cols)))
+    else:
+        blk[:, 208:210] = _f16_bytes(rng.uniform(1e-3, 1e-2, nb))
     return blk.reshape(-1)
 
 
-def random_q8_0(rng: np.random.Generator, n_rows: int, n_cols: int) -> np.ndarray:
+def random_q8_0(rng: np.random.Generator, n_rows: int, n_cols: int, balanced: bool = False) -> np.ndarray:
     """Row-major Q8_0 matrix [n_rows, n_cols] as raw bytes (uint8 array)."""
     assert n_cols % 32 == 0
     nb = n_rows * (n_cols // 32)
     blk = np.empty((nb, 34), dtype=np.uint8)
-    blk[:, 0:2] = _f16_bytes(rng.uniform(1e-3, 1e-2, nb))
+    lo, hi = (0.5 / (73.0 * np.sqrt(n_cols)), 1.5 / (73.0 * np.sqrt(n_cols))) if balanced else (1e-3, 1e-2)
+    blk[:, 0:2] = _f16_bytes(rng.uniform(lo, hi, nb))
     blk[:, 2:34] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
     return blk.reshape(-1)
 
@@ -82,8 +99,8 @@ def random_q8_0(rng: np.random.Generator, n_rows: int, n_cols: int) -> np.ndarra
 RANDOM = {"q4_k": random_q4_k, "q6_k": random_q6_k, "q8_0": random_q8_0}
 
 
-def random_matrix(fmt: str, rng: np.random.Generator, n_rows: int, n_cols: int) -> np.ndarray:
-    return RANDOM[fmt](rng, n_rows, n_cols)
+def random_matrix(fmt: str, rng: np.random.Generator, n_rows: int, n_cols: int, balanced: bool = False) -> np.ndarray:
+    return RANDOM[fmt](rng, n_rows, n_cols, balanced)
 
 
 def matrix_bytes(fmt: str, n_rows: int, n_cols: int) -> int:
