@@ -73,21 +73,73 @@ def gemv_bench(hip, K, fmt, n, k, launches=200, pool_bytes=768 << 20, mfma_batch
     y = DeviceArray(hip, (M, n), np.float32, "y")
     run = (lambda w: K.gemm_mfma(fmt, x, w, y, M, k, n, stream=hip.stream)) if mfma_batch else \
           (lambda w: K.gemv(fmt, x, w, y, M, k, n, stream=hip.stream))
-    for c in range(min(copies, 20)):
-        run(pool.ptr + c * stride)
+    # launches captured into one graph (as inside the decode step), each on the
+    # next cold copy of the weights
+    hip.synchronize()
+    hip.stream_begin_capture()
+    for i in range(launches):
+        run(pool.ptr + (i % copies) * stride)
+    graph = hip.stream_end_capture()
+    gexec = hip.graph_instantiate(graph)
+    hip.graph_launch(gexec)
     hip.synchronize()
     e0, e1 = _events(hip)
     hip.event_record(e0)
-    for i in range(launches):
-        run(pool.ptr + (i % copies) * stride)
+    hip.graph_launch(gexec)
     hip.event_record(e1)
     ms = hip.event_elapsed_ms(e0, e1) / launches
+    hip.graph_exec_destroy(gexec)
+    hip.graph_destroy(graph)
     algo = raw.nbytes + M * k * 4 + M * n * 4
     for d in (pool, first, x, y):
         d.free()
     return {"shape": f"{n}x{k}", "fmt": fmt, "batch": M, "us": round(ms * 1e3, 3),
             "algo_bytes": int(algo), "GBps": round(algo / (ms * 1e-3) / 1e9, 1),
             "frac_hbm_peak": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def attn_bench(hip, K, ctx, split, B=1, fused=True, launches=40):
+    """Split-KV decode attention (12q/2kv, hd 128, fp16 KV) over a cold set of
+    KV caches, graph-captured launches.  Algorithmic bytes: KV = B*ctx*1024 B."""
+    from vte_amd.bridge import DeviceArray
+    n_q, n_kv, D = 12, 2, 128
+    per_seq = ctx * n_kv * D
+    copies = max(2, int(np.ceil((512 << 20) / (2 * 2 * B * per_seq))))
+    kc = [DeviceArray(hip, B * per_seq, np.float16, "kc") for _ in range(copies)]
+    vc = [DeviceArray(hip, B * per_seq, np.float16, "vc") for _ in range(copies)]
+    for i in range(copies):
+        K.fill_normal_f16(kc[i], B * per_seq, 10 + i, 0.5, stream=hip.stream)
+        K.fill_normal_f16(vc[i], B * per_seq, 100 + i, 0.5, stream=hip.stream)
+    q = DeviceArray.from_numpy(hip, np.random.default_rng(0).standard_normal((B, n_q, D)).astype(np.float16), "q")
+    offs = DeviceArray.from_numpy(hip, np.full(B, ctx - 1, np.int32), "offs")
+    ms_ = (ctx + split - 1) // split
+    pm = DeviceArray(hip, B * n_q * ms_, np.float32, "pm")
+    pl = DeviceArray(hip, B * n_q * ms_, np.float32, "pl")
+    po = DeviceArray(hip, B * n_q * ms_ * D, np.float32, "po")
+    out = DeviceArray(hip, B * n_q * D, np.float16, "out")
+    ctr = DeviceArray(hip, B * n_kv, np.int32, "ctr")
+    ctr.zero()
+    hip.synchronize()
+    hip.stream_begin_capture()
+    for i in range(launches):
+        K.attn_split_kv(q, kc[i % copies], vc[i % copies], pm, pl, po, out, B, n_q, n_kv, D, 1 / np.sqrt(D), offs,
+                        per_seq, split, ms_, dtype="f16", counters=ctr if fused else None, stream=hip.stream)
+    g = hip.stream_end_capture()
+    ge = hip.graph_instantiate(g)
+    hip.graph_launch(ge)
+    hip.synchronize()
+    e0, e1 = _events(hip)
+    hip.event_record(e0)
+    hip.graph_launch(ge)
+    hip.event_record(e1)
+    ms = hip.event_elapsed_ms(e0, e1) / launches
+    hip.graph_exec_destroy(ge)
+    hip.graph_destroy(g)
+    for d in kc + vc + [q, offs, pm, pl, po, out, ctr]:
+        d.free()
+    algo = B * ctx * 1024
+    return {"ctx": ctx, "batch": B, "split": split, "fused_combine": fused, "us": round(ms * 1e3, 3),
+            "kv_bytes": algo, "GBps": round(algo / (ms * 1e-3) / 1e9, 1)}
 
 
 def cpu_baseline(seconds_budget=20.0):
@@ -174,6 +226,13 @@ def main():
         gemv.append(gemv_bench(hip, K, "q6_k", 151936, 1536, launches=50, pool_bytes=600 << 20))
         gemv.append(gemv_bench(hip, K, "q8_0", 2048, 2048))
         gemv.append(gemv_bench(hip, K, "q4_k", 8960, 1536, mfma_batch=16))
+    attn = []
+    if not args.quick:
+        for ctx in (512, 4096, 32768):
+            attn.append(attn_bench(hip, K, ctx, 256 if ctx < 32768 else 512))
+        attn.append(attn_bench(hip, K, 2049, 128, fused=True))
+        attn.append(attn_bench(hip, K, 2049, 128, fused=False))
+        attn.append(attn_bench(hip, K, 2049, 512, B=16, fused=True))
     dom = gemv[0] if gemv else None
     cpu = None if args.no_cpu else cpu_baseline()
     r1 = result[1]
@@ -198,6 +257,8 @@ def main():
                      "e2e_tok_s_b16": round(16e3 / r16["e2e_ms_per_step"], 2)})
     if gemv:
         line["gemv"] = gemv
+    if attn:
+        line["attention"] = attn
     if dom:
         line["roofline"] = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                             "frac": dom["frac_hbm_peak"], "traffic": None,

@@ -16,7 +16,7 @@ NQ, NKV, D = 12, 2, 128
 SCALE = 1.0 / math.sqrt(D)
 
 
-def _run(hip, K, q, kc, vc, offsets, split, dtype="f32"):
+def _run(hip, K, q, kc, vc, offsets, split, dtype="f32", fused=False):
     """q [B,NQ,D]; caches [B,max_seq,NKV,D] fp16; offsets [B] (position of last token)."""
     B, max_seq = kc.shape[0], kc.shape[1]
     max_splits = (max_seq + split - 1) // split
@@ -24,9 +24,12 @@ def _run(hip, K, q, kc, vc, offsets, split, dtype="f32"):
     part_l = empty(hip, (B, NQ, max_splits), np.float32)
     part_o = empty(hip, (B, NQ, max_splits, D), np.float32)
     out = empty(hip, (B, NQ, D), np.float32 if dtype == "f32" else np.float16)
+    ctr = empty(hip, B * NKV, np.int32) if fused else None
     K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), part_m, part_l, part_o, out, B, NQ, NKV, D, SCALE,
                     up(hip, np.asarray(offsets, np.int32)), max_seq * NKV * D, split, max_splits, dtype=dtype,
-                    stream=hip.stream)
+                    counters=ctr, stream=hip.stream)
+    if fused:  # the kernel leaves its counters at zero for the next call
+        assert not down(ctr).any()
     return down(out)
 
 
@@ -45,6 +48,20 @@ def test_config2_single_sequence(hip, K, ctx, split):
     got = _run(hip, K, q, kc, vc, [ctx - 1], split)
     ref = attention_ref(q[0], kc[0], vc[0], ctx, SCALE)
     assert rel_l2(got[0], ref) <= TOL
+
+
+@pytest.mark.parametrize("ctx,split", [(4096, 256), (777, 128), (33, 128)])
+def test_in_kernel_combine_matches_separate(hip, K, ctx, split):
+    """The last-block LSE combine agrees with the separate combine kernel (same
+    terms, different fp32 summation order) and with the float64 oracle."""
+    rng = np.random.default_rng(ctx)
+    q, kc, vc = _inputs(rng, 3, ctx)
+    offs = [ctx - 1, ctx // 2, 0]
+    a = _run(hip, K, q, kc, vc, offs, split)
+    b = _run(hip, K, q, kc, vc, offs, split, fused=True)
+    assert rel_l2(b, a) <= 1e-5
+    for i, o in enumerate(offs):
+        assert rel_l2(b[i], attention_ref(q[i], kc[i], vc[i], o + 1, SCALE)) <= TOL
 
 
 @pytest.mark.parametrize("B", [8, 16, 32])

@@ -68,16 +68,17 @@ def test_embedding_q6k_bit_exact(hip, K):
         assert np.array_equal(got[i], st.embedding_q6k(table, int(t), H))
 
 
-@pytest.mark.parametrize("k", [1, 40, 64])
-def test_topk_exact(hip, K, k):
+@pytest.mark.parametrize("k,vocab", [(1, 151936), (40, 151936), (64, 151936), (40, 64), (40, 1000), (7, 300)])
+def test_topk_exact(hip, K, k, vocab):
     rng = np.random.default_rng(5)
-    rows, vocab = 4, 151936
+    rows = 4
     logits = rng.standard_normal((rows, vocab)).astype(np.float32)
     logits[1, :] = -3.0          # heavy ties: lowest indices must win
-    logits[1, 70000] = 5.0
-    logits[2, 1000:1100] = 9.0    # a tied block above everything else
+    logits[1, vocab // 2] = 5.0
+    logits[2, vocab // 4:vocab // 4 + 50] = 9.0    # a tied block above everything else
     vals, idx = empty(hip, (rows, k), np.float32), empty(hip, (rows, k), np.int32)
-    K.topk(up(hip, logits), rows, vocab, k, vals, idx, stream=hip.stream)
+    scratch = empty(hip, K.topk_scratch_bytes(rows), np.uint8)
+    K.topk(up(hip, logits), rows, vocab, k, vals, idx, scratch, stream=hip.stream)
     gv, gi = down(vals), down(idx)
     for r in range(rows):
         order = np.lexsort((np.arange(vocab), -logits[r]))[:k]  # value desc, index asc

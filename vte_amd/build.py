@@ -20,7 +20,7 @@ CSRC = HERE / "csrc"
 ARCH = "gfx950"
 LIB = HERE / "libvte_amd.so"
 HSACO = HERE / f"vte_kernels_{ARCH}.hsaco"
-SOURCES = ["gemv.hip", "gemm_mfma.hip", "attention.hip", "glue.hip", "capi.hip"]
+SOURCES = ["gemv.hip", "qmv.hip", "gemm_mfma.hip", "attention.hip", "glue.hip", "capi.hip"]
 MODULE_SOURCE = "module.hip"
 # Packed FP32 instructions are disabled for every HIP compile (see DESIGN notes).
 COMMON = ["-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
@@ -58,7 +58,7 @@ def build(verbose: bool = False) -> None:
         objs = [f.result() for f in futs]
         hs.result()
     tmp = LIB.with_suffix(".so.tmp")
-    _run([cc, *COMMON, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    _run([cc, *COMMON, "-shared", "-fPIC", "-Wl,--no-undefined", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
     os.replace(str(HSACO) + ".tmp", HSACO)
     if verbose:

@@ -93,6 +93,7 @@ class HIPGraphExecutor:
         self.logits = A((B, cfg.vocab), np.float32, "logits")
         self.topk_val = A((B, max(top_k, 1)), np.float32, "topk_val")
         self.topk_idx = A((B, max(top_k, 1)), np.int32, "topk_idx")
+        self.topk_scratch = A(self.K.topk_scratch_bytes(B), np.uint8, "topk_scratch")
         self.staging_input = A(B, np.int32, "staging_tokens")
         self.staging_kv_offset = A(B, np.int32, "staging_kv_offset")
         cos_c, sin_c = build_rope_cache(self.max_seq, cfg.head_dim, cfg.rope_theta)
@@ -142,7 +143,7 @@ class HIPGraphExecutor:
         K.rmsnorm(self.h[cur], self.output_norm, self.xn, B, H, cfg.eps, stream=st)
         self._linear("q6_k", self.xn, self.token_embd, self.logits, H, cfg.vocab, out_dtype="f32")
         if self.top_k > 0:
-            K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, stream=st)
+            K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st)
 
     # -------------------------------------------------------------------- graph
     def build_decode_graph(self) -> None:

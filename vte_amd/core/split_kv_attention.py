@@ -5,9 +5,10 @@ Mirrors the reference's SplitKVAttentionDispatcher
 partial-result scratchpad once (shared by every layer, since layers run in
 sequence) and issues the launches of one layer.  MI355X choices:
 
-* one launch pair per layer (GQA-aware partial kernel + LSE combine) instead
-  of append/partial/reduce with one block per query head; the KV append is a
-  separate tiny launch as in the reference;
+* a GQA-aware partial kernel (one block serves every query head of a KV head)
+  and the LSE combine, either as a second launch or, with ``fuse_combine``,
+  inside the partial kernel's last block per (sequence, KV head); the KV
+  append is a separate tiny launch as in the reference;
 * the split is a token count per block (multiple of 32, at least 128 so each
   of the block's four waves has a full 32-token MFMA step), chosen so
   batch x kv_heads x splits covers the GPU about twice at the longest context
@@ -34,7 +35,7 @@ def choose_split(max_context: int, batch: int, n_kv: int, num_cus: int) -> int:
 
 class SplitKVAttentionDispatcher:
     def __init__(self, hip, n_q: int, n_kv: int, head_dim: int, max_context: int, batch_size: int = 1,
-                 split: int | None = None, allocator=None):
+                 split: int | None = None, allocator=None, fuse_combine: bool = False):
         self.hip = hip
         self.n_q, self.n_kv, self.head_dim = n_q, n_kv, head_dim
         self.batch = batch_size
@@ -42,6 +43,10 @@ class SplitKVAttentionDispatcher:
         self.split = split or choose_split(max_context, batch_size, n_kv, hip.get_num_cus() if hip else 256)
         self.max_splits = math.ceil(max_context / self.split)
         self.scale = 1.0 / math.sqrt(head_dim)
+        # In-kernel (last-block) combine saves a launch but pays a device-scope
+        # fence per block; measured slower than the separate combine launch at
+        # 2K context on MI355X, so it is opt-in.
+        self.fuse_combine = fuse_combine
         self.K = kernels()
         from ..bridge.memory import DeviceArray, MemoryRegion
         import numpy as np
@@ -49,6 +54,10 @@ class SplitKVAttentionDispatcher:
         self.part_m = DeviceArray(hip, nstat, np.float32, "attn_part_m", allocator, MemoryRegion.SCRATCH)
         self.part_l = DeviceArray(hip, nstat, np.float32, "attn_part_l", allocator, MemoryRegion.SCRATCH)
         self.part_o = DeviceArray(hip, nstat * head_dim, np.float32, "attn_part_o", allocator, MemoryRegion.SCRATCH)
+        # split-completion counters of the in-kernel LSE combine: zeroed once here,
+        # returned to zero by the kernel itself after every combine
+        self.counters = DeviceArray(hip, batch_size * n_kv, np.int32, "attn_counters", allocator, MemoryRegion.SCRATCH)
+        self.counters.zero()
 
     def scratch_bytes(self) -> int:
         return self.part_m.nbytes + self.part_l.nbytes + self.part_o.nbytes
@@ -58,4 +67,5 @@ class SplitKVAttentionDispatcher:
         """Partial + combine for one layer.  q [B, n_q, hd]; out [B, n_q, hd]."""
         self.K.attn_split_kv(q, k_cache, v_cache, self.part_m, self.part_l, self.part_o, out, batch or self.batch,
                              self.n_q, self.n_kv, self.head_dim, self.scale, kv_offset, kv_batch_stride, self.split,
-                             self.max_splits, dtype=dtype, stream=stream if stream is not None else self.hip.stream)
+                             self.max_splits, dtype=dtype, counters=self.counters if self.fuse_combine else None,
+                             stream=stream if stream is not None else self.hip.stream)

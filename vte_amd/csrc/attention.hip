@@ -14,8 +14,11 @@
 //  * Scores S^T[token][head] = K . Q^T come from MFMA 16x16x32 f16: K rows are
 //    loaded straight into the A operand (16-byte loads), Q^T (padded to 16 heads)
 //    is a per-block constant B operand.  fp32 accumulation.
-//  * Online softmax on the MFMA C registers (one head per lane column), P staged
-//    through LDS, P.V accumulated in fp32 on the VALU with coalesced V row reads.
+//  * Online softmax on the MFMA C registers (one head per lane column).  P.V is
+//    a second MFMA: P (fp16) is already in the A-operand layout in registers,
+//    V rows are loaded coalesced and transposed through LDS (v_perm pairs) so
+//    each lane reads its 8 B-operand tokens of one dimension with two 8-byte
+//    LDS reads.  Both products accumulate in fp32.
 //  * Ragged batches: per-sequence split count ceil((kv_offset[b]+1) / split);
 //    blocks past a sequence's last split exit at once, and the combine reads
 //    only that sequence's splits, so each sequence's result is independent of
@@ -29,6 +32,8 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 #define ATT_WAVES 4
 #define ATT_TILE 32  // tokens per wave step (two 16-token MFMA tiles)
 #define ATT_MAXG 8   // query heads per KV head served by one block
+#define ATT_MAX_COMBINE 512  // splits per sequence the in-kernel combine handles
+#define ATT_VT_STRIDE 36     // halves per row of the transposed V tile (32 tokens + pad)
 
 // ---------------------------------------------------------------------------
 // KV append (reference ABI, vte/compiler/templates/rdna/kv_cache_append.hip.template:13-39)
@@ -51,13 +56,13 @@ extern "C" __global__ void kv_cache_append_kernel(const __half* __restrict__ k, 
 // ---------------------------------------------------------------------------
 // Native partial pass
 // ---------------------------------------------------------------------------
-template <typename TQ>
+template <typename TQ, typename TO>
 __global__ __launch_bounds__(256) void attn_partial_gqa(
     const TQ* __restrict__ q,            // [B][n_q][D]
     const __half* __restrict__ k_cache, const __half* __restrict__ v_cache,
     float* __restrict__ part_m, float* __restrict__ part_l, float* __restrict__ part_o,
     int n_q, int n_kv, float scale, const int* __restrict__ kv_offset, int kv_batch_stride,
-    int split, int max_splits) {
+    int split, int max_splits, int* __restrict__ counters, TO* __restrict__ out) {
     const int sp = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int len = kv_offset[b] + 1;
     const int t_begin = sp * split;
@@ -68,10 +73,19 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
     const int col = lane & 15;   // head (MFMA N index) / token row (A operand)
     const int grp = lane >> 4;   // 0..3
 
-    __shared__ float p_sh[ATT_WAVES][ATT_TILE][17];   // P tile per wave, [token][head]
-    __shared__ float corr_sh[ATT_WAVES][16];
+    // V tile of a wave, transposed: vt[d][t] (fp16, rows of 36 halves so the
+    // 8-byte reads of 16 consecutive d rows hit distinct LDS banks)
+    // Phases use disjoint LDS lifetimes: the V^T tiles (tile loop), the
+    // per-wave O rows (block combine) and the split weights (LSE combine).
+    union AttnLDS {
+        uint32_t vt[ATT_WAVES][ATT_D][ATT_VT_STRIDE / 2];
+        float o[ATT_WAVES][ATT_MAXG][ATT_D + 4];
+        float w[ATT_MAXG][ATT_MAX_COMBINE];
+    };
+    __shared__ AttnLDS lds;
     __shared__ float m_sh[ATT_WAVES][16], l_sh[ATT_WAVES][16];
-    __shared__ float o_sh[ATT_WAVES][ATT_MAXG][ATT_D + 4];
+    auto& vt_sh = lds.vt;
+    auto& o_sh = lds.o;
 
     // B operand: Q^T for this KV head's G query heads, fp16, zero-padded to 16.
     half8_t qb[ATT_D / 32];
@@ -94,24 +108,43 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
 
     float m_run = -1e30f;  // running max of head `col` (identical across grp)
     float l_run = 0.f;     // per-lane partial denominator of head `col`
-    float o_acc[ATT_MAXG][2];  // O[h][2*lane .. 2*lane+1], h < G
+    // O[h][d] in the MFMA C layout: lane (col, grp) holds heads 4*grp + i, dim 16*dt + col
+    floatx4_t o_acc[ATT_D / 16];
 #pragma unroll
-    for (int h = 0; h < ATT_MAXG; ++h) { o_acc[h][0] = 0.f; o_acc[h][1] = 0.f; }
+    for (int dt = 0; dt < ATT_D / 16; ++dt) o_acc[dt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
     for (int t0 = t_begin + wv * ATT_TILE; t0 < t_end; t0 += ATT_WAVES * ATT_TILE) {
+        // ---- all loads of the tile at once: K rows (MFMA A operands) and V rows ----
+        half8_t ka[2][ATT_D / 32];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int tok = t0 + 16 * tt + col;
+            const __half* kr = kb + (size_t)(tok < t_end ? tok : t_begin) * row_stride;
+#pragma unroll
+            for (int s = 0; s < ATT_D / 32; ++s) ka[tt][s] = *reinterpret_cast<const half8_t*>(kr + 32 * s + 8 * grp);
+        }
+        uint32_t vv[ATT_TILE];  // V[t0 + t][2*lane .. 2*lane+1]; rows past the end are
+                                // loaded from t_begin and weighted by p = 0
+#pragma unroll
+        for (int t = 0; t < ATT_TILE; ++t) {
+            const int tok = (t0 + t < t_end) ? t0 + t : t_begin;
+            vv[t] = *reinterpret_cast<const uint32_t*>(vb + (size_t)tok * row_stride + 2 * lane);
+        }
         // ---- scores for 32 tokens: two 16x16 S^T tiles ----
         floatx4_t acc[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             acc[tt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-            const int tok = t0 + 16 * tt + col;
-            const bool valid = tok < t_end;
-            const __half* kr = kb + (size_t)(valid ? tok : t_begin) * row_stride;
 #pragma unroll
-            for (int s = 0; s < ATT_D / 32; ++s) {
-                half8_t a = *reinterpret_cast<const half8_t*>(kr + 32 * s + 8 * grp);
-                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[s], acc[tt], 0, 0, 0);
-            }
+            for (int s = 0; s < ATT_D / 32; ++s)
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[tt][s], qb[s], acc[tt], 0, 0, 0);
+        }
+        // ---- V^T into LDS: dword (V[t][d], V[t+1][d]) at vt[d][t/2] ----
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int t = 0; t < ATT_TILE; t += 2) {
+            vt_sh[wv][2 * lane][t / 2] = __builtin_amdgcn_perm(vv[t + 1], vv[t], 0x05040100u);
+            vt_sh[wv][2 * lane + 1][t / 2] = __builtin_amdgcn_perm(vv[t + 1], vv[t], 0x07060302u);
         }
         // lane holds S^T[token = t0 + 16*tt + 4*grp + i][head = col]
         float sc[2][4];
@@ -121,53 +154,52 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tok = t0 + 16 * tt + 4 * grp + i;
-                float s = acc[tt][i] * scale;
-                s = (tok < t_end) ? s : -INFINITY;
-                sc[tt][i] = s;
-                tmax = fmaxf(tmax, s);
+                float sv = acc[tt][i] * scale;
+                sv = (tok < t_end) ? sv : -INFINITY;
+                sc[tt][i] = sv;
+                tmax = fmaxf(tmax, sv);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         const float m_new = fmaxf(m_run, tmax);
         const float corr = __expf(m_run - m_new);
+        // A operand of P.V: P[head = col][token slots (grp, j)], j < 4 -> tile 0, j >= 4 -> tile 1
+        half8_t pa;
         float psum = 0.f;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = __expf(sc[tt][i] - m_new);
-                psum += p;
-                p_sh[wv][16 * tt + 4 * grp + i][col] = p;
+                const float pv = __expf(sc[tt][i] - m_new);
+                psum += pv;
+                pa[4 * tt + i] = (_Float16)pv;
             }
         l_run = l_run * corr + psum;
         m_run = m_new;
-        if (grp == 0) corr_sh[wv][col] = corr;
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        // rescale O rows (heads 4*grp + i) by their corr, held by lanes 4*grp + i
+        float cr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * grp + i, 64);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
-
-        // ---- O = O * corr + P . V  (lane owns dims 2*lane, 2*lane+1) ----
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int h = 0; h < ATT_MAXG; ++h) {
-            if (h < G) {
-                const float c = corr_sh[wv][h];
-                o_acc[h][0] *= c;
-                o_acc[h][1] *= c;
-            }
-        }
-        const int nt = min(ATT_TILE, t_end - t0);
-        for (int t = 0; t < nt; ++t) {
-            const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vb + (size_t)(t0 + t) * row_stride + 2 * lane);
-            const float v0 = h2f_bits(v2), v1 = h2f_bits(v2 >> 16);
+        for (int dt = 0; dt < ATT_D / 16; ++dt) {
 #pragma unroll
-            for (int h = 0; h < ATT_MAXG; ++h) {
-                if (h < G) {
-                    const float p = p_sh[wv][t][h];
-                    o_acc[h][0] = fmaf(p, v0, o_acc[h][0]);
-                    o_acc[h][1] = fmaf(p, v1, o_acc[h][1]);
-                }
+            for (int i = 0; i < 4; ++i) o_acc[dt][i] *= cr[i];
+            // B operand: V[token slots][d = 16*dt + col]
+            const uint32_t* vr = &vt_sh[wv][16 * dt + col][0];
+            const uint2 lo = *reinterpret_cast<const uint2*>(vr + 2 * grp);       // tokens 4g .. 4g+3
+            const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8 + 2 * grp);   // tokens 16+4g ..
+            half8_t vb8;
+            const uint32_t w4[4] = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                vb8[2 * j] = __builtin_bit_cast(_Float16, (unsigned short)(w4[j] & 0xFFFFu));
+                vb8[2 * j + 1] = __builtin_bit_cast(_Float16, (unsigned short)(w4[j] >> 16));
             }
+            o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb8, o_acc[dt], 0, 0, 0);
         }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
         __builtin_amdgcn_wave_barrier();
     }
 
@@ -175,13 +207,14 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
     if (grp == 0) { m_sh[wv][col] = m_run; l_sh[wv][col] = l_run; }
+    __syncthreads();  // every wave is done with its V^T tile (o_sh overlays it)
 #pragma unroll
-    for (int h = 0; h < ATT_MAXG; ++h) {
-        if (h < G) {
-            o_sh[wv][h][2 * lane] = o_acc[h][0];
-            o_sh[wv][h][2 * lane + 1] = o_acc[h][1];
+    for (int dt = 0; dt < ATT_D / 16; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = 4 * grp + i;
+            if (h < G) o_sh[wv][h][16 * dt + col] = o_acc[dt][i];
         }
-    }
     __syncthreads();
     // thread -> (head h, dim pair): 256 threads cover 2 heads x 128 dims per pass
     for (int idx = threadIdx.x; idx < G * ATT_D; idx += 256) {
@@ -200,6 +233,83 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
         const size_t st = ((size_t)b * n_q + qh) * max_splits + sp;
         part_o[st * ATT_D + d] = O;
         if (d == 0) { part_m[st] = M; part_l[st] = L; }
+    }
+    if (counters == nullptr) return;  // separate combine launch
+
+    // ---- last block of this (sequence, KV head) performs the LSE combine ----
+    // Release the partials at device scope, count this split, and let the block
+    // that completes the count read every split back (acquire) and combine.
+    // The counter is reset by that block, so a captured graph can be replayed.
+    __shared__ int s_last;
+    __threadfence();
+    __syncthreads();
+    const int ns = (len + split - 1) / split;
+    if (threadIdx.x == 0) {
+        int* ctr = counters + (size_t)b * n_kv + kvh;
+        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (prev == ns - 1);
+        if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    // per-split weights w[h][c] = exp(m_c - M_h) and L_h in LDS (parallel loads),
+    // then each thread combines its (head, dim) outputs with unrolled loads.
+    auto& wsh = lds.w;  // o_sh is dead once the partials are in global memory
+    __shared__ float Msh[ATT_MAXG], Lsh[ATT_MAXG];
+    for (int i = threadIdx.x; i < G * ns; i += 256) {
+        const int h = i / ns, c = i - h * ns;
+        wsh[h][c] = part_m[((size_t)b * n_q + kvh * G + h) * max_splits + c];
+    }
+    __syncthreads();
+    if (wv < G) {  // wave h: max and denominator of head h
+        const int h = wv;
+        const size_t base = ((size_t)b * n_q + kvh * G + h) * max_splits;
+        float M = -1e30f;
+        for (int c = lane; c < ns; c += 64) M = fmaxf(M, wsh[h][c]);
+        M = wave_max(M);
+        float L = 0.f;
+        for (int c = lane; c < ns; c += 64) {
+            const float wgt = __expf(wsh[h][c] - M);
+            wsh[h][c] = wgt;
+            L = fmaf(part_l[base + c], wgt, L);
+        }
+        L = wave_sum(L);
+        if (lane == 0) { Msh[h] = M; Lsh[h] = L; }
+    }
+    __syncthreads();
+    if (G > 4) {  // heads 4..G-1 (four waves per block)
+        for (int h = 4 + wv; h < G; h += 4) {
+            const size_t base = ((size_t)b * n_q + kvh * G + h) * max_splits;
+            float M = -1e30f;
+            for (int c = lane; c < ns; c += 64) M = fmaxf(M, wsh[h][c]);
+            M = wave_max(M);
+            float L = 0.f;
+            for (int c = lane; c < ns; c += 64) {
+                const float wgt = __expf(wsh[h][c] - M);
+                wsh[h][c] = wgt;
+                L = fmaf(part_l[base + c], wgt, L);
+            }
+            L = wave_sum(L);
+            if (lane == 0) { Msh[h] = M; Lsh[h] = L; }
+        }
+        __syncthreads();
+    }
+    for (int idx = threadIdx.x; idx < G * ATT_D; idx += 256) {
+        const int h = idx / ATT_D, d = idx % ATT_D;
+        const int qh = kvh * G + h;
+        const float* po = part_o + ((size_t)b * n_q + qh) * max_splits * ATT_D + d;
+        float O = 0.f;
+        int c = 0;
+        for (; c + 8 <= ns; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = po[(size_t)(c + j) * ATT_D];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) O = fmaf(v[j], wsh[h][c + j], O);
+        }
+        for (; c < ns; ++c) O = fmaf(po[(size_t)c * ATT_D], wsh[h][c], O);
+        st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(Lsh[h], 1e-20f));
     }
 }
 
@@ -306,13 +416,13 @@ namespace vte {
 template <typename TQ, typename TO>
 hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache, float* part_m, float* part_l,
                          float* part_o, void* out, int B, int n_q, int n_kv, float scale, const int* kv_offset,
-                         int kv_batch_stride, int split, int max_splits, hipStream_t st) {
+                         int kv_batch_stride, int split, int max_splits, int* counters, hipStream_t st) {
     dim3 g1(max_splits, n_kv, B), b1(256);
-    hipLaunchKernelGGL((attn_partial_gqa<TQ>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,
+    hipLaunchKernelGGL((attn_partial_gqa<TQ, TO>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,
                        (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset,
-                       kv_batch_stride, split, max_splits);
+                       kv_batch_stride, split, max_splits, counters, (TO*)out);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || counters != nullptr) return e;
     dim3 g2(n_q, B), b2(ATT_D);
     hipLaunchKernelGGL((attn_combine<TO>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q, kv_offset, split,
                        max_splits);
@@ -320,10 +430,10 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
 }
 
 template hipError_t attn_split_kv<float, float>(const void*, const void*, const void*, float*, float*, float*,
-                                                void*, int, int, int, float, const int*, int, int, int,
+                                                void*, int, int, int, float, const int*, int, int, int, int*,
                                                 hipStream_t);
 template hipError_t attn_split_kv<__half, __half>(const void*, const void*, const void*, float*, float*, float*,
-                                                  void*, int, int, int, float, const int*, int, int, int,
+                                                  void*, int, int, int, float, const int*, int, int, int, int*,
                                                   hipStream_t);
 
 hipError_t kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int B, int n_kv, int head_dim,

@@ -20,11 +20,13 @@ hipError_t gemv_valu(int fmt, const void* x, const void* w, void* y, int M, int 
                      const void* residual, float rs, hipStream_t st);
 hipError_t gemm_mfma(int fmt, int in_dt, int out_dt, const void* x, const void* w, void* y, int M, int K, int N,
                      const void* bias, const void* residual, float rs, hipStream_t st);
+hipError_t qmv(int fmt, bool in_f32, bool out_f32, const void* x, const void* w, void* y, int M, int K, int N,
+               const void* bias, const void* residual, float rs, hipStream_t st);
 hipError_t dequantize(int fmt, const void* src, float* dst, long long n_elements, hipStream_t st);
 template <typename TQ, typename TO>
 hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache, float* part_m, float* part_l,
                          float* part_o, void* out, int B, int n_q, int n_kv, float scale, const int* kv_offset,
-                         int kv_batch_stride, int split, int max_splits, hipStream_t st);
+                         int kv_batch_stride, int split, int max_splits, int* counters, hipStream_t st);
 hipError_t kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int B, int n_kv, int head_dim,
                      const int* kv_offset, int kv_batch_stride, hipStream_t st);
 hipError_t rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps, hipStream_t st);
@@ -34,7 +36,9 @@ hipError_t swiglu(const void* g, const void* u, void* out, int n, hipStream_t st
 hipError_t add(const void* r, const void* in, void* out, int n, float scale, hipStream_t st);
 hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
                          hipStream_t st);
-hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, hipStream_t st);
+size_t topk_scratch_bytes(int rows);
+hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
+                hipStream_t st);
 hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, hipStream_t st);
 }  // namespace vte
 
@@ -97,6 +101,9 @@ int vte_gemv(int fmt, int in_dtype, int out_dtype, const void* x, const void* w,
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
+    e = vte::qmv(fmt, in_dtype == VTE_F32, out_dtype == VTE_F32, x, w, y, M, K, N, bias, residual, residual_scale,
+                 st);
+    if (e != hipErrorNotSupported) return hip_status(e, "vte_gemv launch");
     if (in_dtype == VTE_F32 && out_dtype == VTE_F32)
         e = vte::gemv_valu<float, float>(fmt, x, w, y, M, K, N, bias, residual, residual_scale, st);
     else if (in_dtype == VTE_F16 && out_dtype == VTE_F16)
@@ -136,7 +143,7 @@ long long vte_attn_scratch_floats(int batch, int n_q, int max_splits) {
 int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void* v_cache, float* part_m,
                       float* part_l, float* part_o, void* out, int batch, int n_q, int n_kv, int head_dim,
                       float scale, const int* kv_offset, int kv_batch_stride, int split, int max_splits,
-                      void* stream) {
+                      int* counters, void* stream) {
     REQUIRE(dtype == VTE_F32 || dtype == VTE_F16, "attn: dtype must be 0 (f32) or 1 (f16)");
     REQUIRE(q && k_cache && v_cache && part_m && part_l && part_o && out && kv_offset, "attn: null pointer");
     REQUIRE(head_dim == 128, "attn: head_dim %d unsupported (128 only)", head_dim);
@@ -144,16 +151,17 @@ int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void*
     REQUIRE(n_q / n_kv <= 8, "attn: GQA group %d > 8 unsupported", n_q / n_kv);
     REQUIRE(split >= 32 && split % 32 == 0, "attn: split %d must be a positive multiple of 32", split);
     REQUIRE(max_splits >= 1 && max_splits <= 65535, "attn: max_splits %d out of range", max_splits);
+    REQUIRE(counters == nullptr || max_splits <= 512, "attn: in-kernel combine supports at most 512 splits");
     REQUIRE(aligned(k_cache, 16) && aligned(v_cache, 16), "attn: KV cache must be 16-byte aligned");
     REQUIRE(kv_batch_stride % 8 == 0, "attn: kv_batch_stride must keep rows 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     hipError_t e = (dtype == VTE_F32)
                        ? vte::attn_split_kv<float, float>(q, k_cache, v_cache, part_m, part_l, part_o, out, batch,
                                                           n_q, n_kv, scale, kv_offset, kv_batch_stride, split,
-                                                          max_splits, st)
+                                                          max_splits, counters, st)
                        : vte::attn_split_kv<__half, __half>(q, k_cache, v_cache, part_m, part_l, part_o, out,
                                                             batch, n_q, n_kv, scale, kv_offset, kv_batch_stride,
-                                                            split, max_splits, st);
+                                                            split, max_splits, counters, st);
     return hip_status(e, "vte_attn_split_kv launch");
 }
 
@@ -204,10 +212,15 @@ int vte_embedding_q6k(const int* tokens, const void* table, void* out, int n_tok
                       "vte_embedding_q6k launch");
 }
 
-int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* stream) {
-    REQUIRE(logits && out_val && out_idx, "topk: null pointer");
+long long vte_topk_scratch_bytes(int rows) { return (long long)vte::topk_scratch_bytes(rows); }
+
+int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
+             void* stream) {
+    REQUIRE(logits && out_val && out_idx && scratch, "topk: null pointer");
     REQUIRE(rows >= 1 && k >= 1 && k <= 64 && vocab >= k, "topk: need 1 <= k <= min(64, vocab)");
-    return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, (hipStream_t)stream), "vte_topk launch");
+    REQUIRE(rows <= 65535, "topk: rows %d out of range", rows);
+    return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream),
+                      "vte_topk launch");
 }
 
 int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, void* stream) {

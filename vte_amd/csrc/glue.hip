@@ -156,113 +156,88 @@ extern "C" __global__ __launch_bounds__(256) void embedding_lookup_q6k_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Top-k over fp32 logits (one 1024-thread block per row).  Exact radix select
-// on order-preserving 32-bit keys (4 passes of 8 bits), then a gather that
-// keeps every key above the threshold and the lowest-index ties at it, then a
-// bitonic sort (value descending, index ascending).  k <= 64.
-// out_val / out_idx: [rows][k].
+// Top-k over fp32 logits, k <= 64, exact, ordered by (value desc, index asc):
+// the order np.lexsort((index, -value)) gives.  Two launches:
+//  1. grid (TOPK_P, rows), 4 waves per block: each wave keeps the top 64 of its
+//     slice as a bitonic-sorted 64-lane list, merging in one 64-element group
+//     at a time (sort the group, take max(list[l], group[63 - l]) which is
+//     bitonic and holds the top 64 of the union, then a bitonic merge);
+//  2. one block per row merges the TOPK_P * 4 lists the same way and writes
+//     the first k entries.
+// Padding entries are (-inf, INT_MAX) so they rank after every real logit.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t f2key(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+#define TOPK_P 64
+#define TOPK_WAVES 4
+
+__device__ __forceinline__ bool tk_better(float a, int ia, float b, int ib) {
+    return a > b || (a == b && ia < ib);
 }
 
-__global__ __launch_bounds__(1024) void topk_rows_kernel(const float* __restrict__ logits, int vocab, int k,
-                                                         float* __restrict__ out_val, int* __restrict__ out_idx) {
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t sel_prefix, sel_need;
-    __shared__ int wave_cnt[16];
-    __shared__ int n_above;
-    __shared__ float cand_v[64];
-    __shared__ int cand_i[64];
-    const float* row = logits + (size_t)blockIdx.x * vocab;
-    const int tid = threadIdx.x;
-    if (tid == 0) { sel_prefix = 0; sel_need = (uint32_t)k; n_above = 0; }
-    if (tid < 64) { cand_v[tid] = -INFINITY; cand_i[tid] = 0x7fffffff; }
+// One compare-exchange stage of a bitonic network across the wave.
+__device__ __forceinline__ void tk_stage(float& v, int& ix, int lane, int stride, bool desc) {
+    const float ov = __shfl_xor(v, stride, 64);
+    const int oi = __shfl_xor(ix, stride, 64);
+    const bool lower = (lane & stride) == 0;
+    const bool ob = tk_better(ov, oi, v, ix);
+    if ((lower == desc) ? ob : (!ob && !(ov == v && oi == ix))) { v = ov; ix = oi; }
+}
+
+__device__ __forceinline__ void tk_sort64(float& v, int& ix, int lane) {
+    for (int size = 2; size <= 64; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) tk_stage(v, ix, lane, stride, (lane & size) == 0);
+}
+
+// (v, ix): sorted top list; (gv, gi): another sorted list -> top 64 of the union, sorted.
+__device__ __forceinline__ void tk_merge64(float& v, int& ix, float gv, int gi, int lane) {
+    const float rv = __shfl(gv, 63 - lane, 64);
+    const int ri = __shfl(gi, 63 - lane, 64);
+    if (tk_better(rv, ri, v, ix)) { v = rv; ix = ri; }
+    for (int stride = 32; stride > 0; stride >>= 1) tk_stage(v, ix, lane, stride, true);
+}
+
+__global__ __launch_bounds__(64 * TOPK_WAVES) void topk_partial_kernel(const float* __restrict__ logits, int vocab,
+                                                                         float* __restrict__ sv, int* __restrict__ si) {
+    const int row = blockIdx.y, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int gw = blockIdx.x * TOPK_WAVES + wv, nw = TOPK_P * TOPK_WAVES;
+    const int per = ((vocab + nw - 1) / nw + 63) & ~63;
+    const int lo = gw * per, hi = min(lo + per, vocab);
+    const float* r = logits + (size_t)row * vocab;
+    float v = -INFINITY;
+    int ix = 0x7fffffff;
+    for (int base = lo; base < hi; base += 64) {
+        const int i = base + lane;
+        float gv = (i < hi) ? r[i] : -INFINITY;
+        int gi = (i < hi) ? i : 0x7fffffff;
+        tk_sort64(gv, gi, lane);
+        if (base == lo) { v = gv; ix = gi; }
+        else tk_merge64(v, ix, gv, gi, lane);
+    }
+    const size_t o = ((size_t)row * nw + gw) * 64 + lane;
+    sv[o] = v;
+    si[o] = ix;
+}
+
+__global__ __launch_bounds__(64 * TOPK_WAVES) void topk_final_kernel(const float* __restrict__ sv,
+                                                                       const int* __restrict__ si, int k,
+                                                                       float* __restrict__ out_val,
+                                                                       int* __restrict__ out_idx) {
+    __shared__ float lv[TOPK_WAVES][64];
+    __shared__ int li[TOPK_WAVES][64];
+    const int row = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int nl = TOPK_P * TOPK_WAVES;
+    const size_t base = (size_t)row * nl * 64;
+    float v = sv[base + (size_t)wv * 64 + lane];
+    int ix = si[base + (size_t)wv * 64 + lane];
+    for (int l = wv + TOPK_WAVES; l < nl; l += TOPK_WAVES)
+        tk_merge64(v, ix, sv[base + (size_t)l * 64 + lane], si[base + (size_t)l * 64 + lane], lane);
+    lv[wv][lane] = v;
+    li[wv][lane] = ix;
     __syncthreads();
-    // radix select of the k-th largest key
-    for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
-        for (int i = tid; i < 256; i += blockDim.x) hist[i] = 0;
-        __syncthreads();
-        const uint32_t prefix = sel_prefix;
-        const uint32_t pmask = (pass == 0) ? 0u : (0xFFFFFFFFu << (shift + 8));
-        for (int i = tid; i < vocab; i += blockDim.x) {
-            const uint32_t key = f2key(row[i]);
-            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t need = sel_need, cum = 0;
-            int bin = 255;
-            for (; bin > 0; --bin) {
-                if (cum + hist[bin] >= need) break;
-                cum += hist[bin];
-            }
-            sel_prefix = prefix | ((uint32_t)bin << shift);
-            sel_need = need - cum;
-        }
-        __syncthreads();
-    }
-    const uint32_t thr = sel_prefix;   // exact key of the k-th largest value
-    const int ties_needed = (int)sel_need;
-    // gather: keys above thr (fewer than k of them) go in any order; ties at thr
-    // are ranked by index through a block-wide scan over contiguous ranges.
-    const int per = (vocab + blockDim.x - 1) / blockDim.x;
-    const int lo = tid * per, hi = min(lo + per, vocab);
-    int my_ties = 0;
-    for (int i = lo; i < hi; ++i) {
-        const uint32_t key = f2key(row[i]);
-        if (key > thr) {
-            const int slot = atomicAdd(&n_above, 1);
-            cand_v[slot] = row[i];
-            cand_i[slot] = i;
-        } else if (key == thr) {
-            ++my_ties;
-        }
-    }
-    // exclusive scan of my_ties across the block (wave scan + wave totals)
-    int incl = my_ties;
-    const int lane = tid & 63, wv = tid >> 6;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += t;
-    }
-    if (lane == 63) wave_cnt[wv] = incl;
-    __syncthreads();
-    int base = 0;
-    for (int w = 0; w < wv; ++w) base += wave_cnt[w];
-    int rank = base + incl - my_ties;
-    const int above = k - ties_needed;
-    if (my_ties > 0 && rank < ties_needed) {
-        for (int i = lo; i < hi && rank < ties_needed; ++i) {
-            if (f2key(row[i]) == thr) {
-                cand_v[above + rank] = row[i];
-                cand_i[above + rank] = i;
-                ++rank;
-            }
-        }
-    }
-    __syncthreads();
-    // bitonic sort of 64 candidates in wave 0: value desc, index asc
-    if (tid < 64) {
-        float v = cand_v[tid];
-        int ix = cand_i[tid];
-        for (int size = 2; size <= 64; size <<= 1) {
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                const float ov = __shfl_xor(v, stride, 64);
-                const int oi = __shfl_xor(ix, stride, 64);
-                const bool up = ((tid & size) == 0);          // block sorted "descending-first"
-                const bool lower = ((tid & stride) == 0);
-                const bool other_first = (ov > v) || (ov == v && oi < ix);
-                const bool take = (lower == up) ? other_first : !other_first;
-                if (take) { v = ov; ix = oi; }
-            }
-        }
-        if (tid < k) {
-            out_val[(size_t)blockIdx.x * k + tid] = v;
-            out_idx[(size_t)blockIdx.x * k + tid] = ix;
+    if (wv == 0) {
+        for (int w = 1; w < TOPK_WAVES; ++w) tk_merge64(v, ix, lv[w][lane], li[w][lane], lane);
+        if (lane < k) {
+            out_val[(size_t)row * k + lane] = v;
+            out_idx[(size_t)row * k + lane] = ix;
         }
     }
 }
@@ -336,8 +311,16 @@ hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_
     return hipGetLastError();
 }
 
-hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, hipStream_t st) {
-    hipLaunchKernelGGL(topk_rows_kernel, dim3(rows), dim3(1024), 0, st, logits, vocab, k, out_val, out_idx);
+size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_P * TOPK_WAVES * 64 * (sizeof(float) + sizeof(int)); }
+
+hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
+                hipStream_t st) {
+    float* sv = (float*)scratch;
+    int* si = (int*)((char*)scratch + (size_t)rows * TOPK_P * TOPK_WAVES * 64 * sizeof(float));
+    hipLaunchKernelGGL(topk_partial_kernel, dim3(TOPK_P, rows), dim3(64 * TOPK_WAVES), 0, st, logits, vocab, sv, si);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(64 * TOPK_WAVES), 0, st, sv, si, k, out_val, out_idx);
     return hipGetLastError();
 }
 

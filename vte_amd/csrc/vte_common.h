@@ -21,6 +21,13 @@ __device__ __forceinline__ float h2f_bits(uint32_t bits16) {
     return __half2float(__half(r));
 }
 
+// 16-byte streaming load (weights are read once per step: non-temporal hint).
+typedef unsigned int vte_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg_stream16(const void* p) {
+    const vte_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const vte_u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Activation loads: the same kernels serve fp16 (reference ABI) and fp32
 // (benchmark configs) activations.
 template <typename T> __device__ __forceinline__ float ld_act(const T* p);

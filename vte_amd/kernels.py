@@ -30,18 +30,19 @@ SIGNATURES = {
     "vte_gemm_mfma": [_i, _i, _i, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _f, _vp],
     "vte_dequantize": [_i, _vp, _vp, _ll, _vp],
     "vte_attn_scratch_floats": [_i, _i, _i],
-    "vte_attn_split_kv": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _i, _i, _i, _vp],
+    "vte_attn_split_kv": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _i, _i, _i, _vp, _vp],
     "vte_kv_append": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp],
     "vte_rmsnorm": [_vp, _vp, _vp, _i, _i, _f, _vp],
     "vte_rope": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i, _i, _vp],
     "vte_swiglu": [_vp, _vp, _vp, _i, _vp],
     "vte_add": [_vp, _vp, _vp, _i, _f, _vp],
     "vte_embedding_q6k": [_vp, _vp, _vp, _i, _i, _f, _vp],
-    "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp],
+    "vte_topk_scratch_bytes": [_i],
+    "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
     "vte_fill_normal_f16": [_vp, _ll, ctypes.c_ulonglong, _f, _vp],
     "vte_last_error": [],
 }
-RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll}
+RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll, "vte_topk_scratch_bytes": _ll}
 
 
 def _p(x) -> Optional[int]:
@@ -104,10 +105,12 @@ class VTEKernels:
         return int(self.lib.vte_attn_scratch_floats(batch, n_q, max_splits))
 
     def attn_split_kv(self, q, k_cache, v_cache, part_m, part_l, part_o, out, batch, n_q, n_kv, head_dim, scale,
-                      kv_offset, kv_batch_stride, split, max_splits, dtype="f32", stream=None) -> None:
+                      kv_offset, kv_batch_stride, split, max_splits, dtype="f32", counters=None, stream=None) -> None:
+        """Split-KV decode attention.  With ``counters`` (zeroed int32 [batch * n_kv],
+        kept zero by the kernel) the combine runs inside the partial kernel."""
         self._check(self.lib.vte_attn_split_kv(DT[dtype], _p(q), _p(k_cache), _p(v_cache), _p(part_m), _p(part_l),
                                                _p(part_o), _p(out), batch, n_q, n_kv, head_dim, scale, _p(kv_offset),
-                                               kv_batch_stride, split, max_splits, self._st(stream)),
+                                               kv_batch_stride, split, max_splits, _p(counters), self._st(stream)),
                     "vte_attn_split_kv")
 
     def kv_append(self, k, v, k_cache, v_cache, batch, n_kv, head_dim, kv_offset, kv_batch_stride, stream=None):
@@ -132,9 +135,13 @@ class VTEKernels:
         self._check(self.lib.vte_embedding_q6k(_p(tokens), _p(table), _p(out), n_tokens, hidden, scale,
                                                self._st(stream)), "vte_embedding_q6k")
 
-    def topk(self, logits, rows, vocab, k, out_val, out_idx, stream=None):
-        self._check(self.lib.vte_topk(_p(logits), rows, vocab, k, _p(out_val), _p(out_idx), self._st(stream)),
-                    "vte_topk")
+    def topk_scratch_bytes(self, rows: int) -> int:
+        return int(self.lib.vte_topk_scratch_bytes(rows))
+
+    def topk(self, logits, rows, vocab, k, out_val, out_idx, scratch, stream=None):
+        """Top-k (k <= 64) per row, (value desc, index asc); scratch of topk_scratch_bytes(rows)."""
+        self._check(self.lib.vte_topk(_p(logits), rows, vocab, k, _p(out_val), _p(out_idx), _p(scratch),
+                                      self._st(stream)), "vte_topk")
 
     def fill_normal_f16(self, dst, n, seed, scale=1.0, stream=None):
         self._check(self.lib.vte_fill_normal_f16(_p(dst), n, seed, scale, self._st(stream)), "vte_fill_normal_f16")
