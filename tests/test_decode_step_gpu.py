@@ -63,6 +63,28 @@ def test_tiny_step_matches_oracle(hip, tiny_model, B):
         ex.close()
 
 
+@pytest.mark.parametrize("B", [1, 2, 4])
+def test_fused_step_matches_unfused(hip, tiny_model, B):
+    """Fused norm/QKV/RoPE/append, gate/up/SwiGLU and norm/LM-head kernels give the
+    same step as the separate kernels (same rounding points, fp32 sums reordered)."""
+    outs = []
+    for fused in (False, True):
+        ex = HIPGraphExecutor(hip, tiny_model, batch_size=B, max_seq=256, fused=fused)
+        try:
+            ex.fill_kv_prefix(seed=4)
+            ex.execute_decode_batch(list(range(3, 3 + B)), [100 + 7 * b for b in range(B)])
+            outs.append((ex.read_logits(), [ex.k_cache[L].numpy() for L in range(tiny_model.cfg.n_layers)]))
+        finally:
+            ex.close()
+    for b in range(B):
+        assert rel_l2(outs[1][0][b], outs[0][0][b]) <= TOL
+    for L in range(tiny_model.cfg.n_layers):  # the appended K rows agree to fp16 rounding
+        for b in range(B):
+            k0 = outs[0][1][L][b, 100 + 7 * b].astype(np.float32)
+            k1 = outs[1][1][L][b, 100 + 7 * b].astype(np.float32)
+            assert rel_l2(k1, k0) <= 5e-3
+
+
 def test_graph_replay_equals_eager(hip, tiny_model):
     cfg = tiny_model.cfg
     ex = HIPGraphExecutor(hip, tiny_model, batch_size=2, max_seq=128)

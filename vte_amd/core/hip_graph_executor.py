@@ -41,7 +41,7 @@ class GraphCaptureError(RuntimeError):
 
 class HIPGraphExecutor:
     def __init__(self, hip: HIPRuntime, model: SyntheticQwen2, batch_size: int = 1, max_seq: Optional[int] = None,
-                 top_k: int = 40, gemm_min_batch: int = 8, split: Optional[int] = None):
+                 top_k: int = 40, gemm_min_batch: int = 8, split: Optional[int] = None, fused: bool = True):
         self.hip = hip
         self.cfg: Qwen2Config = model.cfg
         cfg = self.cfg
@@ -49,6 +49,8 @@ class HIPGraphExecutor:
         self.max_seq = max_seq or cfg.max_seq
         self.top_k = top_k
         self.gemm_min_batch = gemm_min_batch
+        # fused norm+QKV+RoPE+append / norm+gate+up+SwiGLU / norm+LM-head kernels (batch <= 4)
+        self.fused = fused and batch_size <= 4
         self.K = kernels()
         self.graph = None
         self.graph_exec = None
@@ -113,8 +115,38 @@ class HIPGraphExecutor:
             self.K.gemv(fmt, x, w, y, self.B, K_in, N, bias=bias, residual=residual, in_dtype="f16",
                         out_dtype=out_dtype, stream=st)
 
+    def _enqueue_fused(self) -> None:
+        """Six launches per layer: norm+QKV+RoPE+append, attention (2), o-proj,
+        norm+gate/up+SwiGLU, down; then norm+LM head and top-k."""
+        cfg, K, st, B = self.cfg, self.K, self.hip.stream, self.B
+        H = cfg.hidden
+        offs = self.staging_kv_offset
+        cur = 0
+        K.embedding_q6k(self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
+        for L, lw in enumerate(self.layers):
+            K.attn_in(self.h[cur], lw["attn_norm"], cfg.eps, lw["q"], lw["q_bias"], lw["q_fmt"], lw["k"], lw["k_bias"],
+                      lw["k_fmt"], lw["v"], lw["v_bias"], lw["v_fmt"], self.q, self.k_cache[L], self.v_cache[L], offs,
+                      self.kv_batch_stride, self.rope_cos, self.rope_sin, B, H, cfg.n_q, cfg.n_kv, cfg.head_dim,
+                      stream=st)
+            self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], self.att, offs, self.kv_batch_stride,
+                             dtype="f16", batch=B, stream=st)
+            self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
+            cur = 1 - cur
+            K.ffn_in(self.h[cur], lw["ffn_norm"], cfg.eps, lw["gate"], lw["up"], lw["gate_fmt"], self.a, B, H, cfg.ffn,
+                     stream=st)
+            self._linear(lw["down_fmt"], self.a, lw["down"], self.h[1 - cur], cfg.ffn, H, residual=self.h[cur])
+            cur = 1 - cur
+        self.h_final = cur
+        K.norm_gemv(self.h[cur], self.output_norm, cfg.eps, self.token_embd, "q6_k", self.logits, B, H, cfg.vocab,
+                    out_dtype="f32", stream=st)
+        if self.top_k > 0:
+            K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st)
+
     def enqueue_step(self) -> None:
         """Issue every kernel of one decode step on the runtime stream."""
+        if self.fused:
+            self._enqueue_fused()
+            return
         cfg, K, st, B = self.cfg, self.K, self.hip.stream, self.B
         H = cfg.hidden
         offs = self.staging_kv_offset

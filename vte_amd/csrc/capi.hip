@@ -40,6 +40,14 @@ size_t topk_scratch_bytes(int rows);
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
                 hipStream_t st);
 hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, hipStream_t st);
+hipError_t attn_in(const void* x, const void* norm_w, float eps, const void* wq, const void* q_bias, int fmt_q,
+                   const void* wk, const void* k_bias, int fmt_k, const void* wv, const void* v_bias, int fmt_v,
+                   void* q_out, void* k_cache, void* v_cache, const int* kv_offset, int kv_batch_stride,
+                   const void* rope_cos, const void* rope_sin, int M, int K, int n_q, int n_kv, hipStream_t st);
+hipError_t ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up, int fmt,
+                  void* out, int M, int K, int ffn, hipStream_t st);
+hipError_t norm_mv(const void* x, const void* norm_w, float eps, const void* w, int fmt, void* out, bool out_f32,
+                   const void* bias, const void* residual, float rs, int M, int K, int N, hipStream_t st);
 }  // namespace vte
 
 static thread_local char g_err[512] = "";
@@ -221,6 +229,53 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
     REQUIRE(rows <= 65535, "topk: rows %d out of range", rows);
     return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream),
                       "vte_topk launch");
+}
+
+int vte_attn_in(const void* x, const void* norm_w, float eps, const void* wq, const void* q_bias, int fmt_q,
+                const void* wk, const void* k_bias, int fmt_k, const void* wv, const void* v_bias, int fmt_v,
+                void* q_out, void* k_cache, void* v_cache, const int* kv_offset, int kv_batch_stride,
+                const void* rope_cos, const void* rope_sin, int batch, int hidden, int n_q, int n_kv, int head_dim,
+                void* stream) {
+    REQUIRE(x && norm_w && wq && wk && wv && q_out && k_cache && v_cache && kv_offset && rope_cos && rope_sin,
+            "attn_in: null pointer");
+    REQUIRE(head_dim == 128, "attn_in: head_dim must be 128");
+    REQUIRE(batch >= 1 && batch <= 4, "attn_in: batch %d outside 1..4 (larger batches use the MFMA path)", batch);
+    REQUIRE(hidden % 256 == 0 && hidden <= 8192, "attn_in: hidden %d unsupported", hidden);
+    REQUIRE(fmt_q == 4 && fmt_k == 4 && (fmt_v == 4 || fmt_v == 6), "attn_in: q/k must be Q4_K, v Q4_K or Q6_K");
+    REQUIRE(n_kv >= 1 && n_q >= n_kv && n_q % n_kv == 0, "attn_in: bad head counts");
+    REQUIRE(aligned(x, 16) && aligned(wq, 16) && aligned(wk, 16) && aligned(wv, 16), "attn_in: 16-byte alignment");
+    hipError_t e = vte::attn_in(x, norm_w, eps, wq, q_bias, fmt_q, wk, k_bias, fmt_k, wv, v_bias, fmt_v, q_out,
+                                k_cache, v_cache, kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q,
+                                n_kv, (hipStream_t)stream);
+    if (e == hipErrorNotSupported) return fail("attn_in: shape does not fit the fused kernel's LDS plan");
+    return hip_status(e, "vte_attn_in launch");
+}
+
+int vte_ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up, int fmt,
+               void* out, int batch, int hidden, int ffn, void* stream) {
+    REQUIRE(x && norm_w && w_gate && w_up && out, "ffn_in: null pointer");
+    REQUIRE(fmt == 4, "ffn_in: gate/up must be Q4_K");
+    REQUIRE(batch >= 1 && batch <= 4, "ffn_in: batch %d outside 1..4", batch);
+    REQUIRE(hidden % 256 == 0 && hidden <= 8192 && ffn >= 1, "ffn_in: bad shape");
+    REQUIRE(aligned(x, 16) && aligned(w_gate, 16) && aligned(w_up, 16), "ffn_in: 16-byte alignment");
+    hipError_t e = vte::ffn_in(x, norm_w, eps, w_gate, w_up, fmt, out, batch, hidden, ffn, (hipStream_t)stream);
+    if (e == hipErrorNotSupported) return fail("ffn_in: shape does not fit the fused kernel's LDS plan");
+    return hip_status(e, "vte_ffn_in launch");
+}
+
+int vte_norm_gemv(const void* x, const void* norm_w, float eps, const void* w, int fmt, void* out, int out_dtype,
+                  const void* bias, const void* residual, float residual_scale, int batch, int K, int N,
+                  void* stream) {
+    REQUIRE(x && norm_w && w && out, "norm_gemv: null pointer");
+    REQUIRE(fmt == 4 || fmt == 6, "norm_gemv: Q4_K or Q6_K");
+    REQUIRE(out_dtype == VTE_F32 || out_dtype == VTE_F16, "norm_gemv: bad out dtype");
+    REQUIRE(batch >= 1 && batch <= 4, "norm_gemv: batch %d outside 1..4", batch);
+    REQUIRE(K % 256 == 0 && K <= 8192 && N >= 1, "norm_gemv: bad shape");
+    REQUIRE(aligned(x, 16) && aligned(w, 16), "norm_gemv: 16-byte alignment");
+    hipError_t e = vte::norm_mv(x, norm_w, eps, w, fmt, out, out_dtype == VTE_F32, bias, residual, residual_scale,
+                                batch, K, N, (hipStream_t)stream);
+    if (e == hipErrorNotSupported) return fail("norm_gemv: shape does not fit the fused kernel's LDS plan");
+    return hip_status(e, "vte_norm_gemv launch");
 }
 
 int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, void* stream) {

@@ -6,12 +6,15 @@
 // epilogue).  The row-dot engine (work units, packed-fp16 inner product,
 // deterministic row reduction) is rows.h.
 //
-// Per block (256 threads) and rows [r0, r0 + R):
-//  1. weight loads are issued first: Q4_K units straight into registers,
-//     Q6_K rows as 16-byte aligned chunks bound for LDS;
-//  2. the activations are staged into LDS as fp16 with their per-16 sums;
-//  3. each thread computes the partial of its units, rows are summed by waves
-//     and the epilogue applies bias, residual scale and residual.
+// Persistent: grid = CUs x resident blocks, each block walks tiles of R rows.
+// Per block (256 threads):
+//  1. the activations are staged once into LDS as fp16 with their per-16 sums;
+//  2. per tile, the next tile's weights are loaded while the current one is
+//     consumed: Q4_K units straight into registers, Q6_K rows as 16-byte
+//     aligned chunks that go through LDS (Q6_K blocks are 2-byte aligned);
+//  3. each thread computes the partial of its units, rows are summed with one
+//     thread per (column, row) and the epilogue applies bias, residual scale
+//     and residual.
 #include "rows.h"
 
 #define QMV_MAX_LDS 65536
@@ -103,12 +106,7 @@ __global__ __launch_bounds__(ROWS_THREADS) void qmv_kernel(const void* __restric
     load_tile(t, cur);
     // activations -> LDS fp16, then per-16 sums
     const int ldx = xpad_len(K);
-    for (int i = tid; i < NC * K; i += ROWS_THREADS) {
-        const int m = i / K, e = i - m * K;
-        float v = 0.f;
-        if (m < M) v = x_f32 ? reinterpret_cast<const float*>(x)[i] : (float)reinterpret_cast<const _Float16*>(x)[i];
-        xs[m * ldx + xpad(e)] = (_Float16)v;
-    }
+    stage_act<NC>(x, x_f32 != 0, M, K, xs);
     if (FMT == 6) store_stage(t);
     __syncthreads();
     act_sums<NC>(ActLDS{xs, s16}, K);
@@ -201,12 +199,12 @@ static hipError_t qmv_go(const void* x, bool x_f32, const void* w, void* y, int 
     if (FMT == 4 && R * (K / 256) * 4 > ROWS_THREADS * Q4_UNITS_PER_THREAD) return hipErrorNotSupported;
     if (FMT == 6 && ((size_t)R * (K / 256) * 210 + 48) > (size_t)ROWS_THREADS * Q6_STAGE_PER_THREAD * 16)
         return hipErrorNotSupported;
-    static int per_cu[2] = {0, 0};  // cached occupancy per LDS size class is approximate; recompute when 0
+    // staging reads x in 16-byte chunks
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || (K & 7)) return hipErrorNotSupported;
     int blocks = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, (const void*)qmv_kernel<NC, FMT, TO>, ROWS_THREADS,
                                                      L.total) != hipSuccess || blocks <= 0)
         blocks = 1;
-    (void)per_cu;
     const int n_tiles = (N + R - 1) / R;
     int grid = num_cus() * blocks;
     if (grid > n_tiles) grid = n_tiles;

@@ -53,6 +53,54 @@ struct ActLDS {
     float* s16;    // [NC][K/16]
 };
 
+// Stage NC activation columns ([M][K], fp32 or fp16; columns >= M are zero)
+// into the padded fp16 LDS layout.  Each thread issues up to 8 independent
+// 16-byte loads before it stores any, so the staging costs one memory latency
+// rather than one per element.  Chunks of 8 elements stay contiguous in the
+// padded layout (pads fall every 64 elements).
+template <int NC>
+__device__ __forceinline__ void stage_act(const void* __restrict__ x, bool x_f32, int M, int K, _Float16* xs) {
+    const int ldx = xpad_len(K);
+    const int per_col = K / 8;
+    const int nch = NC * per_col;
+    for (int c0 = 0; c0 < nch; c0 += 8 * ROWS_THREADS) {
+        uint4 v[8][2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = c0 + j * ROWS_THREADS + threadIdx.x;
+            const int m = c / per_col;
+            if (c < nch && m < M) {
+                if (x_f32) {
+                    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(x) + (size_t)c * 8);
+                    v[j][0] = p[0];
+                    v[j][1] = p[1];
+                } else {
+                    v[j][0] = reinterpret_cast<const uint4*>(x)[c];
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = c0 + j * ROWS_THREADS + threadIdx.x;
+            if (c >= nch) break;
+            const int m = c / per_col, e = (c - m * per_col) * 8;
+            uint4 o = make_uint4(0, 0, 0, 0);
+            if (m < M) {
+                if (x_f32) {
+                    const float* f = reinterpret_cast<const float*>(&v[j][0]);
+                    _Float16 hh[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) hh[i] = (_Float16)f[i];
+                    o = *reinterpret_cast<const uint4*>(hh);
+                } else {
+                    o = v[j][0];
+                }
+            }
+            *reinterpret_cast<uint4*>(xs + (size_t)m * ldx + xpad(e)) = o;
+        }
+    }
+}
+
 // After x is in LDS (and a barrier), fill the per-16 sums.  Caller places a
 // barrier afterwards.
 template <int NC>

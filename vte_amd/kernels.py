@@ -40,6 +40,10 @@ SIGNATURES = {
     "vte_topk_scratch_bytes": [_i],
     "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
     "vte_fill_normal_f16": [_vp, _ll, ctypes.c_ulonglong, _f, _vp],
+    "vte_attn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp,
+                    _i, _i, _i, _i, _i, _vp],
+    "vte_ffn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp],
+    "vte_norm_gemv": [_vp, _vp, _f, _vp, _i, _vp, _i, _vp, _vp, _f, _i, _i, _i, _vp],
     "vte_last_error": [],
 }
 RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll, "vte_topk_scratch_bytes": _ll}
@@ -142,6 +146,27 @@ class VTEKernels:
         """Top-k (k <= 64) per row, (value desc, index asc); scratch of topk_scratch_bytes(rows)."""
         self._check(self.lib.vte_topk(_p(logits), rows, vocab, k, _p(out_val), _p(out_idx), _p(scratch),
                                       self._st(stream)), "vte_topk")
+
+    def attn_in(self, x, norm_w, eps, wq, q_bias, fmt_q, wk, k_bias, fmt_k, wv, v_bias, fmt_v, q_out, k_cache,
+                v_cache, kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q, n_kv, head_dim=128,
+                stream=None):
+        """Fused rmsnorm -> q/k/v GEMV (+bias) -> RoPE(q, k) -> K/V append (batch <= 4)."""
+        self._check(self.lib.vte_attn_in(_p(x), _p(norm_w), eps, _p(wq), _p(q_bias), FMT[fmt_q], _p(wk), _p(k_bias),
+                                         FMT[fmt_k], _p(wv), _p(v_bias), FMT[fmt_v], _p(q_out), _p(k_cache),
+                                         _p(v_cache), _p(kv_offset), kv_batch_stride, _p(rope_cos), _p(rope_sin),
+                                         batch, hidden, n_q, n_kv, head_dim, self._st(stream)), "vte_attn_in")
+
+    def ffn_in(self, x, norm_w, eps, w_gate, w_up, fmt, out, batch, hidden, ffn, stream=None):
+        """Fused rmsnorm -> gate/up GEMV -> SwiGLU (batch <= 4)."""
+        self._check(self.lib.vte_ffn_in(_p(x), _p(norm_w), eps, _p(w_gate), _p(w_up), FMT[fmt], _p(out), batch,
+                                        hidden, ffn, self._st(stream)), "vte_ffn_in")
+
+    def norm_gemv(self, x, norm_w, eps, w, fmt, out, batch, K, N, out_dtype="f16", bias=None, residual=None,
+                  residual_scale=1.0, stream=None):
+        """Fused rmsnorm -> GEMV with the store epilogue (batch <= 4)."""
+        self._check(self.lib.vte_norm_gemv(_p(x), _p(norm_w), eps, _p(w), FMT[fmt], _p(out), DT[out_dtype], _p(bias),
+                                           _p(residual), residual_scale, batch, K, N, self._st(stream)),
+                    "vte_norm_gemv")
 
     def fill_normal_f16(self, dst, n, seed, scale=1.0, stream=None):
         self._check(self.lib.vte_fill_normal_f16(_p(dst), n, seed, scale, self._st(stream)), "vte_fill_normal_f16")
