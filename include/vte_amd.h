@@ -1,0 +1,176 @@
+/*
+ * libvte_amd.so — C ABI of the MI355X (gfx950) decode hot path.
+ *
+ * Plain pointers, sizes and a hipStream_t passed as void* (NULL = the null
+ * stream).  Every device pointer is a device address the caller owns (e.g. a
+ * slice of one slab allocation); no entry point allocates or frees device
+ * memory, and every launch is asynchronous on `stream`.
+ *
+ * Return value: 0 on success, VTE_EINVAL (-1) when host-side validation
+ * rejects an argument (nothing is launched), otherwise the hipError_t of the
+ * failed launch.  vte_last_error() returns the message of the last failure.
+ *
+ * Codes:  dtype  VTE_F32 = 0, VTE_F16 = 1
+ *         fmt    VTE_Q4_K = 4 (144 B / 256 elements), VTE_Q6_K = 6 (210 B / 256),
+ *                VTE_Q8_0 = 8 (34 B / 32)
+ * Weight matrices are raw GGUF super-block rows: row r of an N x K matrix
+ * starts at byte r * (K / block_elems) * block_bytes.
+ *
+ * Each declaration names the reference interface it replaces
+ * (kyuubyN/VTE, paths relative to the repository root).  The same kernels are
+ * also exported under the reference's own kernel symbols from the code object
+ * vte_kernels_gfx950.hsaco (hipModuleGetFunction drop-in): gemv_q4k_kernel,
+ * gemv_q6k_kernel, gemv_q8_0_kernel, kv_cache_append_kernel,
+ * flash_attention_split_kv_partial_kernel, flash_attention_split_kv_reduce_kernel,
+ * rmsnorm_kernel, rope_kernel, swiglu_kernel, add_kernel,
+ * embedding_lookup_q6k_kernel.
+ */
+#ifndef VTE_AMD_H
+#define VTE_AMD_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VTE_EINVAL (-1)
+#define VTE_F32 0
+#define VTE_F16 1
+#define VTE_Q4_K 4
+#define VTE_Q6_K 6
+#define VTE_Q8_0 8
+
+/* Message of the last failed call (thread-unsafe static buffer).
+ * Replaces: HIPRuntimeError text, vte/bridge/hip_runtime.py:342-344. */
+const char* vte_last_error(void);
+
+/* ABI revision of this header (1). */
+int vte_abi_version(void);
+
+/* CU count, HBM bytes and gfx arch name of `device`.
+ * Replaces: HIPRuntime.get_num_cus / get_gpu_architecture, vte/bridge/hip_runtime.py. */
+int vte_device_info(int device, int* n_cu, long long* total_mem, char* arch, int arch_len);
+
+/* y[m][n] = ((sum_k W[n][k] x[m][k]) + bias[n]) * residual_scale + residual[m][n]
+ * for m < M (batch rows), fp32 accumulation.  x [M][K] in in_dtype, y [M][N]
+ * in out_dtype; bias fp16/f32 [N] and residual [M][N] (out_dtype) nullable.
+ * fmt Q4_K / Q6_K / Q8_0; K a multiple of 256 (Q8_0: 32).  M <= 4 runs the
+ * persistent bandwidth kernel, larger M the wave-per-row kernel.
+ * Replaces: gemv_q4k_kernel (vte/compiler/templates/rdna/gemv_q4k.hip.template:56-168),
+ *           gemv_q6k_kernel (gemv_q6k.hip.template:25-104),
+ *           gemv_q8_0_kernel (gemv_q8_0.hip.template:26-93),
+ *           launch geometry vte/core/fallback_executor.py:140-148,
+ *           arguments vte/core/kernel_arg_builder.py:327-386. */
+int vte_gemv(int fmt, int in_dtype, int out_dtype, const void* x, const void* w, void* y, int M, int K, int N,
+             const void* bias, const void* residual, float residual_scale, void* stream);
+
+/* Same contract as vte_gemv, batched (M >= 8) on MFMA: super-blocks are
+ * dequantised to fp16 in registers and multiplied with
+ * mfma_f32_16x16x32_f16, fp32 accumulation.  Q4_K and Q6_K.
+ * Replaces: the per-row GEMV launches with grid.y = batch of
+ * vte/core/batched_hip_graph_executor.py:231-251 (the reference has no MFMA path). */
+int vte_gemm_mfma(int fmt, int in_dtype, int out_dtype, const void* x, const void* w, void* y, int M, int K,
+                  int N, const void* bias, const void* residual, float residual_scale, void* stream);
+
+/* Dequantise n_elements (a multiple of the block size) to fp32, bit-exact with
+ * the reference's NumPy dequantiser.
+ * Replaces: dequantize_q4_k / dequantize_q6_k / dequantize_q8_0
+ *           (vte/compiler/dequantizer.py:26-70, 129-169, 172-196). */
+int vte_dequantize(int fmt, const void* src, float* dst, long long n_elements, void* stream);
+
+/* Floats of split-KV scratch (part_m + part_l + part_o) for a shape. */
+long long vte_attn_scratch_floats(int batch, int n_q, int max_splits);
+
+/* Split-KV flash decoding with log-sum-exp combine, ragged batches.
+ * q [B][n_q][128] (dtype), caches fp16 [B][max_seq][n_kv][128] with
+ * kv_batch_stride elements between sequences, out [B][n_q][128] (dtype).
+ * Sequence b attends to positions 0..kv_offset[b] (device int array), split
+ * tokens per partial block (multiple of 32), max_splits >= ceil(max_seq/split)
+ * (at most 4096).  part_m/part_l [B][n_q][max_splits], part_o
+ * [B][n_q][max_splits][128] fp32 scratch.  counters: NULL = separate combine
+ * launch; else B*n_kv zeroed ints and the combine runs in the last partial
+ * block of each (sequence, KV head) (max_splits <= 512), leaving them zero.
+ * Replaces: SplitKVAttentionDispatcher launches (vte/core/split_kv_attention.py:187-217),
+ *           flash_attention_split_kv_partial_kernel (flash_attention_split_kv_partial.hip.template:31-120),
+ *           flash_attention_split_kv_reduce_kernel (flash_attention_split_kv_reduce.hip.template:14-67). */
+int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void* v_cache, float* part_m,
+                      float* part_l, float* part_o, void* out, int batch, int n_q, int n_kv, int head_dim,
+                      float scale, const int* kv_offset, int kv_batch_stride, int split, int max_splits,
+                      int* counters, void* stream);
+
+/* k_cache[b][kv_offset[b]] = k[b], v_cache likewise (fp16 [B][n_kv][head_dim]).
+ * Replaces: kv_cache_append_kernel (kv_cache_append.hip.template:13-39). */
+int vte_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int batch, int n_kv, int head_dim,
+                  const int* kv_offset, int kv_batch_stride, void* stream);
+
+/* out = fp16(x * rsqrt(mean(x^2) + eps) * w), rows x hidden, fp16.
+ * Replaces: rmsnorm_kernel (rmsnorm.hip.template:6-117). */
+int vte_rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps, void* stream);
+
+/* In-place rotary embedding of q [B][seq][n_q][hd] and k [B][seq][n_kv][hd]
+ * at positions kv_offset[b] + s, fp16 cos/sin caches [max_seq][hd].
+ * rope_type 0 = NORM (adjacent pairs), 1 = NEOX (i, i + hd/2), 2 = partial
+ * NEOX over rotary_dim.
+ * Replaces: rope_kernel (rope.hip.template:17-137; NEOX at :82-97). */
+int vte_rope(void* q, void* k, const void* cos_cache, const void* sin_cache, int batch, int seq_len, int n_q,
+             int n_kv, int head_dim, const int* kv_offset, int rope_type, int rotary_dim, void* stream);
+
+/* out = fp16(silu(gate) * up), n fp16 elements.
+ * Replaces: swiglu_kernel (swiglu.hip.template:4-26). */
+int vte_swiglu(const void* gate, const void* up, void* out, int n, void* stream);
+
+/* out = fp16(residual + scale * input), n fp16 elements.
+ * Replaces: add_kernel (add.hip.template:4-17). */
+int vte_add(const void* residual, const void* input, void* out, int n, float scale, void* stream);
+
+/* out[t] = fp16(dequant(table row tokens[t]) * scale), Q6_K table [vocab][hidden].
+ * Replaces: embedding_lookup_q6k_kernel (embedding_lookup_q6k.hip.template:17-58). */
+int vte_embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
+                      void* stream);
+
+/* Bytes of device scratch vte_topk needs for `rows` rows. */
+long long vte_topk_scratch_bytes(int rows);
+
+/* Per row of fp32 logits [rows][vocab]: the k (1..64) largest values in
+ * descending order, ties broken by the lower index, with their indices.
+ * Replaces: the argpartition top-k of Sampler.sample (vte/core/sampler.py:54-129)
+ *           and topk_reduce_greedy_kernel (topk_reduce_greedy.hip.template:52-83). */
+int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
+             void* stream);
+
+/* One launch: RMSNorm(x) -> q/k/v projections (+bias) -> NEOX RoPE on q and k
+ * -> q to q_out [B][n_q*128], k and v appended to the caches at kv_offset[b].
+ * Same rounding points as the unfused nodes.  batch 1..4, head_dim 128,
+ * q/k Q4_K, v Q4_K or Q6_K.
+ * Replaces: the rmsnorm -> q/k/v gemv -> rope -> kv_cache_append nodes
+ *           (vte/compiler/qwen_compute.py:100-282) and their fused forms
+ *           FusedQKVDispatcher (vte/core/fused_qkv_dispatch.py:12-198),
+ *           fused_norm_matmul_rope_kernel (fused_norm_matmul_rope.hip.template:34-199). */
+int vte_attn_in(const void* x, const void* norm_w, float eps, const void* wq, const void* q_bias, int fmt_q,
+                const void* wk, const void* k_bias, int fmt_k, const void* wv, const void* v_bias, int fmt_v,
+                void* q_out, void* k_cache, void* v_cache, const int* kv_offset, int kv_batch_stride,
+                const void* rope_cos, const void* rope_sin, int batch, int hidden, int n_q, int n_kv, int head_dim,
+                void* stream);
+
+/* One launch: RMSNorm(x) -> gate and up projections -> fp16(silu(g) * u),
+ * out [B][ffn].  batch 1..4, Q4_K gate/up.
+ * Replaces: FusedFFNDispatcher (vte/core/fused_qkv_dispatch.py:200-270) with
+ *           fused_gate_up_silu_kernel (fused_rmsnorm_gate_up_silu.hip.template:66-111). */
+int vte_ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up, int fmt,
+               void* out, int batch, int hidden, int ffn, void* stream);
+
+/* One launch: RMSNorm(x) followed by the vte_gemv contract (the LM head with
+ * out_dtype f32).  batch 1..4.
+ * Replaces: the output_norm + LM-head capture (vte/core/hip_graph_executor.py:429-474). */
+int vte_norm_gemv(const void* x, const void* norm_w, float eps, const void* w, int fmt, void* out, int out_dtype,
+                  const void* bias, const void* residual, float residual_scale, int batch, int K, int N,
+                  void* stream);
+
+/* dst[i] = fp16(scale * N(0,1)) from a counter-based generator (synthetic KV
+ * prefixes); no reference counterpart (test and benchmark input). */
+int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VTE_AMD_H */

@@ -1,0 +1,66 @@
+"""The C ABI library loads on a host without a GPU, exports every function that
+include/vte_amd.h declares with the argument count the ctypes binding uses,
+and rejects bad arguments on the host before anything is launched."""
+import ctypes
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+HEADER = ROOT / "include" / "vte_amd.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(vte_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def _lib():
+    from vte_amd.kernels import LIB_PATH
+    if not LIB_PATH.exists():
+        pytest.fail(f"{LIB_PATH} missing: run __graft_entry__.build() first")
+    return ctypes.CDLL(str(LIB_PATH))
+
+
+def test_header_declares_the_api():
+    decl = _declared()
+    assert len(decl) >= 20, decl
+    for name in ("vte_gemv", "vte_gemm_mfma", "vte_dequantize", "vte_attn_split_kv", "vte_topk", "vte_attn_in"):
+        assert name in decl
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_ctypes_signatures_match_header():
+    from vte_amd.kernels import SIGNATURES
+    decl = _declared()
+    assert set(SIGNATURES) == set(decl), set(SIGNATURES) ^ set(decl)
+    for name, n in decl.items():
+        assert len(SIGNATURES[name]) == n, (name, len(SIGNATURES[name]), n)
+
+
+def test_host_side_queries_and_validation():
+    from vte_amd.kernels import kernels
+    K = kernels()
+    lib = K.lib
+    assert lib.vte_abi_version() == 1
+    assert K.topk_scratch_bytes(4) > 0
+    assert lib.vte_attn_scratch_floats(2, 12, 16) == 2 * 12 * 16 * 130
+    # rejected on the host: unknown format, K not a multiple of the block, bad top-k
+    assert lib.vte_gemv(5, 0, 0, 16, 16, 16, 1, 256, 8, None, None, ctypes.c_float(1.0), None) == -1
+    assert b"format" in lib.vte_last_error()
+    assert lib.vte_gemv(4, 0, 0, 16, 16, 16, 1, 100, 8, None, None, ctypes.c_float(1.0), None) == -1
+    assert lib.vte_topk(16, 1, 100, 65, 16, 16, 16, None) == -1
+    assert lib.vte_attn_split_kv(0, 16, 16, 16, 16, 16, 16, 16, 1, 12, 2, 64, ctypes.c_float(1.0), 16, 0, 256, 4,
+                                 None, None) == -1
+    assert b"head_dim" in lib.vte_last_error()
+    assert lib.vte_dequantize(6, 16, 16, 100, None) == -1

@@ -33,6 +33,7 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 #define ATT_TILE 32  // tokens per wave step (two 16-token MFMA tiles)
 #define ATT_MAXG 8   // query heads per KV head served by one block
 #define ATT_MAX_COMBINE 512  // splits per sequence the in-kernel combine handles
+#define ATT_MAX_SPLITS 4096  // splits per sequence the separate combine handles
 #define ATT_VT_STRIDE 36     // halves per row of the transposed V tile (32 tokens + pad)
 
 // ---------------------------------------------------------------------------
@@ -320,18 +321,45 @@ __global__ __launch_bounds__(128) void attn_combine(const float* __restrict__ pa
                                                     const float* __restrict__ part_o, TO* __restrict__ out,
                                                     int n_q, const int* __restrict__ kv_offset, int split,
                                                     int max_splits) {
-    const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    // All loads are issued before any result is needed: split statistics are
+    // read one split per thread, the partial outputs eight splits at a time.
+    __shared__ float w_sh[ATT_MAX_SPLITS];
+    __shared__ float red[2][2];
+    const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x, lane = d & 63, wv = d >> 6;
     const int len = kv_offset[b] + 1;
     const int ns = (len + split - 1) / split;
     const size_t base = ((size_t)b * n_q + qh) * max_splits;
-    float M = -1e30f;
-    for (int c = 0; c < ns; ++c) M = fmaxf(M, part_m[base + c]);
-    float L = 0.f, O = 0.f;
-    for (int c = 0; c < ns; ++c) {
-        const float w = __expf(part_m[base + c] - M);
-        L = fmaf(part_l[base + c], w, L);
-        O = fmaf(part_o[(base + c) * ATT_D + d], w, O);
+    float mloc = -1e30f;
+    for (int c = d; c < ns; c += 128) {
+        const float m = part_m[base + c];
+        w_sh[c] = m;
+        mloc = fmaxf(mloc, m);
     }
+    mloc = wave_max(mloc);
+    if (lane == 0) red[0][wv] = mloc;
+    __syncthreads();
+    const float M = fmaxf(red[0][0], red[0][1]);
+    float lloc = 0.f;
+    for (int c = d; c < ns; c += 128) {
+        const float w = __expf(w_sh[c] - M);
+        w_sh[c] = w;
+        lloc = fmaf(part_l[base + c], w, lloc);
+    }
+    lloc = wave_sum(lloc);
+    if (lane == 0) red[1][wv] = lloc;
+    __syncthreads();
+    const float L = red[1][0] + red[1][1];
+    const float* po = part_o + base * ATT_D + d;
+    float O = 0.f;
+    int c = 0;
+    for (; c + 8 <= ns; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = po[(size_t)(c + i) * ATT_D];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) O = fmaf(v[i], w_sh[c + i], O);
+    }
+    for (; c < ns; ++c) O = fmaf(po[(size_t)c * ATT_D], w_sh[c], O);
     st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(L, 1e-20f));
 }
 

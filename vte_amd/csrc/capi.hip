@@ -3,16 +3,14 @@
 // a kernel never runs with a geometry it does not support.  Return value: 0 on
 // success, VTE_EINVAL (-1) for a rejected argument, otherwise the hipError_t
 // of the failed launch; vte_last_error() gives the message.  Declarations and
-// reference citations: include/vte_amd.h.
+// reference citations: include/vte_amd.h (included, so the compiler checks
+// every definition against its declaration).
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 
+#include "../../include/vte_amd.h"
 #include "vte_common.h"
-
-#define VTE_EINVAL (-1)
-#define VTE_F32 0
-#define VTE_F16 1
 
 namespace vte {
 template <typename TI, typename TO>
@@ -158,7 +156,7 @@ int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void*
     REQUIRE(batch >= 1 && n_kv >= 1 && n_q >= n_kv && n_q % n_kv == 0, "attn: bad head counts %d/%d", n_q, n_kv);
     REQUIRE(n_q / n_kv <= 8, "attn: GQA group %d > 8 unsupported", n_q / n_kv);
     REQUIRE(split >= 32 && split % 32 == 0, "attn: split %d must be a positive multiple of 32", split);
-    REQUIRE(max_splits >= 1 && max_splits <= 65535, "attn: max_splits %d out of range", max_splits);
+    REQUIRE(max_splits >= 1 && max_splits <= 4096, "attn: max_splits %d out of range (1..4096)", max_splits);
     REQUIRE(counters == nullptr || max_splits <= 512, "attn: in-kernel combine supports at most 512 splits");
     REQUIRE(aligned(k_cache, 16) && aligned(v_cache, 16), "attn: KV cache must be 16-byte aligned");
     REQUIRE(kv_batch_stride % 8 == 0, "attn: kv_batch_stride must keep rows 16-byte aligned");
@@ -243,7 +241,7 @@ int vte_attn_in(const void* x, const void* norm_w, float eps, const void* wq, co
     REQUIRE(hidden % 256 == 0 && hidden <= 8192, "attn_in: hidden %d unsupported", hidden);
     REQUIRE(fmt_q == 4 && fmt_k == 4 && (fmt_v == 4 || fmt_v == 6), "attn_in: q/k must be Q4_K, v Q4_K or Q6_K");
     REQUIRE(n_kv >= 1 && n_q >= n_kv && n_q % n_kv == 0, "attn_in: bad head counts");
-    REQUIRE(aligned(x, 16) && aligned(wq, 16) && aligned(wk, 16) && aligned(wv, 16), "attn_in: 16-byte alignment");
+    REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(wq, 16) && aligned(wk, 16) && aligned(wv, 16), "attn_in: 16-byte alignment");
     hipError_t e = vte::attn_in(x, norm_w, eps, wq, q_bias, fmt_q, wk, k_bias, fmt_k, wv, v_bias, fmt_v, q_out,
                                 k_cache, v_cache, kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q,
                                 n_kv, (hipStream_t)stream);
@@ -257,7 +255,7 @@ int vte_ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate,
     REQUIRE(fmt == 4, "ffn_in: gate/up must be Q4_K");
     REQUIRE(batch >= 1 && batch <= 4, "ffn_in: batch %d outside 1..4", batch);
     REQUIRE(hidden % 256 == 0 && hidden <= 8192 && ffn >= 1, "ffn_in: bad shape");
-    REQUIRE(aligned(x, 16) && aligned(w_gate, 16) && aligned(w_up, 16), "ffn_in: 16-byte alignment");
+    REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(w_gate, 16) && aligned(w_up, 16), "ffn_in: 16-byte alignment");
     hipError_t e = vte::ffn_in(x, norm_w, eps, w_gate, w_up, fmt, out, batch, hidden, ffn, (hipStream_t)stream);
     if (e == hipErrorNotSupported) return fail("ffn_in: shape does not fit the fused kernel's LDS plan");
     return hip_status(e, "vte_ffn_in launch");
@@ -271,7 +269,7 @@ int vte_norm_gemv(const void* x, const void* norm_w, float eps, const void* w, i
     REQUIRE(out_dtype == VTE_F32 || out_dtype == VTE_F16, "norm_gemv: bad out dtype");
     REQUIRE(batch >= 1 && batch <= 4, "norm_gemv: batch %d outside 1..4", batch);
     REQUIRE(K % 256 == 0 && K <= 8192 && N >= 1, "norm_gemv: bad shape");
-    REQUIRE(aligned(x, 16) && aligned(w, 16), "norm_gemv: 16-byte alignment");
+    REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(w, 16), "norm_gemv: 16-byte alignment");
     hipError_t e = vte::norm_mv(x, norm_w, eps, w, fmt, out, out_dtype == VTE_F32, bias, residual, residual_scale,
                                 batch, K, N, (hipStream_t)stream);
     if (e == hipErrorNotSupported) return fail("norm_gemv: shape does not fit the fused kernel's LDS plan");

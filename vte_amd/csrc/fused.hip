@@ -115,7 +115,8 @@ __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __
     const int n_sb = K / QK_K;
     const int per_row = n_sb * 4;
     const int ldx = xpad_len(K);
-    // LDS plan: x [NC][ldx] fp16 | s16 [NC][K/16] | part [NC][FMV_MAX_R*per_row] | rsum [NC][FMV_MAX_R] | stage
+    // LDS plan: x [NC][ldx] fp16 | s16 [NC][K/16] | part [NC][FMV_MAX_R*per_row] | rsum [NC][FMV_MAX_R] |
+    //           norm weights [ldx] fp16 (with a norm) | stage
     _Float16* xs = reinterpret_cast<_Float16*>(lds);
     size_t o = ((size_t)NC * ldx * 2 + 15) & ~(size_t)15;
     float* s16 = reinterpret_cast<float*>(lds + o);
@@ -127,8 +128,11 @@ __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __
     float* rsum = reinterpret_cast<float*>(lds + o);
     o += (size_t)NC * FMV_MAX_R * 4;
     o = (o + 15) & ~(size_t)15;
+    _Float16* wn_s = reinterpret_cast<_Float16*>(lds + o);
+    if (P.norm_w != nullptr) o += ((size_t)ldx * 2 + 15) & ~(size_t)15;
     uint8_t* stage = lds + o;
     __shared__ float red[4][NC];
+    __shared__ int pos_s[NC];  // kv_offset[m], read once per block
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     int total = 0;
@@ -184,9 +188,10 @@ __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __
     };
 
     int g = blockIdx.x;
+    if (tid < M && P.kv_offset != nullptr) pos_s[tid] = P.kv_offset[tid];
     load_tile(g, cur);
     // ---- activations: fp16 [M][K] -> LDS, optional RMSNorm ----
-    stage_act<NC>(x, false, M, K, xs);
+    stage_act<NC>(x, false, M, K, xs, P.norm_w, wn_s);
     store_stage(g);
     __syncthreads();
     if (P.norm_w != nullptr) {
@@ -211,7 +216,7 @@ __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __
         for (int m = 0; m < NC; ++m)
             inv[m] = rsqrtf((red[0][m] + red[1][m] + red[2][m] + red[3][m]) / (float)K + P.eps);
         for (int e = tid; e < K; e += ROWS_THREADS) {
-            const float wn = __half2float(P.norm_w[e]);
+            const float wn = (float)wn_s[xpad(e)];
 #pragma unroll
             for (int m = 0; m < NC; ++m) {
                 _Float16& xv = xs[m * ldx + xpad(e)];
@@ -281,7 +286,7 @@ __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __
                 float v = rsum[m * FMV_MAX_R + r];
                 if (S.bias) v += __half2float(S.bias[row]);
                 if (S.mode == FMV_VCACHE) {
-                    const int pos = P.kv_offset[m];
+                    const int pos = pos_s[m];
                     P.v_cache[(size_t)m * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128 + (row % 128)] =
                         __float2half(v);
                     continue;
@@ -310,7 +315,7 @@ __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __
                 }
                 if (S.bias) { a += __half2float(S.bias[row1]); bv += __half2float(S.bias[row2]); }
                 const float x1 = __half2float(__float2half(a)), x2 = __half2float(__float2half(bv));
-                const int pos = P.kv_offset[m];
+                const int pos = pos_s[m];
                 const int d = row1 % 128;
                 const float c = __half2float(P.rope_cos[(size_t)pos * 128 + d]);
                 const float sn = __half2float(P.rope_sin[(size_t)pos * 128 + d]);
@@ -344,7 +349,7 @@ static int fmv_num_cus() {
     return n;
 }
 
-size_t fmv_lds_bytes(int NC, int K, bool has_q6) {
+size_t fmv_lds_bytes(int NC, int K, bool has_q6, bool has_norm) {
     const int per_row = (K / 256) * 4;
     size_t o = ((size_t)NC * xpad_len(K) * 2 + 15) & ~(size_t)15;
     o += (size_t)NC * (K / 16) * 4;
@@ -352,6 +357,7 @@ size_t fmv_lds_bytes(int NC, int K, bool has_q6) {
     o += (size_t)NC * FMV_MAX_R * per_row * 4;
     o += (size_t)NC * FMV_MAX_R * 4;
     o = (o + 15) & ~(size_t)15;
+    if (has_norm) o += ((size_t)xpad_len(K) * 2 + 15) & ~(size_t)15;
     if (has_q6) o += (size_t)ROWS_THREADS * FMV_Q6_CHUNKS * 16;
     return o;
 }
@@ -390,7 +396,8 @@ hipError_t fused_mv(const __half* x, FmvPlan plan, hipStream_t st) {
         total += S.tiles;
     }
     const int NC = plan.M <= 1 ? 1 : (plan.M <= 2 ? 2 : 4);
-    const size_t lds = fmv_lds_bytes(NC, plan.K, has_q6);
+    const size_t lds = fmv_lds_bytes(NC, plan.K, has_q6, plan.norm_w != nullptr);
+    if (plan.norm_w != nullptr && (reinterpret_cast<uintptr_t>(plan.norm_w) & 15)) return hipErrorInvalidValue;
     if (lds > 65536 || plan.M > 4) return hipErrorNotSupported;
     if ((reinterpret_cast<uintptr_t>(x) & 15) || (plan.K & 7)) return hipErrorInvalidValue;  // 16-byte staging
     int blocks = 0;

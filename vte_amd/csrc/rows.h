@@ -54,28 +54,36 @@ struct ActLDS {
 };
 
 // Stage NC activation columns ([M][K], fp32 or fp16; columns >= M are zero)
-// into the padded fp16 LDS layout.  Each thread issues up to 8 independent
-// 16-byte loads before it stores any, so the staging costs one memory latency
-// rather than one per element.  Chunks of 8 elements stay contiguous in the
-// padded layout (pads fall every 64 elements).
+// into the padded fp16 LDS layout, plus optionally one more fp16 vector of K
+// elements (`extra`, e.g. RMSNorm weights) into `extra_dst` with the same
+// layout.  Each thread issues up to 8 independent 16-byte loads before it
+// stores any, so the staging costs one memory latency rather than one per
+// element.  Chunks of 8 elements stay contiguous in the padded layout (pads
+// fall every 64 elements).
 template <int NC>
-__device__ __forceinline__ void stage_act(const void* __restrict__ x, bool x_f32, int M, int K, _Float16* xs) {
+__device__ __forceinline__ void stage_act(const void* __restrict__ x, bool x_f32, int M, int K, _Float16* xs,
+                                          const __half* __restrict__ extra = nullptr, _Float16* extra_dst = nullptr) {
     const int ldx = xpad_len(K);
     const int per_col = K / 8;
-    const int nch = NC * per_col;
+    const int ncol = NC + (extra != nullptr ? 1 : 0);
+    const int nch = ncol * per_col;
     for (int c0 = 0; c0 < nch; c0 += 8 * ROWS_THREADS) {
         uint4 v[8][2];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int c = c0 + j * ROWS_THREADS + threadIdx.x;
             const int m = c / per_col;
-            if (c < nch && m < M) {
-                if (x_f32) {
-                    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(x) + (size_t)c * 8);
-                    v[j][0] = p[0];
-                    v[j][1] = p[1];
-                } else {
-                    v[j][0] = reinterpret_cast<const uint4*>(x)[c];
+            if (c < nch) {
+                if (m == NC) {
+                    v[j][0] = reinterpret_cast<const uint4*>(extra)[c - NC * per_col];
+                } else if (m < M) {
+                    if (x_f32) {
+                        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(x) + (size_t)c * 8);
+                        v[j][0] = p[0];
+                        v[j][1] = p[1];
+                    } else {
+                        v[j][0] = reinterpret_cast<const uint4*>(x)[c];
+                    }
                 }
             }
         }
@@ -84,6 +92,10 @@ __device__ __forceinline__ void stage_act(const void* __restrict__ x, bool x_f32
             const int c = c0 + j * ROWS_THREADS + threadIdx.x;
             if (c >= nch) break;
             const int m = c / per_col, e = (c - m * per_col) * 8;
+            if (m == NC) {
+                *reinterpret_cast<uint4*>(extra_dst + xpad(e)) = v[j][0];
+                continue;
+            }
             uint4 o = make_uint4(0, 0, 0, 0);
             if (m < M) {
                 if (x_f32) {
