@@ -40,6 +40,18 @@ def test_dequant_known_answer_block(hip, K):
     assert down(out)[0] == 18.5
 
 
+@pytest.mark.parametrize("fmt,per", [("q4_k", 256), ("q6_k", 256), ("q8_0", 32)])
+def test_dequant_matches_reference_golden_vectors(hip, K, fmt, per):
+    """Bit-exact against outputs of the reference's NumPy dequantiser, including
+    edge blocks (saturated scales, negative and subnormal super-scales)."""
+    from pathlib import Path
+    g = np.load(Path(__file__).resolve().parent / "golden" / "dequant.npz", allow_pickle=False)
+    raw, want = g[f"{fmt}_raw"], g[f"{fmt}_out"]
+    out = empty(hip, want.size, np.float32)
+    K.dequantize(fmt, up(hip, raw.reshape(-1)), out, want.size, stream=hip.stream)
+    assert np.array_equal(down(out).view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("fmt,n,k,seed", [
     ("q4_k", 8960, 1536, 42),    # config 0
     ("q6_k", 1536, 8960, 42),    # config 1, FFN down

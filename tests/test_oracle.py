@@ -178,3 +178,76 @@ def test_attention_oracle_invariants():
     for chunk in (32, 64, 300):
         sp = split_kv_ref(q, k, v, ctx, 1 / np.sqrt(d), chunk)
         assert np.linalg.norm(sp - full) / np.linalg.norm(full) < 1e-5
+
+
+# ---------------------------------------------------------------- step ops
+from oracle import step as ost  # noqa: E402
+
+
+def test_rmsnorm_unit_rms_and_scale_invariance():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((3, 1536)).astype(np.float16)
+    one = np.ones(1536, np.float16)
+    y = ost.rmsnorm(x, one, 1e-6).astype(np.float64)
+    assert np.allclose(np.sqrt((y ** 2).mean(-1)), 1.0, atol=2e-3)
+    # a power-of-two scale of x leaves the normalised vector unchanged (up to eps)
+    y4 = ost.rmsnorm((x.astype(np.float32) * 4).astype(np.float16), one, 1e-6)
+    assert np.array_equal(y4, ost.rmsnorm(x, one, 1e-6)) or np.abs(y4.astype(np.float64) - y).max() < 1e-3
+    # the weight multiplies elementwise: w = 2 doubles the output exactly
+    assert np.array_equal(ost.rmsnorm(x, (one * 2).astype(np.float16), 1e-6).astype(np.float32),
+                          2 * ost.rmsnorm(x, one, 1e-6).astype(np.float32))
+
+
+def test_swiglu_closed_forms():
+    g = np.array([0.0, 1.0, -1.0, 30.0, -30.0], np.float16)
+    u = np.array([5.0, 2.0, 2.0, 0.5, 3.0], np.float16)
+    want = np.array([0.0, 2 * 0.7310585786, -2 * 0.2689414214, 15.0, 0.0])
+    assert np.allclose(ost.swiglu(g, u).astype(np.float64), want, atol=2e-3)
+
+
+def test_rope_neox_is_a_rotation_by_pos_times_freq():
+    rng = np.random.default_rng(2)
+    hd, theta = 128, 1.0e6
+    cos_c, sin_c = ost.rope_cache(4096, hd, theta)
+    x = rng.standard_normal((3, hd)).astype(np.float16)
+    assert np.array_equal(ost.rope_neox(x, 0, cos_c, sin_c), x)          # position 0: identity
+    for pos in (1, 17, 3000):
+        y = ost.rope_neox(x, pos, cos_c, sin_c).astype(np.float64)
+        i = np.arange(hd // 2)
+        ang = pos * theta ** (-i / (hd // 2))                               # float64 textbook angles
+        a, b = x[:, :64].astype(np.float64), x[:, 64:].astype(np.float64)
+        ya = a * np.cos(ang) - b * np.sin(ang)
+        yb = a * np.sin(ang) + b * np.cos(ang)
+        assert np.abs(y - np.concatenate([ya, yb], 1)).max() < 6e-3, pos   # fp16 tables and output
+        # each (i, i+64) pair keeps its length
+        assert np.allclose(np.hypot(y[:, :64], y[:, 64:]), np.hypot(a, b), rtol=4e-3, atol=2e-3)
+
+
+def test_decode_step_residual_path_and_tied_lm_head():
+    """With every projection of every layer zero, the step reduces to
+    logits = dequant(token_embd) @ rmsnorm(embedding(token), output_norm) and
+    appends zero K/V at the step's position: pins the residual wiring, the
+    final norm and the tied LM head of the composed step."""
+    from vte_amd.core.model_config import TINY
+    from vte_amd.core.weights import SyntheticQwen2
+    m = SyntheticQwen2(TINY, seed=5)
+    for lw in m.layers:
+        for name in ("q", "k", "v", "o", "gate", "up", "down"):
+            lw[name] = np.zeros_like(lw[name])        # d = dmin = 0 -> all-zero weights
+        for b in ("q_bias", "k_bias", "v_bias"):
+            if lw.get(b) is not None:
+                lw[b] = np.zeros_like(lw[b])
+    cfg = m.cfg
+    B, max_seq = 2, 16
+    ks = [np.full((B, max_seq, cfg.n_kv, cfg.head_dim), 7, np.float16) for _ in range(cfg.n_layers)]
+    vs = [k.copy() for k in ks]
+    toks, pos = np.array([3, 4000]), np.array([0, 9])
+    logits = ost.decode_step(m, toks, pos, ks, vs)
+    W = dq.dequantize_matrix("q6_k", m.token_embd, cfg.vocab, cfg.hidden)
+    for b in range(B):
+        h = ost.embedding_q6k(m.token_embd, int(toks[b]), cfg.hidden)
+        want = W @ ost.rmsnorm(h, m.output_norm, cfg.eps).astype(np.float32)
+        assert np.allclose(logits[b], want, rtol=1e-5, atol=1e-5)
+        for L in range(cfg.n_layers):
+            assert not ks[L][b, pos[b]].any() and not vs[L][b, pos[b]].any()
+            assert (ks[L][b, pos[b] + 1] == 7).all()

@@ -22,7 +22,8 @@ LIB = HERE / "libvte_amd.so"
 HSACO = HERE / f"vte_kernels_{ARCH}.hsaco"
 SOURCES = ["gemv.hip", "qmv.hip", "fused.hip", "gemm_mfma.hip", "attention.hip", "glue.hip", "capi.hip"]
 MODULE_SOURCE = "module.hip"
-# Packed FP32 instructions are disabled for every HIP compile (see DESIGN notes).
+# Packed FP32 instructions are disabled for every HIP compile: some of their
+# forms have given silently wrong results on the target machines.
 COMMON = ["-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
           "-packed-fp32-ops", "-Wno-unused-result"]
 

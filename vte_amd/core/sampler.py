@@ -47,7 +47,8 @@ class Sampler:
         logits = logits_or_vals
         if temperature != 1.0:
             logits = logits / temperature
-        if 0 < top_k < len(logits):
+        if top_k > 0:  # argpartition even when top_k == len: its order decides the draw
+            top_k = min(top_k, len(logits))
             top = np.argpartition(logits, -top_k)[-top_k:]
         else:
             top = np.arange(len(logits))
