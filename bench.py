@@ -44,6 +44,64 @@ def time_graph(hip, ex, steps, warmup):
     return ms / steps, wall
 
 
+def time_classes(hip, ex, classes, reps=20):
+    """Average time of the launches of ``classes`` in one step, measured with
+    HIP events on the executor's stream around replays of a graph holding only
+    those launches (same buffers and shapes as the full step)."""
+    g, ge = ex.capture_classes(classes)
+    try:
+        hip.graph_launch(ge)
+        hip.synchronize()
+        e0, e1 = _events(hip)
+        hip.event_record(e0)
+        for _ in range(reps):
+            hip.graph_launch(ge)
+        hip.event_record(e1)
+        ms = hip.event_elapsed_ms(e0, e1) / reps
+    finally:
+        hip.graph_exec_destroy(ge)
+        hip.graph_destroy(g)
+    return ms
+
+
+def step_breakdown(hip, ex, prefix, reps=20):
+    """Per launch class: launches per step, time per step (us) and GB/s."""
+    cfg = ex.cfg
+    algo = ex.class_algorithmic_bytes()
+    algo["attn"] += cfg.n_layers * ex.B * (prefix + 1) * cfg.n_kv * cfg.head_dim * 2 * 2
+    n = {"embed": 1, "attn_in": cfg.n_layers, "attn": cfg.n_layers, "o_proj": cfg.n_layers, "ffn_in": cfg.n_layers,
+         "down": cfg.n_layers, "lm_head": 1, "topk": 1}
+    out = {}
+    for c in ex.FUSED_CLASSES:
+        ms = time_classes(hip, ex, [c], reps)
+        out[c] = {"launches": n[c], "us_per_step": round(ms * 1e3, 2), "algo_bytes": int(algo[c]),
+                  "GBps": round(algo[c] / (ms * 1e-3) / 1e9, 1)}
+    return out
+
+
+def fused_mv_roofline(hip, ex, reps=20):
+    """Roofline of the step's dominant kernel, fused_mv_kernel (the 28 norm+QKV,
+    28 norm+gate/up and 1 norm+LM-head launches of a batch-1 step): algorithmic
+    bytes per launch over its average launch duration (HIP events around
+    replays of a graph of exactly those launches)."""
+    classes = ["attn_in", "ffn_in", "lm_head"]
+    algo = ex.class_algorithmic_bytes()
+    launches = 2 * ex.cfg.n_layers + 1
+    per_launch_bytes = sum(algo[c] for c in classes) / launches
+    ms = time_classes(hip, ex, classes, reps) / launches
+    gbps = per_launch_bytes / (ms * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "fused_mv_decode_b1_traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+            "kernel": "fused_mv_kernel<1> (batch-1 step: 28 norm+QKV+RoPE+append, 28 norm+gate/up+SwiGLU, "
+                      "1 norm+LM head launch)",
+            "avg_launch_us": round(ms * 1e3, 3), "algo_bytes_per_launch": int(per_launch_bytes)}
+
+
 def time_e2e(hip, ex, steps, start_pos):
     """Per-token loop as a caller runs it: stage token/offset, replay, read top-k, sample."""
     from vte_amd.core.sampler import Sampler
@@ -178,6 +236,39 @@ def cpu_baseline(seconds_budget=20.0):
                       f"(dequant cached), {n} trials, per-layer time x28 + LM head"}
 
 
+def profile_step(B, steps, prefix=2048):
+    """Kernel-trace / counter workload: one plain device-to-device copy of
+    256 MiB (reads and writes exactly 256 MiB: the scale of FETCH_SIZE and
+    WRITE_SIZE), then ``steps`` replays of the batch-B decode-step graph."""
+    from vte_amd.bridge import DeviceArray, HIPRuntime
+    from vte_amd.core.hip_graph_executor import HIPGraphExecutor
+    from vte_amd.core.model_config import QWEN25_1P5B
+    from vte_amd.core.weights import SyntheticQwen2
+    hip = HIPRuntime()
+    if not hip.initialize():
+        raise SystemExit("HIP initialisation failed")
+    a = DeviceArray(hip, 256 << 20, np.uint8, "calib_src")
+    b = DeviceArray(hip, 256 << 20, np.uint8, "calib_dst")
+    a.zero()
+    hip.synchronize()
+    hip.memcpy_device_to_device(b.ptr, a.ptr, 256 << 20)
+    hip.synchronize()
+    a.free()
+    b.free()
+    ex = HIPGraphExecutor(hip, SyntheticQwen2(QWEN25_1P5B, seed=0), batch_size=B, max_seq=prefix + 256)
+    ex.fill_kv_prefix(seed=B)
+    ex._update_staging_buffers([1] * B, [prefix] * B)
+    ex.build_decode_graph()
+    for i in range(steps):
+        ex.replay(1)
+        if i % 10 == 0:
+            hip.synchronize()
+            print(f"profile-step: batch {B}, step {i}/{steps}", flush=True)
+    hip.synchronize()
+    ex.close()
+    hip.cleanup()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -185,10 +276,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="skip the batch-16 step and GEMV sweep")
+    ap.add_argument("--profile-step", type=int, default=0, metavar="B",
+                    help="profiling run only: a 256 MiB calibration copy, then --steps replays of the batch-B "
+                         "step graph (for rocprofv3 kernel traces and counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        print(json.dumps({"error": "this build runs on one GPU only (no multi-GPU path is built); "
+                                   "--gpus must be 1"}))
         sys.exit(2)
+    if args.profile_step:
+        profile_step(args.profile_step, args.steps)
+        return
 
     from vte_amd.bridge import HIPRuntime
     from vte_amd.core.hip_graph_executor import HIPGraphExecutor
@@ -207,12 +305,17 @@ def main():
     wbytes = model.weight_bytes()
     prefix = 2048
     result = {}
+    roof, breakdown = None, None
     for B in ([1] if args.quick else [1, 16]):
         ex = HIPGraphExecutor(hip, model, batch_size=B, max_seq=prefix + 256)
         ex.fill_kv_prefix(seed=B)
         ex._update_staging_buffers([1] * B, [prefix] * B)
         ms, wall = time_graph(hip, ex, args.steps, args.warmup)
         e2e = time_e2e(hip, ex, 20, prefix)
+        if B == 1:
+            ex._update_staging_buffers([1] * B, [prefix] * B)
+            roof = fused_mv_roofline(hip, ex)
+            breakdown = step_breakdown(hip, ex, prefix)
         kv_read = QWEN25_1P5B.n_layers * (prefix + 1) * QWEN25_1P5B.n_kv * QWEN25_1P5B.head_dim * 2 * 2 * B
         step_bytes = wbytes + kv_read
         result[B] = {"ms_per_step": ms, "tok_s": B / (ms * 1e-3), "wall_s": wall, "e2e_ms_per_step": e2e * 1e3,
@@ -233,7 +336,6 @@ def main():
         attn.append(attn_bench(hip, K, 2049, 128, fused=True))
         attn.append(attn_bench(hip, K, 2049, 128, fused=False))
         attn.append(attn_bench(hip, K, 2049, 512, B=16, fused=True))
-    dom = gemv[0] if gemv else None
     cpu = None if args.no_cpu else cpu_baseline()
     r1 = result[1]
     line = {
@@ -259,10 +361,8 @@ def main():
         line["gemv"] = gemv
     if attn:
         line["attention"] = attn
-    if dom:
-        line["roofline"] = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                            "frac": dom["frac_hbm_peak"], "traffic": None,
-                            "kernel": "gemv_q4k_rows (config 0: Q4_K 8960x1536, batch 1, cold pool)"}
+    line["roofline"] = roof
+    line["step_breakdown_b1"] = breakdown
     if cpu:
         line["cpu_baseline"] = cpu
     print(json.dumps(line))

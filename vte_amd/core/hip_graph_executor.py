@@ -115,32 +115,80 @@ class HIPGraphExecutor:
             self.K.gemv(fmt, x, w, y, self.B, K_in, N, bias=bias, residual=residual, in_dtype="f16",
                         out_dtype=out_dtype, stream=st)
 
-    def _enqueue_fused(self) -> None:
-        """Six launches per layer: norm+QKV+RoPE+append, attention (2), o-proj,
-        norm+gate/up+SwiGLU, down; then norm+LM head and top-k."""
+    # launch classes of the fused step (kernel symbol in brackets)
+    FUSED_CLASSES = ("embed", "attn_in", "attn", "o_proj", "ffn_in", "down", "lm_head", "topk")
+
+    def _enqueue_fused(self, only=None) -> None:
+        """Six launches per layer: norm+QKV+RoPE+append [fused_mv_kernel],
+        attention [attn_partial_gqa + attn_combine], o-proj [qmv_kernel],
+        norm+gate/up+SwiGLU [fused_mv_kernel], down [qmv_kernel]; then
+        norm+LM head [fused_mv_kernel] and top-k.  ``only``: a set of
+        FUSED_CLASSES to issue (timing of one class over the same buffers)."""
         cfg, K, st, B = self.cfg, self.K, self.hip.stream, self.B
         H = cfg.hidden
         offs = self.staging_kv_offset
+        on = (lambda c: True) if only is None else (lambda c: c in only)
         cur = 0
-        K.embedding_q6k(self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
+        if on("embed"):
+            K.embedding_q6k(self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
         for L, lw in enumerate(self.layers):
-            K.attn_in(self.h[cur], lw["attn_norm"], cfg.eps, lw["q"], lw["q_bias"], lw["q_fmt"], lw["k"], lw["k_bias"],
-                      lw["k_fmt"], lw["v"], lw["v_bias"], lw["v_fmt"], self.q, self.k_cache[L], self.v_cache[L], offs,
-                      self.kv_batch_stride, self.rope_cos, self.rope_sin, B, H, cfg.n_q, cfg.n_kv, cfg.head_dim,
-                      stream=st)
-            self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], self.att, offs, self.kv_batch_stride,
-                             dtype="f16", batch=B, stream=st)
-            self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
+            if on("attn_in"):
+                K.attn_in(self.h[cur], lw["attn_norm"], cfg.eps, lw["q"], lw["q_bias"], lw["q_fmt"], lw["k"],
+                          lw["k_bias"], lw["k_fmt"], lw["v"], lw["v_bias"], lw["v_fmt"], self.q, self.k_cache[L],
+                          self.v_cache[L], offs, self.kv_batch_stride, self.rope_cos, self.rope_sin, B, H, cfg.n_q,
+                          cfg.n_kv, cfg.head_dim, stream=st)
+            if on("attn"):
+                self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], self.att, offs, self.kv_batch_stride,
+                                 dtype="f16", batch=B, stream=st)
+            if on("o_proj"):
+                self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
             cur = 1 - cur
-            K.ffn_in(self.h[cur], lw["ffn_norm"], cfg.eps, lw["gate"], lw["up"], lw["gate_fmt"], self.a, B, H, cfg.ffn,
-                     stream=st)
-            self._linear(lw["down_fmt"], self.a, lw["down"], self.h[1 - cur], cfg.ffn, H, residual=self.h[cur])
+            if on("ffn_in"):
+                K.ffn_in(self.h[cur], lw["ffn_norm"], cfg.eps, lw["gate"], lw["up"], lw["gate_fmt"], self.a, B, H,
+                         cfg.ffn, stream=st)
+            if on("down"):
+                self._linear(lw["down_fmt"], self.a, lw["down"], self.h[1 - cur], cfg.ffn, H, residual=self.h[cur])
             cur = 1 - cur
         self.h_final = cur
-        K.norm_gemv(self.h[cur], self.output_norm, cfg.eps, self.token_embd, "q6_k", self.logits, B, H, cfg.vocab,
-                    out_dtype="f32", stream=st)
-        if self.top_k > 0:
+        if on("lm_head"):
+            K.norm_gemv(self.h[cur], self.output_norm, cfg.eps, self.token_embd, "q6_k", self.logits, B, H,
+                        cfg.vocab, out_dtype="f32", stream=st)
+        if self.top_k > 0 and on("topk"):
             K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st)
+
+    def class_algorithmic_bytes(self) -> dict:
+        """Algorithmic HBM bytes of one step per launch class of the fused path
+        (weights + activations read + results written; KV read by attention at
+        the current kv offsets is added by the caller)."""
+        cfg, B = self.cfg, self.B
+        H, F, qd, kvd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim
+        from vte_amd import synthetic as syn
+        wb = lambda fmt, n, k: syn.matrix_bytes(fmt, n, k)
+        out = dict.fromkeys(self.FUSED_CLASSES, 0)
+        out["embed"] = B * (wb("q6_k", 1, H) + 4 + 2 * H)
+        for lw in self.layers:
+            out["attn_in"] += (wb(lw["q_fmt"], qd, H) + wb(lw["k_fmt"], kvd, H) + wb(lw["v_fmt"], kvd, H)
+                               + 2 * (qd + 2 * kvd)                 # biases
+                               + 2 * H + B * 2 * H                  # norm weights, x
+                               + B * 2 * (qd + 2 * kvd)             # q out, k/v appended
+                               + B * 2 * 2 * cfg.head_dim)          # cos/sin rows
+            out["attn"] += B * 2 * qd + B * 2 * qd                  # q in, output (KV added by caller)
+            out["o_proj"] += wb(lw["o_fmt"], H, qd) + B * 2 * (qd + 2 * H)
+            out["ffn_in"] += wb(lw["gate_fmt"], F, H) + wb(lw["up_fmt"], F, H) + 2 * H + B * 2 * (H + F)
+            out["down"] += wb(lw["down_fmt"], H, F) + B * 2 * (F + 2 * H)
+        out["lm_head"] = wb("q6_k", cfg.vocab, H) + 2 * H + B * (2 * H + 4 * cfg.vocab)
+        out["topk"] = B * (4 * cfg.vocab + 8 * self.top_k)
+        return out
+
+    def capture_classes(self, only) -> tuple:
+        """(graph, graph_exec) of the fused step restricted to launch classes ``only``."""
+        self.hip.stream_synchronize()
+        self.hip.stream_begin_capture()
+        try:
+            self._enqueue_fused(only=set(only))
+        finally:
+            g = self.hip.stream_end_capture()
+        return g, self.hip.graph_instantiate(g)
 
     def enqueue_step(self) -> None:
         """Issue every kernel of one decode step on the runtime stream."""

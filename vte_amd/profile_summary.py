@@ -1,0 +1,90 @@
+"""Summarise rocprofv3 CSV output of ``bench.py --profile-step`` into the text
+kept under profiles/.
+
+    python -m vte_amd.profile_summary stats   <kernel_stats.csv>  <out.md> "<command>"
+    python -m vte_amd.profile_summary traffic <fetch counter_collection.csv> <write counter_collection.csv>
+                                              <kernel substring> <out.json> <out.md> "<commands>"
+
+``traffic``: FETCH_SIZE / WRITE_SIZE are averaged per dispatch of the named
+kernel and converted to bytes with the factor that makes the run's 256 MiB
+calibration copy (``__amd_rocclr_copyBuffer`` dispatch of that size) read and
+write exactly 256 MiB.
+"""
+from __future__ import annotations
+
+import csv
+import json
+import sys
+from collections import defaultdict
+
+CALIB_BYTES = 256 << 20
+
+
+def _rows(path):
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def stats(path, out_md, command):
+    rows = _rows(path)
+    lines = ["# Kernel trace summary", "", f"Command: `{command}`", "",
+             "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
+    for r in rows:
+        lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                     f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+def _per_kernel(path, counter):
+    vals = defaultdict(list)
+    for r in _rows(path):
+        if r["Counter_Name"] == counter:
+            vals[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return vals
+
+
+def _calibration(vals, expect_kib):
+    """Counter KiB of the calibration copy = the largest copyBuffer dispatch."""
+    cands = [v for k, vs in vals.items() if "copyBuffer" in k for v in vs]
+    if not cands:
+        raise SystemExit("no calibration copy dispatch found")
+    return expect_kib / max(cands)
+
+
+def traffic(fetch_csv, write_csv, kernel, out_json, out_md, commands):
+    fv, wv = _per_kernel(fetch_csv, "FETCH_SIZE"), _per_kernel(write_csv, "WRITE_SIZE")
+    kib = CALIB_BYTES / 1024
+    f_scale, w_scale = _calibration(fv, kib), _calibration(wv, kib)
+    res = {"kernel": kernel, "fetch_scale": f_scale, "write_scale": w_scale, "per_kernel": {}}
+    lines = ["# HBM traffic per dispatch (rocprofv3 counters)", "", "Commands:", ""]
+    lines += [f"    {c}" for c in commands.split(" && ")]
+    lines += ["", f"Calibration: a 256 MiB device-to-device copy reads/writes 262144 KiB; its FETCH_SIZE "
+              f"reads {kib / f_scale:.1f} and WRITE_SIZE {kib / w_scale:.1f}, so counter values are scaled by "
+              f"{f_scale:.4f} (fetch) and {w_scale:.4f} (write).", "",
+              "| kernel | dispatches | fetch MB/dispatch | write MB/dispatch |", "|---|---|---|---|"]
+    for name in sorted(set(fv) | set(wv)):
+        f = sum(fv[name]) / max(len(fv[name]), 1) * f_scale * 1024
+        w = sum(wv[name]) / max(len(wv[name]), 1) * w_scale * 1024
+        res["per_kernel"][name] = {"dispatches": len(fv[name]), "fetch_bytes": f, "write_bytes": w}
+        lines.append(f"| `{name[:100]}` | {len(fv[name])} | {f / 1e6:.3f} | {w / 1e6:.3f} |")
+    sel = [k for k in res["per_kernel"] if kernel in k]
+    if not sel:
+        raise SystemExit(f"kernel {kernel!r} not in the counter output")
+    k = sel[0]
+    res["hbm_bytes_per_launch"] = int(res["per_kernel"][k]["fetch_bytes"] + res["per_kernel"][k]["write_bytes"])
+    lines += ["", f"`{k}`: {res['hbm_bytes_per_launch'] / 1e6:.3f} MB of HBM traffic per launch (fetch + write)."]
+    with open(out_json, "w") as f:
+        json.dump({"kernel": k, "hbm_bytes_per_launch": res["hbm_bytes_per_launch"],
+                   "fetch_scale": f_scale, "write_scale": w_scale}, f, indent=1)
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+if __name__ == "__main__":
+    if sys.argv[1] == "stats":
+        stats(sys.argv[2], sys.argv[3], sys.argv[4])
+    elif sys.argv[1] == "traffic":
+        traffic(*sys.argv[2:8])
+    else:
+        raise SystemExit(__doc__)
