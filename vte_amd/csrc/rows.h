@@ -180,11 +180,14 @@ __device__ __forceinline__ float q4k_unit_dot(const Q4KUnitData& u, int mblk, co
 // Q6_K (from an LDS copy of the rows; blocks are 2-byte aligned)
 // ---------------------------------------------------------------------------
 // Four little-endian dwords starting at a 2-byte aligned LDS address: five
-// aligned dword reads (volatile, so they are not fused into unaligned wide
-// LDS reads, which stall) and byte alignment in registers.
+// 4-byte aligned LDS reads (the pointer is cast to the LDS address space, so
+// they are ds_read instructions, which the compiler may pair into
+// ds_read2_b32 -- each still naturally aligned, as misaligned wide LDS reads
+// stall) and byte alignment in registers (the shift is 0 or 2).
+typedef __attribute__((address_space(3))) const uint32_t lds_u32_t;
 __device__ __forceinline__ void lds_16b_a2(const uint8_t* p, uint32_t (&o)[4]) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const volatile uint32_t* q = reinterpret_cast<const volatile uint32_t*>(a & ~(uintptr_t)3);
+    lds_u32_t* q = (lds_u32_t*)(reinterpret_cast<const uint8_t*>(a & ~(uintptr_t)3));
     const uint32_t sh = (uint32_t)(a & 3);
     uint32_t d[5];
 #pragma unroll
