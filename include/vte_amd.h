@@ -130,8 +130,9 @@ int vte_embedding_q6k(const int* tokens, const void* table, void* out, int n_tok
 /* Bytes of device scratch vte_topk needs for `rows` rows. */
 long long vte_topk_scratch_bytes(int rows);
 
-/* Per row of fp32 logits [rows][vocab]: the k (1..64) largest values in
- * descending order, ties broken by the lower index, with their indices.
+/* Per row of fp32 logits [rows][vocab] (vocab <= 262144): the k (1..64)
+ * largest values in descending order, ties broken by the lower index, with
+ * their indices.
  * Replaces: the argpartition top-k of Sampler.sample (vte/core/sampler.py:54-129)
  *           and topk_reduce_greedy_kernel (topk_reduce_greedy.hip.template:52-83). */
 int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,

@@ -225,6 +225,7 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
     REQUIRE(logits && out_val && out_idx && scratch, "topk: null pointer");
     REQUIRE(rows >= 1 && k >= 1 && k <= 64 && vocab >= k, "topk: need 1 <= k <= min(64, vocab)");
     REQUIRE(rows <= 65535, "topk: rows %d out of range", rows);
+    REQUIRE(vocab <= 262144, "topk: vocab %d above 262144", vocab);
     return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream),
                       "vte_topk launch");
 }

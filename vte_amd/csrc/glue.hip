@@ -158,85 +158,242 @@ extern "C" __global__ __launch_bounds__(256) void embedding_lookup_q6k_kernel(
 // ---------------------------------------------------------------------------
 // Top-k over fp32 logits, k <= 64, exact, ordered by (value desc, index asc):
 // the order np.lexsort((index, -value)) gives.  Two launches:
-//  1. grid (TOPK_P, rows), 4 waves per block: each wave keeps the top 64 of its
-//     slice as a bitonic-sorted 64-lane list, merging in one 64-element group
-//     at a time (sort the group, take max(list[l], group[63 - l]) which is
-//     bitonic and holds the top 64 of the union, then a bitonic merge);
-//  2. one block per row merges the TOPK_P * 4 lists the same way and writes
-//     the first k entries.
-// Padding entries are (-inf, INT_MAX) so they rank after every real logit.
+//  1. grid (TOPK_P, rows): each block selects the 64 best entries of its
+//     slice (at most TOPK_SLICE logits) by radix selection of the 64th
+//     largest key in LDS (three rounds of 11/11/10-bit digit histograms),
+//     then keeps every key above it plus the lowest-indexed ties, and writes
+//     them in index order with their count;
+//  2. one block per row selects the best 64 of the <= TOPK_P * 64 candidates
+//     the same way and sorts them with a 64-lane bitonic network.
+// Keys map fp32 to an order-preserving uint32 (-0.0 taken as +0.0, as the
+// reference's comparison does).
 // ---------------------------------------------------------------------------
 #define TOPK_P 64
-#define TOPK_WAVES 4
+#define TOPK_SLICE 4096
+#define TOPK_THREADS 256
+#define TOPK_BINS 2048
 
-__device__ __forceinline__ bool tk_better(float a, int ia, float b, int ib) {
+__device__ __forceinline__ uint32_t tk_key(float v) {
+    uint32_t u = __float_as_uint(v);
+    if (u == 0x80000000u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float tk_val(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Block-wide exclusive scan of one int per thread (TOPK_THREADS threads).
+__device__ __forceinline__ int tk_excl_scan(int v, int* wsum, int& total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[wv] = x;
+    __syncthreads();
+    int base = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < TOPK_THREADS / 64; ++w) {
+        base += (w < wv) ? wsum[w] : 0;
+        total += wsum[w];
+    }
+    __syncthreads();
+    return base + x - v;
+}
+
+struct TkShared {
+    int hist[TOPK_BINS];
+    int wsum[TOPK_THREADS / 64];
+    int sel_digit, sel_need;
+};
+
+// Key of rank `need` (1 = largest) among keys[0..n): returns it and the number
+// of entries equal to it that belong to the top `need` (in index order).
+__device__ uint32_t tk_radix_select(const uint32_t* keys, int n, int need, TkShared& sh, int& need_eq) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    uint32_t prefix = 0, mask = 0;
+    const int shifts[3] = {21, 10, 0};
+    const int widths[3] = {11, 11, 10};
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+        const int shift = shifts[r], nb = 1 << widths[r];
+        for (int i = tid; i < nb; i += TOPK_THREADS) sh.hist[i] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += TOPK_THREADS) {
+            const uint32_t k = keys[i];
+            if ((k & mask) == prefix) atomicAdd(&sh.hist[(k >> shift) & (nb - 1)], 1);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            // lane l owns nb/64 consecutive bins, lanes ordered from the top digit down
+            const int per = nb >> 6;
+            const int top = nb - 1 - lane * per;
+            int s = 0;
+            for (int j = 0; j < per; ++j) s += sh.hist[top - j];
+            int incl = s;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += y;
+            }
+            const int excl = incl - s;
+            if (excl < need && need <= incl) {  // exactly one lane
+                int c = excl;
+                for (int j = 0; j < per; ++j) {
+                    const int h = sh.hist[top - j];
+                    if (need <= c + h) {
+                        sh.sel_digit = top - j;
+                        sh.sel_need = need - c;
+                        break;
+                    }
+                    c += h;
+                }
+            }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)sh.sel_digit << shift;
+        mask |= (uint32_t)(nb - 1) << shift;
+        need = sh.sel_need;
+        __syncthreads();
+    }
+    need_eq = need;
+    return prefix;
+}
+
+// Keep keys[i] > T plus the first need_eq entries equal to T (positions in
+// ascending order); returns the number kept (= min(64, n) by construction)
+// and writes the kept positions, in order, to out_pos.
+__device__ int tk_compact(const uint32_t* keys, int n, uint32_t T, int need_eq, int* out_pos, TkShared& sh) {
+    const int tid = threadIdx.x;
+    const int per = (n + TOPK_THREADS - 1) / TOPK_THREADS;
+    const int lo = min(n, tid * per), hi = min(n, lo + per);
+    int eq = 0;
+    for (int i = lo; i < hi; ++i) eq += keys[i] == T;
+    int tot;
+    const int eq_before = tk_excl_scan(eq, sh.wsum, tot);
+    int keep = 0, e = eq_before;
+    for (int i = lo; i < hi; ++i) {
+        const uint32_t k = keys[i];
+        if (k > T) ++keep;
+        else if (k == T) { keep += e < need_eq; ++e; }
+    }
+    const int base = tk_excl_scan(keep, sh.wsum, tot);
+    int o = base;
+    e = eq_before;
+    for (int i = lo; i < hi; ++i) {
+        const uint32_t k = keys[i];
+        bool take = k > T;
+        if (k == T) { take = e < need_eq; ++e; }
+        if (take) out_pos[o++] = i;
+    }
+    __syncthreads();
+    return tot;
+}
+
+__global__ __launch_bounds__(TOPK_THREADS) void topk_partial_kernel(const float* __restrict__ logits, int vocab,
+                                                                      int slice, uint32_t* __restrict__ cand_key,
+                                                                      int* __restrict__ cand_idx,
+                                                                      int* __restrict__ cand_cnt) {
+    __shared__ uint32_t keys[TOPK_SLICE];
+    __shared__ int pos[64];
+    __shared__ TkShared sh;
+    const int row = blockIdx.y, p = blockIdx.x, tid = threadIdx.x;
+    const int lo = p * slice, n = max(0, min(slice, vocab - lo));
+    const float* r = logits + (size_t)row * vocab + lo;
+    for (int i0 = 0; i0 < n; i0 += 4 * TOPK_THREADS) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = i0 + j * TOPK_THREADS + tid;
+            v[j] = r[i < n ? i : 0];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = i0 + j * TOPK_THREADS + tid;
+            if (i < n) keys[i] = tk_key(v[j]);
+        }
+    }
+    __syncthreads();
+    const size_t o = ((size_t)row * gridDim.x + p) * 64;
+    if (n <= 64) {
+        if (tid < n) { cand_key[o + tid] = keys[tid]; cand_idx[o + tid] = lo + tid; }
+        if (tid == 0) cand_cnt[(size_t)row * gridDim.x + p] = n;
+        return;
+    }
+    int need_eq;
+    const uint32_t T = tk_radix_select(keys, n, 64, sh, need_eq);
+    const int kept = tk_compact(keys, n, T, need_eq, pos, sh);
+    if (tid < kept) { cand_key[o + tid] = keys[pos[tid]]; cand_idx[o + tid] = lo + pos[tid]; }
+    if (tid == 0) cand_cnt[(size_t)row * gridDim.x + p] = kept;
+}
+
+// Bitonic network over 64 lanes on (key desc, index asc).
+__device__ __forceinline__ bool tk_before(uint32_t a, int ia, uint32_t b, int ib) {
     return a > b || (a == b && ia < ib);
 }
-
-// One compare-exchange stage of a bitonic network across the wave.
-__device__ __forceinline__ void tk_stage(float& v, int& ix, int lane, int stride, bool desc) {
-    const float ov = __shfl_xor(v, stride, 64);
-    const int oi = __shfl_xor(ix, stride, 64);
-    const bool lower = (lane & stride) == 0;
-    const bool ob = tk_better(ov, oi, v, ix);
-    if ((lower == desc) ? ob : (!ob && !(ov == v && oi == ix))) { v = ov; ix = oi; }
-}
-
-__device__ __forceinline__ void tk_sort64(float& v, int& ix, int lane) {
+__device__ __forceinline__ void tk_sort64(uint32_t& k, int& ix, int lane) {
     for (int size = 2; size <= 64; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) tk_stage(v, ix, lane, stride, (lane & size) == 0);
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint32_t ok = __shfl_xor(k, stride, 64);
+            const int oi = __shfl_xor(ix, stride, 64);
+            const bool lower = (lane & stride) == 0;
+            const bool desc = (lane & size) == 0;
+            const bool other_first = tk_before(ok, oi, k, ix);
+            if ((lower == desc) == other_first) { k = ok; ix = oi; }
+        }
 }
 
-// (v, ix): sorted top list; (gv, gi): another sorted list -> top 64 of the union, sorted.
-__device__ __forceinline__ void tk_merge64(float& v, int& ix, float gv, int gi, int lane) {
-    const float rv = __shfl(gv, 63 - lane, 64);
-    const int ri = __shfl(gi, 63 - lane, 64);
-    if (tk_better(rv, ri, v, ix)) { v = rv; ix = ri; }
-    for (int stride = 32; stride > 0; stride >>= 1) tk_stage(v, ix, lane, stride, true);
-}
-
-__global__ __launch_bounds__(64 * TOPK_WAVES) void topk_partial_kernel(const float* __restrict__ logits, int vocab,
-                                                                         float* __restrict__ sv, int* __restrict__ si) {
-    const int row = blockIdx.y, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int gw = blockIdx.x * TOPK_WAVES + wv, nw = TOPK_P * TOPK_WAVES;
-    const int per = ((vocab + nw - 1) / nw + 63) & ~63;
-    const int lo = gw * per, hi = min(lo + per, vocab);
-    const float* r = logits + (size_t)row * vocab;
-    float v = -INFINITY;
-    int ix = 0x7fffffff;
-    for (int base = lo; base < hi; base += 64) {
-        const int i = base + lane;
-        float gv = (i < hi) ? r[i] : -INFINITY;
-        int gi = (i < hi) ? i : 0x7fffffff;
-        tk_sort64(gv, gi, lane);
-        if (base == lo) { v = gv; ix = gi; }
-        else tk_merge64(v, ix, gv, gi, lane);
+__global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint32_t* __restrict__ cand_key,
+                                                                    const int* __restrict__ cand_idx,
+                                                                    const int* __restrict__ cand_cnt, int P, int k,
+                                                                    float* __restrict__ out_val,
+                                                                    int* __restrict__ out_idx) {
+    __shared__ uint32_t keys[TOPK_P * 64];
+    __shared__ int idx[TOPK_P * 64];
+    __shared__ int offs[TOPK_P + 1];
+    __shared__ int pos[64];
+    __shared__ TkShared sh;
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64) {
+        const int c = tid < P ? cand_cnt[(size_t)row * P + tid] : 0;
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        offs[tid] = incl - c;
+        if (tid == 63) offs[TOPK_P] = incl;
     }
-    const size_t o = ((size_t)row * nw + gw) * 64 + lane;
-    sv[o] = v;
-    si[o] = ix;
-}
-
-__global__ __launch_bounds__(64 * TOPK_WAVES) void topk_final_kernel(const float* __restrict__ sv,
-                                                                       const int* __restrict__ si, int k,
-                                                                       float* __restrict__ out_val,
-                                                                       int* __restrict__ out_idx) {
-    __shared__ float lv[TOPK_WAVES][64];
-    __shared__ int li[TOPK_WAVES][64];
-    const int row = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int nl = TOPK_P * TOPK_WAVES;
-    const size_t base = (size_t)row * nl * 64;
-    float v = sv[base + (size_t)wv * 64 + lane];
-    int ix = si[base + (size_t)wv * 64 + lane];
-    for (int l = wv + TOPK_WAVES; l < nl; l += TOPK_WAVES)
-        tk_merge64(v, ix, sv[base + (size_t)l * 64 + lane], si[base + (size_t)l * 64 + lane], lane);
-    lv[wv][lane] = v;
-    li[wv][lane] = ix;
     __syncthreads();
-    if (wv == 0) {
-        for (int w = 1; w < TOPK_WAVES; ++w) tk_merge64(v, ix, lv[w][lane], li[w][lane], lane);
+    const int n = offs[TOPK_P];
+    for (int i = tid; i < P * 64; i += TOPK_THREADS) {
+        const int p = i >> 6, j = i & 63;
+        if (j < offs[p + 1] - offs[p] || (p == TOPK_P - 1 && j < n - offs[p])) {
+            keys[offs[p] + j] = cand_key[(size_t)row * P * 64 + i];
+            idx[offs[p] + j] = cand_idx[(size_t)row * P * 64 + i];
+        }
+    }
+    __syncthreads();
+    int kept = n;
+    if (n > 64) {
+        int need_eq;
+        const uint32_t T = tk_radix_select(keys, n, 64, sh, need_eq);
+        kept = tk_compact(keys, n, T, need_eq, pos, sh);
+    } else if (tid < n) {
+        pos[tid] = tid;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        uint32_t kk = 0;
+        int ix = 0x7fffffff;
+        if (tid < kept) { kk = keys[pos[tid]]; ix = idx[pos[tid]]; }
+        tk_sort64(kk, ix, lane);
         if (lane < k) {
-            out_val[(size_t)row * k + lane] = v;
+            out_val[(size_t)row * k + lane] = tk_val(kk);
             out_idx[(size_t)row * k + lane] = ix;
         }
     }
@@ -311,16 +468,22 @@ hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_
     return hipGetLastError();
 }
 
-size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_P * TOPK_WAVES * 64 * (sizeof(float) + sizeof(int)); }
+size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_P * (64 * 8 + 4); }
 
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
                 hipStream_t st) {
-    float* sv = (float*)scratch;
-    int* si = (int*)((char*)scratch + (size_t)rows * TOPK_P * TOPK_WAVES * 64 * sizeof(float));
-    hipLaunchKernelGGL(topk_partial_kernel, dim3(TOPK_P, rows), dim3(64 * TOPK_WAVES), 0, st, logits, vocab, sv, si);
+    if (vocab > TOPK_P * TOPK_SLICE) return hipErrorInvalidValue;
+    // as many slices as needed, each at most TOPK_SLICE, at most TOPK_P of them
+    int P = (vocab + 2047) / 2048;
+    if (P > TOPK_P) P = TOPK_P;
+    const int slice = (vocab + P - 1) / P;
+    uint32_t* ck = (uint32_t*)scratch;
+    int* ci = (int*)((char*)scratch + (size_t)rows * TOPK_P * 64 * 4);
+    int* cc = (int*)((char*)scratch + (size_t)rows * TOPK_P * 64 * 8);
+    hipLaunchKernelGGL(topk_partial_kernel, dim3(P, rows), dim3(TOPK_THREADS), 0, st, logits, vocab, slice, ck, ci, cc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(64 * TOPK_WAVES), 0, st, sv, si, k, out_val, out_idx);
+    hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(TOPK_THREADS), 0, st, ck, ci, cc, P, k, out_val, out_idx);
     return hipGetLastError();
 }
 
