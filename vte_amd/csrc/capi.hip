@@ -18,8 +18,8 @@ hipError_t gemv_valu(int fmt, const void* x, const void* w, void* y, int M, int 
                      const void* residual, float rs, hipStream_t st);
 hipError_t gemm_mfma(int fmt, int in_dt, int out_dt, const void* x, const void* w, void* y, int M, int K, int N,
                      const void* bias, const void* residual, float rs, hipStream_t st);
-hipError_t qmv(int fmt, bool in_f32, bool out_f32, const void* x, const void* w, void* y, int M, int K, int N,
-               const void* bias, const void* residual, float rs, hipStream_t st);
+hipError_t stream_mv(int fmt, bool in_f32, bool out_f32, const void* x, const void* w, void* y, int M, int K, int N,
+                     const void* bias, const void* residual, float rs, hipStream_t st);
 hipError_t dequantize(int fmt, const void* src, float* dst, long long n_elements, hipStream_t st);
 template <typename TQ, typename TO>
 hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache, float* part_m, float* part_l,
@@ -107,8 +107,8 @@ int vte_gemv(int fmt, int in_dtype, int out_dtype, const void* x, const void* w,
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
-    e = vte::qmv(fmt, in_dtype == VTE_F32, out_dtype == VTE_F32, x, w, y, M, K, N, bias, residual, residual_scale,
-                 st);
+    e = vte::stream_mv(fmt, in_dtype == VTE_F32, out_dtype == VTE_F32, x, w, y, M, K, N, bias, residual,
+                       residual_scale, st);
     if (e != hipErrorNotSupported) return hip_status(e, "vte_gemv launch");
     if (in_dtype == VTE_F32 && out_dtype == VTE_F32)
         e = vte::gemv_valu<float, float>(fmt, x, w, y, M, K, N, bias, residual, residual_scale, st);

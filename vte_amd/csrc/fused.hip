@@ -1,35 +1,45 @@
-// Planned quantised mat-vec: one persistent launch computes several weight
-// segments against the same activations with per-segment epilogues, fusing the
-// decode-step glue into the GEMV (gfx950).
+// Quantised mat-vec for batch 1..4 (gfx950), the bandwidth kernel of the
+// decode step.  One launch computes up to three weight segments against the
+// same activations, each with its own epilogue, so the decode-step glue is
+// fused into the GEMV:
 //
-// Reference nodes replaced, per layer (vte/compiler/qwen_compute.py:100-282,
-// captured in vte/core/hip_graph_executor.py:504-738):
 //   rmsnorm -> gemv q/k/v (+bias) -> rope -> kv_cache_append     => one launch
 //   rmsnorm -> gemv gate/up -> swiglu                            => one launch
 //   rmsnorm(output_norm) -> LM-head gemv                         => one launch
-// with the same rounding points as those nodes: normalised activations,
-// projections (+bias), rotated q/k and the SwiGLU output are fp16 values,
-// computed in fp32 from fp16 inputs:
+//   gemv (+bias, *scale, +residual), e.g. o-proj / down          => one launch
+//
+// (reference nodes: vte/compiler/qwen_compute.py:100-282, captured by
+// vte/core/hip_graph_executor.py:504-738), with the same rounding points as
+// those nodes: normalised activations, projections (+bias), rotated q/k and
+// the SwiGLU output are fp16 values computed in fp32 from fp16 inputs:
 //   rmsnorm   fp16(x * rsqrt(mean(x^2) + eps) * w)            rmsnorm.hip.template:19-71
 //   rope      fp16(a*c - b*s), fp16(a*s + b*c) on (d, d+64)    rope.hip.template:82-97
 //   swiglu    fp16(g / (1 + exp(-g)) * u)                      swiglu.hip.template:11-25
 //
-// Row tiles: plain tiles are R consecutive rows; paired tiles are R/2 rows
-// plus R/2 partner rows (RoPE: d and d + 64 of the same head; SwiGLU: the same
-// row of the gate and up matrices), so a pair's two dot products finish in
-// the same block.  Dot products use the engine in rows.h.
+// One block (256 threads) per tile, one work unit (64 weights sharing a scale
+// pair) per thread.  A tile is R rows whose units fill the block -- plain
+// tiles are consecutive rows; paired tiles are R/2 rows plus their partner
+// rows (RoPE d and d + 64 of one head, or gate row j and up row j), so a
+// pair's two dot products finish in the same block.  Everything a block reads
+// is requested up front -- its weights (straight into registers: no LDS copy,
+// no pipeline), the epilogue operands and the activations -- so a block costs
+// one memory latency plus its arithmetic, and the GPU overlaps many blocks
+// (low register and LDS use keep several blocks resident per CU).  Partials
+// meet in LDS and each output is summed in a fixed order (graph replays are
+// bit for bit reproducible).
+#include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 #include "rows.h"
 
-#define FMV_MAX_SEG 3
-#define FMV_Q6_CHUNKS 8   // 16-byte chunks per thread for a staged Q6_K tile
-#define FMV_Q4_UNITS 2    // Q4_K units per thread per tile
-#define FMV_MAX_R 32
+#define TMV_MAX_SEG 3
+#define TMV_MAX_R 64
+#define TMV_XR 4  // activation chunks per thread per staging round
 
 enum FmvMode : int {
     FMV_STORE_F16 = 0,   // out[m][row] = fp16((acc + bias) * rs + residual)
-    FMV_STORE_F32 = 1,   // same, fp32 output (logits)
+    FMV_STORE_F32 = 1,   // same, fp32 output
     FMV_ROPE_Q = 2,      // fp16(acc + bias), rotated, -> out (q buffer [m][rows])
     FMV_ROPE_KCACHE = 3, // fp16(acc + bias), rotated, -> k_cache at kv_offset[m]
     FMV_VCACHE = 4,      // fp16(acc + bias) -> v_cache at kv_offset[m]
@@ -37,26 +47,29 @@ enum FmvMode : int {
 };
 
 struct FmvSeg {
-    const uint8_t* w;      // weight rows (gate for SwiGLU)
-    const uint8_t* w2;     // up rows (SwiGLU only)
+    const uint8_t* w;        // weight rows (gate for SwiGLU)
+    const uint8_t* w2;       // up rows (SwiGLU only)
     void* out;
-    const __half* bias;    // nullable, fp16 [n_rows]
-    const __half* residual;  // nullable, fp16 [M][n_rows]
-    int fmt;               // 4 = Q4_K, 6 = Q6_K
-    int n_rows;            // output rows of this segment
-    int R;                 // rows per tile (paired modes: even, R/2 divides 64 for RoPE)
+    const void* bias;        // nullable, [n_rows] in the output type (fp16 for fused modes)
+    const void* residual;    // nullable, [M][n_rows] in the output type
+    int fmt;                 // 4 = Q4_K, 6 = Q6_K
+    int n_rows;              // output rows of this segment
+    int R;                   // rows per tile (paired modes: even; RoPE: R/2 a power of two dividing 64)
     int mode;
     int tiles;
+    int row_bytes;
 };
 
 struct FmvPlan {
-    FmvSeg seg[FMV_MAX_SEG];
+    FmvSeg seg[TMV_MAX_SEG];
     int nseg;
+    int total;               // tiles over all segments (= blocks)
     int K;
     int M;
-    const __half* norm_w;  // nullable: RMSNorm prologue on the activations
+    int x_f32;               // activations fp32 (else fp16)
+    const __half* norm_w;    // nullable: RMSNorm prologue on the activations
     float eps;
-    float rs;              // residual scale of store epilogues
+    float rs;                // residual scale of store epilogues
     const __half* rope_cos;
     const __half* rope_sin;
     const int* kv_offset;
@@ -66,142 +79,314 @@ struct FmvPlan {
     int n_kv;
 };
 
-struct FmvTile {
-    int seg, t;
+__host__ __device__ __forceinline__ bool fmv_paired(int mode) {
+    return mode == FMV_ROPE_Q || mode == FMV_ROPE_KCACHE || mode == FMV_SWIGLU;
+}
+
+// Tile g: its segment's parameters, rows and row bases (A: local rows
+// [0, hA), B: local rows [hA, nr)).  Segments are selected with a fixed
+// if-chain (an indexed struct access would reload the kernel argument).
+struct TileGeo {
+    int nr, hA, j0;
+    const uint8_t* bA;
+    const uint8_t* bB;
+    int fmt, mode, rb, n_rows;
+    void* out;
+    const void* bias;
+    const void* residual;
 };
 
-__device__ __forceinline__ FmvTile fmv_tile(const FmvPlan& P, int g) {
-    FmvTile r{-1, 0};
-    for (int s = 0; s < P.nseg; ++s) {
-        if (g < P.seg[s].tiles) { r.seg = s; r.t = g; return r; }
-        g -= P.seg[s].tiles;
+__device__ __forceinline__ void geo_from_seg(const FmvSeg& S, int g, TileGeo& T) {
+    const int rb = S.row_bytes;
+    T.fmt = S.fmt;
+    T.mode = S.mode;
+    T.rb = rb;
+    T.n_rows = S.n_rows;
+    T.out = S.out;
+    T.bias = S.bias;
+    T.residual = S.residual;
+    if (!fmv_paired(S.mode)) {
+        T.j0 = g * S.R;
+        T.nr = min(S.R, S.n_rows - T.j0);
+        T.hA = T.nr;
+        T.bA = S.w + (size_t)T.j0 * rb;
+        T.bB = T.bA;
+    } else if (S.mode == FMV_SWIGLU) {
+        const int h = S.R >> 1;
+        T.j0 = g * h;
+        const int nf = min(h, S.n_rows - T.j0);
+        T.hA = nf;
+        T.nr = 2 * nf;
+        T.bA = S.w + (size_t)T.j0 * rb;
+        T.bB = S.w2 + (size_t)T.j0 * rb;
+    } else {  // RoPE pairs (d, d + 64) of one 128-wide head
+        const int h = S.R >> 1;
+        const int lh = 31 - __builtin_clz(h);  // log2 h
+        const int ltph = 6 - lh;               // log2 of tiles per head
+        T.j0 = ((g >> ltph) << 7) + ((g & ((1 << ltph) - 1)) << lh);
+        T.hA = h;
+        T.nr = S.R;
+        T.bA = S.w + (size_t)T.j0 * rb;
+        T.bB = S.w + (size_t)(T.j0 + 64) * rb;
+    }
+}
+
+__device__ __forceinline__ TileGeo tile_geo(const FmvPlan& P, int g) {
+    TileGeo T;
+    const int t0 = P.seg[0].tiles, t1 = P.seg[1].tiles;
+    if (P.nseg == 1 || g < t0) geo_from_seg(P.seg[0], g, T);
+    else if (P.nseg == 2 || g < t0 + t1) geo_from_seg(P.seg[1], g - t0, T);
+    else geo_from_seg(P.seg[2], g - t0 - t1, T);
+    return T;
+}
+
+// 16 bytes from a global address of any alignment (Q6_K blocks are 2-byte
+// aligned); the hardware handles the misaligned vector load.
+__device__ __forceinline__ uint4 ldg_u16b(const uint8_t* p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+
+// Q6_K unit (h, l16) from registers: 64 weights at 128h + l16 + i + 32g
+// (i < 16, g < 4).  la/lb: ql[64h + l16 ..], ql[64h + 32 + l16 ..]; hq:
+// qh[32h + l16 ..]; sc8: bytes 192 + 8h .. +7; d: fp16 bits.
+__device__ __forceinline__ float q6k_unit_dot_r(const uint4& la4, const uint4& lb4, const uint4& hq4, uint2 sc8,
+                                                uint32_t dbits, int l16, const _Float16* xsb, const float* s16sb,
+                                                int h) {
+    const float d = h2f_bits(dbits);
+    const uint32_t la[4] = {la4.x, la4.y, la4.z, la4.w};
+    const uint32_t lb[4] = {lb4.x, lb4.y, lb4.z, lb4.w};
+    const uint32_t hw[4] = {hq4.x, hq4.y, hq4.z, hq4.w};
+    const uint64_t scw = ((uint64_t)sc8.y << 32) | sc8.x;
+    const int c = l16 >> 4;
+    float r = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const uint4* xp = reinterpret_cast<const uint4*>(xsb + xpad(128 * h + l16 + 32 * g));
+        const uint4 x0 = xp[0], x1 = xp[1];
+        float S = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t l = (g & 1) ? lb[i] : la[i];
+            const uint32_t nib = (g < 2) ? (l & 0x0F0F0F0Fu) : ((l >> 4) & 0x0F0F0F0Fu);
+            const uint32_t u = nib | (((hw[i] >> (2 * g)) & 0x03030303u) << 4);
+            const uint4 xv = (i < 2) ? x0 : x1;
+            const uint32_t x01 = (i & 1) ? xv.z : xv.x;
+            const uint32_t x23 = (i & 1) ? xv.w : xv.y;
+            S = dot4_codes(u, x01, x23, S);
+        }
+        const float X = s16sb[(128 * h + l16 + 32 * g) >> 4];
+        const int8_t sc = (int8_t)((scw >> (8 * (c + 2 * g))) & 0xFF);
+        r = fmaf(d * (float)sc, fmaf(-1056.f, X, S), r);
     }
     return r;
 }
 
-__device__ __forceinline__ bool fmv_paired(int mode) {
-    return mode == FMV_ROPE_Q || mode == FMV_ROPE_KCACHE || mode == FMV_SWIGLU;
+// Scalar global loads through the global address space (a generic pointer
+// would make them flat loads, which also count against the LDS counter).
+__device__ __forceinline__ uint32_t ldg_b16(const void* p, size_t i) {
+    return ((__attribute__((address_space(1))) const uint16_t*)p)[i];
+}
+__device__ __forceinline__ uint32_t ldg_b32(const void* p, size_t i) {
+    return ((__attribute__((address_space(1))) const uint32_t*)p)[i];
 }
 
-// Local row lr of tile t -> (matrix base, global row).  Returns rows in tile.
-__device__ __forceinline__ int fmv_rows(const FmvSeg& S, int t) {
-    if (!fmv_paired(S.mode)) return min(S.R, S.n_rows - t * S.R);
-    if (S.mode == FMV_SWIGLU) return 2 * min(S.R / 2, S.n_rows - t * (S.R / 2));
-    return S.R;
-}
-
-// For paired modes the "first" rows of tile t start at j0 and the partner of
-// local row i < R/2 is local row i + R/2.
-__device__ __forceinline__ void fmv_row(const FmvSeg& S, int t, int lr, const uint8_t*& base, int& row) {
-    const int h = S.R / 2;
-    if (!fmv_paired(S.mode)) { base = S.w; row = t * S.R + lr; return; }
-    if (S.mode == FMV_SWIGLU) {
-        const int nf = min(h, S.n_rows - t * h);  // rows per half in this tile
-        const int j0 = t * h;
-        if (lr < nf) { base = S.w; row = j0 + lr; } else { base = S.w2; row = j0 + lr - nf; }
-        return;
+__device__ __forceinline__ float row_sum(const float* p, int per_row) {
+    const float4* v = reinterpret_cast<const float4*>(p);
+    float a = 0.f, b = 0.f;
+    int j = 0;
+    for (; j + 2 <= per_row / 4; j += 2) {
+        const float4 x = v[j], y = v[j + 1];
+        a += (x.x + x.y) + (x.z + x.w);
+        b += (y.x + y.y) + (y.z + y.w);
     }
-    const int tiles_per_head = 64 / h;
-    const int head = t / tiles_per_head, j0 = (t % tiles_per_head) * h;
-    base = S.w;
-    row = head * 128 + j0 + (lr < h ? lr : lr - h + 64);
+    if (j < per_row / 4) {
+        const float4 x = v[j];
+        a += (x.x + x.y) + (x.z + x.w);
+    }
+    return a + b;
 }
 
-template <int NC>
-__global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __restrict__ x, FmvPlan P) {
-    extern __shared__ uint4 smem_fmv[];
-    uint8_t* lds = reinterpret_cast<uint8_t*>(smem_fmv);
+// Activations (and RMSNorm weights) -> LDS in rounds of TMV_XR 16-byte
+// chunks per thread; a round's loads are unconditional (chunks past the end
+// re-read chunk 0), so they overlap each other.  All rounds but the last are
+// completed here; the last round's chunks are returned in `v` and stored by
+// stage_x_finish, so the caller can issue other loads in between.
+template <bool F32>
+struct XRound {
+    uint4 v[TMV_XR][F32 ? 2 : 1];
+    int c0;
+};
+
+template <int NC, bool F32>
+__device__ __forceinline__ void stage_x_load(const FmvPlan& P, const void* __restrict__ x, int c0, XRound<F32>& r,
+                                             int tid) {
+    const int per_col = P.K / 8;
+    const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * per_col;
+    const uint4* xv = reinterpret_cast<const uint4*>(x);
+    const uint4* nv = reinterpret_cast<const uint4*>(P.norm_w != nullptr ? (const void*)P.norm_w : x);
+    r.c0 = c0;
+#pragma unroll
+    for (int j = 0; j < TMV_XR; ++j) {
+        const int c = c0 + j * ROWS_THREADS + tid;
+        const int m = c / per_col;
+        const bool xcol = c < nch && m < P.M;
+        const bool ncol = c < nch && m == NC;
+        if (F32) {
+            const uint4* p = xv + 2 * (size_t)(xcol ? c : 0);
+            r.v[j][0] = ncol ? nv[c - NC * per_col] : p[0];
+            r.v[j][1] = p[1];
+        } else {
+            r.v[j][0] = ncol ? nv[c - NC * per_col] : xv[xcol ? c : 0];
+        }
+    }
+}
+
+template <int NC, bool F32>
+__device__ __forceinline__ void stage_x_store(const FmvPlan& P, const XRound<F32>& r, _Float16* xs, _Float16* wn_s,
+                                              int tid) {
+    const int ldx = xpad_len(P.K);
+    const int per_col = P.K / 8;
+    const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * per_col;
+#pragma unroll
+    for (int j = 0; j < TMV_XR; ++j) {
+        const int c = r.c0 + j * ROWS_THREADS + tid;
+        const int m = c / per_col, e = (c - m * per_col) * 8;
+        if (c < nch) {
+            if (m == NC) {
+                *reinterpret_cast<uint4*>(wn_s + xpad(e)) = r.v[j][0];
+            } else {
+                uint4 ov = make_uint4(0, 0, 0, 0);
+                if (m < P.M) {
+                    if (F32) {
+                        const uint32_t w[8] = {r.v[j][0].x, r.v[j][0].y, r.v[j][0].z, r.v[j][0].w,
+                                               r.v[j][1].x, r.v[j][1].y, r.v[j][1].z, r.v[j][1].w};
+                        uint32_t hh[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const _Float16 lo = (_Float16)__uint_as_float(w[2 * i]);
+                            const _Float16 hi = (_Float16)__uint_as_float(w[2 * i + 1]);
+                            hh[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+                        }
+                        ov = make_uint4(hh[0], hh[1], hh[2], hh[3]);
+                    } else {
+                        ov = r.v[j][0];
+                    }
+                }
+                *reinterpret_cast<uint4*>(xs + (size_t)m * ldx + xpad(e)) = ov;
+            }
+        }
+    }
+}
+
+// 32-bit aligned load holding element i of an fp16 (f32 = false) or fp32
+// array; returns the element's bits (0 for a null array).  The load is
+// unconditional (a null array reads `dummy`), which keeps the vector-memory
+// counter the same on every path.
+__device__ __forceinline__ uint32_t ld_elem_bits(const void* a, const void* dummy, size_t i, bool f32) {
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(a != nullptr ? a : dummy);
+    const size_t byte = a != nullptr ? (f32 ? 4 * i : 2 * i) : 0;
+    const uint32_t w = ldg_b32(base + (byte & ~(size_t)3), 0);
+    const uint32_t v = f32 ? w : ((w >> (8 * (byte & 2))) & 0xFFFFu);
+    return a != nullptr ? v : 0u;
+}
+
+template <int NC, bool F32, int UPT, int FMT>
+__device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPlan& P, const TileGeo& T,
+                                         uint8_t* lds, float (*red)[NC], int* pos_s) {
     const int K = P.K, M = P.M;
-    const int n_sb = K / QK_K;
-    const int per_row = n_sb * 4;
-    const int ldx = xpad_len(K);
-    // LDS plan: x [NC][ldx] fp16 | s16 [NC][K/16] | part [NC][FMV_MAX_R*per_row] | rsum [NC][FMV_MAX_R] |
-    //           norm weights [ldx] fp16 (with a norm) | stage
+    const int n_sb = K / QK_K, per_row = n_sb * 4, ldx = xpad_len(K);
+    // LDS: x [NC][ldx] fp16 | s16 [NC][K/16] | norm weights [ldx] (with a norm) | part [NC][UPT * 256]
     _Float16* xs = reinterpret_cast<_Float16*>(lds);
     size_t o = ((size_t)NC * ldx * 2 + 15) & ~(size_t)15;
     float* s16 = reinterpret_cast<float*>(lds + o);
     o += (size_t)NC * (K / 16) * 4;
     o = (o + 15) & ~(size_t)15;
-    float* part = reinterpret_cast<float*>(lds + o);
-    const int ustride = FMV_MAX_R * per_row;
-    o += (size_t)NC * ustride * 4;
-    float* rsum = reinterpret_cast<float*>(lds + o);
-    o += (size_t)NC * FMV_MAX_R * 4;
-    o = (o + 15) & ~(size_t)15;
     _Float16* wn_s = reinterpret_cast<_Float16*>(lds + o);
     if (P.norm_w != nullptr) o += ((size_t)ldx * 2 + 15) & ~(size_t)15;
-    uint8_t* stage = lds + o;
-    __shared__ float red[4][NC];
-    __shared__ int pos_s[NC];  // kv_offset[m], read once per block
+    float* part = reinterpret_cast<float*>(lds + o);
+    const int pstride = UPT * ROWS_THREADS;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    int total = 0;
-    for (int s = 0; s < P.nseg; ++s) total += P.seg[s].tiles;
-    const int G = gridDim.x;
+    const bool paired = fmv_paired(T.mode);
+    const int nout = paired ? T.hA : T.nr;  // outputs (per column) this block writes
+    const void* dummy = P.seg[0].w;
 
-    Q4KUnitData cur[FMV_Q4_UNITS], nxt[FMV_Q4_UNITS];
-    uint4 chunk[FMV_Q6_CHUNKS];
-    auto load_tile = [&](int g, Q4KUnitData (&q4)[FMV_Q4_UNITS]) {
-        if (g >= total) return;
-        const FmvTile T = fmv_tile(P, g);
-        const FmvSeg& S = P.seg[T.seg];
-        const int nr = fmv_rows(S, T.t);
-        if (S.fmt == 4) {
-            const float inv = 1.0f / (float)n_sb;
-#pragma unroll
-            for (int j = 0; j < FMV_Q4_UNITS; ++j) {
-                const int u = tid + j * ROWS_THREADS;
-                if (u < nr * per_row) {
-                    const int sbg = u >> 2;
-                    const int lr = (int)(((float)sbg + 0.5f) * inv);
-                    const uint8_t* base;
-                    int row;
-                    fmv_row(S, T.t, lr, base, row);
-                    q4[j] = q4k_unit_load(base + ((size_t)row * n_sb + (sbg - lr * n_sb)) * Q4K_BYTES, u & 3);
-                }
-            }
-        } else {  // Q6_K plain tile: contiguous rows, stage the aligned byte range
-            const uintptr_t a = reinterpret_cast<uintptr_t>(S.w + (size_t)T.t * S.R * n_sb * Q6K_BYTES);
-            const uintptr_t a0 = a & ~(uintptr_t)15;
-            const int nchunk = (int)((a + (size_t)nr * n_sb * Q6K_BYTES - a0 + 15) >> 4);
-#pragma unroll
-            for (int j = 0; j < FMV_Q6_CHUNKS; ++j) {
-                const int c = tid + j * ROWS_THREADS;
-                if (c < nchunk) chunk[j] = ldg_stream16(reinterpret_cast<const uint8_t*>(a0) + 16 * (size_t)c);
-            }
+    // ---- 0. kv offsets and activations first (all staging rounds but the
+    // last complete here): consuming them waits only for them ----
+    const int pos_reg = (int)ld_elem_bits(P.kv_offset, dummy, min(tid, M - 1), true);
+    XRound<F32> xr;
+    {
+        const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * (K / 8);
+        int c0 = 0;
+        for (; c0 + TMV_XR * ROWS_THREADS < nch; c0 += TMV_XR * ROWS_THREADS) {
+            stage_x_load<NC, F32>(P, x, c0, xr, tid);
+            stage_x_store<NC, F32>(P, xr, xs, wn_s, tid);
         }
-    };
-    auto store_stage = [&](int g) {
-        if (g >= total) return;
-        const FmvTile T = fmv_tile(P, g);
-        const FmvSeg& S = P.seg[T.seg];
-        if (S.fmt != 6) return;
-        const int nr = fmv_rows(S, T.t);
-        const uintptr_t a = reinterpret_cast<uintptr_t>(S.w + (size_t)T.t * S.R * n_sb * Q6K_BYTES);
-        const uintptr_t a0 = a & ~(uintptr_t)15;
-        const int nchunk = (int)((a + (size_t)nr * n_sb * Q6K_BYTES - a0 + 15) >> 4);
-#pragma unroll
-        for (int j = 0; j < FMV_Q6_CHUNKS; ++j) {
-            const int c = tid + j * ROWS_THREADS;
-            if (c < nchunk) reinterpret_cast<uint4*>(stage)[c] = chunk[j];
-        }
-    };
+        stage_x_load<NC, F32>(P, x, c0, xr, tid);
+    }
 
-    int g = blockIdx.x;
-    if (tid < M && P.kv_offset != nullptr) pos_s[tid] = P.kv_offset[tid];
-    load_tile(g, cur);
-    // ---- activations: fp16 [M][K] -> LDS, optional RMSNorm ----
-    stage_act<NC>(x, false, M, K, xs, P.norm_w, wn_s);
-    store_stage(g);
+    // ---- 1. this thread's UPT work units: weights straight into registers ----
+    const int units = T.nr * per_row;
+    uint4 w0[UPT], w1[UPT], w2[UPT];
+    uint2 sc8[UPT];
+    uint32_t dbits[UPT];
+    int usb[UPT];
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+        const int u = min(tid + i * ROWS_THREADS, units - 1);  // past the end: re-read the last unit
+        const int sbg = u >> 2, q = u & 3;
+        const int lr = (int)(((float)sbg + 0.5f) * (1.0f / (float)n_sb));
+        const int sb = sbg - lr * n_sb;
+        usb[i] = sb;
+        const uint8_t* rowp = lr < T.hA ? T.bA + (size_t)lr * T.rb : T.bB + (size_t)(lr - T.hA) * T.rb;
+        if (FMT == 4) {
+            const uint8_t* blk = rowp + sb * Q4K_BYTES;
+            w0[i] = ldg_stream16(blk);
+            w1[i] = ldg_stream16(blk + 16 + 32 * q);
+            w2[i] = ldg_stream16(blk + 32 + 32 * q);
+        } else {
+            const uint8_t* blk = rowp + sb * Q6K_BYTES;
+            const int h = q >> 1, l16 = (q & 1) * 16;
+            w0[i] = ldg_u16b(blk + 64 * h + l16);
+            w1[i] = ldg_u16b(blk + 64 * h + 32 + l16);
+            w2[i] = ldg_u16b(blk + 128 + 32 * h + l16);
+            __builtin_memcpy(&sc8[i], blk + 192 + 8 * h, 8);
+            dbits[i] = ldg_b16(blk + 208, 0);
+        }
+    }
+
+    // ---- 2. epilogue operands (unconditional loads; ignored by threads with
+    // no output) ----
+    const bool eth = tid < M * nout;  // M * nout <= 256 (checked on the host)
+    const int tt = eth ? tid : 0;
+    const int em = tt / nout, er = tt - em * nout;
+    const int row1 = T.j0 + er;
+    const bool f32o = T.mode == FMV_STORE_F32;
+    const uint32_t b1 = ld_elem_bits(T.bias, dummy, row1, f32o);
+    const uint32_t b2 = ld_elem_bits(paired ? T.bias : nullptr, dummy, row1 + 64, false);
+    const uint32_t res = ld_elem_bits(T.residual, dummy, (size_t)em * T.n_rows + row1, f32o);
+
+    // ---- 3. activations -> LDS, RMSNorm, per-16 sums ----
+    stage_x_store<NC, F32>(P, xr, xs, wn_s, tid);
+    if (tid < M) pos_s[tid] = pos_reg;
     __syncthreads();
+    uint32_t cb = 0x3C00u, sbits = 0u;
+    if (T.mode == FMV_ROPE_Q || T.mode == FMV_ROPE_KCACHE) {  // cos/sin need the position
+        const size_t ci = (size_t)pos_s[em] * 128 + (row1 & 127);
+        cb = ldg_b16(P.rope_cos, ci);
+        sbits = ldg_b16(P.rope_sin, ci);
+    }
     if (P.norm_w != nullptr) {
         float ss[NC];
 #pragma unroll
         for (int m = 0; m < NC; ++m) ss[m] = 0.f;
-        for (int e = tid; e < K; e += ROWS_THREADS) {
+        for (int i = tid; i < K; i += ROWS_THREADS) {
 #pragma unroll
             for (int m = 0; m < NC; ++m) {
-                const float v = (float)xs[m * ldx + xpad(e)];
+                const float v = (float)xs[m * ldx + xpad(i)];
                 ss[m] = fmaf(v, v, ss[m]);
             }
         }
@@ -215,11 +400,11 @@ __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __
 #pragma unroll
         for (int m = 0; m < NC; ++m)
             inv[m] = rsqrtf((red[0][m] + red[1][m] + red[2][m] + red[3][m]) / (float)K + P.eps);
-        for (int e = tid; e < K; e += ROWS_THREADS) {
-            const float wn = (float)wn_s[xpad(e)];
+        for (int i = tid; i < K; i += ROWS_THREADS) {
+            const float wn = (float)wn_s[xpad(i)];
 #pragma unroll
             for (int m = 0; m < NC; ++m) {
-                _Float16& xv = xs[m * ldx + xpad(e)];
+                _Float16& xv = xs[m * ldx + xpad(i)];
                 xv = (_Float16)((float)xv * inv[m] * wn);
             }
         }
@@ -228,116 +413,128 @@ __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const __half* __
     act_sums<NC>(ActLDS{xs, s16}, K);
     __syncthreads();
 
-    for (; g < total; g += G) {
-        const FmvTile T = fmv_tile(P, g);
-        const FmvSeg& S = P.seg[T.seg];
-        const int nr = fmv_rows(S, T.t);
-        const int units = nr * per_row;
-        const int gn = g + G;
-        load_tile(gn, nxt);
-        const float inv_nsb = 1.0f / (float)n_sb;
-        if (S.fmt == 4) {
+    // ---- 4. the units' partials for every column ----
 #pragma unroll
-            for (int j = 0; j < FMV_Q4_UNITS; ++j) {
-                const int u = tid + j * ROWS_THREADS;
-                if (u >= units) break;
-                const int sbg = u >> 2, q = u & 3;
-                const int lr = (int)(((float)sbg + 0.5f) * inv_nsb);
-                const int sb = sbg - lr * n_sb;
+    for (int i = 0; i < UPT; ++i) {
+        const int u = tid + i * ROWS_THREADS;
+        if (u < units) {
+            const int q = u & 3, sb = usb[i];
+            if (FMT == 4) {
+                const Q4KUnitData d{w0[i], w1[i], w2[i]};
 #pragma unroll
                 for (int m = 0; m < NC; ++m)
-                    part[m * ustride + u] = q4k_unit_dot(cur[j], q, xs + (size_t)m * ldx + xpad(sb * QK_K + 64 * q),
+                    part[m * pstride + u] = q4k_unit_dot(d, q, xs + (size_t)m * ldx + xpad(sb * QK_K + 64 * q),
                                                          s16 + m * (K / 16) + sb * 16 + 4 * q);
-            }
-        } else {
-            const uint8_t* rows_lds =
-                stage + (reinterpret_cast<uintptr_t>(S.w + (size_t)T.t * S.R * n_sb * Q6K_BYTES) & 15);
-            for (int u = tid; u < units; u += ROWS_THREADS) {
-                const int sbg = u >> 2, q = u & 3;
-                const int lr = (int)(((float)sbg + 0.5f) * inv_nsb);
-                const int sb = sbg - lr * n_sb;
-                const uint8_t* blk = rows_lds + (size_t)sbg * Q6K_BYTES;
+            } else {
+                const int h = q >> 1, l16 = (q & 1) * 16;
 #pragma unroll
                 for (int m = 0; m < NC; ++m)
-                    part[m * ustride + u] = q6k_unit_dot(blk, q >> 1, (q & 1) * 16, xs + (size_t)m * ldx + xpad(sb * QK_K),
-                                                         s16 + m * (K / 16) + sb * 16);
+                    part[m * pstride + u] = q6k_unit_dot_r(w0[i], w1[i], w2[i], sc8[i], dbits[i], l16,
+                                                           xs + (size_t)m * ldx + xpad(sb * QK_K),
+                                                           s16 + m * (K / 16) + sb * 16, h);
             }
         }
-        __syncthreads();
-        for (int i = tid; i < NC * nr; i += ROWS_THREADS) {
-            const int m = i / nr, r = i - m * nr;
-            const float4* p = reinterpret_cast<const float4*>(part + m * ustride + r * per_row);
-            float sacc = 0.f;
-            for (int j = 0; j < per_row / 4; ++j) {
-                const float4 v = p[j];
-                sacc += (v.x + v.y) + (v.z + v.w);
-            }
-            rsum[m * FMV_MAX_R + r] = sacc;
+    }
+    __syncthreads();
+
+    // ---- 5. epilogue: one output (column em, row er) per thread ----
+    if (!eth) return;
+    if (!paired) {
+        float v = row_sum(part + em * pstride + er * per_row, per_row) +
+                  (f32o ? __uint_as_float(b1) : h2f_bits(b1));
+        if (T.mode == FMV_VCACHE) {
+            P.v_cache[(size_t)em * P.kv_batch_stride + ((size_t)pos_s[em] * P.n_kv + row1 / 128) * 128 +
+                      (row1 % 128)] = __float2half(v);
+            return;
         }
-        store_stage(gn);
-        __syncthreads();
-        // ---- epilogue ----
-        if (!fmv_paired(S.mode)) {
-            for (int i = tid; i < M * nr; i += ROWS_THREADS) {
-                const int m = i / nr, r = i - m * nr;
-                const uint8_t* base;
-                int row;
-                fmv_row(S, T.t, r, base, row);
-                float v = rsum[m * FMV_MAX_R + r];
-                if (S.bias) v += __half2float(S.bias[row]);
-                if (S.mode == FMV_VCACHE) {
-                    const int pos = pos_s[m];
-                    P.v_cache[(size_t)m * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128 + (row % 128)] =
-                        __float2half(v);
-                    continue;
-                }
-                v *= P.rs;
-                const size_t oi = (size_t)m * S.n_rows + row;
-                if (S.residual) v += __half2float(S.residual[oi]);
-                if (S.mode == FMV_STORE_F32) reinterpret_cast<float*>(S.out)[oi] = v;
-                else reinterpret_cast<__half*>(S.out)[oi] = __float2half(v);
-            }
-        } else {
-            const int hp = nr / 2;
-            for (int i = tid; i < M * hp; i += ROWS_THREADS) {
-                const int m = i / hp, r = i - m * hp;
-                const uint8_t* base;
-                int row1, row2;
-                fmv_row(S, T.t, r, base, row1);
-                fmv_row(S, T.t, r + hp, base, row2);
-                float a = rsum[m * FMV_MAX_R + r], bv = rsum[m * FMV_MAX_R + r + hp];
-                if (S.mode == FMV_SWIGLU) {
-                    const float gg = __half2float(__float2half(a));
-                    const float uu = __half2float(__float2half(bv));
-                    const float sig = 1.0f / (1.0f + expf(-gg));
-                    reinterpret_cast<__half*>(S.out)[(size_t)m * S.n_rows + row1] = __float2half(gg * sig * uu);
-                    continue;
-                }
-                if (S.bias) { a += __half2float(S.bias[row1]); bv += __half2float(S.bias[row2]); }
-                const float x1 = __half2float(__float2half(a)), x2 = __half2float(__float2half(bv));
-                const int pos = pos_s[m];
-                const int d = row1 % 128;
-                const float c = __half2float(P.rope_cos[(size_t)pos * 128 + d]);
-                const float sn = __half2float(P.rope_sin[(size_t)pos * 128 + d]);
-                const __half o1 = __float2half(x1 * c - x2 * sn), o2 = __float2half(x1 * sn + x2 * c);
-                if (S.mode == FMV_ROPE_Q) {
-                    __half* q = reinterpret_cast<__half*>(S.out) + (size_t)m * S.n_rows;
-                    q[row1] = o1;
-                    q[row2] = o2;
-                } else {
-                    __half* kc = P.k_cache + (size_t)m * P.kv_batch_stride + ((size_t)pos * P.n_kv + row1 / 128) * 128;
-                    kc[d] = o1;
-                    kc[d + 64] = o2;
-                }
-            }
-        }
-        // the next tile's Q4_K units (if it is a Q4_K tile) become current
-#pragma unroll
-        for (int j = 0; j < FMV_Q4_UNITS; ++j) cur[j] = nxt[j];
+        v = v * P.rs + (f32o ? __uint_as_float(res) : h2f_bits(res));
+        const size_t oi = (size_t)em * T.n_rows + row1;
+        if (f32o) reinterpret_cast<float*>(T.out)[oi] = v;
+        else reinterpret_cast<__half*>(T.out)[oi] = __float2half(v);
+        return;
+    }
+    const float a = row_sum(part + em * pstride + er * per_row, per_row);
+    const float bv = row_sum(part + em * pstride + (er + T.hA) * per_row, per_row);
+    if (T.mode == FMV_SWIGLU) {
+        const float gg = __half2float(__float2half(a));
+        const float uu = __half2float(__float2half(bv));
+        const float sig = 1.0f / (1.0f + expf(-gg));
+        reinterpret_cast<__half*>(T.out)[(size_t)em * T.n_rows + row1] = __float2half(gg * sig * uu);
+        return;
+    }
+    const float x1 = __half2float(__float2half(a + h2f_bits(b1)));
+    const float x2 = __half2float(__float2half(bv + h2f_bits(b2)));
+    const float c = h2f_bits(cb), sn = h2f_bits(sbits);
+    const __half o1 = __float2half(x1 * c - x2 * sn), o2 = __float2half(x1 * sn + x2 * c);
+    if (T.mode == FMV_ROPE_Q) {
+        __half* qo = reinterpret_cast<__half*>(T.out) + (size_t)em * T.n_rows;
+        qo[row1] = o1;
+        qo[row1 + 64] = o2;
+    } else {
+        const int d = row1 & 127;
+        __half* kc = P.k_cache + (size_t)em * P.kv_batch_stride + ((size_t)pos_s[em] * P.n_kv + row1 / 128) * 128;
+        kc[d] = o1;
+        kc[d + 64] = o2;
     }
 }
 
+template <int NC, bool F32, int UPT>
+__global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const void* __restrict__ x, FmvPlan P) {
+    extern __shared__ uint4 smem_fmv[];
+    __shared__ float red[4][NC];
+    __shared__ int pos_s[NC];
+    const TileGeo T = tile_geo(P, blockIdx.x);
+    uint8_t* lds = reinterpret_cast<uint8_t*>(smem_fmv);
+    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4>(x, P, T, lds, red, pos_s);
+    else tmv_body<NC, F32, UPT, 6>(x, P, T, lds, red, pos_s);
+}
+
 namespace vte {
+
+static size_t fmv_max_lds() {
+    static size_t n = 0;
+    if (n == 0) {
+        int dev = 0, v = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 65536;
+        n = (size_t)v;
+    }
+    return n;
+}
+
+static size_t fmv_lds_bytes(int NC, int K, bool has_norm, int upt) {
+    size_t o = ((size_t)NC * xpad_len(K) * 2 + 15) & ~(size_t)15;
+    o += (size_t)NC * (K / 16) * 4;
+    o = (o + 15) & ~(size_t)15;
+    if (has_norm) o += ((size_t)xpad_len(K) * 2 + 15) & ~(size_t)15;
+    o += (size_t)NC * upt * ROWS_THREADS * 4;
+    return o;
+}
+
+// Rows per tile: as many as fill the block with one unit per thread (0 if a
+// single row has more units than threads).  RoPE tiles take a power-of-two
+// number of rows per half so tiles never straddle a head.
+static int fmv_rows_per_tile(int mode, int K, int upt) {
+    const int per_row = (K / QK_K) * 4;
+    const int R = upt * ROWS_THREADS / per_row;
+    if (R < 1) return 0;
+    if (mode == FMV_SWIGLU) return R >= 2 ? std::min(R & ~1, TMV_MAX_R) : 0;
+    if (mode == FMV_ROPE_Q || mode == FMV_ROPE_KCACHE) {
+        int h = 1;
+        while (4 * h <= R && 2 * h <= 64) h *= 2;
+        return R >= 2 ? 2 * h : 0;
+    }
+    return std::min(R, TMV_MAX_R);
+}
+
+template <int NC, bool F32>
+static void fmv_launch(int upt, int total, size_t lds, hipStream_t st, const void* x, const FmvPlan& plan) {
+    const dim3 g(total), b(ROWS_THREADS);
+    if (upt == 4) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4>), g, b, lds, st, x, plan);
+    else if (upt == 2) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 2>), g, b, lds, st, x, plan);
+    else hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 1>), g, b, lds, st, x, plan);
+}
 
 static int fmv_num_cus() {
     static int n = 0;
@@ -349,69 +546,60 @@ static int fmv_num_cus() {
     return n;
 }
 
-size_t fmv_lds_bytes(int NC, int K, bool has_q6, bool has_norm) {
-    const int per_row = (K / 256) * 4;
-    size_t o = ((size_t)NC * xpad_len(K) * 2 + 15) & ~(size_t)15;
-    o += (size_t)NC * (K / 16) * 4;
-    o = (o + 15) & ~(size_t)15;
-    o += (size_t)NC * FMV_MAX_R * per_row * 4;
-    o += (size_t)NC * FMV_MAX_R * 4;
-    o = (o + 15) & ~(size_t)15;
-    if (has_norm) o += ((size_t)xpad_len(K) * 2 + 15) & ~(size_t)15;
-    if (has_q6) o += (size_t)ROWS_THREADS * FMV_Q6_CHUNKS * 16;
-    return o;
-}
-
-// Rows per tile for a segment (0 if the shape cannot be tiled).
-int fmv_rows_per_tile(int fmt, int mode, int K, int n_rows) {
-    const int n_sb = K / 256;
-    if (fmt == 4) {
-        int R = ROWS_THREADS * FMV_Q4_UNITS / (n_sb * 4);
-        if (R > FMV_MAX_R) R = FMV_MAX_R;
-        if (mode == FMV_ROPE_Q || mode == FMV_ROPE_KCACHE) {  // R/2 must divide 64
-            int h = 1;
-            while (2 * h <= R / 2 && 64 % (2 * h) == 0) h *= 2;
-            return 2 * h;
-        }
-        if (mode == FMV_SWIGLU) return R >= 2 ? (R & ~1) : 0;
-        return R >= 1 ? R : 0;
-    }
-    if (mode != FMV_STORE_F16 && mode != FMV_STORE_F32 && mode != FMV_VCACHE) return 0;  // Q6_K: plain tiles only
-    int R = (int)(((size_t)ROWS_THREADS * FMV_Q6_CHUNKS * 16 - 48) / ((size_t)n_sb * Q6K_BYTES));
-    if (R > FMV_MAX_R) R = FMV_MAX_R;
-    (void)n_rows;
-    return R;
-}
-
-hipError_t fused_mv(const __half* x, FmvPlan plan, hipStream_t st) {
-    bool has_q6 = false;
-    int total = 0;
-    for (int s = 0; s < plan.nseg; ++s) {
-        FmvSeg& S = plan.seg[s];
-        if (S.R <= 0) return hipErrorInvalidValue;
-        if (S.fmt == 6) has_q6 = true;
-        if (S.mode == FMV_SWIGLU) S.tiles = (S.n_rows + S.R / 2 - 1) / (S.R / 2);
-        else if (S.mode == FMV_ROPE_Q || S.mode == FMV_ROPE_KCACHE) S.tiles = S.n_rows / S.R;
-        else S.tiles = (S.n_rows + S.R - 1) / S.R;
-        total += S.tiles;
-    }
-    const int NC = plan.M <= 1 ? 1 : (plan.M <= 2 ? 2 : 4);
-    const size_t lds = fmv_lds_bytes(NC, plan.K, has_q6, plan.norm_w != nullptr);
+// Completes the plan (units per thread, rows per tile, tile counts) and
+// launches one block per tile.  Units per thread (1, 2 or 4) are as many as
+// keep at least two tiles per CU: larger tiles spread the per-block prologue
+// (activation staging, RMSNorm) over more weights.
+hipError_t fused_mv(const void* x, FmvPlan plan, hipStream_t st) {
+    if (plan.M < 1 || plan.M > 4 || plan.nseg < 1 || plan.nseg > TMV_MAX_SEG) return hipErrorNotSupported;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || (plan.K % QK_K) != 0) return hipErrorInvalidValue;
     if (plan.norm_w != nullptr && (reinterpret_cast<uintptr_t>(plan.norm_w) & 15)) return hipErrorInvalidValue;
-    if (lds > 65536 || plan.M > 4) return hipErrorNotSupported;
-    if ((reinterpret_cast<uintptr_t>(x) & 15) || (plan.K & 7)) return hipErrorInvalidValue;  // 16-byte staging
-    int blocks = 0;
-    hipError_t e;
-    if (NC == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, (const void*)fused_mv_kernel<1>, ROWS_THREADS, lds);
-    else if (NC == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, (const void*)fused_mv_kernel<2>, ROWS_THREADS, lds);
-    else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, (const void*)fused_mv_kernel<4>, ROWS_THREADS, lds);
-    if (e != hipSuccess || blocks <= 0) blocks = 1;
-    int grid = fmv_num_cus() * blocks;
-    if (grid > total) grid = total;
-    if (NC == 1) hipLaunchKernelGGL(fused_mv_kernel<1>, dim3(grid), dim3(ROWS_THREADS), lds, st, x, plan);
-    else if (NC == 2) hipLaunchKernelGGL(fused_mv_kernel<2>, dim3(grid), dim3(ROWS_THREADS), lds, st, x, plan);
-    else hipLaunchKernelGGL(fused_mv_kernel<4>, dim3(grid), dim3(ROWS_THREADS), lds, st, x, plan);
-    return hipGetLastError();
+    const int NC = plan.M <= 1 ? 1 : (plan.M <= 2 ? 2 : 4);
+    const int n_sb = plan.K / QK_K;
+    static int upt_force = -1;  // VTE_FMV_UPT=1|2|4 pins units per thread (tuning)
+    if (upt_force < 0) {
+        const char* e = getenv("VTE_FMV_UPT");
+        upt_force = e ? atoi(e) : 0;
+    }
+    for (int upt : {4, 2, 1}) {
+        if (upt_force > 0 && upt != upt_force) continue;
+        FmvPlan P = plan;
+        int total = 0;
+        bool ok = true;
+        for (int s = 0; s < P.nseg && ok; ++s) {
+            FmvSeg& S = P.seg[s];
+            if (S.fmt != 4 && S.fmt != 6) return hipErrorInvalidValue;
+            if (fmv_paired(S.mode) && S.fmt != 4) return hipErrorInvalidValue;
+            S.row_bytes = n_sb * (S.fmt == 4 ? Q4K_BYTES : Q6K_BYTES);
+            S.R = fmv_rows_per_tile(S.mode, P.K, upt);
+            if (S.R <= 0 || P.M * S.R > ROWS_THREADS) { ok = false; break; }
+            if (S.mode == FMV_SWIGLU) {
+                S.tiles = (S.n_rows + S.R / 2 - 1) / (S.R / 2);
+            } else if (S.mode == FMV_ROPE_Q || S.mode == FMV_ROPE_KCACHE) {
+                if (S.n_rows % 128 != 0) return hipErrorInvalidValue;
+                S.tiles = S.n_rows / S.R;
+            } else {
+                S.tiles = (S.n_rows + S.R - 1) / S.R;
+            }
+            total += S.tiles;
+        }
+        if (!ok) continue;
+        if (upt_force <= 0 && upt > 1 && total < 2 * fmv_num_cus()) continue;
+        P.total = total;
+        const size_t lds = fmv_lds_bytes(NC, P.K, P.norm_w != nullptr, upt);
+        if (lds + 64 > fmv_max_lds()) continue;
+        if (P.x_f32) {
+            if (NC == 1) fmv_launch<1, true>(upt, total, lds, st, x, P);
+            else if (NC == 2) fmv_launch<2, true>(upt, total, lds, st, x, P);
+            else fmv_launch<4, true>(upt, total, lds, st, x, P);
+        } else {
+            if (NC == 1) fmv_launch<1, false>(upt, total, lds, st, x, P);
+            else if (NC == 2) fmv_launch<2, false>(upt, total, lds, st, x, P);
+            else fmv_launch<4, false>(upt, total, lds, st, x, P);
+        }
+        return hipGetLastError();
+    }
+    return hipErrorNotSupported;
 }
 
 static FmvPlan plan_base(int M, int K, const void* norm_w, float eps) {
@@ -426,18 +614,17 @@ static FmvPlan plan_base(int M, int K, const void* norm_w, float eps) {
 }
 
 static FmvSeg seg(const void* w, const void* w2, void* out, const void* bias, const void* residual, int fmt,
-                  int n_rows, int mode, int K) {
+                  int n_rows, int mode) {
     FmvSeg S;
+    memset(&S, 0, sizeof(S));
     S.w = (const uint8_t*)w;
     S.w2 = (const uint8_t*)w2;
     S.out = out;
-    S.bias = (const __half*)bias;
-    S.residual = (const __half*)residual;
+    S.bias = bias;
+    S.residual = residual;
     S.fmt = fmt;
     S.n_rows = n_rows;
     S.mode = mode;
-    S.R = fmv_rows_per_tile(fmt, mode, K, n_rows);
-    S.tiles = 0;
     return S;
 }
 
@@ -446,9 +633,9 @@ hipError_t attn_in(const void* x, const void* norm_w, float eps, const void* wq,
                    void* q_out, void* k_cache, void* v_cache, const int* kv_offset, int kv_batch_stride,
                    const void* rope_cos, const void* rope_sin, int M, int K, int n_q, int n_kv, hipStream_t st) {
     FmvPlan P = plan_base(M, K, norm_w, eps);
-    P.seg[0] = seg(wq, nullptr, q_out, q_bias, nullptr, fmt_q, n_q * 128, FMV_ROPE_Q, K);
-    P.seg[1] = seg(wk, nullptr, nullptr, k_bias, nullptr, fmt_k, n_kv * 128, FMV_ROPE_KCACHE, K);
-    P.seg[2] = seg(wv, nullptr, nullptr, v_bias, nullptr, fmt_v, n_kv * 128, FMV_VCACHE, K);
+    P.seg[0] = seg(wq, nullptr, q_out, q_bias, nullptr, fmt_q, n_q * 128, FMV_ROPE_Q);
+    P.seg[1] = seg(wk, nullptr, nullptr, k_bias, nullptr, fmt_k, n_kv * 128, FMV_ROPE_KCACHE);
+    P.seg[2] = seg(wv, nullptr, nullptr, v_bias, nullptr, fmt_v, n_kv * 128, FMV_VCACHE);
     P.nseg = 3;
     P.rope_cos = (const __half*)rope_cos;
     P.rope_sin = (const __half*)rope_sin;
@@ -457,24 +644,39 @@ hipError_t attn_in(const void* x, const void* norm_w, float eps, const void* wq,
     P.v_cache = (__half*)v_cache;
     P.kv_batch_stride = kv_batch_stride;
     P.n_kv = n_kv;
-    return fused_mv((const __half*)x, P, st);
+    return fused_mv(x, P, st);
 }
 
 hipError_t ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up, int fmt,
                   void* out, int M, int K, int ffn, hipStream_t st) {
     FmvPlan P = plan_base(M, K, norm_w, eps);
-    P.seg[0] = seg(w_gate, w_up, out, nullptr, nullptr, fmt, ffn, FMV_SWIGLU, K);
+    P.seg[0] = seg(w_gate, w_up, out, nullptr, nullptr, fmt, ffn, FMV_SWIGLU);
     P.nseg = 1;
-    return fused_mv((const __half*)x, P, st);
+    return fused_mv(x, P, st);
 }
 
 hipError_t norm_mv(const void* x, const void* norm_w, float eps, const void* w, int fmt, void* out, bool out_f32,
                    const void* bias, const void* residual, float rs, int M, int K, int N, hipStream_t st) {
     FmvPlan P = plan_base(M, K, norm_w, eps);
     P.rs = rs;
-    P.seg[0] = seg(w, nullptr, out, bias, residual, fmt, N, out_f32 ? FMV_STORE_F32 : FMV_STORE_F16, K);
+    P.seg[0] = seg(w, nullptr, out, bias, residual, fmt, N, out_f32 ? FMV_STORE_F32 : FMV_STORE_F16);
     P.nseg = 1;
-    return fused_mv((const __half*)x, P, st);
+    return fused_mv(x, P, st);
+}
+
+// Plain y = (W x + bias) * rs + residual for batch 1..4 (no norm); x fp32 or
+// fp16, y / bias / residual in the output type.  hipErrorNotSupported (nothing
+// launched) when the shape does not fit: rows longer than 256 units (K > 16384).
+hipError_t stream_mv(int fmt, bool in_f32, bool out_f32, const void* x, const void* w, void* y, int M, int K, int N,
+                     const void* bias, const void* residual, float rs, hipStream_t st) {
+    if (fmt != 4 && fmt != 6) return hipErrorNotSupported;
+    if (M > 4) return hipErrorNotSupported;
+    FmvPlan P = plan_base(M, K, nullptr, 0.f);
+    P.x_f32 = in_f32 ? 1 : 0;
+    P.rs = rs;
+    P.seg[0] = seg(w, nullptr, y, bias, residual, fmt, N, out_f32 ? FMV_STORE_F32 : FMV_STORE_F16);
+    P.nseg = 1;
+    return fused_mv(x, P, st);
 }
 
 }  // namespace vte
