@@ -89,6 +89,8 @@ long long vte_attn_scratch_floats(int batch, int n_q, int max_splits);
  * [B][n_q][max_splits][128] fp32 scratch.  counters: NULL = separate combine
  * launch; else B*n_kv zeroed ints and the combine runs in the last partial
  * block of each (sequence, KV head) (max_splits <= 512), leaving them zero.
+ * out NULL (with counters NULL): only the partials are written, for
+ * vte_attn_out_gemv to combine.
  * Replaces: SplitKVAttentionDispatcher launches (vte/core/split_kv_attention.py:187-217),
  *           flash_attention_split_kv_partial_kernel (flash_attention_split_kv_partial.hip.template:31-120),
  *           flash_attention_split_kv_reduce_kernel (flash_attention_split_kv_reduce.hip.template:14-67). */
@@ -165,6 +167,17 @@ int vte_ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate,
 int vte_norm_gemv(const void* x, const void* norm_w, float eps, const void* w, int fmt, void* out, int out_dtype,
                   const void* bias, const void* residual, float residual_scale, int batch, int K, int N,
                   void* stream);
+
+/* Attention output projection with the split-KV combine fused in:
+ * out[b][n] = fp16(sum_k W[n][k] a[b][k] * residual_scale + residual[b][n]),
+ * a[b][h*128 + d] = fp16(log-sum-exp combine of the partials of
+ * vte_attn_split_kv for sequence b, head h), K = n_q * 128, N outputs,
+ * fp16 residual nullable.  batch 1..4, max_splits <= 64, Q4_K or Q6_K.
+ * Replaces: flash_attention_split_kv_reduce_kernel (flash_attention_split_kv_reduce.hip.template:14-67)
+ *           followed by the o-proj gemv with residual (vte/compiler/qwen_compute.py:100-282). */
+int vte_attn_out_gemv(const float* part_m, const float* part_l, const float* part_o, const int* kv_offset, int batch,
+                      int n_q, int max_splits, int split, const void* w, int fmt, void* out, const void* residual,
+                      float residual_scale, int N, void* stream);
 
 /* dst[i] = fp16(scale * N(0,1)) from a counter-based generator (synthetic KV
  * prefixes); no reference counterpart (test and benchmark input). */

@@ -155,3 +155,34 @@ def test_reference_abi_split_kv_kernels(hip):
     for b in range(B):
         ref = attention_ref(q16[b].astype(np.float32), kc[b], vc[b], int(offs[b]) + 1, SCALE)
         assert rel_l2(got[b], ref) <= TOL
+
+
+@pytest.mark.parametrize("B,fmt", [(1, "q4_k"), (3, "q6_k")])
+def test_attn_out_gemv_combines_partials(hip, K, B, fmt):
+    """o-proj with the LSE combine in its prologue equals combine-then-GEMV:
+    y = W . fp16(attention) + residual against the float64 oracle."""
+    from oracle import dequant as odq
+    from vte_amd import synthetic as syn
+    rng = np.random.default_rng(40 + B)
+    max_seq, split = 1024, 128
+    q, kc, vc = _inputs(rng, B, max_seq)
+    offs = np.array([1023, 130, 7][:B], np.int32)
+    ms = max_seq // split
+    pm = empty(hip, (B, NQ, ms), np.float32)
+    pl = empty(hip, (B, NQ, ms), np.float32)
+    po = empty(hip, (B, NQ, ms, D), np.float32)
+    doffs = up(hip, offs)
+    K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), pm, pl, po, None, B, NQ, NKV, D, SCALE, doffs,
+                    max_seq * NKV * D, split, ms, dtype="f32", stream=hip.stream)
+    N, Kd = 1536, NQ * D
+    raw = syn.random_matrix(fmt, rng, N, Kd)
+    res = rng.standard_normal((B, N)).astype(np.float16)
+    out = empty(hip, (B, N), np.float16)
+    K.attn_out_gemv(pm, pl, po, doffs, B, NQ, ms, split, up(hip, raw), fmt, out, N, residual=up(hip, res),
+                    stream=hip.stream)
+    got = down(out).astype(np.float64)
+    W = odq.dequantize_matrix(fmt, raw, N, Kd).astype(np.float64)
+    for b in range(B):
+        att = attention_ref(q[b], kc[b], vc[b], int(offs[b]) + 1, SCALE).reshape(-1).astype(np.float16)
+        ref = W @ att.astype(np.float64) + res[b].astype(np.float64)
+        assert rel_l2(got[b], ref) <= 2e-3, b   # fp16 attention output and fp16 result

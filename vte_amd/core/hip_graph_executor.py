@@ -119,9 +119,10 @@ class HIPGraphExecutor:
     FUSED_CLASSES = ("embed", "attn_in", "attn", "o_proj", "ffn_in", "down", "lm_head", "topk")
 
     def _enqueue_fused(self, only=None) -> None:
-        """Six launches per layer: norm+QKV+RoPE+append [fused_mv_kernel],
-        attention [attn_partial_gqa + attn_combine], o-proj [qmv_kernel],
-        norm+gate/up+SwiGLU [fused_mv_kernel], down [qmv_kernel]; then
+        """Five launches per layer: norm+QKV+RoPE+append [fused_mv_kernel],
+        split-KV attention partials [attn_partial_gqa], LSE combine + o-proj
+        + residual [fused_mv_kernel], norm+gate/up+SwiGLU [fused_mv_kernel],
+        down + residual [fused_mv_kernel]; then
         norm+LM head [fused_mv_kernel] and top-k.  ``only``: a set of
         FUSED_CLASSES to issue (timing of one class over the same buffers)."""
         cfg, K, st, B = self.cfg, self.K, self.hip.stream, self.B
@@ -137,11 +138,19 @@ class HIPGraphExecutor:
                           lw["k_bias"], lw["k_fmt"], lw["v"], lw["v_bias"], lw["v_fmt"], self.q, self.k_cache[L],
                           self.v_cache[L], offs, self.kv_batch_stride, self.rope_cos, self.rope_sin, B, H, cfg.n_q,
                           cfg.n_kv, cfg.head_dim, stream=st)
+            # the o-proj blocks each re-read every split's partials, so the fused
+            # combine only pays off while there are few splits (short caches)
+            combine_in_oproj = self.attn.max_splits <= 8
             if on("attn"):
-                self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], self.att, offs, self.kv_batch_stride,
-                                 dtype="f16", batch=B, stream=st)
+                self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], None if combine_in_oproj else self.att,
+                                 offs, self.kv_batch_stride, dtype="f16", batch=B, stream=st)
             if on("o_proj"):
-                self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
+                if combine_in_oproj:  # LSE combine of the partials fused into the o-proj prologue
+                    K.attn_out_gemv(self.attn.part_m, self.attn.part_l, self.attn.part_o, offs, B, cfg.n_q,
+                                    self.attn.max_splits, self.attn.split, lw["o"], lw["o_fmt"], self.h[1 - cur], H,
+                                    residual=self.h[cur], stream=st)
+                else:
+                    self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
             cur = 1 - cur
             if on("ffn_in"):
                 K.ffn_in(self.h[cur], lw["ffn_norm"], cfg.eps, lw["gate"], lw["up"], lw["gate_fmt"], self.a, B, H,

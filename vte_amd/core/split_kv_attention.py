@@ -64,8 +64,11 @@ class SplitKVAttentionDispatcher:
 
     def launch(self, q, k_cache, v_cache, out, kv_offset, kv_batch_stride: int, dtype: str = "f16",
                batch: int | None = None, stream=None) -> None:
-        """Partial + combine for one layer.  q [B, n_q, hd]; out [B, n_q, hd]."""
+        """Partial + combine for one layer.  q [B, n_q, hd]; out [B, n_q, hd].
+        ``out=None``: partials only (part_m / part_l / part_o), combined later
+        by the output projection (``vte_attn_out_gemv``)."""
         self.K.attn_split_kv(q, k_cache, v_cache, self.part_m, self.part_l, self.part_o, out, batch or self.batch,
                              self.n_q, self.n_kv, self.head_dim, self.scale, kv_offset, kv_batch_stride, self.split,
-                             self.max_splits, dtype=dtype, counters=self.counters if self.fuse_combine else None,
+                             self.max_splits, dtype=dtype,
+                             counters=self.counters if (self.fuse_combine and out is not None) else None,
                              stream=stream if stream is not None else self.hip.stream)

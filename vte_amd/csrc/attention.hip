@@ -450,7 +450,7 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
                        (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset,
                        kv_batch_stride, split, max_splits, counters, (TO*)out);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || counters != nullptr) return e;
+    if (e != hipSuccess || counters != nullptr || out == nullptr) return e;  // out == nullptr: partials only
     dim3 g2(n_q, B), b2(ATT_D);
     hipLaunchKernelGGL((attn_combine<TO>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q, kv_offset, split,
                        max_splits);

@@ -18,6 +18,9 @@ hipError_t gemv_valu(int fmt, const void* x, const void* w, void* y, int M, int 
                      const void* residual, float rs, hipStream_t st);
 hipError_t gemm_mfma(int fmt, int in_dt, int out_dt, const void* x, const void* w, void* y, int M, int K, int N,
                      const void* bias, const void* residual, float rs, hipStream_t st);
+hipError_t attn_out_mv(const float* part_m, const float* part_l, const float* part_o, const int* kv_offset, int M,
+                       int n_q, int max_splits, int split, const void* w, int fmt, void* out, const void* residual,
+                       float rs, int N, hipStream_t st);
 hipError_t stream_mv(int fmt, bool in_f32, bool out_f32, const void* x, const void* w, void* y, int M, int K, int N,
                      const void* bias, const void* residual, float rs, hipStream_t st);
 hipError_t dequantize(int fmt, const void* src, float* dst, long long n_elements, hipStream_t st);
@@ -151,7 +154,8 @@ int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void*
                       float scale, const int* kv_offset, int kv_batch_stride, int split, int max_splits,
                       int* counters, void* stream) {
     REQUIRE(dtype == VTE_F32 || dtype == VTE_F16, "attn: dtype must be 0 (f32) or 1 (f16)");
-    REQUIRE(q && k_cache && v_cache && part_m && part_l && part_o && out && kv_offset, "attn: null pointer");
+    REQUIRE(q && k_cache && v_cache && part_m && part_l && part_o && kv_offset, "attn: null pointer");
+    REQUIRE(out != nullptr || counters == nullptr, "attn: the in-kernel combine needs an output");
     REQUIRE(head_dim == 128, "attn: head_dim %d unsupported (128 only)", head_dim);
     REQUIRE(batch >= 1 && n_kv >= 1 && n_q >= n_kv && n_q % n_kv == 0, "attn: bad head counts %d/%d", n_q, n_kv);
     REQUIRE(n_q / n_kv <= 8, "attn: GQA group %d > 8 unsupported", n_q / n_kv);
@@ -275,6 +279,22 @@ int vte_norm_gemv(const void* x, const void* norm_w, float eps, const void* w, i
                                 batch, K, N, (hipStream_t)stream);
     if (e == hipErrorNotSupported) return fail("norm_gemv: shape does not fit the fused kernel's LDS plan");
     return hip_status(e, "vte_norm_gemv launch");
+}
+
+int vte_attn_out_gemv(const float* part_m, const float* part_l, const float* part_o, const int* kv_offset, int batch,
+                      int n_q, int max_splits, int split, const void* w, int fmt, void* out, const void* residual,
+                      float residual_scale, int N, void* stream) {
+    REQUIRE(part_m && part_l && part_o && kv_offset && w && out, "attn_out_gemv: null pointer");
+    REQUIRE(fmt == 4 || fmt == 6, "attn_out_gemv: Q4_K or Q6_K");
+    REQUIRE(batch >= 1 && batch <= 4, "attn_out_gemv: batch %d outside 1..4", batch);
+    REQUIRE(n_q >= 1 && (n_q * 128) % 256 == 0 && n_q * 128 <= 8192 && N >= 1, "attn_out_gemv: bad shape");
+    REQUIRE(max_splits >= 1 && max_splits <= 64, "attn_out_gemv: max_splits %d outside 1..64", max_splits);
+    REQUIRE(split >= 1, "attn_out_gemv: split must be positive");
+    REQUIRE(aligned(part_o, 16) && aligned(w, 16), "attn_out_gemv: 16-byte alignment");
+    hipError_t e = vte::attn_out_mv(part_m, part_l, part_o, kv_offset, batch, n_q, max_splits, split, w, fmt, out,
+                                    residual, residual_scale, N, (hipStream_t)stream);
+    if (e == hipErrorNotSupported) return fail("attn_out_gemv: shape does not fit the kernel's LDS plan");
+    return hip_status(e, "vte_attn_out_gemv launch");
 }
 
 int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, void* stream) {

@@ -77,6 +77,11 @@ struct FmvPlan {
     __half* v_cache;
     int kv_batch_stride;
     int n_kv;
+    // activations from split-KV partials (log-sum-exp combine in the prologue)
+    const float* att_m;      // nullable: [M][att_nq][att_S] running maxima
+    const float* att_l;      // [M][att_nq][att_S] denominators
+    const float* att_o;      // [M][att_nq][att_S][128] unnormalised outputs
+    int att_nq, att_S, att_split;
 };
 
 __host__ __device__ __forceinline__ bool fmv_paired(int mode) {
@@ -281,6 +286,62 @@ __device__ __forceinline__ void stage_x_store(const FmvPlan& P, const XRound<F32
     }
 }
 
+// Activations = the split-KV attention output, combined here from the
+// partials: x[m][h*128 + d] = fp16(sum_s w_s o_s[d] / sum_s w_s l_s) with
+// w_s = exp(m_s - max_s m_s) over the splits of sequence m (those below its
+// length); the same terms as the separate combine kernel.  `wb` holds
+// [NC][att_nq][att_S] floats of LDS.
+#define TMV_ATT_MAX_S 64
+template <int NC>
+__device__ __forceinline__ void stage_combine(const FmvPlan& P, _Float16* xs, float* wb, const int* pos_s, int tid) {
+    const int M = P.M, nq = P.att_nq, S = P.att_S, K = P.K, ldx = xpad_len(K);
+    const int per_col = nq * S;
+    for (int i = tid; i < M * per_col; i += ROWS_THREADS) {
+        const int m = i / per_col, sidx = i - m * per_col, sp = sidx % S;
+        const int ns = (pos_s[m] + 1 + P.att_split - 1) / P.att_split;
+        wb[i] = sp < ns ? P.att_m[(size_t)m * per_col + sidx] : -INFINITY;
+    }
+    __syncthreads();
+    if (tid < M * nq) {  // per (sequence, head): normalised split weights
+        const int m = tid / nq;
+        const int ns = (pos_s[m] + 1 + P.att_split - 1) / P.att_split;
+        float* w = wb + (size_t)tid * S;
+        const float* l = P.att_l + (size_t)tid * S;
+        float mx = -INFINITY;
+        for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, w[sp]);
+        float L = 0.f;
+        for (int sp = 0; sp < ns; ++sp) {
+            const float e = __expf(w[sp] - mx);
+            w[sp] = e;
+            L = fmaf(l[sp], e, L);
+        }
+        const float inv = 1.0f / fmaxf(L, 1e-20f);
+        for (int sp = 0; sp < ns; ++sp) w[sp] *= inv;
+    }
+    __syncthreads();
+    for (int j = tid; j < M * K; j += ROWS_THREADS) {
+        const int m = j / K, e = j - m * K, h = e >> 7, d = e & 127;
+        const int ns = (pos_s[m] + 1 + P.att_split - 1) / P.att_split;
+        const float* w = wb + ((size_t)m * nq + h) * S;
+        const float* o = P.att_o + (((size_t)m * nq + h) * S) * 128 + d;
+        float acc = 0.f;
+        int sp = 0;
+        for (; sp + 8 <= ns; sp += 8) {
+            float v[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = o[(size_t)(sp + t) * 128];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc = fmaf(v[t], w[sp + t], acc);
+        }
+        for (; sp < ns; ++sp) acc = fmaf(o[(size_t)sp * 128], w[sp], acc);
+        xs[(size_t)m * ldx + xpad(e)] = (_Float16)acc;
+    }
+    for (int j = tid; j < (NC - M) * K; j += ROWS_THREADS) {  // padding columns
+        const int m = M + j / K, e = j % K;
+        xs[(size_t)m * ldx + xpad(e)] = (_Float16)0.f;
+    }
+}
+
 // 32-bit aligned load holding element i of an fp16 (f32 = false) or fp32
 // array; returns the element's bits (0 for a null array).  The load is
 // unconditional (a null array reads `dummy`), which keeps the vector-memory
@@ -308,9 +369,11 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     if (P.norm_w != nullptr) o += ((size_t)ldx * 2 + 15) & ~(size_t)15;
     float* part = reinterpret_cast<float*>(lds + o);
     const int pstride = UPT * ROWS_THREADS;
+    float* wb = part + (size_t)NC * pstride;  // combine weights (attention-output source only)
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const bool paired = fmv_paired(T.mode);
+    const bool att_src = P.att_o != nullptr;
     const int nout = paired ? T.hA : T.nr;  // outputs (per column) this block writes
     const void* dummy = P.seg[0].w;
 
@@ -318,7 +381,7 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     // last complete here): consuming them waits only for them ----
     const int pos_reg = (int)ld_elem_bits(P.kv_offset, dummy, min(tid, M - 1), true);
     XRound<F32> xr;
-    {
+    if (!att_src) {
         const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * (K / 8);
         int c0 = 0;
         for (; c0 + TMV_XR * ROWS_THREADS < nch; c0 += TMV_XR * ROWS_THREADS) {
@@ -370,9 +433,13 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     const uint32_t res = ld_elem_bits(T.residual, dummy, (size_t)em * T.n_rows + row1, f32o);
 
     // ---- 3. activations -> LDS, RMSNorm, per-16 sums ----
-    stage_x_store<NC, F32>(P, xr, xs, wn_s, tid);
+    if (!att_src) stage_x_store<NC, F32>(P, xr, xs, wn_s, tid);
     if (tid < M) pos_s[tid] = pos_reg;
     __syncthreads();
+    if (att_src) {
+        stage_combine<NC>(P, xs, wb, pos_s, tid);
+        __syncthreads();
+    }
     uint32_t cb = 0x3C00u, sbits = 0u;
     if (T.mode == FMV_ROPE_Q || T.mode == FMV_ROPE_KCACHE) {  // cos/sin need the position
         const size_t ci = (size_t)pos_s[em] * 128 + (row1 & 127);
@@ -503,12 +570,13 @@ static size_t fmv_max_lds() {
     return n;
 }
 
-static size_t fmv_lds_bytes(int NC, int K, bool has_norm, int upt) {
+static size_t fmv_lds_bytes(int NC, int K, bool has_norm, int upt, int att_rows) {
     size_t o = ((size_t)NC * xpad_len(K) * 2 + 15) & ~(size_t)15;
     o += (size_t)NC * (K / 16) * 4;
     o = (o + 15) & ~(size_t)15;
     if (has_norm) o += ((size_t)xpad_len(K) * 2 + 15) & ~(size_t)15;
     o += (size_t)NC * upt * ROWS_THREADS * 4;
+    o += (size_t)att_rows * 4;
     return o;
 }
 
@@ -586,7 +654,8 @@ hipError_t fused_mv(const void* x, FmvPlan plan, hipStream_t st) {
         if (!ok) continue;
         if (upt_force <= 0 && upt > 1 && total < 2 * fmv_num_cus()) continue;
         P.total = total;
-        const size_t lds = fmv_lds_bytes(NC, P.K, P.norm_w != nullptr, upt);
+        const size_t lds = fmv_lds_bytes(NC, P.K, P.norm_w != nullptr, upt,
+                                         P.att_o != nullptr ? P.M * P.att_nq * P.att_S : 0);
         if (lds + 64 > fmv_max_lds()) continue;
         if (P.x_f32) {
             if (NC == 1) fmv_launch<1, true>(upt, total, lds, st, x, P);
@@ -662,6 +731,27 @@ hipError_t norm_mv(const void* x, const void* norm_w, float eps, const void* w, 
     P.seg[0] = seg(w, nullptr, out, bias, residual, fmt, N, out_f32 ? FMV_STORE_F32 : FMV_STORE_F16);
     P.nseg = 1;
     return fused_mv(x, P, st);
+}
+
+// y = W · combine(split-KV partials) + residual for batch 1..4 (fp16 output):
+// the attention output projection with the log-sum-exp combine in its
+// prologue.  hipErrorNotSupported when there are more than TMV_ATT_MAX_S splits.
+hipError_t attn_out_mv(const float* part_m, const float* part_l, const float* part_o, const int* kv_offset, int M,
+                       int n_q, int max_splits, int split, const void* w, int fmt, void* out, const void* residual,
+                       float rs, int N, hipStream_t st) {
+    if (max_splits > TMV_ATT_MAX_S || split < 1) return hipErrorNotSupported;
+    FmvPlan P = plan_base(M, n_q * 128, nullptr, 0.f);
+    P.rs = rs;
+    P.kv_offset = kv_offset;
+    P.att_m = part_m;
+    P.att_l = part_l;
+    P.att_o = part_o;
+    P.att_nq = n_q;
+    P.att_S = max_splits;
+    P.att_split = split;
+    P.seg[0] = seg(w, nullptr, out, nullptr, residual, fmt, N, FMV_STORE_F16);
+    P.nseg = 1;
+    return fused_mv(part_o, P, st);
 }
 
 // Plain y = (W x + bias) * rs + residual for batch 1..4 (no norm); x fp32 or

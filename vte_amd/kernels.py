@@ -44,6 +44,7 @@ SIGNATURES = {
                     _i, _i, _i, _i, _i, _vp],
     "vte_ffn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp],
     "vte_norm_gemv": [_vp, _vp, _f, _vp, _i, _vp, _i, _vp, _vp, _f, _i, _i, _i, _vp],
+    "vte_attn_out_gemv": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _f, _i, _vp],
     "vte_last_error": [],
 }
 RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll, "vte_topk_scratch_bytes": _ll}
@@ -167,6 +168,13 @@ class VTEKernels:
         self._check(self.lib.vte_norm_gemv(_p(x), _p(norm_w), eps, _p(w), FMT[fmt], _p(out), DT[out_dtype], _p(bias),
                                            _p(residual), residual_scale, batch, K, N, self._st(stream)),
                     "vte_norm_gemv")
+
+    def attn_out_gemv(self, part_m, part_l, part_o, kv_offset, batch, n_q, max_splits, split, w, fmt, out, N,
+                      residual=None, residual_scale=1.0, stream=None):
+        """o-proj GEMV whose activations are the LSE combine of split-KV partials (batch <= 4)."""
+        self._check(self.lib.vte_attn_out_gemv(_p(part_m), _p(part_l), _p(part_o), _p(kv_offset), batch, n_q,
+                                               max_splits, split, _p(w), FMT[fmt], _p(out), _p(residual),
+                                               residual_scale, N, self._st(stream)), "vte_attn_out_gemv")
 
     def fill_normal_f16(self, dst, n, seed, scale=1.0, stream=None):
         self._check(self.lib.vte_fill_normal_f16(_p(dst), n, seed, scale, self._st(stream)), "vte_fill_normal_f16")
