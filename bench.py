@@ -236,10 +236,12 @@ def cpu_baseline(seconds_budget=20.0):
                       f"(dequant cached), {n} trials, per-layer time x28 + LM head"}
 
 
-def profile_step(B, steps, prefix=2048):
+def profile_step(B, steps, prefix=2048, classes=None):
     """Kernel-trace / counter workload: one plain device-to-device copy of
     256 MiB (reads and writes exactly 256 MiB: the scale of FETCH_SIZE and
-    WRITE_SIZE), then ``steps`` replays of the batch-B decode-step graph."""
+    WRITE_SIZE), then ``steps`` replays of the batch-B decode-step graph, or
+    of a graph of only the launch classes ``classes`` (the same graph that
+    ``time_classes`` times)."""
     from vte_amd.bridge import DeviceArray, HIPRuntime
     from vte_amd.core.hip_graph_executor import HIPGraphExecutor
     from vte_amd.core.model_config import QWEN25_1P5B
@@ -258,13 +260,21 @@ def profile_step(B, steps, prefix=2048):
     ex = HIPGraphExecutor(hip, SyntheticQwen2(QWEN25_1P5B, seed=0), batch_size=B, max_seq=prefix + 256)
     ex.fill_kv_prefix(seed=B)
     ex._update_staging_buffers([1] * B, [prefix] * B)
-    ex.build_decode_graph()
+    if classes:
+        g, ge = ex.capture_classes(classes)
+        replay = lambda: hip.graph_launch(ge)
+    else:
+        ex.build_decode_graph()
+        replay = lambda: ex.replay(1)
     for i in range(steps):
-        ex.replay(1)
+        replay()
         if i % 10 == 0:
             hip.synchronize()
             print(f"profile-step: batch {B}, step {i}/{steps}", flush=True)
     hip.synchronize()
+    if classes:
+        hip.graph_exec_destroy(ge)
+        hip.graph_destroy(g)
     ex.close()
     hip.cleanup()
 
@@ -279,13 +289,16 @@ def main():
     ap.add_argument("--profile-step", type=int, default=0, metavar="B",
                     help="profiling run only: a 256 MiB calibration copy, then --steps replays of the batch-B "
                          "step graph (for rocprofv3 kernel traces and counters)")
+    ap.add_argument("--profile-classes", default="", metavar="C1,C2",
+                    help="with --profile-step: replay only these launch classes (e.g. attn_in,ffn_in,lm_head)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only (no multi-GPU path is built); "
                                    "--gpus must be 1"}))
         sys.exit(2)
     if args.profile_step:
-        profile_step(args.profile_step, args.steps)
+        profile_step(args.profile_step, args.steps,
+                     classes=[c for c in args.profile_classes.split(",") if c] or None)
         return
 
     from vte_amd.bridge import HIPRuntime

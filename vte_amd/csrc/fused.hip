@@ -225,9 +225,9 @@ struct XRound {
 };
 
 template <int NC, bool F32>
-__device__ __forceinline__ void stage_x_load(const FmvPlan& P, const void* __restrict__ x, int c0, XRound<F32>& r,
-                                             int tid) {
-    const int per_col = P.K / 8;
+__device__ __forceinline__ void stage_x_load(const FmvPlan& P, const void* __restrict__ x, int K, int c0,
+                                             XRound<F32>& r, int tid) {
+    const int per_col = K / 8;
     const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * per_col;
     const uint4* xv = reinterpret_cast<const uint4*>(x);
     const uint4* nv = reinterpret_cast<const uint4*>(P.norm_w != nullptr ? (const void*)P.norm_w : x);
@@ -249,10 +249,10 @@ __device__ __forceinline__ void stage_x_load(const FmvPlan& P, const void* __res
 }
 
 template <int NC, bool F32>
-__device__ __forceinline__ void stage_x_store(const FmvPlan& P, const XRound<F32>& r, _Float16* xs, _Float16* wn_s,
-                                              int tid) {
-    const int ldx = xpad_len(P.K);
-    const int per_col = P.K / 8;
+__device__ __forceinline__ void stage_x_store(const FmvPlan& P, int K, const XRound<F32>& r, _Float16* xs,
+                                              _Float16* wn_s, int tid) {
+    const int ldx = xpad_len(K);
+    const int per_col = K / 8;
     const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * per_col;
 #pragma unroll
     for (int j = 0; j < TMV_XR; ++j) {
@@ -354,10 +354,10 @@ __device__ __forceinline__ uint32_t ld_elem_bits(const void* a, const void* dumm
     return a != nullptr ? v : 0u;
 }
 
-template <int NC, bool F32, int UPT, int FMT>
+template <int NC, bool F32, int UPT, int FMT, int KC>
 __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPlan& P, const TileGeo& T,
                                          uint8_t* lds, float (*red)[NC], int* pos_s) {
-    const int K = P.K, M = P.M;
+    const int K = KC > 0 ? KC : P.K, M = NC == 1 ? 1 : P.M;
     const int n_sb = K / QK_K, per_row = n_sb * 4, ldx = xpad_len(K);
     // LDS: x [NC][ldx] fp16 | s16 [NC][K/16] | norm weights [ldx] (with a norm) | part [NC][UPT * 256]
     _Float16* xs = reinterpret_cast<_Float16*>(lds);
@@ -385,10 +385,10 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
         const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * (K / 8);
         int c0 = 0;
         for (; c0 + TMV_XR * ROWS_THREADS < nch; c0 += TMV_XR * ROWS_THREADS) {
-            stage_x_load<NC, F32>(P, x, c0, xr, tid);
-            stage_x_store<NC, F32>(P, xr, xs, wn_s, tid);
+            stage_x_load<NC, F32>(P, x, K, c0, xr, tid);
+            stage_x_store<NC, F32>(P, K, xr, xs, wn_s, tid);
         }
-        stage_x_load<NC, F32>(P, x, c0, xr, tid);
+        stage_x_load<NC, F32>(P, x, K, c0, xr, tid);
     }
 
     // ---- 1. this thread's UPT work units: weights straight into registers ----
@@ -425,7 +425,9 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     // no output) ----
     const bool eth = tid < M * nout;  // M * nout <= 256 (checked on the host)
     const int tt = eth ? tid : 0;
-    const int em = tt / nout, er = tt - em * nout;
+    // tt / nout for tt < 256, nout <= 256: the float quotient is exact enough
+    const int em = NC == 1 ? 0 : (int)(((float)tt + 0.5f) * (1.0f / (float)nout));
+    const int er = tt - em * nout;
     const int row1 = T.j0 + er;
     const bool f32o = T.mode == FMV_STORE_F32;
     const uint32_t b1 = ld_elem_bits(T.bias, dummy, row1, f32o);
@@ -433,7 +435,7 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     const uint32_t res = ld_elem_bits(T.residual, dummy, (size_t)em * T.n_rows + row1, f32o);
 
     // ---- 3. activations -> LDS, RMSNorm, per-16 sums ----
-    if (!att_src) stage_x_store<NC, F32>(P, xr, xs, wn_s, tid);
+    if (!att_src) stage_x_store<NC, F32>(P, K, xr, xs, wn_s, tid);
     if (tid < M) pos_s[tid] = pos_reg;
     __syncthreads();
     if (att_src) {
@@ -545,15 +547,17 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     }
 }
 
-template <int NC, bool F32, int UPT>
+// KC: the activation length K when fixed at compile time (0: P.K), so the
+// staging, norm and row-sum loops have constant trip counts and no divisions.
+template <int NC, bool F32, int UPT, int KC>
 __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const void* __restrict__ x, FmvPlan P) {
     extern __shared__ uint4 smem_fmv[];
     __shared__ float red[4][NC];
     __shared__ int pos_s[NC];
     const TileGeo T = tile_geo(P, blockIdx.x);
     uint8_t* lds = reinterpret_cast<uint8_t*>(smem_fmv);
-    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4>(x, P, T, lds, red, pos_s);
-    else tmv_body<NC, F32, UPT, 6>(x, P, T, lds, red, pos_s);
+    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4, KC>(x, P, T, lds, red, pos_s);
+    else tmv_body<NC, F32, UPT, 6, KC>(x, P, T, lds, red, pos_s);
 }
 
 namespace vte {
@@ -596,12 +600,21 @@ static int fmv_rows_per_tile(int mode, int K, int upt) {
     return std::min(R, TMV_MAX_R);
 }
 
+template <int NC, bool F32, int KC>
+static void fmv_launch_k(int upt, int total, size_t lds, hipStream_t st, const void* x, const FmvPlan& plan) {
+    const dim3 g(total), b(ROWS_THREADS);
+    if (upt == 4) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4, KC>), g, b, lds, st, x, plan);
+    else if (upt == 2) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 2, KC>), g, b, lds, st, x, plan);
+    else hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 1, KC>), g, b, lds, st, x, plan);
+}
+
+// Compile-time K for the fp16-activation shapes of the 1.5B decode step
+// (hidden 1536, FFN 8960); any other K takes the runtime-K kernels.
 template <int NC, bool F32>
 static void fmv_launch(int upt, int total, size_t lds, hipStream_t st, const void* x, const FmvPlan& plan) {
-    const dim3 g(total), b(ROWS_THREADS);
-    if (upt == 4) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4>), g, b, lds, st, x, plan);
-    else if (upt == 2) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 2>), g, b, lds, st, x, plan);
-    else hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 1>), g, b, lds, st, x, plan);
+    if (!F32 && plan.K == 1536) fmv_launch_k<NC, F32, F32 ? 0 : 1536>(upt, total, lds, st, x, plan);
+    else if (!F32 && plan.K == 8960) fmv_launch_k<NC, F32, F32 ? 0 : 8960>(upt, total, lds, st, x, plan);
+    else fmv_launch_k<NC, F32, 0>(upt, total, lds, st, x, plan);
 }
 
 static int fmv_num_cus() {

@@ -1,7 +1,7 @@
 """Summarise rocprofv3 CSV output of ``bench.py --profile-step`` into the text
 kept under profiles/.
 
-    python -m vte_amd.profile_summary stats   <kernel_stats.csv>  <out.md> "<command>"
+    python -m vte_amd.profile_summary stats   <kernel_stats.csv>  <out.md> "<command>" [<kernel substring>]
     python -m vte_amd.profile_summary traffic <fetch counter_collection.csv> <write counter_collection.csv>
                                               <kernel substring> <out.json> <out.md> "<commands>"
 
@@ -25,13 +25,19 @@ def _rows(path):
         return list(csv.DictReader(f))
 
 
-def stats(path, out_md, command):
+def stats(path, out_md, command, kernel=None):
     rows = _rows(path)
     lines = ["# Kernel trace summary", "", f"Command: `{command}`", "",
              "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
     for r in rows:
         lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                      f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    if kernel:
+        sel = [r for r in rows if kernel in r["Name"]]
+        n = sum(int(r["Calls"]) for r in sel)
+        tot = sum(float(r["TotalDurationNs"]) for r in sel)
+        lines += ["", f"All `{kernel}*` dispatches ({len(sel)} instantiations): {n} calls, "
+                  f"average {tot / max(n, 1) / 1e3:.3f} us per launch."]
     with open(out_md, "w") as f:
         f.write("\n".join(lines) + "\n")
 
@@ -68,14 +74,19 @@ def traffic(fetch_csv, write_csv, kernel, out_json, out_md, commands):
         w = sum(wv[name]) / max(len(wv[name]), 1) * w_scale * 1024
         res["per_kernel"][name] = {"dispatches": len(fv[name]), "fetch_bytes": f, "write_bytes": w}
         lines.append(f"| `{name[:100]}` | {len(fv[name])} | {f / 1e6:.3f} | {w / 1e6:.3f} |")
+    # every instantiation whose name contains ``kernel``, weighted by dispatches
     sel = [k for k in res["per_kernel"] if kernel in k]
     if not sel:
         raise SystemExit(f"kernel {kernel!r} not in the counter output")
-    k = sel[0]
-    res["hbm_bytes_per_launch"] = int(res["per_kernel"][k]["fetch_bytes"] + res["per_kernel"][k]["write_bytes"])
-    lines += ["", f"`{k}`: {res['hbm_bytes_per_launch'] / 1e6:.3f} MB of HBM traffic per launch (fetch + write)."]
+    n = sum(res["per_kernel"][k]["dispatches"] for k in sel)
+    tot = sum((res["per_kernel"][k]["fetch_bytes"] + res["per_kernel"][k]["write_bytes"])
+              * res["per_kernel"][k]["dispatches"] for k in sel)
+    res["hbm_bytes_per_launch"] = int(tot / max(n, 1))
+    lines += ["", f"`{kernel}*` ({len(sel)} instantiations, {n} dispatches): "
+              f"{res['hbm_bytes_per_launch'] / 1e6:.3f} MB of HBM traffic per launch (fetch + write)."]
     with open(out_json, "w") as f:
-        json.dump({"kernel": k, "hbm_bytes_per_launch": res["hbm_bytes_per_launch"],
+        json.dump({"kernel": kernel, "instantiations": sel, "dispatches": n,
+                   "hbm_bytes_per_launch": res["hbm_bytes_per_launch"],
                    "fetch_scale": f_scale, "write_scale": w_scale}, f, indent=1)
     with open(out_md, "w") as f:
         f.write("\n".join(lines) + "\n")
@@ -83,7 +94,7 @@ def traffic(fetch_csv, write_csv, kernel, out_json, out_md, commands):
 
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
-        stats(sys.argv[2], sys.argv[3], sys.argv[4])
+        stats(sys.argv[2], sys.argv[3], sys.argv[4], sys.argv[5] if len(sys.argv) > 5 else None)
     elif sys.argv[1] == "traffic":
         traffic(*sys.argv[2:8])
     else:
