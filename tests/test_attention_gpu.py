@@ -186,3 +186,42 @@ def test_attn_out_gemv_combines_partials(hip, K, B, fmt):
         att = attention_ref(q[b], kc[b], vc[b], int(offs[b]) + 1, SCALE).reshape(-1).astype(np.float16)
         ref = W @ att.astype(np.float64) + res[b].astype(np.float64)
         assert rel_l2(got[b], ref) <= 2e-3, b   # fp16 attention output and fp16 result
+
+
+@pytest.mark.parametrize("max_seq,ctx,split", [(2304, 2049, 128), (2304, 100, 128), (1000, 999, 128),
+                                               (4096, 3000, 256)])
+def test_rows_past_length_and_stale_scratch_are_ignored(hip, K, max_seq, ctx, split):
+    """Cache rows at or past the length and the split scratch hold NaN; neither
+    reaches the output.  (max_seq a multiple of split: the partial kernel reads
+    its first tile before the length arrives; 1000/128: the length-first path.)"""
+    rng = np.random.default_rng(ctx)
+    q, kc, vc = _inputs(rng, 1, max_seq)
+    ref = attention_ref(q[0], kc[0], vc[0], ctx, SCALE)
+    kc[:, ctx:] = np.float16(np.nan)
+    vc[:, ctx:] = np.float16(np.nan)
+    max_splits = (max_seq + split - 1) // split
+    nan_scratch = lambda shape: up(hip, np.full(shape, np.nan, np.float32))
+    part_m = nan_scratch((1, NQ, max_splits))
+    part_l = nan_scratch((1, NQ, max_splits))
+    part_o = nan_scratch((1, NQ, max_splits, D))
+    out = empty(hip, (1, NQ, D), np.float32)
+    K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), part_m, part_l, part_o, out, 1, NQ, NKV, D, SCALE,
+                    up(hip, np.asarray([ctx - 1], np.int32)), max_seq * NKV * D, split, max_splits, dtype="f32",
+                    stream=hip.stream)
+    got = down(out)
+    assert np.isfinite(got).all()
+    assert rel_l2(got[0], ref) <= TOL
+
+
+def test_single_sequence_with_zero_batch_stride(hip, K):
+    """kv_batch_stride 0 (one sequence): no read-ahead, same result."""
+    rng = np.random.default_rng(77)
+    q, kc, vc = _inputs(rng, 1, 1024)
+    a = _run(hip, K, q, kc, vc, [700], 128)
+    max_splits = 8
+    pm, pl = empty(hip, (1, NQ, max_splits), np.float32), empty(hip, (1, NQ, max_splits), np.float32)
+    po = empty(hip, (1, NQ, max_splits, D), np.float32)
+    out = empty(hip, (1, NQ, D), np.float32)
+    K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), pm, pl, po, out, 1, NQ, NKV, D, SCALE,
+                    up(hip, np.asarray([700], np.int32)), 0, 128, max_splits, dtype="f32", stream=hip.stream)
+    assert np.array_equal(down(out).view(np.uint32), a.view(np.uint32))

@@ -36,6 +36,16 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 #define ATT_MAX_SPLITS 4096  // splits per sequence the separate combine handles
 #define ATT_VT_STRIDE 36     // halves per row of the transposed V tile (32 tokens + pad)
 
+#ifdef ATT_TRACE
+__device__ unsigned long long att_trace[4096][8];
+__device__ unsigned long long comb_trace[4096][2];
+#define CMB_TS(k) do { if (threadIdx.x == 0) { const int bi = blockIdx.x + gridDim.x * blockIdx.y; if (bi < 4096) comb_trace[bi][k] = wall_clock64(); } } while (0)
+#define ATT_TS(k) do { if (threadIdx.x == 0) { const int bi = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); if (bi < 4096) att_trace[bi][k] = wall_clock64(); } } while (0)
+#else
+#define ATT_TS(k) do { } while (0)
+#define CMB_TS(k) do { } while (0)
+#endif
+
 // ---------------------------------------------------------------------------
 // KV append (reference ABI, vte/compiler/templates/rdna/kv_cache_append.hip.template:13-39)
 // grid (batch, n_kv), block (head_dim)
@@ -57,7 +67,37 @@ extern "C" __global__ void kv_cache_append_kernel(const __half* __restrict__ k, 
 // ---------------------------------------------------------------------------
 // Native partial pass
 // ---------------------------------------------------------------------------
-template <typename TQ, typename TO>
+// One wave's 32-token tile: K rows (MFMA A operands, two 16-token halves) and
+// V rows (two fp16 per lane: d = 2 lane, 2 lane + 1).  Rows past `rmax` read
+// row `rmax` instead (results for them are masked).
+struct AttTile {
+    half8_t ka[2][ATT_D / 32];
+    uint32_t vv[ATT_TILE];
+};
+
+__device__ __forceinline__ void att_load_tile(AttTile& T, const __half* kb, const __half* vb, size_t row_stride,
+                                              int t0, int rmax, int col, int grp, int lane) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int tok = min(t0 + 16 * tt + col, rmax);
+        const __half* kr = kb + (size_t)tok * row_stride;
+#pragma unroll
+        for (int s = 0; s < ATT_D / 32; ++s) T.ka[tt][s] = *reinterpret_cast<const half8_t*>(kr + 32 * s + 8 * grp);
+    }
+#pragma unroll
+    for (int t = 0; t < ATT_TILE; ++t) {
+        const int tok = min(t0 + t, rmax);
+        T.vv[t] = *reinterpret_cast<const uint32_t*>(vb + (size_t)tok * row_stride + 2 * lane);
+    }
+}
+
+// Partials of one split of one (sequence, KV head): grid (max_splits, n_kv, B),
+// four waves, each taking 32-token tiles.  SPEC: the first tile's K/V rows
+// are requested before the sequence length is known (rows up to the split's
+// end, which the host checked lie inside the sequence's cache), so the
+// length and the first tile arrive in one memory round trip; rows at or past
+// the length are masked (scores -inf, V zero).
+template <typename TQ, typename TO, bool SPEC>
 __global__ __launch_bounds__(256) void attn_partial_gqa(
     const TQ* __restrict__ q,            // [B][n_q][D]
     const __half* __restrict__ k_cache, const __half* __restrict__ v_cache,
@@ -65,28 +105,19 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
     int n_q, int n_kv, float scale, const int* __restrict__ kv_offset, int kv_batch_stride,
     int split, int max_splits, int* __restrict__ counters, TO* __restrict__ out) {
     const int sp = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int len = kv_offset[b] + 1;
+    ATT_TS(0);
     const int t_begin = sp * split;
-    if (t_begin >= len) return;  // past this sequence's last split
-    const int t_end = min(t_begin + split, len);
     const int G = n_q / n_kv;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15;   // head (MFMA N index) / token row (A operand)
     const int grp = lane >> 4;   // 0..3
-
-    // V tile of a wave, transposed: vt[d][t] (fp16, rows of 36 halves so the
-    // 8-byte reads of 16 consecutive d rows hit distinct LDS banks)
-    // Phases use disjoint LDS lifetimes: the V^T tiles (tile loop), the
-    // per-wave O rows (block combine) and the split weights (LSE combine).
-    union AttnLDS {
-        uint32_t vt[ATT_WAVES][ATT_D][ATT_VT_STRIDE / 2];
-        float o[ATT_WAVES][ATT_MAXG][ATT_D + 4];
-        float w[ATT_MAXG][ATT_MAX_COMBINE];
-    };
-    __shared__ AttnLDS lds;
-    __shared__ float m_sh[ATT_WAVES][16], l_sh[ATT_WAVES][16];
-    auto& vt_sh = lds.vt;
-    auto& o_sh = lds.o;
+    const size_t row_stride = (size_t)n_kv * ATT_D;  // elements between consecutive positions
+    const __half* kb = k_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
+    const __half* vb = v_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
+    const int len_raw = kv_offset[b];
+    AttTile T;
+    int t0 = t_begin + wv * ATT_TILE;
+    if (SPEC) att_load_tile(T, kb, vb, row_stride, t0, t_begin + split - 1, col, grp, lane);
 
     // B operand: Q^T for this KV head's G query heads, fp16, zero-padded to 16.
     half8_t qb[ATT_D / 32];
@@ -103,9 +134,23 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
         }
     }
 
-    const size_t row_stride = (size_t)n_kv * ATT_D;  // elements between consecutive positions
-    const __half* kb = k_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
-    const __half* vb = v_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
+    const int len = len_raw + 1;
+    if (t_begin >= len) return;  // past this sequence's last split
+    const int t_end = min(t_begin + split, len);
+
+    // V tile of a wave, transposed: vt[d][t] (fp16, rows of 36 halves so the
+    // 8-byte reads of 16 consecutive d rows hit distinct LDS banks)
+    // Phases use disjoint LDS lifetimes: the V^T tiles (tile loop), the
+    // per-wave O rows (block combine) and the split weights (LSE combine).
+    union AttnLDS {
+        uint32_t vt[ATT_WAVES][ATT_D][ATT_VT_STRIDE / 2];
+        float o[ATT_WAVES][ATT_MAXG][ATT_D + 4];
+        float w[ATT_MAXG][ATT_MAX_COMBINE];
+    };
+    __shared__ AttnLDS lds;
+    __shared__ float m_sh[ATT_WAVES][16], l_sh[ATT_WAVES][16];
+    auto& vt_sh = lds.vt;
+    auto& o_sh = lds.o;
 
     float m_run = -1e30f;  // running max of head `col` (identical across grp)
     float l_run = 0.f;     // per-lane partial denominator of head `col`
@@ -114,23 +159,14 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
 #pragma unroll
     for (int dt = 0; dt < ATT_D / 16; ++dt) o_acc[dt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int t0 = t_begin + wv * ATT_TILE; t0 < t_end; t0 += ATT_WAVES * ATT_TILE) {
-        // ---- all loads of the tile at once: K rows (MFMA A operands) and V rows ----
-        half8_t ka[2][ATT_D / 32];
+    if (!SPEC) att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
+    for (; t0 < t_end; t0 += ATT_WAVES * ATT_TILE) {
+        if (t0 != t_begin + wv * ATT_TILE) att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
+        ATT_TS(1);
+        // rows at or past the end contribute p = 0; zero their V so that
+        // whatever the rows hold cannot turn 0 * V into NaN
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int tok = t0 + 16 * tt + col;
-            const __half* kr = kb + (size_t)(tok < t_end ? tok : t_begin) * row_stride;
-#pragma unroll
-            for (int s = 0; s < ATT_D / 32; ++s) ka[tt][s] = *reinterpret_cast<const half8_t*>(kr + 32 * s + 8 * grp);
-        }
-        uint32_t vv[ATT_TILE];  // V[t0 + t][2*lane .. 2*lane+1]; rows past the end are
-                                // loaded from t_begin and weighted by p = 0
-#pragma unroll
-        for (int t = 0; t < ATT_TILE; ++t) {
-            const int tok = (t0 + t < t_end) ? t0 + t : t_begin;
-            vv[t] = *reinterpret_cast<const uint32_t*>(vb + (size_t)tok * row_stride + 2 * lane);
-        }
+        for (int t = 0; t < ATT_TILE; ++t) T.vv[t] = (t0 + t < t_end) ? T.vv[t] : 0u;
         // ---- scores for 32 tokens: two 16x16 S^T tiles ----
         floatx4_t acc[2];
 #pragma unroll
@@ -138,14 +174,14 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
             acc[tt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < ATT_D / 32; ++s)
-                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[tt][s], qb[s], acc[tt], 0, 0, 0);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.ka[tt][s], qb[s], acc[tt], 0, 0, 0);
         }
         // ---- V^T into LDS: dword (V[t][d], V[t+1][d]) at vt[d][t/2] ----
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int t = 0; t < ATT_TILE; t += 2) {
-            vt_sh[wv][2 * lane][t / 2] = __builtin_amdgcn_perm(vv[t + 1], vv[t], 0x05040100u);
-            vt_sh[wv][2 * lane + 1][t / 2] = __builtin_amdgcn_perm(vv[t + 1], vv[t], 0x07060302u);
+            vt_sh[wv][2 * lane][t / 2] = __builtin_amdgcn_perm(T.vv[t + 1], T.vv[t], 0x05040100u);
+            vt_sh[wv][2 * lane + 1][t / 2] = __builtin_amdgcn_perm(T.vv[t + 1], T.vv[t], 0x07060302u);
         }
         // lane holds S^T[token = t0 + 16*tt + 4*grp + i][head = col]
         float sc[2][4];
@@ -204,6 +240,7 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
         __builtin_amdgcn_wave_barrier();
     }
 
+    ATT_TS(2);
     // ---- combine the four waves of this block ----
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
@@ -235,6 +272,7 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
         part_o[st * ATT_D + d] = O;
         if (d == 0) { part_m[st] = M; part_l[st] = L; }
     }
+    ATT_TS(3);
     if (counters == nullptr) return;  // separate combine launch
 
     // ---- last block of this (sequence, KV head) performs the LSE combine ----
@@ -326,6 +364,7 @@ __global__ __launch_bounds__(128) void attn_combine(const float* __restrict__ pa
     __shared__ float w_sh[ATT_MAX_SPLITS];
     __shared__ float red[2][2];
     const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x, lane = d & 63, wv = d >> 6;
+    CMB_TS(0);
     const int len = kv_offset[b] + 1;
     const int ns = (len + split - 1) / split;
     const size_t base = ((size_t)b * n_q + qh) * max_splits;
@@ -361,6 +400,7 @@ __global__ __launch_bounds__(128) void attn_combine(const float* __restrict__ pa
     }
     for (; c < ns; ++c) O = fmaf(po[(size_t)c * ATT_D], w_sh[c], O);
     st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(L, 1e-20f));
+    CMB_TS(1);
 }
 
 // ---------------------------------------------------------------------------
@@ -436,6 +476,44 @@ extern "C" __global__ __launch_bounds__(256) void flash_attention_split_kv_reduc
     if (tid < head_dim) output[((size_t)b * num_q_heads + qh) * head_dim + tid] = __float2half(O / fmaxf(L, 1e-20f));
 }
 
+// LSE combine for max_splits <= 64 in one memory round trip: every load
+// (length, split statistics, partial outputs of all max_splits splits) is
+// issued before any result is needed; splits at or past the sequence's
+// split count are masked by selects, so stale scratch cannot leak in.  Each
+// wave reduces the split statistics on its own (lane c holds split c), so
+// there is no barrier.  grid (n_q, B), block 128 (one thread per dim).
+template <typename TO, int NSMAX>
+__global__ __launch_bounds__(128) void attn_combine_small(const float* __restrict__ part_m,
+                                                          const float* __restrict__ part_l,
+                                                          const float* __restrict__ part_o, TO* __restrict__ out,
+                                                          int n_q, const int* __restrict__ kv_offset, int split,
+                                                          int max_splits) {
+    const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x, lane = d & 63;
+    CMB_TS(0);
+    const size_t base = ((size_t)b * n_q + qh) * max_splits;
+    const int len_raw = kv_offset[b];
+    const int cl = min(lane, max_splits - 1);
+    const float m_l = part_m[base + cl];
+    const float l_l = part_l[base + cl];
+    const float* po = part_o + base * ATT_D + d;
+    float o[NSMAX];
+#pragma unroll
+    for (int c = 0; c < NSMAX; ++c) o[c] = po[(size_t)min(c, max_splits - 1) * ATT_D];
+    const int ns = (len_raw + 1 + split - 1) / split;
+    const float m = lane < ns ? m_l : -INFINITY;
+    const float M = wave_max(m);
+    const float w = lane < ns ? __expf(m - M) : 0.f;
+    const float L = wave_sum(lane < ns ? l_l * w : 0.f);
+    float O = 0.f;
+#pragma unroll
+    for (int c = 0; c < NSMAX; ++c) {
+        const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c));
+        O = c < ns ? fmaf(o[c], wc, O) : O;
+    }
+    st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(L, 1e-20f));
+    CMB_TS(1);
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
@@ -446,14 +524,33 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
                          float* part_o, void* out, int B, int n_q, int n_kv, float scale, const int* kv_offset,
                          int kv_batch_stride, int split, int max_splits, int* counters, hipStream_t st) {
     dim3 g1(max_splits, n_kv, B), b1(256);
-    hipLaunchKernelGGL((attn_partial_gqa<TQ, TO>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,
-                       (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset,
-                       kv_batch_stride, split, max_splits, counters, (TO*)out);
+    // positions every split may read ahead of knowing the length: all of
+    // max_splits * split must lie inside one sequence's kv_batch_stride
+    const long long rows_cap = kv_batch_stride / ((long long)n_kv * ATT_D);
+    const bool spec = (long long)max_splits * split <= rows_cap;
+    if (spec)
+        hipLaunchKernelGGL((attn_partial_gqa<TQ, TO, true>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,
+                           (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset,
+                           kv_batch_stride, split, max_splits, counters, (TO*)out);
+    else
+        hipLaunchKernelGGL((attn_partial_gqa<TQ, TO, false>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,
+                           (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset,
+                           kv_batch_stride, split, max_splits, counters, (TO*)out);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || counters != nullptr || out == nullptr) return e;  // out == nullptr: partials only
     dim3 g2(n_q, B), b2(ATT_D);
-    hipLaunchKernelGGL((attn_combine<TO>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q, kv_offset, split,
-                       max_splits);
+    if (max_splits <= 16)
+        hipLaunchKernelGGL((attn_combine_small<TO, 16>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q,
+                           kv_offset, split, max_splits);
+    else if (max_splits <= 32)
+        hipLaunchKernelGGL((attn_combine_small<TO, 32>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q,
+                           kv_offset, split, max_splits);
+    else if (max_splits <= 64)
+        hipLaunchKernelGGL((attn_combine_small<TO, 64>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q,
+                           kv_offset, split, max_splits);
+    else
+        hipLaunchKernelGGL((attn_combine<TO>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q, kv_offset,
+                           split, max_splits);
     return hipGetLastError();
 }
 
@@ -473,3 +570,12 @@ hipError_t kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
 }
 
 }  // namespace vte
+
+#ifdef ATT_TRACE
+extern "C" int vte_dbg_comb_trace_read(void* host, int blocks) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(comb_trace), (size_t)blocks * 16, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int vte_dbg_att_trace_read(void* host, int blocks) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(att_trace), (size_t)blocks * 64, 0, hipMemcpyDeviceToHost);
+}
+#endif

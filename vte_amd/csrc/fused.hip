@@ -35,7 +35,13 @@
 
 #define TMV_MAX_SEG 3
 #define TMV_MAX_R 64
-#define TMV_XR 4  // activation chunks per thread per staging round
+
+#ifdef TMV_TRACE
+__device__ unsigned long long tmv_trace[8192][8];
+#define TMV_TS(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) tmv_trace[blockIdx.x][k] = wall_clock64(); } while (0)
+#else
+#define TMV_TS(k) do { } while (0)
+#endif
 
 enum FmvMode : int {
     FMV_STORE_F16 = 0,   // out[m][row] = fp16((acc + bias) * rs + residual)
@@ -213,79 +219,6 @@ __device__ __forceinline__ float row_sum(const float* p, int per_row) {
     return a + b;
 }
 
-// Activations (and RMSNorm weights) -> LDS in rounds of TMV_XR 16-byte
-// chunks per thread; a round's loads are unconditional (chunks past the end
-// re-read chunk 0), so they overlap each other.  All rounds but the last are
-// completed here; the last round's chunks are returned in `v` and stored by
-// stage_x_finish, so the caller can issue other loads in between.
-template <bool F32>
-struct XRound {
-    uint4 v[TMV_XR][F32 ? 2 : 1];
-    int c0;
-};
-
-template <int NC, bool F32>
-__device__ __forceinline__ void stage_x_load(const FmvPlan& P, const void* __restrict__ x, int K, int c0,
-                                             XRound<F32>& r, int tid) {
-    const int per_col = K / 8;
-    const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * per_col;
-    const uint4* xv = reinterpret_cast<const uint4*>(x);
-    const uint4* nv = reinterpret_cast<const uint4*>(P.norm_w != nullptr ? (const void*)P.norm_w : x);
-    r.c0 = c0;
-#pragma unroll
-    for (int j = 0; j < TMV_XR; ++j) {
-        const int c = c0 + j * ROWS_THREADS + tid;
-        const int m = c / per_col;
-        const bool xcol = c < nch && m < P.M;
-        const bool ncol = c < nch && m == NC;
-        if (F32) {
-            const uint4* p = xv + 2 * (size_t)(xcol ? c : 0);
-            r.v[j][0] = ncol ? nv[c - NC * per_col] : p[0];
-            r.v[j][1] = p[1];
-        } else {
-            r.v[j][0] = ncol ? nv[c - NC * per_col] : xv[xcol ? c : 0];
-        }
-    }
-}
-
-template <int NC, bool F32>
-__device__ __forceinline__ void stage_x_store(const FmvPlan& P, int K, const XRound<F32>& r, _Float16* xs,
-                                              _Float16* wn_s, int tid) {
-    const int ldx = xpad_len(K);
-    const int per_col = K / 8;
-    const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * per_col;
-#pragma unroll
-    for (int j = 0; j < TMV_XR; ++j) {
-        const int c = r.c0 + j * ROWS_THREADS + tid;
-        const int m = c / per_col, e = (c - m * per_col) * 8;
-        if (c < nch) {
-            if (m == NC) {
-                *reinterpret_cast<uint4*>(wn_s + xpad(e)) = r.v[j][0];
-            } else {
-                uint4 ov = make_uint4(0, 0, 0, 0);
-                if (m < P.M) {
-                    if (F32) {
-                        const uint32_t w[8] = {r.v[j][0].x, r.v[j][0].y, r.v[j][0].z, r.v[j][0].w,
-                                               r.v[j][1].x, r.v[j][1].y, r.v[j][1].z, r.v[j][1].w};
-                        uint32_t hh[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const _Float16 lo = (_Float16)__uint_as_float(w[2 * i]);
-                            const _Float16 hi = (_Float16)__uint_as_float(w[2 * i + 1]);
-                            hh[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-                        }
-                        ov = make_uint4(hh[0], hh[1], hh[2], hh[3]);
-                    } else {
-                        ov = r.v[j][0];
-                    }
-                }
-                *reinterpret_cast<uint4*>(xs + (size_t)m * ldx + xpad(e)) = ov;
-            }
-        }
-    }
-}
-
 // Activations = the split-KV attention output, combined here from the
 // partials: x[m][h*128 + d] = fp16(sum_s w_s o_s[d] / sum_s w_s l_s) with
 // w_s = exp(m_s - max_s m_s) over the splits of sequence m (those below its
@@ -354,142 +287,204 @@ __device__ __forceinline__ uint32_t ld_elem_bits(const void* a, const void* dumm
     return a != nullptr ? v : 0u;
 }
 
-template <int NC, bool F32, int UPT, int FMT, int KC>
-__device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPlan& P, const TileGeo& T,
-                                         uint8_t* lds, float (*red)[NC], int* pos_s) {
-    const int K = KC > 0 ? KC : P.K, M = NC == 1 ? 1 : P.M;
-    const int n_sb = K / QK_K, per_row = n_sb * 4, ldx = xpad_len(K);
-    // LDS: x [NC][ldx] fp16 | s16 [NC][K/16] | norm weights [ldx] (with a norm) | part [NC][UPT * 256]
-    _Float16* xs = reinterpret_cast<_Float16*>(lds);
-    size_t o = ((size_t)NC * ldx * 2 + 15) & ~(size_t)15;
-    float* s16 = reinterpret_cast<float*>(lds + o);
-    o += (size_t)NC * (K / 16) * 4;
-    o = (o + 15) & ~(size_t)15;
-    _Float16* wn_s = reinterpret_cast<_Float16*>(lds + o);
-    if (P.norm_w != nullptr) o += ((size_t)ldx * 2 + 15) & ~(size_t)15;
-    float* part = reinterpret_cast<float*>(lds + o);
-    const int pstride = UPT * ROWS_THREADS;
-    float* wb = part + (size_t)NC * pstride;  // combine weights (attention-output source only)
-
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const bool paired = fmv_paired(T.mode);
-    const bool att_src = P.att_o != nullptr;
-    const int nout = paired ? T.hA : T.nr;  // outputs (per column) this block writes
-    const void* dummy = P.seg[0].w;
-
-    // ---- 0. kv offsets and activations first (all staging rounds but the
-    // last complete here): consuming them waits only for them ----
-    const int pos_reg = (int)ld_elem_bits(P.kv_offset, dummy, min(tid, M - 1), true);
-    XRound<F32> xr;
-    if (!att_src) {
-        const int nch = (NC + (P.norm_w != nullptr ? 1 : 0)) * (K / 8);
-        int c0 = 0;
-        for (; c0 + TMV_XR * ROWS_THREADS < nch; c0 += TMV_XR * ROWS_THREADS) {
-            stage_x_load<NC, F32>(P, x, K, c0, xr, tid);
-            stage_x_store<NC, F32>(P, K, xr, xs, wn_s, tid);
-        }
-        stage_x_load<NC, F32>(P, x, K, c0, xr, tid);
+// Sum of the 8 fp16 values of a 16-byte chunk, in fp32.
+__device__ __forceinline__ float chunk_sum(const uint32_t (&h)[4]) {
+    float a = rdot2(h[0], 0x3C003C00u, 0.f);
+    a = rdot2(h[1], 0x3C003C00u, a);
+    a = rdot2(h[2], 0x3C003C00u, a);
+    return rdot2(h[3], 0x3C003C00u, a);
+}
+// Sum of squares of the 8 fp16 values of a chunk, in fp32.
+__device__ __forceinline__ float chunk_sumsq(const uint32_t (&h)[4]) {
+    float a = rdot2(h[0], h[0], 0.f);
+    a = rdot2(h[1], h[1], a);
+    a = rdot2(h[2], h[2], a);
+    return rdot2(h[3], h[3], a);
+}
+// value of the lane with the neighbouring index (lane ^ 1)
+__device__ __forceinline__ float lane_pair(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+// Chunk (8 fp16, as 4 words) -> fp16(x * inv * w) with w the matching norm weights.
+__device__ __forceinline__ void chunk_norm(uint32_t (&h)[4], const uint4& w, float inv) {
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const _Float16 lo = (_Float16)(h2f_bits(h[i]) * inv * h2f_bits(ww[i]));
+        const _Float16 hi = (_Float16)(h2f_bits(h[i] >> 16) * inv * h2f_bits(ww[i] >> 16));
+        h[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
     }
+}
 
-    // ---- 1. this thread's UPT work units: weights straight into registers ----
-    const int units = T.nr * per_row;
+// Activation chunks of one staging round: chunk c = c0 + 256 j + tid holds
+// x[c / per_col][8 (c % per_col) ..] (columns >= M read as zero) as fp16 words.
+template <bool F32, int XR>
+struct XChunks {
+    uint32_t h[XR][4];
+    uint4 w[XR];  // matching norm weights (with a norm)
+};
+
+template <int NC, bool F32, int XR>
+__device__ __forceinline__ void xr_load(const FmvPlan& P, const void* __restrict__ x, int K, int c0, bool norm,
+                                        XChunks<F32, XR>& r, int tid) {
+    const int per_col = K / 8;
+    const int M = NC == 1 ? 1 : P.M;
+    const uint4* nv = reinterpret_cast<const uint4*>(norm ? (const void*)P.norm_w : x);
+    uint4 raw[XR][F32 ? 2 : 1];
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c = c0 + j * ROWS_THREADS + tid;
+        const int m = NC == 1 ? 0 : c / per_col;
+        const bool ok = c < NC * per_col && m < M;
+        const int cc = ok ? c : 0;
+        if (c0 + j * ROWS_THREADS >= NC * per_col) {  // uniform: no lane of this slot has a chunk
+            raw[j][0] = raw[j][F32 ? 1 : 0] = r.w[j] = make_uint4(0, 0, 0, 0);
+            continue;
+        }
+        if (F32) {
+            const uint4* p = reinterpret_cast<const uint4*>(x) + 2 * (size_t)cc;
+            raw[j][0] = p[0];
+            raw[j][1] = p[1];
+        } else {
+            raw[j][0] = reinterpret_cast<const uint4*>(x)[cc];
+        }
+        if (norm) r.w[j] = nv[ok ? c - m * per_col : 0];
+    }
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c = c0 + j * ROWS_THREADS + tid;
+        const int m = NC == 1 ? 0 : c / per_col;
+        const bool ok = c < NC * per_col && m < M;
+        if (F32) {
+            const uint32_t w[8] = {raw[j][0].x, raw[j][0].y, raw[j][0].z, raw[j][0].w,
+                                   raw[j][1].x, raw[j][1].y, raw[j][1].z, raw[j][1].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 lo = (_Float16)__uint_as_float(w[2 * i]);
+                const _Float16 hi = (_Float16)__uint_as_float(w[2 * i + 1]);
+                r.h[j][i] = ok ? ((uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                                  ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16)) : 0u;
+            }
+        } else {
+            r.h[j][0] = ok ? raw[j][0].x : 0u;
+            r.h[j][1] = ok ? raw[j][0].y : 0u;
+            r.h[j][2] = ok ? raw[j][0].z : 0u;
+            r.h[j][3] = ok ? raw[j][0].w : 0u;
+        }
+    }
+}
+
+// Store a round's chunks (fp16) to the padded LDS layout and, when `sums`,
+// their per-16 sums (chunks c and c ^ 1 sit in lanes tid and tid ^ 1).
+template <int NC, bool F32, int XR>
+__device__ __forceinline__ void xr_store(int K, int c0, const XChunks<F32, XR>& r, _Float16* xs, float* s16,
+                                         bool sums, int tid) {
+    const int per_col = K / 8, ldx = xpad_len(K);
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c = c0 + j * ROWS_THREADS + tid;
+        const int m = NC == 1 ? 0 : c / per_col;
+        const int cl = c - m * per_col;
+        float s = 0.f;
+        if (sums) {
+            s = chunk_sum(r.h[j]);
+            s += lane_pair(s);
+        }
+        if (c < NC * per_col) {
+            *reinterpret_cast<uint4*>(xs + (size_t)m * ldx + xpad(8 * cl)) =
+                make_uint4(r.h[j][0], r.h[j][1], r.h[j][2], r.h[j][3]);
+            if (sums && (cl & 1) == 0) s16[m * (K / 16) + (cl >> 1)] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-tile pieces of the kernel: weight loads, epilogue operands, unit dots,
+// epilogue; and the block prologue (activation staging)
+// ---------------------------------------------------------------------------
+
+// This thread's UPT work units of a tile, loaded straight into registers.
+template <int UPT>
+struct TileW {
     uint4 w0[UPT], w1[UPT], w2[UPT];
     uint2 sc8[UPT];
     uint32_t dbits[UPT];
     int usb[UPT];
+};
+
+template <int UPT, int FMT>
+__device__ __forceinline__ void tile_w_issue(TileW<UPT>& W, const TileGeo& T, int n_sb, int per_row, int tid) {
+    const int units = T.nr * per_row;
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
         const int u = min(tid + i * ROWS_THREADS, units - 1);  // past the end: re-read the last unit
         const int sbg = u >> 2, q = u & 3;
         const int lr = (int)(((float)sbg + 0.5f) * (1.0f / (float)n_sb));
         const int sb = sbg - lr * n_sb;
-        usb[i] = sb;
+        W.usb[i] = sb;
         const uint8_t* rowp = lr < T.hA ? T.bA + (size_t)lr * T.rb : T.bB + (size_t)(lr - T.hA) * T.rb;
         if (FMT == 4) {
             const uint8_t* blk = rowp + sb * Q4K_BYTES;
-            w0[i] = ldg_stream16(blk);
-            w1[i] = ldg_stream16(blk + 16 + 32 * q);
-            w2[i] = ldg_stream16(blk + 32 + 32 * q);
+            W.w0[i] = ldg_stream16(blk);
+            W.w1[i] = ldg_stream16(blk + 16 + 32 * q);
+            W.w2[i] = ldg_stream16(blk + 32 + 32 * q);
         } else {
             const uint8_t* blk = rowp + sb * Q6K_BYTES;
             const int h = q >> 1, l16 = (q & 1) * 16;
-            w0[i] = ldg_u16b(blk + 64 * h + l16);
-            w1[i] = ldg_u16b(blk + 64 * h + 32 + l16);
-            w2[i] = ldg_u16b(blk + 128 + 32 * h + l16);
-            __builtin_memcpy(&sc8[i], blk + 192 + 8 * h, 8);
-            dbits[i] = ldg_b16(blk + 208, 0);
+            W.w0[i] = ldg_u16b(blk + 64 * h + l16);
+            W.w1[i] = ldg_u16b(blk + 64 * h + 32 + l16);
+            W.w2[i] = ldg_u16b(blk + 128 + 32 * h + l16);
+            __builtin_memcpy(&W.sc8[i], blk + 192 + 8 * h, 8);
+            W.dbits[i] = ldg_b16(blk + 208, 0);
         }
     }
+}
 
-    // ---- 2. epilogue operands (unconditional loads; ignored by threads with
-    // no output) ----
-    const bool eth = tid < M * nout;  // M * nout <= 256 (checked on the host)
-    const int tt = eth ? tid : 0;
+// Epilogue operands of this thread's output (column em, row row1) of a tile.
+struct TileE {
+    int em, row1;
+    bool eth;
+    uint32_t b1, b2, res, cb, sbits;
+};
+
+// Output slot and bias / residual (unconditional loads: read as 0 when absent).
+template <int NC>
+__device__ __forceinline__ void tile_e_issue(TileE& E, const FmvPlan& P, const TileGeo& T, int M, const void* dummy,
+                                             int tid) {
+    const bool paired = fmv_paired(T.mode);
+    const int nout = paired ? T.hA : T.nr;  // outputs (per column) of the tile
+    E.eth = tid < M * nout;                 // M * nout <= 256 (checked on the host)
+    const int tt = E.eth ? tid : 0;
     // tt / nout for tt < 256, nout <= 256: the float quotient is exact enough
-    const int em = NC == 1 ? 0 : (int)(((float)tt + 0.5f) * (1.0f / (float)nout));
-    const int er = tt - em * nout;
-    const int row1 = T.j0 + er;
+    E.em = NC == 1 ? 0 : (int)(((float)tt + 0.5f) * (1.0f / (float)nout));
+    E.row1 = T.j0 + (tt - E.em * nout);
     const bool f32o = T.mode == FMV_STORE_F32;
-    const uint32_t b1 = ld_elem_bits(T.bias, dummy, row1, f32o);
-    const uint32_t b2 = ld_elem_bits(paired ? T.bias : nullptr, dummy, row1 + 64, false);
-    const uint32_t res = ld_elem_bits(T.residual, dummy, (size_t)em * T.n_rows + row1, f32o);
+    E.b1 = ld_elem_bits(T.bias, dummy, E.row1, f32o);
+    E.b2 = ld_elem_bits(paired ? T.bias : nullptr, dummy, E.row1 + 64, false);
+    E.res = ld_elem_bits(T.residual, dummy, (size_t)E.em * T.n_rows + E.row1, f32o);
+}
 
-    // ---- 3. activations -> LDS, RMSNorm, per-16 sums ----
-    if (!att_src) stage_x_store<NC, F32>(P, K, xr, xs, wn_s, tid);
-    if (tid < M) pos_s[tid] = pos_reg;
-    __syncthreads();
-    if (att_src) {
-        stage_combine<NC>(P, xs, wb, pos_s, tid);
-        __syncthreads();
-    }
-    uint32_t cb = 0x3C00u, sbits = 0u;
-    if (T.mode == FMV_ROPE_Q || T.mode == FMV_ROPE_KCACHE) {  // cos/sin need the position
-        const size_t ci = (size_t)pos_s[em] * 128 + (row1 & 127);
-        cb = ldg_b16(P.rope_cos, ci);
-        sbits = ldg_b16(P.rope_sin, ci);
-    }
-    if (P.norm_w != nullptr) {
-        float ss[NC];
-#pragma unroll
-        for (int m = 0; m < NC; ++m) ss[m] = 0.f;
-        for (int i = tid; i < K; i += ROWS_THREADS) {
-#pragma unroll
-            for (int m = 0; m < NC; ++m) {
-                const float v = (float)xs[m * ldx + xpad(i)];
-                ss[m] = fmaf(v, v, ss[m]);
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < NC; ++m) {
-            ss[m] = wave_sum(ss[m]);
-            if (lane == 0) red[wv][m] = ss[m];
-        }
-        __syncthreads();
-        float inv[NC];
-#pragma unroll
-        for (int m = 0; m < NC; ++m)
-            inv[m] = rsqrtf((red[0][m] + red[1][m] + red[2][m] + red[3][m]) / (float)K + P.eps);
-        for (int i = tid; i < K; i += ROWS_THREADS) {
-            const float wn = (float)wn_s[xpad(i)];
-#pragma unroll
-            for (int m = 0; m < NC; ++m) {
-                _Float16& xv = xs[m * ldx + xpad(i)];
-                xv = (_Float16)((float)xv * inv[m] * wn);
-            }
-        }
-        __syncthreads();
-    }
-    act_sums<NC>(ActLDS{xs, s16}, K);
-    __syncthreads();
+// cos/sin of the output's position (read as 0 when the mode has no rotation).
+__device__ __forceinline__ void tile_e_rope(TileE& E, const FmvPlan& P, const TileGeo& T, int pos,
+                                            const void* dummy) {
+    const bool rope = T.mode == FMV_ROPE_Q || T.mode == FMV_ROPE_KCACHE;
+    const size_t ci = rope ? (size_t)pos * 128 + (E.row1 & 127) : 0;
+    E.cb = ld_elem_bits(rope ? (const void*)P.rope_cos : nullptr, dummy, ci, false);
+    E.sbits = ld_elem_bits(rope ? (const void*)P.rope_sin : nullptr, dummy, ci, false);
+}
 
-    // ---- 4. the units' partials for every column ----
+// The units' partials for every column -> part[m * pstride + unit].
+template <int NC, int UPT, int FMT>
+__device__ __forceinline__ void tile_dot(const TileW<UPT>& W, int units, int K, const _Float16* xs, const float* s16,
+                                         float* part, int pstride, int tid) {
+    const int ldx = xpad_len(K);
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
         const int u = tid + i * ROWS_THREADS;
         if (u < units) {
-            const int q = u & 3, sb = usb[i];
+            const int q = u & 3, sb = W.usb[i];
             if (FMT == 4) {
-                const Q4KUnitData d{w0[i], w1[i], w2[i]};
+                const Q4KUnitData d{W.w0[i], W.w1[i], W.w2[i]};
 #pragma unroll
                 for (int m = 0; m < NC; ++m)
                     part[m * pstride + u] = q4k_unit_dot(d, q, xs + (size_t)m * ldx + xpad(sb * QK_K + 64 * q),
@@ -498,25 +493,32 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
                 const int h = q >> 1, l16 = (q & 1) * 16;
 #pragma unroll
                 for (int m = 0; m < NC; ++m)
-                    part[m * pstride + u] = q6k_unit_dot_r(w0[i], w1[i], w2[i], sc8[i], dbits[i], l16,
+                    part[m * pstride + u] = q6k_unit_dot_r(W.w0[i], W.w1[i], W.w2[i], W.sc8[i], W.dbits[i], l16,
                                                            xs + (size_t)m * ldx + xpad(sb * QK_K),
                                                            s16 + m * (K / 16) + sb * 16, h);
             }
         }
     }
-    __syncthreads();
+}
 
-    // ---- 5. epilogue: one output (column em, row er) per thread ----
-    if (!eth) return;
-    if (!paired) {
+// One output per thread (threads with E.eth): row sums of the partials and
+// the mode's epilogue.
+template <int NC>
+__device__ __forceinline__ void tile_epilogue(const FmvPlan& P, const TileGeo& T, const TileE& E, const float* part,
+                                              int pstride, int per_row, const int* pos_s) {
+    if (!E.eth) return;
+    const int em = E.em, row1 = E.row1;
+    const int er = row1 - T.j0;
+    const bool f32o = T.mode == FMV_STORE_F32;
+    if (!fmv_paired(T.mode)) {
         float v = row_sum(part + em * pstride + er * per_row, per_row) +
-                  (f32o ? __uint_as_float(b1) : h2f_bits(b1));
+                  (f32o ? __uint_as_float(E.b1) : h2f_bits(E.b1));
         if (T.mode == FMV_VCACHE) {
             P.v_cache[(size_t)em * P.kv_batch_stride + ((size_t)pos_s[em] * P.n_kv + row1 / 128) * 128 +
                       (row1 % 128)] = __float2half(v);
             return;
         }
-        v = v * P.rs + (f32o ? __uint_as_float(res) : h2f_bits(res));
+        v = v * P.rs + (f32o ? __uint_as_float(E.res) : h2f_bits(E.res));
         const size_t oi = (size_t)em * T.n_rows + row1;
         if (f32o) reinterpret_cast<float*>(T.out)[oi] = v;
         else reinterpret_cast<__half*>(T.out)[oi] = __float2half(v);
@@ -531,9 +533,9 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
         reinterpret_cast<__half*>(T.out)[(size_t)em * T.n_rows + row1] = __float2half(gg * sig * uu);
         return;
     }
-    const float x1 = __half2float(__float2half(a + h2f_bits(b1)));
-    const float x2 = __half2float(__float2half(bv + h2f_bits(b2)));
-    const float c = h2f_bits(cb), sn = h2f_bits(sbits);
+    const float x1 = __half2float(__float2half(a + h2f_bits(E.b1)));
+    const float x2 = __half2float(__float2half(bv + h2f_bits(E.b2)));
+    const float c = h2f_bits(E.cb), sn = h2f_bits(E.sbits);
     const __half o1 = __float2half(x1 * c - x2 * sn), o2 = __float2half(x1 * sn + x2 * c);
     if (T.mode == FMV_ROPE_Q) {
         __half* qo = reinterpret_cast<__half*>(T.out) + (size_t)em * T.n_rows;
@@ -545,6 +547,163 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
         kc[d] = o1;
         kc[d + 64] = o2;
     }
+}
+
+// LDS layout of a block: x [NC][ldx] fp16 | s16 [NC][K/16] | part [NC][UPT * 256]
+// | combine weights (attention-output source only).
+struct FmvLDS {
+    _Float16* xs;
+    float* s16;
+    float* part;
+};
+
+__device__ __forceinline__ FmvLDS fmv_lds(uint8_t* lds, int NC, int K, int UPT) {
+    FmvLDS L;
+    L.xs = reinterpret_cast<_Float16*>(lds);
+    size_t o = ((size_t)NC * xpad_len(K) * 2 + 15) & ~(size_t)15;
+    L.s16 = reinterpret_cast<float*>(lds + o);
+    o += (size_t)NC * (K / 16) * 4;
+    o = (o + 15) & ~(size_t)15;
+    L.part = reinterpret_cast<float*>(lds + o);
+    return L;
+}
+
+// Block prologue: kv offsets -> pos_s, activations (RMSNorm-ed when the plan
+// has a norm, or combined from split-KV partials) and their per-16 sums into
+// LDS.  The activations are requested first; `issue()` runs right after the
+// first barrier (the activations are in), so the caller's weight loads do not
+// queue ahead of them; the normalisation then runs while those are in flight.
+// Ends with a barrier.
+template <int NC, bool F32, int KC, typename IssueFn>
+__device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const FmvPlan& P, const FmvLDS& L,
+                                             float* wb, float (*red)[NC], int* pos_s, IssueFn issue) {
+    const int K = KC > 0 ? KC : P.K, M = NC == 1 ? 1 : P.M;
+    const int ldx = xpad_len(K);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const bool att_src = P.att_o != nullptr;
+    const bool norm = P.norm_w != nullptr;
+    const void* dummy = P.seg[0].w;
+    const int pos_reg = (int)ld_elem_bits(P.kv_offset, dummy, min(tid, M - 1), true);
+
+    constexpr int XR = F32 ? 4 : 8;
+    const int nchx = NC * (K / 8);
+    const bool one_round = nchx <= XR * ROWS_THREADS;
+    XChunks<F32, XR> xr;
+    float ss[NC];
+#pragma unroll
+    for (int m = 0; m < NC; ++m) ss[m] = 0.f;
+    if (!att_src) {
+        for (int c0 = 0; c0 < nchx; c0 += XR * ROWS_THREADS) {
+            xr_load<NC, F32, XR>(P, x, K, c0, norm, xr, tid);
+            if (norm) {
+#pragma unroll
+                for (int j = 0; j < XR; ++j) {
+                    const int c = c0 + j * ROWS_THREADS + tid;
+                    const int m = NC == 1 ? 0 : c / (K / 8);
+                    const float q = chunk_sumsq(xr.h[j]);
+#pragma unroll
+                    for (int mm = 0; mm < NC; ++mm) ss[mm] += (m == mm) ? q : 0.f;
+                }
+                // one round: the chunks stay in registers until the scale is known
+                if (!one_round) xr_store<NC, F32, XR>(K, c0, xr, L.xs, L.s16, false, tid);
+            } else {
+                xr_store<NC, F32, XR>(K, c0, xr, L.xs, L.s16, true, tid);
+            }
+        }
+        if (norm) {
+#pragma unroll
+            for (int m = 0; m < NC; ++m) {
+                ss[m] = wave_sum(ss[m]);
+                if (lane == 0) red[wv][m] = ss[m];
+            }
+        }
+    }
+    if (tid < M) pos_s[tid] = pos_reg;
+    __syncthreads();
+    TMV_TS(1);
+    issue();
+
+    if (att_src) {
+        stage_combine<NC>(P, L.xs, wb, pos_s, tid);
+        __syncthreads();
+        act_sums<NC>(ActLDS{L.xs, L.s16}, K);
+    } else if (norm) {
+        float inv[NC];
+#pragma unroll
+        for (int m = 0; m < NC; ++m)
+            inv[m] = rsqrtf((red[0][m] + red[1][m] + red[2][m] + red[3][m]) / (float)K + P.eps);
+        if (one_round) {
+#pragma unroll
+            for (int j = 0; j < XR; ++j) {
+                const int c = j * ROWS_THREADS + tid;
+                const int m = NC == 1 ? 0 : c / (K / 8);
+                float iv = inv[0];
+#pragma unroll
+                for (int mm = 1; mm < NC; ++mm) iv = (m == mm) ? inv[mm] : iv;
+                chunk_norm(xr.h[j], xr.w[j], iv);
+            }
+            xr_store<NC, F32, XR>(K, 0, xr, L.xs, L.s16, true, tid);
+        } else {  // raw chunks are in LDS: scale them there
+            const int per_col = K / 8;
+            const uint4* nv = reinterpret_cast<const uint4*>(P.norm_w);
+            for (int c = tid; c - tid < nchx; c += ROWS_THREADS) {
+                const bool ok = c < nchx;
+                const int m = ok ? c / per_col : 0, cl = ok ? c - m * per_col : 0;
+                float iv = inv[0];
+#pragma unroll
+                for (int mm = 1; mm < NC; ++mm) iv = (m == mm) ? inv[mm] : iv;
+                uint4* px = reinterpret_cast<uint4*>(L.xs + (size_t)m * ldx + xpad(8 * cl));
+                const uint4 v = *px;
+                uint32_t h[4] = {v.x, v.y, v.z, v.w};
+                chunk_norm(h, nv[cl], iv);
+                float s = chunk_sum(h);
+                s += lane_pair(s);
+                if (ok) {
+                    *px = make_uint4(h[0], h[1], h[2], h[3]);
+                    if ((cl & 1) == 0) L.s16[m * (K / 16) + (cl >> 1)] = s;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    TMV_TS(2);
+}
+
+// One tile per block (grid = tiles): everything a block reads is requested
+// up front, so a block costs about one memory latency plus its arithmetic.
+template <int NC, bool F32, int UPT, int FMT, int KC>
+__device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPlan& P, const TileGeo& T,
+                                         uint8_t* lds, float (*red)[NC], int* pos_s) {
+    const int K = KC > 0 ? KC : P.K, M = NC == 1 ? 1 : P.M;
+    const int n_sb = K / QK_K, per_row = n_sb * 4;
+    const FmvLDS L = fmv_lds(lds, NC, K, UPT);
+    const int pstride = UPT * ROWS_THREADS;
+    float* wb = L.part + (size_t)NC * pstride;
+    const int tid = threadIdx.x;
+    TMV_TS(0);
+    const void* dummy = P.seg[0].w;
+    TileE E;
+    tile_e_issue<NC>(E, P, T, M, dummy, tid);
+    const int pos_e = (int)ld_elem_bits(P.kv_offset, dummy, E.em, true);
+    TileW<UPT> W;
+    fmv_prologue<NC, F32, KC>(x, P, L, wb, red, pos_s, [&]() {
+        tile_w_issue<UPT, FMT>(W, T, n_sb, per_row, tid);
+        tile_e_rope(E, P, T, pos_e, dummy);
+    });
+    tile_dot<NC, UPT, FMT>(W, T.nr * per_row, K, L.xs, L.s16, L.part, pstride, tid);
+    __syncthreads();
+    TMV_TS(3);
+#ifdef TMV_TRACE
+    if (tid == 0 && blockIdx.x < 8192) {
+        unsigned hw;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        tmv_trace[blockIdx.x][5] = ((unsigned long long)xcc << 32) | hw;
+        tmv_trace[blockIdx.x][4] = wall_clock64();
+    }
+#endif
+    tile_epilogue<NC>(P, T, E, L.part, pstride, per_row, pos_s);
 }
 
 // KC: the activation length K when fixed at compile time (0: P.K), so the
@@ -574,11 +733,10 @@ static size_t fmv_max_lds() {
     return n;
 }
 
-static size_t fmv_lds_bytes(int NC, int K, bool has_norm, int upt, int att_rows) {
+static size_t fmv_lds_bytes(int NC, int K, int upt, int att_rows) {
     size_t o = ((size_t)NC * xpad_len(K) * 2 + 15) & ~(size_t)15;
     o += (size_t)NC * (K / 16) * 4;
     o = (o + 15) & ~(size_t)15;
-    if (has_norm) o += ((size_t)xpad_len(K) * 2 + 15) & ~(size_t)15;
     o += (size_t)NC * upt * ROWS_THREADS * 4;
     o += (size_t)att_rows * 4;
     return o;
@@ -617,6 +775,11 @@ static void fmv_launch(int upt, int total, size_t lds, hipStream_t st, const voi
     else fmv_launch_k<NC, F32, 0>(upt, total, lds, st, x, plan);
 }
 
+static int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
 static int fmv_num_cus() {
     static int n = 0;
     if (n == 0) {
@@ -625,6 +788,34 @@ static int fmv_num_cus() {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     }
     return n;
+}
+
+// Fills in a plan's per-segment geometry for `upt` units per thread.
+// Returns hipSuccess, hipErrorNotSupported (the shape does not fit this upt)
+// or hipErrorInvalidValue.
+static hipError_t fmv_complete(const FmvPlan& plan, int upt, FmvPlan& P) {
+    const int n_sb = plan.K / QK_K;
+    P = plan;
+    int total = 0;
+    for (int s = 0; s < P.nseg; ++s) {
+        FmvSeg& S = P.seg[s];
+        if (S.fmt != 4 && S.fmt != 6) return hipErrorInvalidValue;
+        if (fmv_paired(S.mode) && S.fmt != 4) return hipErrorInvalidValue;
+        S.row_bytes = n_sb * (S.fmt == 4 ? Q4K_BYTES : Q6K_BYTES);
+        S.R = fmv_rows_per_tile(S.mode, P.K, upt);
+        if (S.R <= 0 || P.M * S.R > ROWS_THREADS) return hipErrorNotSupported;
+        if (S.mode == FMV_SWIGLU) {
+            S.tiles = (S.n_rows + S.R / 2 - 1) / (S.R / 2);
+        } else if (S.mode == FMV_ROPE_Q || S.mode == FMV_ROPE_KCACHE) {
+            if (S.n_rows % 128 != 0) return hipErrorInvalidValue;
+            S.tiles = S.n_rows / S.R;
+        } else {
+            S.tiles = (S.n_rows + S.R - 1) / S.R;
+        }
+        total += S.tiles;
+    }
+    P.total = total;
+    return hipSuccess;
 }
 
 // Completes the plan (units per thread, rows per tile, tile counts) and
@@ -636,48 +827,26 @@ hipError_t fused_mv(const void* x, FmvPlan plan, hipStream_t st) {
     if ((reinterpret_cast<uintptr_t>(x) & 15) || (plan.K % QK_K) != 0) return hipErrorInvalidValue;
     if (plan.norm_w != nullptr && (reinterpret_cast<uintptr_t>(plan.norm_w) & 15)) return hipErrorInvalidValue;
     const int NC = plan.M <= 1 ? 1 : (plan.M <= 2 ? 2 : 4);
-    const int n_sb = plan.K / QK_K;
+    const int att_rows = plan.att_o != nullptr ? plan.M * plan.att_nq * plan.att_S : 0;
     static int upt_force = -1;  // VTE_FMV_UPT=1|2|4 pins units per thread (tuning)
-    if (upt_force < 0) {
-        const char* e = getenv("VTE_FMV_UPT");
-        upt_force = e ? atoi(e) : 0;
-    }
+    if (upt_force < 0) upt_force = env_int("VTE_FMV_UPT", 0);
     for (int upt : {4, 2, 1}) {
         if (upt_force > 0 && upt != upt_force) continue;
-        FmvPlan P = plan;
-        int total = 0;
-        bool ok = true;
-        for (int s = 0; s < P.nseg && ok; ++s) {
-            FmvSeg& S = P.seg[s];
-            if (S.fmt != 4 && S.fmt != 6) return hipErrorInvalidValue;
-            if (fmv_paired(S.mode) && S.fmt != 4) return hipErrorInvalidValue;
-            S.row_bytes = n_sb * (S.fmt == 4 ? Q4K_BYTES : Q6K_BYTES);
-            S.R = fmv_rows_per_tile(S.mode, P.K, upt);
-            if (S.R <= 0 || P.M * S.R > ROWS_THREADS) { ok = false; break; }
-            if (S.mode == FMV_SWIGLU) {
-                S.tiles = (S.n_rows + S.R / 2 - 1) / (S.R / 2);
-            } else if (S.mode == FMV_ROPE_Q || S.mode == FMV_ROPE_KCACHE) {
-                if (S.n_rows % 128 != 0) return hipErrorInvalidValue;
-                S.tiles = S.n_rows / S.R;
-            } else {
-                S.tiles = (S.n_rows + S.R - 1) / S.R;
-            }
-            total += S.tiles;
-        }
-        if (!ok) continue;
-        if (upt_force <= 0 && upt > 1 && total < 2 * fmv_num_cus()) continue;
-        P.total = total;
-        const size_t lds = fmv_lds_bytes(NC, P.K, P.norm_w != nullptr, upt,
-                                         P.att_o != nullptr ? P.M * P.att_nq * P.att_S : 0);
+        FmvPlan P;
+        const hipError_t e = fmv_complete(plan, upt, P);
+        if (e == hipErrorInvalidValue) return e;
+        if (e != hipSuccess) continue;
+        if (upt_force <= 0 && upt > 1 && P.total < 2 * fmv_num_cus()) continue;
+        const size_t lds = fmv_lds_bytes(NC, P.K, upt, att_rows);
         if (lds + 64 > fmv_max_lds()) continue;
         if (P.x_f32) {
-            if (NC == 1) fmv_launch<1, true>(upt, total, lds, st, x, P);
-            else if (NC == 2) fmv_launch<2, true>(upt, total, lds, st, x, P);
-            else fmv_launch<4, true>(upt, total, lds, st, x, P);
+            if (NC == 1) fmv_launch<1, true>(upt, P.total, lds, st, x, P);
+            else if (NC == 2) fmv_launch<2, true>(upt, P.total, lds, st, x, P);
+            else fmv_launch<4, true>(upt, P.total, lds, st, x, P);
         } else {
-            if (NC == 1) fmv_launch<1, false>(upt, total, lds, st, x, P);
-            else if (NC == 2) fmv_launch<2, false>(upt, total, lds, st, x, P);
-            else fmv_launch<4, false>(upt, total, lds, st, x, P);
+            if (NC == 1) fmv_launch<1, false>(upt, P.total, lds, st, x, P);
+            else if (NC == 2) fmv_launch<2, false>(upt, P.total, lds, st, x, P);
+            else fmv_launch<4, false>(upt, P.total, lds, st, x, P);
         }
         return hipGetLastError();
     }
@@ -783,3 +952,9 @@ hipError_t stream_mv(int fmt, bool in_f32, bool out_f32, const void* x, const vo
 }
 
 }  // namespace vte
+
+#ifdef TMV_TRACE
+extern "C" int vte_dbg_trace_read(void* host, int blocks) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(tmv_trace), (size_t)blocks * 64, 0, hipMemcpyDeviceToHost);
+}
+#endif
