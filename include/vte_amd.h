@@ -179,14 +179,6 @@ int vte_attn_out_gemv(const float* part_m, const float* part_l, const float* par
                       int n_q, int max_splits, int split, const void* w, int fmt, void* out, const void* residual,
                       float residual_scale, int N, void* stream);
 
-/* Cache warming: reads one dword of every 64-byte line of n <= 8 device
- * ranges (ptrs[i], bytes[i]) with `blocks` 256-thread blocks and writes
- * nothing, so that kernels issued later find those bytes in the device-side
- * caches.  Used inside the decode graph to pull the next weights in while
- * latency-bound kernels run.  No reference counterpart (an MI355X
- * scheduling aid: the reference streams every weight from memory on demand). */
-int vte_prefetch(int n, const void* const* ptrs, const long long* bytes, int blocks, void* stream);
-
 /* dst[i] = fp16(scale * N(0,1)) from a counter-based generator (synthetic KV
  * prefixes); no reference counterpart (test and benchmark input). */
 int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, void* stream);

@@ -41,7 +41,6 @@ size_t topk_scratch_bytes(int rows);
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
                 hipStream_t st);
 hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, hipStream_t st);
-hipError_t prefetch(int n, const void* const* ptrs, const long long* bytes, int blocks, hipStream_t st);
 hipError_t attn_in(const void* x, const void* norm_w, float eps, const void* wq, const void* q_bias, int fmt_q,
                    const void* wk, const void* k_bias, int fmt_k, const void* wv, const void* v_bias, int fmt_v,
                    void* q_out, void* k_cache, void* v_cache, const int* kv_offset, int kv_batch_stride,
@@ -301,13 +300,6 @@ int vte_attn_out_gemv(const float* part_m, const float* part_l, const float* par
 int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, void* stream) {
     REQUIRE(dst && n >= 1 && n / 256 < (1LL << 31), "fill_normal_f16: bad arguments");
     return hip_status(vte::fill_normal_f16(dst, n, seed, scale, (hipStream_t)stream), "vte_fill_normal_f16 launch");
-}
-
-int vte_prefetch(int n, const void* const* ptrs, const long long* bytes, int blocks, void* stream) {
-    REQUIRE(n >= 0 && n <= 8 && blocks >= 1 && blocks <= 65536 && (n == 0 || (ptrs && bytes)),
-            "prefetch: need 0..8 ranges and 1..65536 blocks");
-    for (int i = 0; i < n; ++i) REQUIRE(ptrs[i] && bytes[i] >= 0, "prefetch: null range or negative size");
-    return hip_status(vte::prefetch(n, ptrs, bytes, blocks, (hipStream_t)stream), "vte_prefetch launch");
 }
 
 }  // extern "C"

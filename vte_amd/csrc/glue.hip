@@ -8,8 +8,6 @@
 //   add_kernel                   vte/compiler/templates/rdna/add.hip.template:4-17
 //   embedding_lookup_q6k_kernel  vte/compiler/templates/rdna/embedding_lookup_q6k.hip.template:17-58
 // plus a top-k selector over fp32 logits for on-device sampling candidates.
-#include <cstring>
-
 #include "vte_common.h"
 
 // ---------------------------------------------------------------------------
@@ -425,57 +423,9 @@ __global__ __launch_bounds__(256) void fill_normal_f16_kernel(__half* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Cache warming: touch one dword of every 64-byte line of up to 8 ranges, so
-// a later kernel's reads of them hit the device-side caches (L2 and the
-// memory-attached last-level cache) instead of HBM.  The loaded values are
-// folded into one word that is stored only if it equals a value the caller
-// never passes, which keeps the loads without writing anything.
-// ---------------------------------------------------------------------------
-#define PF_MAX_RANGES 8
-struct PfRanges {
-    const uint8_t* p[PF_MAX_RANGES];
-    long long lines[PF_MAX_RANGES];
-    int n;
-};
-
-__global__ __launch_bounds__(256) void prefetch_kernel(PfRanges R, uint32_t* __restrict__ sink) {
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    const long long t0 = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    uint32_t acc = 0;
-    for (int r = 0; r < R.n; ++r) {
-        const __attribute__((address_space(1))) uint32_t* base =
-            (const __attribute__((address_space(1))) uint32_t*)R.p[r];
-        const long long nl = R.lines[r];
-        long long l = t0;
-        for (; l + 7 * stride < nl; l += 8 * stride) {
-            uint32_t v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = base[(l + j * stride) * 16];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc ^= v[j];
-        }
-        for (; l < nl; l += stride) acc ^= base[l * 16];
-    }
-    if (sink != nullptr && acc == 0x7FC00001u) sink[0] = acc;
-}
-
-// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 namespace vte {
-
-hipError_t prefetch(int n, const void* const* ptrs, const long long* bytes, int blocks, hipStream_t st) {
-    if (n < 0 || n > PF_MAX_RANGES || blocks < 1) return hipErrorInvalidValue;
-    PfRanges R;
-    memset(&R, 0, sizeof(R));
-    R.n = n;
-    for (int i = 0; i < n; ++i) {
-        R.p[i] = (const uint8_t*)ptrs[i];
-        R.lines[i] = bytes[i] / 64;
-    }
-    hipLaunchKernelGGL(prefetch_kernel, dim3(blocks), dim3(256), 0, st, R, (uint32_t*)nullptr);
-    return hipGetLastError();
-}
 
 hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, hipStream_t st) {
     hipLaunchKernelGGL(fill_normal_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (__half*)dst, n,

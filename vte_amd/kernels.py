@@ -40,7 +40,6 @@ SIGNATURES = {
     "vte_topk_scratch_bytes": [_i],
     "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
     "vte_fill_normal_f16": [_vp, _ll, ctypes.c_ulonglong, _f, _vp],
-    "vte_prefetch": [_i, _vp, _vp, _i, _vp],
     "vte_attn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp,
                     _i, _i, _i, _i, _i, _vp],
     "vte_ffn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp],
@@ -176,14 +175,6 @@ class VTEKernels:
         self._check(self.lib.vte_attn_out_gemv(_p(part_m), _p(part_l), _p(part_o), _p(kv_offset), batch, n_q,
                                                max_splits, split, _p(w), FMT[fmt], _p(out), _p(residual),
                                                residual_scale, N, self._st(stream)), "vte_attn_out_gemv")
-
-    def prefetch(self, ranges, blocks=64, stream=None):
-        """Warm the device caches with [(device_ptr_or_array, nbytes), ...] (at most 8)."""
-        n = len(ranges)
-        ptrs = (ctypes.c_void_p * max(n, 1))(*[_p(r[0]) for r in ranges])
-        sizes = (ctypes.c_longlong * max(n, 1))(*[int(r[1]) for r in ranges])
-        self._check(self.lib.vte_prefetch(n, ctypes.cast(ptrs, ctypes.c_void_p),
-                                                    ctypes.cast(sizes, ctypes.c_void_p), blocks, self._st(stream)), "vte_prefetch")
 
     def fill_normal_f16(self, dst, n, seed, scale=1.0, stream=None):
         self._check(self.lib.vte_fill_normal_f16(_p(dst), n, seed, scale, self._st(stream)), "vte_fill_normal_f16")
