@@ -268,8 +268,11 @@ def profile_step(B, steps, prefix=2048, classes=None):
         replay = lambda: ex.replay(1)
     for i in range(steps):
         replay()
+        # one replay in flight at a time: the profiler's per-dispatch records
+        # stay bounded (thousands of unsynchronised graph dispatches have
+        # crashed rocprofv3's kernel tracing)
+        hip.synchronize()
         if i % 10 == 0:
-            hip.synchronize()
             print(f"profile-step: batch {B}, step {i}/{steps}", flush=True)
     hip.synchronize()
     if classes:

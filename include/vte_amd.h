@@ -129,7 +129,7 @@ int vte_add(const void* residual, const void* input, void* out, int n, float sca
 int vte_embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
                       void* stream);
 
-/* Bytes of device scratch vte_topk needs for `rows` rows. */
+/* Bytes of device scratch (8-byte aligned) vte_topk needs for `rows` rows. */
 long long vte_topk_scratch_bytes(int rows);
 
 /* Per row of fp32 logits [rows][vocab] (vocab <= 262144): the k (1..64)

@@ -41,7 +41,7 @@ def _inputs(rng, B, max_seq):
 
 
 @pytest.mark.parametrize("ctx", [512, 4096, 32768])
-@pytest.mark.parametrize("split", [256, 512, 1024])
+@pytest.mark.parametrize("split", [32, 128, 256, 512, 1024])
 def test_config2_single_sequence(hip, K, ctx, split):
     rng = np.random.default_rng(ctx + split)
     q, kc, vc = _inputs(rng, 1, ctx)
@@ -64,13 +64,12 @@ def test_in_kernel_combine_matches_separate(hip, K, ctx, split):
         assert rel_l2(b[i], attention_ref(q[i], kc[i], vc[i], o + 1, SCALE)) <= TOL
 
 
-@pytest.mark.parametrize("B", [8, 16, 32])
-def test_config3b_ragged_matches_batch1_exactly(hip, K, B):
+@pytest.mark.parametrize("B,split", [(8, 512), (16, 512), (32, 512), (8, 32)])
+def test_config3b_ragged_matches_batch1_exactly(hip, K, B, split):
     rng = np.random.default_rng(1000 + B)
     lens = rng.integers(128, 8193, B)
     max_seq = 8192
     q, kc, vc = _inputs(rng, B, max_seq)
-    split = 512
     got = _run(hip, K, q, kc, vc, lens - 1, split)
     for b in range(B):
         one = _run(hip, K, q[b:b + 1], kc[b:b + 1], vc[b:b + 1], [lens[b] - 1], split)
@@ -80,10 +79,11 @@ def test_config3b_ragged_matches_batch1_exactly(hip, K, B):
 
 
 @pytest.mark.parametrize("ctx", [1, 2, 31, 33, 255, 257])
-def test_short_and_ragged_tails(hip, K, ctx):
+@pytest.mark.parametrize("split", [32, 256])
+def test_short_and_ragged_tails(hip, K, ctx, split):
     rng = np.random.default_rng(ctx)
     q, kc, vc = _inputs(rng, 1, 512)
-    got = _run(hip, K, q, kc, vc, [ctx - 1], 256)
+    got = _run(hip, K, q, kc, vc, [ctx - 1], split)
     assert rel_l2(got[0], attention_ref(q[0], kc[0], vc[0], ctx, SCALE)) <= TOL
     if ctx == 1:  # a single position returns v0 exactly
         for h in range(NQ):
@@ -189,7 +189,8 @@ def test_attn_out_gemv_combines_partials(hip, K, B, fmt):
 
 
 @pytest.mark.parametrize("max_seq,ctx,split", [(2304, 2049, 128), (2304, 100, 128), (1000, 999, 128),
-                                               (4096, 3000, 256)])
+                                               (4096, 3000, 256), (2304, 2049, 32), (1000, 999, 32),
+                                               (2304, 1000, 32)])
 def test_rows_past_length_and_stale_scratch_are_ignored(hip, K, max_seq, ctx, split):
     """Cache rows at or past the length and the split scratch hold NaN; neither
     reaches the output.  (max_seq a multiple of split: the partial kernel reads

@@ -76,6 +76,7 @@ def test_topk_exact(hip, K, k, vocab):
     logits[1, :] = -3.0          # heavy ties: lowest indices must win
     logits[1, vocab // 2] = 5.0
     logits[2, vocab // 4:vocab // 4 + 50] = 9.0    # a tied block above everything else
+    logits[3, :] = rng.integers(0, 10, vocab)       # few distinct values: ties across every block
     vals, idx = empty(hip, (rows, k), np.float32), empty(hip, (rows, k), np.int32)
     scratch = empty(hip, K.topk_scratch_bytes(rows), np.uint8)
     K.topk(up(hip, logits), rows, vocab, k, vals, idx, scratch, stream=hip.stream)

@@ -91,33 +91,125 @@ __device__ __forceinline__ void att_load_tile(AttTile& T, const __half* kb, cons
     }
 }
 
+// One 32-token tile of a wave: scores (MFMA), online softmax, P.V (MFMA)
+// into the running (m_run, l_run, o_acc).  `vt` is the wave's LDS tile for
+// the transposed V.
+__device__ __forceinline__ void att_tile_step(AttTile& T, int t0, int t_end, const half8_t (&qb)[ATT_D / 32],
+                                              float scale, float& m_run, float& l_run,
+                                              floatx4_t (&o_acc)[ATT_D / 16],
+                                              uint32_t (*vt)[ATT_VT_STRIDE / 2], int lane, int col, int grp) {
+    // rows at or past the end contribute p = 0; zero their V so that
+    // whatever the rows hold cannot turn 0 * V into NaN
+#pragma unroll
+    for (int t = 0; t < ATT_TILE; ++t) T.vv[t] = (t0 + t < t_end) ? T.vv[t] : 0u;
+    // ---- scores for 32 tokens: two 16x16 S^T tiles ----
+    floatx4_t acc[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        acc[tt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < ATT_D / 32; ++s)
+            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.ka[tt][s], qb[s], acc[tt], 0, 0, 0);
+    }
+    // ---- V^T into LDS: dword (V[t][d], V[t+1][d]) at vt[d][t/2] ----
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int t = 0; t < ATT_TILE; t += 2) {
+        vt[2 * lane][t / 2] = __builtin_amdgcn_perm(T.vv[t + 1], T.vv[t], 0x05040100u);
+        vt[2 * lane + 1][t / 2] = __builtin_amdgcn_perm(T.vv[t + 1], T.vv[t], 0x07060302u);
+    }
+    // lane holds S^T[token = t0 + 16*tt + 4*grp + i][head = col]
+    float sc[2][4];
+    float tmax = -1e30f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tok = t0 + 16 * tt + 4 * grp + i;
+            float sv = acc[tt][i] * scale;
+            sv = (tok < t_end) ? sv : -INFINITY;
+            sc[tt][i] = sv;
+            tmax = fmaxf(tmax, sv);
+        }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float corr = __expf(m_run - m_new);
+    // A operand of P.V: P[head = col][token slots (grp, j)], j < 4 -> tile 0, j >= 4 -> tile 1
+    half8_t pa;
+    float psum = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float pv = __expf(sc[tt][i] - m_new);
+            psum += pv;
+            pa[4 * tt + i] = (_Float16)pv;
+        }
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+    // rescale O rows (heads 4*grp + i) by their corr, held by lanes 4*grp + i
+    float cr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * grp + i, 64);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int dt = 0; dt < ATT_D / 16; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o_acc[dt][i] *= cr[i];
+        // B operand: V[token slots][d = 16*dt + col]
+        const uint32_t* vr = &vt[16 * dt + col][0];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr + 2 * grp);       // tokens 4g .. 4g+3
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8 + 2 * grp);   // tokens 16+4g ..
+        half8_t vb8;
+        const uint32_t w4[4] = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            vb8[2 * j] = __builtin_bit_cast(_Float16, (unsigned short)(w4[j] & 0xFFFFu));
+            vb8[2 * j + 1] = __builtin_bit_cast(_Float16, (unsigned short)(w4[j] >> 16));
+        }
+        o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb8, o_acc[dt], 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
 // Partials of one split of one (sequence, KV head): grid (max_splits, n_kv, B),
-// four waves, each taking 32-token tiles.  SPEC: the first tile's K/V rows
-// are requested before the sequence length is known (rows up to the split's
+// four waves, each taking 32-token tiles, the first TPW of them (1 or 2)
+// loaded together.  SPEC: those tiles' K/V rows are requested before the
+// sequence length is known (rows up to the split's
 // end, which the host checked lie inside the sequence's cache), so the
 // length and the first tile arrive in one memory round trip; rows at or past
 // the length are masked (scores -inf, V zero).
-template <typename TQ, typename TO, bool SPEC>
+template <typename TQ, typename TO, bool SPEC, int TPW>
 __global__ __launch_bounds__(256) void attn_partial_gqa(
     const TQ* __restrict__ q,            // [B][n_q][D]
     const __half* __restrict__ k_cache, const __half* __restrict__ v_cache,
     float* __restrict__ part_m, float* __restrict__ part_l, float* __restrict__ part_o,
     int n_q, int n_kv, float scale, const int* __restrict__ kv_offset, int kv_batch_stride,
     int split, int max_splits, int* __restrict__ counters, TO* __restrict__ out) {
-    const int sp = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    // TPW == 0: one 32-token split per wave (split == 32), no block combine
+    constexpr bool PW = TPW == 0;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int sp = PW ? blockIdx.x * ATT_WAVES + wv : blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    if (PW && sp >= max_splits) return;
     ATT_TS(0);
     const int t_begin = sp * split;
     const int G = n_q / n_kv;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15;   // head (MFMA N index) / token row (A operand)
     const int grp = lane >> 4;   // 0..3
     const size_t row_stride = (size_t)n_kv * ATT_D;  // elements between consecutive positions
     const __half* kb = k_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
     const __half* vb = v_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
     const int len_raw = kv_offset[b];
-    AttTile T;
-    int t0 = t_begin + wv * ATT_TILE;
-    if (SPEC) att_load_tile(T, kb, vb, row_stride, t0, t_begin + split - 1, col, grp, lane);
+    AttTile T, T1;
+    int t0 = PW ? t_begin : t_begin + wv * ATT_TILE;
+    if (SPEC) {
+        att_load_tile(T, kb, vb, row_stride, t0, t_begin + split - 1, col, grp, lane);
+        if (TPW == 2)
+            att_load_tile(T1, kb, vb, row_stride, t0 + ATT_WAVES * ATT_TILE, t_begin + split - 1, col, grp, lane);
+    }
 
     // B operand: Q^T for this KV head's G query heads, fp16, zero-padded to 16.
     half8_t qb[ATT_D / 32];
@@ -135,7 +227,7 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
     }
 
     const int len = len_raw + 1;
-    if (t_begin >= len) return;  // past this sequence's last split
+    if (t_begin >= len) return;  // past this sequence's last split (PW: this wave's)
     const int t_end = min(t_begin + split, len);
 
     // V tile of a wave, transposed: vt[d][t] (fp16, rows of 36 halves so the
@@ -159,85 +251,37 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
 #pragma unroll
     for (int dt = 0; dt < ATT_D / 16; ++dt) o_acc[dt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-    if (!SPEC) att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
+    if (!SPEC) {
+        att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
+        if (TPW == 2) att_load_tile(T1, kb, vb, row_stride, t0 + ATT_WAVES * ATT_TILE, t_end - 1, col, grp, lane);
+    }
+    ATT_TS(1);
+    if (t0 < t_end) att_tile_step(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
+    if (PW) {  // the wave's split is done: its statistics and outputs are the partials
+        l_run += __shfl_xor(l_run, 16, 64);
+        l_run += __shfl_xor(l_run, 32, 64);
+        const size_t st0 = ((size_t)b * n_q + kvh * G) * max_splits + sp;
+        if (grp == 0 && col < G) {
+            part_m[st0 + (size_t)col * max_splits] = m_run;
+            part_l[st0 + (size_t)col * max_splits] = l_run;
+        }
+#pragma unroll
+        for (int dt = 0; dt < ATT_D / 16; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int h = 4 * grp + i;
+                if (h < G) part_o[(st0 + (size_t)h * max_splits) * ATT_D + 16 * dt + col] = o_acc[dt][i];
+            }
+        return;
+    }
+    t0 += ATT_WAVES * ATT_TILE;
+    if (TPW == 2) {
+        if (t0 < t_end) att_tile_step(T1, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
+        t0 += ATT_WAVES * ATT_TILE;
+    }
     for (; t0 < t_end; t0 += ATT_WAVES * ATT_TILE) {
-        if (t0 != t_begin + wv * ATT_TILE) att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
-        ATT_TS(1);
-        // rows at or past the end contribute p = 0; zero their V so that
-        // whatever the rows hold cannot turn 0 * V into NaN
-#pragma unroll
-        for (int t = 0; t < ATT_TILE; ++t) T.vv[t] = (t0 + t < t_end) ? T.vv[t] : 0u;
-        // ---- scores for 32 tokens: two 16x16 S^T tiles ----
-        floatx4_t acc[2];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            acc[tt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < ATT_D / 32; ++s)
-                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.ka[tt][s], qb[s], acc[tt], 0, 0, 0);
-        }
-        // ---- V^T into LDS: dword (V[t][d], V[t+1][d]) at vt[d][t/2] ----
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int t = 0; t < ATT_TILE; t += 2) {
-            vt_sh[wv][2 * lane][t / 2] = __builtin_amdgcn_perm(T.vv[t + 1], T.vv[t], 0x05040100u);
-            vt_sh[wv][2 * lane + 1][t / 2] = __builtin_amdgcn_perm(T.vv[t + 1], T.vv[t], 0x07060302u);
-        }
-        // lane holds S^T[token = t0 + 16*tt + 4*grp + i][head = col]
-        float sc[2][4];
-        float tmax = -1e30f;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int tok = t0 + 16 * tt + 4 * grp + i;
-                float sv = acc[tt][i] * scale;
-                sv = (tok < t_end) ? sv : -INFINITY;
-                sc[tt][i] = sv;
-                tmax = fmaxf(tmax, sv);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        const float corr = __expf(m_run - m_new);
-        // A operand of P.V: P[head = col][token slots (grp, j)], j < 4 -> tile 0, j >= 4 -> tile 1
-        half8_t pa;
-        float psum = 0.f;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float pv = __expf(sc[tt][i] - m_new);
-                psum += pv;
-                pa[4 * tt + i] = (_Float16)pv;
-            }
-        l_run = l_run * corr + psum;
-        m_run = m_new;
-        // rescale O rows (heads 4*grp + i) by their corr, held by lanes 4*grp + i
-        float cr[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * grp + i, 64);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int dt = 0; dt < ATT_D / 16; ++dt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o_acc[dt][i] *= cr[i];
-            // B operand: V[token slots][d = 16*dt + col]
-            const uint32_t* vr = &vt_sh[wv][16 * dt + col][0];
-            const uint2 lo = *reinterpret_cast<const uint2*>(vr + 2 * grp);       // tokens 4g .. 4g+3
-            const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8 + 2 * grp);   // tokens 16+4g ..
-            half8_t vb8;
-            const uint32_t w4[4] = {lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                vb8[2 * j] = __builtin_bit_cast(_Float16, (unsigned short)(w4[j] & 0xFFFFu));
-                vb8[2 * j + 1] = __builtin_bit_cast(_Float16, (unsigned short)(w4[j] >> 16));
-            }
-            o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb8, o_acc[dt], 0, 0, 0);
-        }
-        __builtin_amdgcn_wave_barrier();
+        att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
+        att_tile_step(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
     }
 
     ATT_TS(2);
@@ -476,38 +520,53 @@ extern "C" __global__ __launch_bounds__(256) void flash_attention_split_kv_reduc
     if (tid < head_dim) output[((size_t)b * num_q_heads + qh) * head_dim + tid] = __float2half(O / fmaxf(L, 1e-20f));
 }
 
-// LSE combine for max_splits <= 64 in one memory round trip: every load
+// LSE combine for max_splits <= 128 in one memory round trip: every load
 // (length, split statistics, partial outputs of all max_splits splits) is
 // issued before any result is needed; splits at or past the sequence's
 // split count are masked by selects, so stale scratch cannot leak in.  Each
-// wave reduces the split statistics on its own (lane c holds split c), so
-// there is no barrier.  grid (n_q, B), block 128 (one thread per dim).
+// wave reduces the split statistics on its own (lane c holds splits c and
+// c + 64), so there is no barrier.  grid (n_q, B), block 128 (one thread per dim).
 template <typename TO, int NSMAX>
 __global__ __launch_bounds__(128) void attn_combine_small(const float* __restrict__ part_m,
                                                           const float* __restrict__ part_l,
                                                           const float* __restrict__ part_o, TO* __restrict__ out,
                                                           int n_q, const int* __restrict__ kv_offset, int split,
                                                           int max_splits) {
+    constexpr int PL = NSMAX > 64 ? 2 : 1;  // splits per lane
     const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x, lane = d & 63;
     CMB_TS(0);
     const size_t base = ((size_t)b * n_q + qh) * max_splits;
     const int len_raw = kv_offset[b];
-    const int cl = min(lane, max_splits - 1);
-    const float m_l = part_m[base + cl];
-    const float l_l = part_l[base + cl];
+    float m_l[PL], l_l[PL];
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+        const int cl = min(lane + 64 * j, max_splits - 1);
+        m_l[j] = part_m[base + cl];
+        l_l[j] = part_l[base + cl];
+    }
     const float* po = part_o + base * ATT_D + d;
     float o[NSMAX];
 #pragma unroll
     for (int c = 0; c < NSMAX; ++c) o[c] = po[(size_t)min(c, max_splits - 1) * ATT_D];
     const int ns = (len_raw + 1 + split - 1) / split;
-    const float m = lane < ns ? m_l : -INFINITY;
-    const float M = wave_max(m);
-    const float w = lane < ns ? __expf(m - M) : 0.f;
-    const float L = wave_sum(lane < ns ? l_l * w : 0.f);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+        m_l[j] = lane + 64 * j < ns ? m_l[j] : -INFINITY;
+        mx = fmaxf(mx, m_l[j]);
+    }
+    const float M = wave_max(mx);
+    float w[PL], ls = 0.f;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+        w[j] = lane + 64 * j < ns ? __expf(m_l[j] - M) : 0.f;
+        ls += lane + 64 * j < ns ? l_l[j] * w[j] : 0.f;
+    }
+    const float L = wave_sum(ls);
     float O = 0.f;
 #pragma unroll
     for (int c = 0; c < NSMAX; ++c) {
-        const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c));
+        const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[c >> 6]), c & 63));
         O = c < ns ? fmaf(o[c], wc, O) : O;
     }
     st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(L, 1e-20f));
@@ -528,14 +587,23 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
     // max_splits * split must lie inside one sequence's kv_batch_stride
     const long long rows_cap = kv_batch_stride / ((long long)n_kv * ATT_D);
     const bool spec = (long long)max_splits * split <= rows_cap;
-    if (spec)
-        hipLaunchKernelGGL((attn_partial_gqa<TQ, TO, true>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,
-                           (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset,
-                           kv_batch_stride, split, max_splits, counters, (TO*)out);
-    else
-        hipLaunchKernelGGL((attn_partial_gqa<TQ, TO, false>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,
-                           (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset,
-                           kv_batch_stride, split, max_splits, counters, (TO*)out);
+#define ATT_LAUNCH_P(SP, TP)                                                                                   \
+    hipLaunchKernelGGL((attn_partial_gqa<TQ, TO, SP, TP>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,   \
+                       (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset, kv_batch_stride, \
+                       split, max_splits, counters, (TO*)out)
+    const bool two = split >= 2 * ATT_WAVES * ATT_TILE;  // two tiles per wave loaded together
+    if (split == ATT_TILE) {  // one split per wave: a block takes four consecutive splits
+        g1.x = (max_splits + ATT_WAVES - 1) / ATT_WAVES;
+        if (spec) ATT_LAUNCH_P(true, 0);
+        else ATT_LAUNCH_P(false, 0);
+    } else if (spec) {
+        if (two) ATT_LAUNCH_P(true, 2);
+        else ATT_LAUNCH_P(true, 1);
+    } else {
+        if (two) ATT_LAUNCH_P(false, 2);
+        else ATT_LAUNCH_P(false, 1);
+    }
+#undef ATT_LAUNCH_P
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || counters != nullptr || out == nullptr) return e;  // out == nullptr: partials only
     dim3 g2(n_q, B), b2(ATT_D);
@@ -547,6 +615,9 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
                            kv_offset, split, max_splits);
     else if (max_splits <= 64)
         hipLaunchKernelGGL((attn_combine_small<TO, 64>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q,
+                           kv_offset, split, max_splits);
+    else if (max_splits <= 128)
+        hipLaunchKernelGGL((attn_combine_small<TO, 128>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q,
                            kv_offset, split, max_splits);
     else
         hipLaunchKernelGGL((attn_combine<TO>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q, kv_offset,

@@ -162,6 +162,7 @@ int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void*
     REQUIRE(split >= 32 && split % 32 == 0, "attn: split %d must be a positive multiple of 32", split);
     REQUIRE(max_splits >= 1 && max_splits <= 4096, "attn: max_splits %d out of range (1..4096)", max_splits);
     REQUIRE(counters == nullptr || max_splits <= 512, "attn: in-kernel combine supports at most 512 splits");
+    REQUIRE(counters == nullptr || split > 32, "attn: in-kernel combine needs splits of more than 32 tokens");
     REQUIRE(aligned(k_cache, 16) && aligned(v_cache, 16), "attn: KV cache must be 16-byte aligned");
     REQUIRE(kv_batch_stride % 8 == 0, "attn: kv_batch_stride must keep rows 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
@@ -230,6 +231,7 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
     REQUIRE(rows >= 1 && k >= 1 && k <= 64 && vocab >= k, "topk: need 1 <= k <= min(64, vocab)");
     REQUIRE(rows <= 65535, "topk: rows %d out of range", rows);
     REQUIRE(vocab <= 262144, "topk: vocab %d above 262144", vocab);
+    REQUIRE(aligned(scratch, 8), "topk: scratch must be 8-byte aligned");
     return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream),
                       "vte_topk launch");
 }

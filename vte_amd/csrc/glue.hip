@@ -158,18 +158,33 @@ extern "C" __global__ __launch_bounds__(256) void embedding_lookup_q6k_kernel(
 // ---------------------------------------------------------------------------
 // Top-k over fp32 logits, k <= 64, exact, ordered by (value desc, index asc):
 // the order np.lexsort((index, -value)) gives.  Two launches:
-//  1. grid (TOPK_P, rows): each block selects the 64 best entries of its
-//     slice (at most TOPK_SLICE logits) by radix selection of the 64th
-//     largest key in LDS (three rounds of 11/11/10-bit digit histograms),
-//     then keeps every key above it plus the lowest-indexed ties, and writes
-//     them in index order with their count;
-//  2. one block per row selects the best 64 of the <= TOPK_P * 64 candidates
-//     the same way and sorts them with a 64-lane bitonic network.
+//  1. grid (TOPK_P, rows): each block takes a slice (at most TOPK_SLICE
+//     logits) into registers, 16 per thread.  T, the smallest of the four
+//     waves' ceil(k/4)-th largest per-thread maxima, has at least k entries
+//     >= T in the slice, so the slice's top k are among the entries >= T;
+//     when those number at most TOPK_CAP they are the block's candidates.
+//     Otherwise (heavy ties) the block
+//     selects its 64 best exactly by radix selection in LDS (11/11/10-bit
+//     digit histograms) and keeps the lowest-indexed ties.
+//  2. one block per row thresholds the <= TOPK_P * TOPK_CAP candidates the same
+//     way; when at most 256 survive, each survivor's rank is the number of
+//     survivors ordered before it, else the exact radix selection runs on all
+//     candidates.
 // Keys map fp32 to an order-preserving uint32 (-0.0 taken as +0.0, as the
 // reference's comparison does).
 // ---------------------------------------------------------------------------
 #define TOPK_P 64
 #define TOPK_SLICE 4096
+#define TOPK_CAP 128  // candidate slots per slice
+#ifdef TK_TRACE
+__device__ unsigned long long tk_trace[2][128][8];
+#define TK_TS(kern, k) do { if (threadIdx.x == 0) tk_trace[kern][blockIdx.x & 127][k] = wall_clock64(); } while (0)
+extern "C" int vte_dbg_tk_trace_read(void* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(tk_trace), sizeof(tk_trace), 0, hipMemcpyDeviceToHost);
+}
+#else
+#define TK_TS(kern, k) do { } while (0)
+#endif
 #define TOPK_THREADS 256
 #define TOPK_BINS 2048
 
@@ -258,6 +273,7 @@ __device__ uint32_t tk_radix_select(const uint32_t* keys, int n, int need, TkSha
         mask |= (uint32_t)(nb - 1) << shift;
         need = sh.sel_need;
         __syncthreads();
+        TK_TS(gridDim.y > 1 ? 0 : (gridDim.x > 1 ? 0 : 1), 2 + r);
     }
     need_eq = need;
     return prefix;
@@ -293,47 +309,110 @@ __device__ int tk_compact(const uint32_t* keys, int n, uint32_t T, int need_eq, 
     return tot;
 }
 
+// A candidate in one 8-byte word: key in the high half, index in the low half.
+__device__ __forceinline__ uint64_t tk_pack(uint32_t key, int idx) {
+    return ((uint64_t)key << 32) | (uint32_t)idx;
+}
+
+// Output order: a before b when its key is larger, or equal with a smaller index.
+__device__ __forceinline__ bool tk_before(uint32_t a, int ia, uint32_t b, int ib) {
+    return a > b || (a == b && ia < ib);
+}
+
+// r-th largest (1-based) of the wave's 64 values, by deciding its bits from
+// the top: the largest t with #{v >= t} >= r.  Ballots and scalar popcounts.
+__device__ __forceinline__ uint32_t tk_wave_kth(uint32_t v, int r) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t trial = t | (1u << b);
+        if (__popcll(__ballot(v >= trial)) >= r) t = trial;
+    }
+    return t;
+}
+
+// Threshold from the per-thread values `tm` (thread maxima): the smallest of
+// the four waves' ceil(kth/4)-th largest, so at least kth values are >= it.
+// Ends with a barrier.
+__device__ __forceinline__ uint32_t tk_block_threshold(uint32_t tm, int kth, uint32_t* wt) {
+    const uint32_t t = tk_wave_kth(tm, (kth + 3) >> 2);
+    if ((threadIdx.x & 63) == 0) wt[threadIdx.x >> 6] = t;
+    __syncthreads();
+    return min(min(wt[0], wt[1]), min(wt[2], wt[3]));
+}
+
+#define TKR (TOPK_SLICE / TOPK_THREADS)  // slice entries per thread
+
 __global__ __launch_bounds__(TOPK_THREADS) void topk_partial_kernel(const float* __restrict__ logits, int vocab,
-                                                                      int slice, uint32_t* __restrict__ cand_key,
-                                                                      int* __restrict__ cand_idx,
+                                                                      int slice, int k,
+                                                                      uint64_t* __restrict__ cand,
                                                                       int* __restrict__ cand_cnt) {
     __shared__ uint32_t keys[TOPK_SLICE];
     __shared__ int pos[64];
     __shared__ TkShared sh;
+    __shared__ uint32_t wt[TOPK_THREADS / 64];
     const int row = blockIdx.y, p = blockIdx.x, tid = threadIdx.x;
+    TK_TS(0, 0);
     const int lo = p * slice, n = max(0, min(slice, vocab - lo));
     const float* r = logits + (size_t)row * vocab + lo;
-    for (int i0 = 0; i0 < n; i0 += 4 * TOPK_THREADS) {
-        float v[4];
+    // entry j * 256 + tid of the slice in register j (all loads issued at once)
+    uint32_t kr[TKR];
+    float v[TKR];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = i0 + j * TOPK_THREADS + tid;
-            v[j] = r[i < n ? i : 0];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = i0 + j * TOPK_THREADS + tid;
-            if (i < n) keys[i] = tk_key(v[j]);
-        }
+    for (int j = 0; j < TKR; ++j) {
+        const int i = j * TOPK_THREADS + tid;
+        v[j] = r[i < n ? i : 0];
     }
-    __syncthreads();
-    const size_t o = ((size_t)row * gridDim.x + p) * 64;
+    uint32_t tm = 0;
+#pragma unroll
+    for (int j = 0; j < TKR; ++j) {
+        const bool ok = j * TOPK_THREADS + tid < n;
+        kr[j] = ok ? tk_key(v[j]) : 0u;
+        tm = ok ? max(tm, kr[j]) : tm;
+    }
+    TK_TS(0, 1);
+    const size_t o = ((size_t)row * gridDim.x + p) * TOPK_CAP;
     if (n <= 64) {
-        if (tid < n) { cand_key[o + tid] = keys[tid]; cand_idx[o + tid] = lo + tid; }
+        if (tid < n) cand[o + tid] = tk_pack(kr[0], lo + tid);
         if (tid == 0) cand_cnt[(size_t)row * gridDim.x + p] = n;
         return;
     }
+    // n > 64 >= k: every wave's ceil(k/4) largest maxima are entries' keys
+    const uint32_t T = tk_block_threshold(tm, k, wt);
+    TK_TS(0, 2);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < TKR; ++j) c += (j * TOPK_THREADS + tid < n && kr[j] >= T) ? 1 : 0;
+    int total;
+    int base = tk_excl_scan(c, sh.wsum, total);
+    if (total <= TOPK_CAP) {
+#pragma unroll
+        for (int j = 0; j < TKR; ++j) {
+            const int i = j * TOPK_THREADS + tid;
+            if (i < n && kr[j] >= T) {
+                cand[o + base] = tk_pack(kr[j], lo + i);
+                ++base;
+            }
+        }
+        if (tid == 0) cand_cnt[(size_t)row * gridDim.x + p] = total;
+        TK_TS(0, 5);
+        return;
+    }
+    // many entries tie at the top: exact selection of the slice's best 64
+#pragma unroll
+    for (int j = 0; j < TKR; ++j) {
+        const int i = j * TOPK_THREADS + tid;
+        if (i < n) keys[i] = kr[j];
+    }
+    __syncthreads();
     int need_eq;
-    const uint32_t T = tk_radix_select(keys, n, 64, sh, need_eq);
-    const int kept = tk_compact(keys, n, T, need_eq, pos, sh);
-    if (tid < kept) { cand_key[o + tid] = keys[pos[tid]]; cand_idx[o + tid] = lo + pos[tid]; }
+    const uint32_t T64 = tk_radix_select(keys, n, 64, sh, need_eq);
+    const int kept = tk_compact(keys, n, T64, need_eq, pos, sh);
+    if (tid < kept) cand[o + tid] = tk_pack(keys[pos[tid]], lo + pos[tid]);
     if (tid == 0) cand_cnt[(size_t)row * gridDim.x + p] = kept;
 }
 
 // Bitonic network over 64 lanes on (key desc, index asc).
-__device__ __forceinline__ bool tk_before(uint32_t a, int ia, uint32_t b, int ib) {
-    return a > b || (a == b && ia < ib);
-}
 __device__ __forceinline__ void tk_sort64(uint32_t& k, int& ix, int lane) {
     for (int size = 2; size <= 64; size <<= 1)
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -346,17 +425,32 @@ __device__ __forceinline__ void tk_sort64(uint32_t& k, int& ix, int lane) {
         }
 }
 
-__global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint32_t* __restrict__ cand_key,
-                                                                    const int* __restrict__ cand_idx,
+__global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint64_t* __restrict__ cand,
                                                                     const int* __restrict__ cand_cnt, int P, int k,
                                                                     float* __restrict__ out_val,
                                                                     int* __restrict__ out_idx) {
-    __shared__ uint32_t keys[TOPK_P * 64];
-    __shared__ int idx[TOPK_P * 64];
+    constexpr int NS = TOPK_P * TOPK_CAP / TOPK_THREADS;  // candidate slots per thread
+    __shared__ uint32_t keys[TOPK_P * TOPK_CAP];
+    __shared__ int idx[TOPK_P * TOPK_CAP];
     __shared__ int offs[TOPK_P + 1];
     __shared__ int pos[64];
     __shared__ TkShared sh;
+    __shared__ uint32_t sk[TOPK_THREADS];
+    __shared__ int si[TOPK_THREADS];
+    __shared__ uint32_t wt[TOPK_THREADS / 64];
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    TK_TS(1, 0);
+    // every slot's candidate and the block counts requested at once
+    const size_t rb = (size_t)row * P * TOPK_CAP;
+    uint32_t ck[NS];
+    int cx[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const int sl = min(j * TOPK_THREADS + tid, P * TOPK_CAP - 1);
+        const uint64_t c = cand[rb + sl];
+        ck[j] = (uint32_t)(c >> 32);
+        cx[j] = (int)(uint32_t)c;
+    }
     if (tid < 64) {
         const int c = tid < P ? cand_cnt[(size_t)row * P + tid] : 0;
         int incl = c;
@@ -369,24 +463,66 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint32_t
         if (tid == 63) offs[TOPK_P] = incl;
     }
     __syncthreads();
+    // compact the candidates: keys[0 .. n)
     const int n = offs[TOPK_P];
-    for (int i = tid; i < P * 64; i += TOPK_THREADS) {
-        const int p = i >> 6, j = i & 63;
-        if (j < offs[p + 1] - offs[p] || (p == TOPK_P - 1 && j < n - offs[p])) {
-            keys[offs[p] + j] = cand_key[(size_t)row * P * 64 + i];
-            idx[offs[p] + j] = cand_idx[(size_t)row * P * 64 + i];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const int sl = j * TOPK_THREADS + tid, seg = sl / TOPK_CAP, off = sl % TOPK_CAP;
+        if (seg < P && off < offs[seg + 1] - offs[seg]) {
+            keys[offs[seg] + off] = ck[j];
+            idx[offs[seg] + off] = cx[j];
         }
     }
     __syncthreads();
-    int kept = n;
-    if (n > 64) {
-        int need_eq;
-        const uint32_t T = tk_radix_select(keys, n, 64, sh, need_eq);
-        kept = tk_compact(keys, n, T, need_eq, pos, sh);
-    } else if (tid < n) {
-        pos[tid] = tid;
+    TK_TS(1, 1);
+    // candidate i in register i / 256 of thread i % 256
+    uint32_t tm = 0;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const int i = j * TOPK_THREADS + tid;
+        ck[j] = i < n ? keys[i] : 0u;
+        cx[j] = i < n ? idx[i] : 0x7fffffff;
+        tm = i < n ? max(tm, ck[j]) : tm;
     }
-    __syncthreads();
+    // n > 256: every thread holds a candidate, so each wave's ceil(k/4)
+    // largest maxima are candidates' keys and at least k candidates are >= T
+    const uint32_t T = n > TOPK_THREADS ? tk_block_threshold(tm, k, wt) : 0u;
+    TK_TS(1, 2);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) c += (j * TOPK_THREADS + tid < n && ck[j] >= T) ? 1 : 0;
+    int total;
+    int base = tk_excl_scan(c, sh.wsum, total);
+    if (total <= TOPK_THREADS) {
+        // survivors -> LDS; each one's rank = survivors ordered before it
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            if (j * TOPK_THREADS + tid < n && ck[j] >= T) {
+                sk[base] = ck[j];
+                si[base] = cx[j];
+                ++base;
+            }
+        }
+        __syncthreads();
+        if (tid < total) {
+            const uint32_t kk = sk[tid];
+            const int ix = si[tid];
+            int rank = 0;
+#pragma unroll 8
+            for (int j = 0; j < total; ++j) rank += tk_before(sk[j], si[j], kk, ix) ? 1 : 0;
+            if (rank < k) {
+                out_val[(size_t)row * k + rank] = tk_val(kk);
+                out_idx[(size_t)row * k + rank] = ix;
+            }
+        }
+        TK_TS(1, 6);
+        return;
+    }
+    // many ties at the top: exact radix selection over all candidates
+    int need_eq;
+    const uint32_t T64 = tk_radix_select(keys, n, 64, sh, need_eq);
+    const int kept = tk_compact(keys, n, T64, need_eq, pos, sh);
+    TK_TS(1, 5);
     if (tid < 64) {
         uint32_t kk = 0;
         int ix = 0x7fffffff;
@@ -468,7 +604,7 @@ hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_
     return hipGetLastError();
 }
 
-size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_P * (64 * 8 + 4); }
+size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_P * (TOPK_CAP * 8 + 4); }
 
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
                 hipStream_t st) {
@@ -477,13 +613,13 @@ hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val,
     int P = (vocab + 2047) / 2048;
     if (P > TOPK_P) P = TOPK_P;
     const int slice = (vocab + P - 1) / P;
-    uint32_t* ck = (uint32_t*)scratch;
-    int* ci = (int*)((char*)scratch + (size_t)rows * TOPK_P * 64 * 4);
-    int* cc = (int*)((char*)scratch + (size_t)rows * TOPK_P * 64 * 8);
-    hipLaunchKernelGGL(topk_partial_kernel, dim3(P, rows), dim3(TOPK_THREADS), 0, st, logits, vocab, slice, ck, ci, cc);
+    uint64_t* cand = (uint64_t*)scratch;
+    int* cc = (int*)((char*)scratch + (size_t)rows * TOPK_P * TOPK_CAP * 8);
+    hipLaunchKernelGGL(topk_partial_kernel, dim3(P, rows), dim3(TOPK_THREADS), 0, st, logits, vocab, slice, k, cand,
+                       cc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(TOPK_THREADS), 0, st, ck, ci, cc, P, k, out_val, out_idx);
+    hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(TOPK_THREADS), 0, st, cand, cc, P, k, out_val, out_idx);
     return hipGetLastError();
 }
 
