@@ -79,16 +79,20 @@ def step_breakdown(hip, ex, prefix, reps=20):
     return out
 
 
+MV_CLASSES = ["attn_in", "o_proj", "ffn_in", "down", "lm_head"]
+
+
 def fused_mv_roofline(hip, ex, reps=20):
-    """Roofline of the step's dominant kernel, fused_mv_kernel (the 28 norm+QKV,
-    28 norm+gate/up and 1 norm+LM-head launches of a batch-1 step): algorithmic
-    bytes per launch over its average launch duration (HIP events around
-    replays of a graph of exactly those launches)."""
-    classes = ["attn_in", "ffn_in", "lm_head"]
+    """Roofline of the step's dominant kernel, fused_mv_kernel: every
+    quantised mat-vec launch of a batch-1 step (28 norm+QKV+RoPE+append, 28
+    o-proj+residual, 28 norm+gate/up+SwiGLU, 28 down+residual, 1 norm+LM
+    head): algorithmic bytes per launch over the average launch duration (HIP
+    events on the executor's stream around replays of a graph of exactly
+    those launches)."""
     algo = ex.class_algorithmic_bytes()
-    launches = 2 * ex.cfg.n_layers + 1
-    per_launch_bytes = sum(algo[c] for c in classes) / launches
-    ms = time_classes(hip, ex, classes, reps) / launches
+    launches = 4 * ex.cfg.n_layers + 1
+    per_launch_bytes = sum(algo[c] for c in MV_CLASSES) / launches
+    ms = time_classes(hip, ex, MV_CLASSES, reps) / launches
     gbps = per_launch_bytes / (ms * 1e-3) / 1e9
     traffic = None
     tf = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "fused_mv_decode_b1_traffic.json")
@@ -97,8 +101,7 @@ def fused_mv_roofline(hip, ex, reps=20):
             traffic = json.load(f).get("hbm_bytes_per_launch")
     return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
-            "kernel": "fused_mv_kernel<1> (batch-1 step: 28 norm+QKV+RoPE+append, 28 norm+gate/up+SwiGLU, "
-                      "1 norm+LM head launch)",
+            "kernel": "fused_mv_kernel (all %d quantised mat-vec launches of the batch-1 step)" % launches,
             "avg_launch_us": round(ms * 1e3, 3), "algo_bytes_per_launch": int(per_launch_bytes)}
 
 
@@ -156,11 +159,15 @@ def gemv_bench(hip, K, fmt, n, k, launches=200, pool_bytes=768 << 20, mfma_batch
             "frac_hbm_peak": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
-def attn_bench(hip, K, ctx, split, B=1, fused=True, launches=40):
+def attn_bench(hip, K, ctx, split=None, B=1, fused=False, launches=40):
     """Split-KV decode attention (12q/2kv, hd 128, fp16 KV) over a cold set of
-    KV caches, graph-captured launches.  Algorithmic bytes: KV = B*ctx*1024 B."""
+    KV caches, graph-captured launches.  Algorithmic bytes: KV = B*ctx*1024 B.
+    split None: the dispatcher's choice for this context and batch."""
     from vte_amd.bridge import DeviceArray
+    from vte_amd.core.split_kv_attention import choose_split
     n_q, n_kv, D = 12, 2, 128
+    if split is None:
+        split = choose_split(ctx, B, n_kv, hip.get_num_cus())
     per_seq = ctx * n_kv * D
     copies = max(2, int(np.ceil((512 << 20) / (2 * 2 * B * per_seq))))
     kc = [DeviceArray(hip, B * per_seq, np.float16, "kc") for _ in range(copies)]
@@ -348,10 +355,10 @@ def main():
     attn = []
     if not args.quick:
         for ctx in (512, 4096, 32768):
-            attn.append(attn_bench(hip, K, ctx, 256 if ctx < 32768 else 512))
-        attn.append(attn_bench(hip, K, 2049, 128, fused=True))
-        attn.append(attn_bench(hip, K, 2049, 128, fused=False))
-        attn.append(attn_bench(hip, K, 2049, 512, B=16, fused=True))
+            attn.append(attn_bench(hip, K, ctx))
+        attn.append(attn_bench(hip, K, 2049))
+        attn.append(attn_bench(hip, K, 2049, fused=True))
+        attn.append(attn_bench(hip, K, 2049, B=16))
     cpu = None if args.no_cpu else cpu_baseline()
     r1 = result[1]
     line = {

@@ -36,6 +36,11 @@
 #define TMV_MAX_SEG 3
 #define TMV_MAX_R 64
 
+#ifdef TMV_MARK
+#define TMV_M(n) asm volatile("; TMVMARK " #n)
+#else
+#define TMV_M(n) do { } while (0)
+#endif
 #ifdef TMV_TRACE
 __device__ unsigned long long tmv_trace[8192][8];
 #define TMV_TS(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) tmv_trace[blockIdx.x][k] = wall_clock64(); } while (0)
@@ -161,10 +166,10 @@ __device__ __forceinline__ uint4 ldg_u16b(const uint8_t* p) {
 
 // Q6_K unit (h, l16) from registers: 64 weights at 128h + l16 + i + 32g
 // (i < 16, g < 4).  la/lb: ql[64h + l16 ..], ql[64h + 32 + l16 ..]; hq:
-// qh[32h + l16 ..]; sc8: bytes 192 + 8h .. +7; d: fp16 bits.
-__device__ __forceinline__ float q6k_unit_dot_r(const uint4& la4, const uint4& lb4, const uint4& hq4, uint2 sc8,
-                                                uint32_t dbits, int l16, const _Float16* xsb, const float* s16sb,
-                                                int h) {
+// qh[32h + l16 ..]; sc8: bytes 192 + 8h .. +7; d: fp16 bits.  x[2g], x[2g+1]:
+// the 16 activations of group g (xperm layout); X[g]: their sum.
+__device__ __forceinline__ float q6k_unit_dot_x(const uint4& la4, const uint4& lb4, const uint4& hq4, uint2 sc8,
+                                                uint32_t dbits, int l16, const uint4 (&x)[8], const float (&X)[4]) {
     const float d = h2f_bits(dbits);
     const uint32_t la[4] = {la4.x, la4.y, la4.z, la4.w};
     const uint32_t lb[4] = {lb4.x, lb4.y, lb4.z, lb4.w};
@@ -174,8 +179,7 @@ __device__ __forceinline__ float q6k_unit_dot_r(const uint4& la4, const uint4& l
     float r = 0.f;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        const uint4* xp = reinterpret_cast<const uint4*>(xsb + xpad(128 * h + l16 + 32 * g));
-        const uint4 x0 = xp[0], x1 = xp[1];
+        const uint4 x0 = x[2 * g], x1 = x[2 * g + 1];
         float S = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -183,15 +187,27 @@ __device__ __forceinline__ float q6k_unit_dot_r(const uint4& la4, const uint4& l
             const uint32_t nib = (g < 2) ? (l & 0x0F0F0F0Fu) : ((l >> 4) & 0x0F0F0F0Fu);
             const uint32_t u = nib | (((hw[i] >> (2 * g)) & 0x03030303u) << 4);
             const uint4 xv = (i < 2) ? x0 : x1;
-            const uint32_t x01 = (i & 1) ? xv.z : xv.x;
-            const uint32_t x23 = (i & 1) ? xv.w : xv.y;
-            S = dot4_codes(u, x01, x23, S);
+            const uint32_t x02 = (i & 1) ? xv.z : xv.x;
+            const uint32_t x13 = (i & 1) ? xv.w : xv.y;
+            S = dot4_codes(u, x02, x13, S);
         }
-        const float X = s16sb[(128 * h + l16 + 32 * g) >> 4];
         const int8_t sc = (int8_t)((scw >> (8 * (c + 2 * g))) & 0xFF);
-        r = fmaf(d * (float)sc, fmaf(-1056.f, X, S), r);
+        r = fmaf(d * (float)sc, fmaf(-1056.f, X[g], S), r);
     }
     return r;
+}
+
+// Activations of a Q6_K unit (h, l16) from LDS: xsb -> the super-block's x
+// (padded xperm layout), s16sb -> its per-16 sums.
+__device__ __forceinline__ void q6k_unit_x(const _Float16* xsb, const float* s16sb, int h, int l16, uint4 (&x)[8],
+                                           float (&X)[4]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const uint4* xp = reinterpret_cast<const uint4*>(xsb + xpad(128 * h + l16 + 32 * g));
+        x[2 * g] = xp[0];
+        x[2 * g + 1] = xp[1];
+        X[g] = s16sb[(128 * h + l16 + 32 * g) >> 4];
+    }
 }
 
 // Scalar global loads through the global address space (a generic pointer
@@ -267,11 +283,11 @@ __device__ __forceinline__ void stage_combine(const FmvPlan& P, _Float16* xs, fl
             for (int t = 0; t < 8; ++t) acc = fmaf(v[t], w[sp + t], acc);
         }
         for (; sp < ns; ++sp) acc = fmaf(o[(size_t)sp * 128], w[sp], acc);
-        xs[(size_t)m * ldx + xpad(e)] = (_Float16)acc;
+        xs[(size_t)m * ldx + xpad(xperm(e))] = (_Float16)acc;
     }
     for (int j = tid; j < (NC - M) * K; j += ROWS_THREADS) {  // padding columns
         const int m = M + j / K, e = j % K;
-        xs[(size_t)m * ldx + xpad(e)] = (_Float16)0.f;
+        xs[(size_t)m * ldx + xpad(xperm(e))] = (_Float16)0.f;
     }
 }
 
@@ -348,7 +364,7 @@ __device__ __forceinline__ void xr_load(const FmvPlan& P, const void* __restrict
         } else {
             raw[j][0] = reinterpret_cast<const uint4*>(x)[cc];
         }
-        if (norm) r.w[j] = nv[ok ? c - m * per_col : 0];
+        r.w[j] = nv[ok ? c - m * per_col : 0];  // unconditional (re-reads x without a norm)
     }
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
@@ -376,6 +392,7 @@ __device__ __forceinline__ void xr_load(const FmvPlan& P, const void* __restrict
 
 // Store a round's chunks (fp16) to the padded LDS layout and, when `sums`,
 // their per-16 sums (chunks c and c ^ 1 sit in lanes tid and tid ^ 1).
+// sums == false stores raw chunks in natural order (to be normalised in LDS).
 template <int NC, bool F32, int XR>
 __device__ __forceinline__ void xr_store(int K, int c0, const XChunks<F32, XR>& r, _Float16* xs, float* s16,
                                          bool sums, int tid) {
@@ -391,8 +408,12 @@ __device__ __forceinline__ void xr_store(int K, int c0, const XChunks<F32, XR>& 
             s += lane_pair(s);
         }
         if (c < NC * per_col) {
-            *reinterpret_cast<uint4*>(xs + (size_t)m * ldx + xpad(8 * cl)) =
-                make_uint4(r.h[j][0], r.h[j][1], r.h[j][2], r.h[j][3]);
+            uint32_t h0 = r.h[j][0], h1 = r.h[j][1], h2 = r.h[j][2], h3 = r.h[j][3];
+            if (sums) {  // final values: the xperm layout; raw chunks (sums == false) stay in natural order
+                xperm_words(h0, h1);
+                xperm_words(h2, h3);
+            }
+            *reinterpret_cast<uint4*>(xs + (size_t)m * ldx + xpad(8 * cl)) = make_uint4(h0, h1, h2, h3);
             if (sums && (cl & 1) == 0) s16[m * (K / 16) + (cl >> 1)] = s;
         }
     }
@@ -412,15 +433,40 @@ struct TileW {
     int usb[UPT];
 };
 
-template <int UPT, int FMT>
+// Unit mapping of a tile (R rows of per_row units):
+//  flat (RO false): unit i of this thread is u = tid + i * STRIDE, row u / per_row;
+//  range-owned (RO true): thread tid = rg * per_row + kr keeps unit range kr
+//    (one 64-weight column slice) for rows rg + G * i, G = 256 / per_row, so
+//    its 64 activations are read once and serve all UPT units.
+struct UnitPos {
+    int lr, kr;  // local row, unit index within the row
+};
+template <int UPT, int STRIDE, bool RO>
+__device__ __forceinline__ UnitPos unit_pos(int tid, int i, int per_row) {
+    UnitPos p;
+    if (RO) {
+        const int G = ROWS_THREADS / per_row;
+        const int rg = (int)(((float)tid + 0.5f) * (1.0f / (float)per_row));
+        p.kr = tid - rg * per_row;
+        p.lr = rg < G ? rg + G * i : 0x7fffffff;  // threads past G * per_row hold no unit
+    } else {
+        const int u = tid + i * STRIDE;
+        const int sbg = u >> 2;
+        const int n_sb = per_row >> 2;
+        p.lr = (int)(((float)sbg + 0.5f) * (1.0f / (float)n_sb));
+        p.kr = u - p.lr * per_row;
+    }
+    return p;
+}
+
+template <int UPT, int FMT, int STRIDE = ROWS_THREADS, bool RO = false>
 __device__ __forceinline__ void tile_w_issue(TileW<UPT>& W, const TileGeo& T, int n_sb, int per_row, int tid) {
-    const int units = T.nr * per_row;
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
-        const int u = min(tid + i * ROWS_THREADS, units - 1);  // past the end: re-read the last unit
-        const int sbg = u >> 2, q = u & 3;
-        const int lr = (int)(((float)sbg + 0.5f) * (1.0f / (float)n_sb));
-        const int sb = sbg - lr * n_sb;
+        const UnitPos up = unit_pos<UPT, STRIDE, RO>(tid, i, per_row);
+        // past the tile's end: re-read its last row
+        const int lr = min(up.lr, T.nr - 1);
+        const int sb = up.kr >> 2, q = up.kr & 3;
         W.usb[i] = sb;
         const uint8_t* rowp = lr < T.hA ? T.bA + (size_t)lr * T.rb : T.bB + (size_t)(lr - T.hA) * T.rb;
         if (FMT == 4) {
@@ -474,28 +520,46 @@ __device__ __forceinline__ void tile_e_rope(TileE& E, const FmvPlan& P, const Ti
 }
 
 // The units' partials for every column -> part[m * pstride + unit].
-template <int NC, int UPT, int FMT>
-__device__ __forceinline__ void tile_dot(const TileW<UPT>& W, int units, int K, const _Float16* xs, const float* s16,
-                                         float* part, int pstride, int tid) {
+template <int NC, int UPT, int FMT, int STRIDE = ROWS_THREADS, bool RO = false>
+__device__ __forceinline__ void tile_dot(const TileW<UPT>& W, int nr, int per_row, int K, const _Float16* xs,
+                                         const float* s16, float* part, int pstride, int tid) {
     const int ldx = xpad_len(K);
+    uint4 x[NC][8];
+    float xs16[NC][4];
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
-        const int u = tid + i * ROWS_THREADS;
-        if (u < units) {
-            const int q = u & 3, sb = W.usb[i];
+        const UnitPos up = unit_pos<UPT, STRIDE, RO>(tid, i, per_row);
+        const int q = up.kr & 3, sb = up.kr >> 2;
+        const int h = q >> 1, l16 = (q & 1) * 16;
+        if (!RO || i == 0) {  // range-owned: the unit range, hence x, is the same for every i
+#pragma unroll
+            for (int m = 0; m < NC; ++m) {
+                if (FMT == 4)
+                    q4k_unit_x(xs + (size_t)m * ldx + xpad(sb * QK_K + 64 * q), s16 + m * (K / 16) + sb * 16 + 4 * q,
+                               x[m], xs16[m]);
+                else
+                    q6k_unit_x(xs + (size_t)m * ldx + xpad(sb * QK_K), s16 + m * (K / 16) + sb * 16, h, l16, x[m],
+                               xs16[m]);
+            }
+        }
+        if (up.lr < nr) {
+            const int u = up.lr * per_row + up.kr;
+#ifdef TMV_ABL_DOT
+            if (true) {
+                part[u] = __uint_as_float((W.w0[i].x ^ W.w1[i].y ^ W.w2[i].z ^ W.w0[i].w ^ W.w1[i].x ^ W.w2[i].w ^
+                                           W.dbits[i] ^ W.sc8[i].x) & 0x3fffffffu) + __uint_as_float(x[0][0].x) +
+                          xs16[0][0];
+            } else
+#endif
             if (FMT == 4) {
                 const Q4KUnitData d{W.w0[i], W.w1[i], W.w2[i]};
 #pragma unroll
-                for (int m = 0; m < NC; ++m)
-                    part[m * pstride + u] = q4k_unit_dot(d, q, xs + (size_t)m * ldx + xpad(sb * QK_K + 64 * q),
-                                                         s16 + m * (K / 16) + sb * 16 + 4 * q);
+                for (int m = 0; m < NC; ++m) part[m * pstride + u] = q4k_unit_dot_x(d, q, x[m], xs16[m]);
             } else {
-                const int h = q >> 1, l16 = (q & 1) * 16;
 #pragma unroll
                 for (int m = 0; m < NC; ++m)
-                    part[m * pstride + u] = q6k_unit_dot_r(W.w0[i], W.w1[i], W.w2[i], W.sc8[i], W.dbits[i], l16,
-                                                           xs + (size_t)m * ldx + xpad(sb * QK_K),
-                                                           s16 + m * (K / 16) + sb * 16, h);
+                    part[m * pstride + u] = q6k_unit_dot_x(W.w0[i], W.w1[i], W.w2[i], W.sc8[i], W.dbits[i], l16,
+                                                           x[m], xs16[m]);
             }
         }
     }
@@ -621,7 +685,9 @@ __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const F
     if (tid < M) pos_s[tid] = pos_reg;
     __syncthreads();
     TMV_TS(1);
+    TMV_M(3);
     issue();
+    TMV_M(4);
 
     if (att_src) {
         stage_combine<NC>(P, L.xs, wb, pos_s, tid);
@@ -658,6 +724,8 @@ __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const F
                 chunk_norm(h, nv[cl], iv);
                 float s = chunk_sum(h);
                 s += lane_pair(s);
+                xperm_words(h[0], h[1]);
+                xperm_words(h[2], h[3]);
                 if (ok) {
                     *px = make_uint4(h[0], h[1], h[2], h[3]);
                     if ((cl & 1) == 0) L.s16[m * (K / 16) + (cl >> 1)] = s;
@@ -671,7 +739,7 @@ __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const F
 
 // One tile per block (grid = tiles): everything a block reads is requested
 // up front, so a block costs about one memory latency plus its arithmetic.
-template <int NC, bool F32, int UPT, int FMT, int KC>
+template <int NC, bool F32, int UPT, int FMT, int KC, bool RO>
 __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPlan& P, const TileGeo& T,
                                          uint8_t* lds, float (*red)[NC], int* pos_s) {
     const int K = KC > 0 ? KC : P.K, M = NC == 1 ? 1 : P.M;
@@ -681,16 +749,19 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     float* wb = L.part + (size_t)NC * pstride;
     const int tid = threadIdx.x;
     TMV_TS(0);
+    TMV_M(1);
     const void* dummy = P.seg[0].w;
     TileE E;
     tile_e_issue<NC>(E, P, T, M, dummy, tid);
-    const int pos_e = (int)ld_elem_bits(P.kv_offset, dummy, E.em, true);
+    TMV_M(2);
     TileW<UPT> W;
     fmv_prologue<NC, F32, KC>(x, P, L, wb, red, pos_s, [&]() {
-        tile_w_issue<UPT, FMT>(W, T, n_sb, per_row, tid);
-        tile_e_rope(E, P, T, pos_e, dummy);
+        tile_w_issue<UPT, FMT, ROWS_THREADS, RO>(W, T, n_sb, per_row, tid);
+        tile_e_rope(E, P, T, pos_s[E.em], dummy);  // kv offsets are in LDS after the first barrier
     });
-    tile_dot<NC, UPT, FMT>(W, T.nr * per_row, K, L.xs, L.s16, L.part, pstride, tid);
+    TMV_M(5);
+    tile_dot<NC, UPT, FMT, ROWS_THREADS, RO>(W, T.nr, per_row, K, L.xs, L.s16, L.part, pstride, tid);
+    TMV_M(6);
     __syncthreads();
     TMV_TS(3);
 #ifdef TMV_TRACE
@@ -703,20 +774,108 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
         tmv_trace[blockIdx.x][4] = wall_clock64();
     }
 #endif
+    TMV_M(7);
     tile_epilogue<NC>(P, T, E, L.part, pstride, per_row, pos_s);
+    TMV_M(8);
 }
 
 // KC: the activation length K when fixed at compile time (0: P.K), so the
 // staging, norm and row-sum loops have constant trip counts and no divisions.
-template <int NC, bool F32, int UPT, int KC>
+// RO: range-owned unit mapping (see unit_pos).
+template <int NC, bool F32, int UPT, int KC, bool RO>
 __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const void* __restrict__ x, FmvPlan P) {
     extern __shared__ uint4 smem_fmv[];
     __shared__ float red[4][NC];
     __shared__ int pos_s[NC];
     const TileGeo T = tile_geo(P, blockIdx.x);
     uint8_t* lds = reinterpret_cast<uint8_t*>(smem_fmv);
-    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4, KC>(x, P, T, lds, red, pos_s);
-    else tmv_body<NC, F32, UPT, 6, KC>(x, P, T, lds, red, pos_s);
+    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4, KC, RO>(x, P, T, lds, red, pos_s);
+    else tmv_body<NC, F32, UPT, 6, KC, RO>(x, P, T, lds, red, pos_s);
+}
+
+// Wave-owned rows (batch 1, store epilogues, one segment): after the block
+// prologue every wave works on its own: group g of R = 64 * UPT / per_row
+// whole rows, units lane + 64 i, groups g = wave id, + waves in the grid, ...
+// with the next group's weights requested before the current group is
+// computed (register sets A and B).  Row sums go through the wave's own LDS
+// slice, so the loop has no block barrier and the waves of a CU drift apart,
+// overlapping one wave's arithmetic with another's loads.  The activations
+// are staged once per block instead of once per tile.
+template <int UPT, int FMT>
+__device__ __forceinline__ TileGeo wave_group_geo(const FmvSeg& S, int g, int R) {
+    TileGeo T;
+    T.fmt = FMT;
+    T.mode = S.mode;
+    T.rb = S.row_bytes;
+    T.n_rows = S.n_rows;
+    T.out = S.out;
+    T.bias = S.bias;
+    T.residual = S.residual;
+    T.j0 = g * R;
+    T.nr = min(R, S.n_rows - T.j0);
+    T.hA = T.nr;
+    T.bA = S.w + (size_t)T.j0 * S.row_bytes;
+    T.bB = T.bA;
+    return T;
+}
+
+template <bool F32, int UPT, int FMT, int KC>
+__global__ __launch_bounds__(ROWS_THREADS) void wave_mv_kernel(const void* __restrict__ x, FmvPlan P) {
+    extern __shared__ uint4 smem_fmv[];
+    __shared__ float red[4][1];
+    __shared__ int pos_s[1];
+    const int K = KC > 0 ? KC : P.K;
+    const int n_sb = K / QK_K, per_row = n_sb * 4;
+    const int R = 64 * UPT / per_row;  // rows per group (the host checked per_row divides 64 * UPT)
+    const FmvLDS L = fmv_lds(reinterpret_cast<uint8_t*>(smem_fmv), 1, K, UPT);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    float* part = L.part + wv * 64 * UPT;  // this wave's partials
+    const FmvSeg& S = P.seg[0];
+    const int groups = (S.n_rows + R - 1) / R, last = groups - 1;
+    const int nW = gridDim.x * (ROWS_THREADS / 64);
+    const bool f32o = S.mode == FMV_STORE_F32;
+    const void* dummy = S.w;
+    int g = blockIdx.x * (ROWS_THREADS / 64) + wv;
+    TileGeo TA = wave_group_geo<UPT, FMT>(S, min(g, last), R), TB;
+    TileW<UPT> WA, WB;
+    uint32_t bA, rA, bB, rB;  // bias / residual of this lane's row (lanes < R)
+    auto issue = [&](TileW<UPT>& W, const TileGeo& T, uint32_t& b, uint32_t& r) {
+        tile_w_issue<UPT, FMT, 64>(W, T, n_sb, per_row, lane);
+        const int row = T.j0 + min(lane, T.nr - 1);
+        b = ld_elem_bits(S.bias, dummy, row, f32o);
+        r = ld_elem_bits(S.residual, dummy, row, f32o);
+    };
+    auto finish = [&](const TileW<UPT>& W, const TileGeo& T, uint32_t b, uint32_t r) {
+        tile_dot<1, UPT, FMT, 64>(W, T.nr, per_row, K, L.xs, L.s16, part, 0, lane);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < T.nr) {
+            float v = row_sum(part + lane * per_row, per_row) + (f32o ? __uint_as_float(b) : h2f_bits(b));
+            v = v * P.rs + (f32o ? __uint_as_float(r) : h2f_bits(r));
+            const size_t oi = (size_t)T.j0 + lane;
+            if (f32o) reinterpret_cast<float*>(S.out)[oi] = v;
+            else reinterpret_cast<__half*>(S.out)[oi] = __float2half(v);
+        }
+        // the partials are re-written by the next group only after every lane read them
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    fmv_prologue<1, F32, KC>(x, P, L, nullptr, red, pos_s, [&]() { issue(WA, TA, bA, rA); });
+    if (g > last) return;
+    for (;;) {
+        const int gb = g + nW;
+        TB = wave_group_geo<UPT, FMT>(S, min(gb, last), R);
+        issue(WB, TB, bB, rB);
+        finish(WA, TA, bA, rA);
+        if (gb > last) break;
+        g = gb + nW;
+        TA = wave_group_geo<UPT, FMT>(S, min(g, last), R);
+        issue(WA, TA, bA, rA);
+        finish(WB, TB, bB, rB);
+        if (g > last) break;
+    }
 }
 
 namespace vte {
@@ -745,9 +904,11 @@ static size_t fmv_lds_bytes(int NC, int K, int upt, int att_rows) {
 // Rows per tile: as many as fill the block with one unit per thread (0 if a
 // single row has more units than threads).  RoPE tiles take a power-of-two
 // number of rows per half so tiles never straddle a head.
+static bool fmv_ro(int K);
 static int fmv_rows_per_tile(int mode, int K, int upt) {
     const int per_row = (K / QK_K) * 4;
-    const int R = upt * ROWS_THREADS / per_row;
+    // range-owned tiles: 256 / per_row row groups of upt rows
+    const int R = fmv_ro(K) ? (ROWS_THREADS / per_row) * upt : upt * ROWS_THREADS / per_row;
     if (R < 1) return 0;
     if (mode == FMV_SWIGLU) return R >= 2 ? std::min(R & ~1, TMV_MAX_R) : 0;
     if (mode == FMV_ROPE_Q || mode == FMV_ROPE_KCACHE) {
@@ -758,21 +919,47 @@ static int fmv_rows_per_tile(int mode, int K, int upt) {
     return std::min(R, TMV_MAX_R);
 }
 
-template <int NC, bool F32, int KC>
+template <int NC, bool F32, int KC, bool RO>
 static void fmv_launch_k(int upt, int total, size_t lds, hipStream_t st, const void* x, const FmvPlan& plan) {
     const dim3 g(total), b(ROWS_THREADS);
-    if (upt == 4) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4, KC>), g, b, lds, st, x, plan);
-    else if (upt == 2) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 2, KC>), g, b, lds, st, x, plan);
-    else hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 1, KC>), g, b, lds, st, x, plan);
+    if (upt == 4) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4, KC, RO>), g, b, lds, st, x, plan);
+    else if (upt == 2) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 2, KC, RO>), g, b, lds, st, x, plan);
+    else hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 1, KC, RO>), g, b, lds, st, x, plan);
+}
+
+// Range-owned mapping when a row's units fill the block's threads with at
+// most 1/16 of them idle (e.g. K = 1536: 24 units per row, 240 of 256
+// threads); otherwise (e.g. K = 8960) the flat mapping.
+static bool fmv_ro(int K) {
+    const int per_row = (K / QK_K) * 4;
+    return per_row <= 64 && (ROWS_THREADS % per_row) * 16 <= ROWS_THREADS;
 }
 
 // Compile-time K for the fp16-activation shapes of the 1.5B decode step
 // (hidden 1536, FFN 8960); any other K takes the runtime-K kernels.
 template <int NC, bool F32>
 static void fmv_launch(int upt, int total, size_t lds, hipStream_t st, const void* x, const FmvPlan& plan) {
-    if (!F32 && plan.K == 1536) fmv_launch_k<NC, F32, F32 ? 0 : 1536>(upt, total, lds, st, x, plan);
-    else if (!F32 && plan.K == 8960) fmv_launch_k<NC, F32, F32 ? 0 : 8960>(upt, total, lds, st, x, plan);
-    else fmv_launch_k<NC, F32, 0>(upt, total, lds, st, x, plan);
+    if (!F32 && plan.K == 1536) fmv_launch_k<NC, F32, F32 ? 0 : 1536, true>(upt, total, lds, st, x, plan);
+    else if (!F32 && plan.K == 8960) fmv_launch_k<NC, F32, F32 ? 0 : 8960, false>(upt, total, lds, st, x, plan);
+    else if (fmv_ro(plan.K)) fmv_launch_k<NC, F32, 0, true>(upt, total, lds, st, x, plan);
+    else fmv_launch_k<NC, F32, 0, false>(upt, total, lds, st, x, plan);
+}
+
+template <bool F32, int UPT, int KC>
+static void wave_launch_k(int fmt, int grid, size_t lds, hipStream_t st, const void* x, const FmvPlan& plan) {
+    if (fmt == 4)
+        hipLaunchKernelGGL((wave_mv_kernel<F32, UPT, 4, KC>), dim3(grid), dim3(ROWS_THREADS), lds, st, x, plan);
+    else
+        hipLaunchKernelGGL((wave_mv_kernel<F32, UPT, 6, KC>), dim3(grid), dim3(ROWS_THREADS), lds, st, x, plan);
+}
+
+template <bool F32>
+static void wave_launch(int upt, int fmt, int grid, size_t lds, hipStream_t st, const void* x, const FmvPlan& plan) {
+    if (plan.K == 1536 && upt == 3) wave_launch_k<F32, 3, 1536>(fmt, grid, lds, st, x, plan);
+    else if (upt == 1) wave_launch_k<F32, 1, 0>(fmt, grid, lds, st, x, plan);
+    else if (upt == 2) wave_launch_k<F32, 2, 0>(fmt, grid, lds, st, x, plan);
+    else if (upt == 3) wave_launch_k<F32, 3, 0>(fmt, grid, lds, st, x, plan);
+    else wave_launch_k<F32, 4, 0>(fmt, grid, lds, st, x, plan);
 }
 
 static int env_int(const char* name, int dflt) {
@@ -828,6 +1015,36 @@ hipError_t fused_mv(const void* x, FmvPlan plan, hipStream_t st) {
     if (plan.norm_w != nullptr && (reinterpret_cast<uintptr_t>(plan.norm_w) & 15)) return hipErrorInvalidValue;
     const int NC = plan.M <= 1 ? 1 : (plan.M <= 2 ? 2 : 4);
     const int att_rows = plan.att_o != nullptr ? plan.M * plan.att_nq * plan.att_S : 0;
+    // Wave-owned rows for long single-segment batch-1 store launches (the LM
+    // head): units per thread such that whole rows fill a wave, enough row
+    // groups for every wave of the grid to take several.  VTE_FMV_WAVE: 0 off,
+    // 2 whenever the shape fits (tuning).
+    static int wave_mode = -1;
+    if (wave_mode < 0) wave_mode = env_int("VTE_FMV_WAVE", 1);
+    const int per_row = (plan.K / QK_K) * 4;
+    if (wave_mode > 0 && NC == 1 && plan.nseg == 1 && plan.att_o == nullptr &&
+        (plan.seg[0].mode == FMV_STORE_F16 || plan.seg[0].mode == FMV_STORE_F32) &&
+        (plan.seg[0].fmt == 4 || plan.seg[0].fmt == 6)) {
+        int upt = 0;
+        for (int u = 1; u <= 4 && upt == 0; ++u)
+            if ((64 * u) % per_row == 0) upt = u;
+        static int wave_bpc = -1;  // blocks per CU (VTE_FMV_WBPC, tuning)
+        if (wave_bpc < 0) wave_bpc = env_int("VTE_FMV_WBPC", 2);
+        const int grid = wave_bpc * fmv_num_cus();
+        if (upt > 0) {
+            const int R = 64 * upt / per_row;
+            const int groups = (plan.seg[0].n_rows + R - 1) / R;
+            const size_t lds = fmv_lds_bytes(1, plan.K, upt, 0);
+            if ((wave_mode == 2 || groups >= 2 * grid * (ROWS_THREADS / 64)) && lds + 64 <= fmv_max_lds()) {
+                FmvPlan P = plan;
+                P.seg[0].row_bytes = (plan.K / QK_K) * (plan.seg[0].fmt == 4 ? Q4K_BYTES : Q6K_BYTES);
+                P.total = groups;
+                if (P.x_f32) wave_launch<true>(upt, P.seg[0].fmt, grid, lds, st, x, P);
+                else wave_launch<false>(upt, P.seg[0].fmt, grid, lds, st, x, P);
+                return hipGetLastError();
+            }
+        }
+    }
     static int upt_force = -1;  // VTE_FMV_UPT=1|2|4 pins units per thread (tuning)
     if (upt_force < 0) upt_force = env_int("VTE_FMV_UPT", 0);
     for (int upt : {4, 2, 1}) {

@@ -67,16 +67,27 @@ template <> __device__ __forceinline__ void ld_act16<__half>(const __half* p, fl
     }
 }
 
-// Full-wave sum (64 lanes); every lane receives the total.
+// Full-wave reductions (all 64 lanes active); every lane receives the result.
+// Within each row of 16 lanes: DPP quad permutes [1,0,3,2] and [2,3,0,1],
+// then row_half_mirror and row_mirror (each pairs a lane with one in the
+// other half); the four row results are read into scalars.  No LDS traffic.
+#define VTE_DPP_F(v, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), 0xF, 0xF, false))
+__device__ __forceinline__ float wave_rows4(float v, int r) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * r));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, VTE_WAVE);
-    return v;
+    v += VTE_DPP_F(v, 0xB1);
+    v += VTE_DPP_F(v, 0x4E);
+    v += VTE_DPP_F(v, 0x141);
+    v += VTE_DPP_F(v, 0x140);
+    return (wave_rows4(v, 0) + wave_rows4(v, 1)) + (wave_rows4(v, 2) + wave_rows4(v, 3));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, VTE_WAVE));
-    return v;
+    v = fmaxf(v, VTE_DPP_F(v, 0xB1));
+    v = fmaxf(v, VTE_DPP_F(v, 0x4E));
+    v = fmaxf(v, VTE_DPP_F(v, 0x141));
+    v = fmaxf(v, VTE_DPP_F(v, 0x140));
+    return fmaxf(fmaxf(wave_rows4(v, 0), wave_rows4(v, 1)), fmaxf(wave_rows4(v, 2), wave_rows4(v, 3)));
 }
 
 // GEMV epilogue shared by every format, same order as the reference:
