@@ -9,10 +9,10 @@ sequence) and issues the launches of one layer.  MI355X choices:
   and the LSE combine, either as a second launch or, with ``fuse_combine``,
   inside the partial kernel's last block per (sequence, KV head); the KV
   append is a separate tiny launch as in the reference;
-* the split is a token count per block (multiple of 32, at least 128 so each
-  of the block's four waves has a full 32-token MFMA step), chosen so
-  batch x kv_heads x splits covers the GPU about twice at the longest context
-  (the reference's 1024/num_cus rule gives 4-token chunks on 256 CUs);
+* the split is a token count per block (multiple of 32; 128 = one 32-token
+  MFMA step per wave of the block's four), kept at 128 while a sequence has
+  at most 128 splits (see ``choose_split``; the reference's 1024/num_cus
+  rule gives 4-token chunks on 256 CUs);
 * the per-sequence split count is derived on the device from kv_offset[b],
   so ragged batches inside one captured graph only touch their own splits.
 """
@@ -24,11 +24,14 @@ from ..kernels import kernels
 
 
 def choose_split(max_context: int, batch: int, n_kv: int, num_cus: int) -> int:
-    """Tokens per split block: power of two in [128, 1024]."""
-    target_blocks = 2 * max(num_cus, 1)
-    want = max_context * batch * n_kv / target_blocks
+    """Tokens per split block: 128 (one 32-token tile per wave, the most
+    blocks in flight) while that leaves at most 128 splits per sequence -- the
+    combine's one-round-trip form -- else the smallest power of two up to 1024
+    that does.  Measured on MI355X: at a 2K context 128-token splits beat
+    256-token ones both at batch 1 and 16 (the two-tile form holds more
+    registers and halves the blocks)."""
     split = 128
-    while split < want and split < 1024:
+    while max_context > 128 * split and split < 1024:
         split *= 2
     return split
 
