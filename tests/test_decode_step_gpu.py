@@ -63,7 +63,7 @@ def test_tiny_step_matches_oracle(hip, tiny_model, B):
         ex.close()
 
 
-@pytest.mark.parametrize("B", [1, 2, 4])
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 20])
 def test_fused_step_matches_unfused(hip, tiny_model, B):
     """Fused norm/QKV/RoPE/append, gate/up/SwiGLU and norm/LM-head kernels give the
     same step as the separate kernels (same rounding points, fp32 sums reordered)."""

@@ -111,3 +111,64 @@ def test_attn_in(hip, K, k, n_q, n_kv, positions):
         # nothing else of this sequence's cache was written
         others = np.delete(np.arange(max_seq), pos)
         assert not got_k[m, others].any() and not got_v[m, others].any()
+
+
+@pytest.mark.parametrize("B,fmt_v", [(8, "q6_k"), (16, "q6_k"), (40, "q4_k")])
+def test_attn_in_batched_mfma(hip, K, B, fmt_v):
+    """Batch > 4 (MFMA, launches of 32 sequences): pre-normalised fp16 x,
+    q/k/v + bias + RoPE + K/V rows at ragged positions."""
+    k, n_q, n_kv, hd, max_seq = 1536, 12, 2, 128, 320
+    rng = np.random.default_rng(B)
+    wq, wk, wv = _mat("q4_k", n_q * hd, k, 11), _mat("q4_k", n_kv * hd, k, 12), _mat(fmt_v, n_kv * hd, k, 13)
+    bq = (0.1 * rng.standard_normal(n_q * hd)).astype(np.float16)
+    bk = (0.1 * rng.standard_normal(n_kv * hd)).astype(np.float16)
+    bv = (0.1 * rng.standard_normal(n_kv * hd)).astype(np.float16)
+    xn = ost.rmsnorm(_x(rng, B, k), _w(rng, k), EPS)
+    positions = rng.integers(0, max_seq, B).astype(np.int32)
+    cos_c, sin_c = ost.rope_cache(max_seq, hd, 1e6)
+    stride = max_seq * n_kv * hd
+    q_out = empty(hip, (B, n_q * hd), np.float16)
+    kc = empty(hip, (B, max_seq, n_kv, hd), np.float16)
+    vc = empty(hip, (B, max_seq, n_kv, hd), np.float16)
+    K.attn_in(up(hip, xn), None, EPS, up(hip, wq), up(hip, bq), "q4_k", up(hip, wk), up(hip, bk), "q4_k",
+              up(hip, wv), up(hip, bv), fmt_v, q_out, kc, vc, up(hip, positions), stride,
+              up(hip, cos_c), up(hip, sin_c), B, k, n_q, n_kv, stream=hip.stream)
+    x32 = xn.astype(np.float32)
+    got_q, got_k, got_v = down(q_out), down(kc), down(vc)
+    q = (dq.gemv("q4_k", wq, n_q * hd, k, x32) + bq.astype(np.float32)).astype(np.float16)
+    kk = (dq.gemv("q4_k", wk, n_kv * hd, k, x32) + bk.astype(np.float32)).astype(np.float16)
+    v = (dq.gemv(fmt_v, wv, n_kv * hd, k, x32) + bv.astype(np.float32)).astype(np.float16)
+    for m, pos in enumerate(positions):
+        assert rel_l2(got_q[m], ost.rope_neox(q[m].reshape(n_q, hd), pos, cos_c, sin_c).reshape(-1)) <= TOL, m
+        assert rel_l2(got_k[m, pos], ost.rope_neox(kk[m].reshape(n_kv, hd), pos, cos_c, sin_c)) <= TOL, m
+        assert rel_l2(got_v[m, pos], v[m].reshape(n_kv, hd)) <= TOL, m
+        others = np.delete(np.arange(max_seq), pos)
+        assert not got_k[m, others].any() and not got_v[m, others].any()
+
+
+@pytest.mark.parametrize("B,ffn", [(8, 8960), (20, 1000), (33, 512)])
+def test_ffn_in_batched_mfma(hip, K, B, ffn):
+    """Batch > 4 (MFMA): gate/up + SwiGLU on pre-normalised fp16 x."""
+    k = 1536
+    rng = np.random.default_rng(ffn + B)
+    wg, wu = _mat("q4_k", ffn, k, 15), _mat("q4_k", ffn, k, 16)
+    xn = (ost.rmsnorm(_x(rng, B, k), _w(rng, k), EPS).astype(np.float32) * 0.05).astype(np.float16)
+    out = empty(hip, (B, ffn), np.float16)
+    K.ffn_in(up(hip, xn), None, EPS, up(hip, wg), up(hip, wu), "q4_k", out, B, k, ffn, stream=hip.stream)
+    x32 = xn.astype(np.float32)
+    g = dq.gemv("q4_k", wg, ffn, k, x32).astype(np.float16)
+    u = dq.gemv("q4_k", wu, ffn, k, x32).astype(np.float16)
+    assert rel_l2(down(out), ost.swiglu(g, u)) <= TOL
+
+
+def test_batch_above_4_rejects_fused_norm(hip, K):
+    """The MFMA path takes normalised activations: passing norm weights is an error."""
+    import ctypes
+    k, ffn, B = 256, 64, 8
+    x = empty(hip, (B, k), np.float16)
+    nw = empty(hip, k, np.float16)
+    w = empty(hip, (ffn, k // 256 * 144), np.uint8)
+    out = empty(hip, (B, ffn), np.float16)
+    rc = K.lib.vte_ffn_in(ctypes.c_void_p(x.ptr), ctypes.c_void_p(nw.ptr), ctypes.c_float(EPS), ctypes.c_void_p(w.ptr),
+                          ctypes.c_void_p(w.ptr), 4, ctypes.c_void_p(out.ptr), B, k, ffn, None)
+    assert rc == -1 and b"norm_w must be NULL" in K.lib.vte_last_error()

@@ -11,7 +11,8 @@ MI355X-specific structure:
 * every tensor lives in one slab (fixed addresses for capture), KV cache per
   layer [B][max_seq][n_kv][hd] fp16 as in vte/compiler/qwen_mapper.py:300-351;
 * projections run the VALU quant GEMV below ``gemm_min_batch`` sequences and
-  the MFMA dequant-to-fp16 GEMM at or above it;
+  the MFMA dequant-to-fp16 GEMM at or above it, where q/k/v + RoPE + K/V
+  append and gate/up + SwiGLU are one launch each (``mm_fused``);
 * attention is the GQA split-KV pair (partial + combine) with per-sequence
   lengths read from ``kv_offset`` on the device, so ragged batches share a graph;
 * the LM head writes fp32 logits and an on-device top-k (default 40) leaves
@@ -51,6 +52,9 @@ class HIPGraphExecutor:
         self.gemm_min_batch = gemm_min_batch
         # fused norm+QKV+RoPE+append / norm+gate+up+SwiGLU / norm+LM-head kernels (batch <= 4)
         self.fused = fused and batch_size <= 4
+        # batch >= gemm_min_batch: MFMA launches with the QKV+RoPE+append and
+        # gate/up+SwiGLU glue fused in (RMSNorm stays its own launch)
+        self.mm_fused = fused and batch_size >= gemm_min_batch
         self.K = kernels()
         self.graph = None
         self.graph_exec = None
@@ -211,21 +215,31 @@ class HIPGraphExecutor:
         K.embedding_q6k(self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
         for L, lw in enumerate(self.layers):
             K.rmsnorm(self.h[cur], lw["attn_norm"], self.xn, B, H, cfg.eps, stream=st)
-            self._linear(lw["q_fmt"], self.xn, lw["q"], self.q, H, cfg.q_dim, bias=lw["q_bias"])
-            self._linear(lw["k_fmt"], self.xn, lw["k"], self.k, H, cfg.kv_dim, bias=lw["k_bias"])
-            self._linear(lw["v_fmt"], self.xn, lw["v"], self.v, H, cfg.kv_dim, bias=lw["v_bias"])
-            K.rope(self.q, self.k, self.rope_cos, self.rope_sin, B, 1, cfg.n_q, cfg.n_kv, cfg.head_dim, offs, 0, 0,
-                   stream=st)
-            K.kv_append(self.k, self.v, self.k_cache[L], self.v_cache[L], B, cfg.n_kv, cfg.head_dim, offs,
-                        self.kv_batch_stride, stream=st)
+            if self.mm_fused:  # q/k/v + bias + RoPE + K/V append in one MFMA launch
+                K.attn_in(self.xn, None, cfg.eps, lw["q"], lw["q_bias"], lw["q_fmt"], lw["k"], lw["k_bias"],
+                          lw["k_fmt"], lw["v"], lw["v_bias"], lw["v_fmt"], self.q, self.k_cache[L], self.v_cache[L],
+                          offs, self.kv_batch_stride, self.rope_cos, self.rope_sin, B, H, cfg.n_q, cfg.n_kv,
+                          cfg.head_dim, stream=st)
+            else:
+                self._linear(lw["q_fmt"], self.xn, lw["q"], self.q, H, cfg.q_dim, bias=lw["q_bias"])
+                self._linear(lw["k_fmt"], self.xn, lw["k"], self.k, H, cfg.kv_dim, bias=lw["k_bias"])
+                self._linear(lw["v_fmt"], self.xn, lw["v"], self.v, H, cfg.kv_dim, bias=lw["v_bias"])
+                K.rope(self.q, self.k, self.rope_cos, self.rope_sin, B, 1, cfg.n_q, cfg.n_kv, cfg.head_dim, offs, 0,
+                       0, stream=st)
+                K.kv_append(self.k, self.v, self.k_cache[L], self.v_cache[L], B, cfg.n_kv, cfg.head_dim, offs,
+                            self.kv_batch_stride, stream=st)
             self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], self.att, offs, self.kv_batch_stride,
                              dtype="f16", batch=B, stream=st)
             self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
             cur = 1 - cur
             K.rmsnorm(self.h[cur], lw["ffn_norm"], self.xn, B, H, cfg.eps, stream=st)
-            self._linear(lw["gate_fmt"], self.xn, lw["gate"], self.g, H, cfg.ffn)
-            self._linear(lw["up_fmt"], self.xn, lw["up"], self.u, H, cfg.ffn)
-            K.swiglu(self.g, self.u, self.a, B * cfg.ffn, stream=st)
+            if self.mm_fused and lw["gate_fmt"] == "q4_k" and lw["up_fmt"] == "q4_k":  # gate/up + SwiGLU
+                K.ffn_in(self.xn, None, cfg.eps, lw["gate"], lw["up"], lw["gate_fmt"], self.a, B, H, cfg.ffn,
+                         stream=st)
+            else:
+                self._linear(lw["gate_fmt"], self.xn, lw["gate"], self.g, H, cfg.ffn)
+                self._linear(lw["up_fmt"], self.xn, lw["up"], self.u, H, cfg.ffn)
+                K.swiglu(self.g, self.u, self.a, B * cfg.ffn, stream=st)
             self._linear(lw["down_fmt"], self.a, lw["down"], self.h[1 - cur], cfg.ffn, H, residual=self.h[cur])
             cur = 1 - cur
         self.h_final = cur

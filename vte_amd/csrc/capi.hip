@@ -47,6 +47,12 @@ hipError_t attn_in(const void* x, const void* norm_w, float eps, const void* wq,
                    const void* rope_cos, const void* rope_sin, int M, int K, int n_q, int n_kv, hipStream_t st);
 hipError_t ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up, int fmt,
                   void* out, int M, int K, int ffn, hipStream_t st);
+hipError_t qkv_mm(const void* xn, const void* wq, const void* q_bias, int fmt_q, const void* wk, const void* k_bias,
+                  int fmt_k, const void* wv, const void* v_bias, int fmt_v, void* q_out, void* k_cache, void* v_cache,
+                  const int* kv_offset, int kv_batch_stride, const void* rope_cos, const void* rope_sin, int B, int K,
+                  int n_q, int n_kv, hipStream_t st);
+hipError_t gate_up_mm(const void* xn, const void* w_gate, const void* w_up, int fmt, void* out, int B, int K, int ffn,
+                      hipStream_t st);
 hipError_t norm_mv(const void* x, const void* norm_w, float eps, const void* w, int fmt, void* out, bool out_f32,
                    const void* bias, const void* residual, float rs, int M, int K, int N, hipStream_t st);
 }  // namespace vte
@@ -241,29 +247,42 @@ int vte_attn_in(const void* x, const void* norm_w, float eps, const void* wq, co
                 void* q_out, void* k_cache, void* v_cache, const int* kv_offset, int kv_batch_stride,
                 const void* rope_cos, const void* rope_sin, int batch, int hidden, int n_q, int n_kv, int head_dim,
                 void* stream) {
-    REQUIRE(x && norm_w && wq && wk && wv && q_out && k_cache && v_cache && kv_offset && rope_cos && rope_sin,
+    REQUIRE(x && wq && wk && wv && q_out && k_cache && v_cache && kv_offset && rope_cos && rope_sin,
             "attn_in: null pointer");
     REQUIRE(head_dim == 128, "attn_in: head_dim must be 128");
-    REQUIRE(batch >= 1 && batch <= 4, "attn_in: batch %d outside 1..4 (larger batches use the MFMA path)", batch);
+    REQUIRE(batch >= 1 && batch <= 4096, "attn_in: batch %d outside 1..4096", batch);
+    REQUIRE(batch <= 4 || norm_w == nullptr,
+            "attn_in: batch %d > 4 takes RMSNorm-ed activations (norm_w must be NULL)", batch);
     REQUIRE(hidden % 256 == 0 && hidden <= 8192, "attn_in: hidden %d unsupported", hidden);
     REQUIRE(fmt_q == 4 && fmt_k == 4 && (fmt_v == 4 || fmt_v == 6), "attn_in: q/k must be Q4_K, v Q4_K or Q6_K");
     REQUIRE(n_kv >= 1 && n_q >= n_kv && n_q % n_kv == 0, "attn_in: bad head counts");
-    REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(wq, 16) && aligned(wk, 16) && aligned(wv, 16), "attn_in: 16-byte alignment");
-    hipError_t e = vte::attn_in(x, norm_w, eps, wq, q_bias, fmt_q, wk, k_bias, fmt_k, wv, v_bias, fmt_v, q_out,
-                                k_cache, v_cache, kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q,
-                                n_kv, (hipStream_t)stream);
+    REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(wq, 16) && aligned(wk, 16) && aligned(wv, 16),
+            "attn_in: 16-byte alignment");
+    hipError_t e;
+    if (batch <= 4)
+        e = vte::attn_in(x, norm_w, eps, wq, q_bias, fmt_q, wk, k_bias, fmt_k, wv, v_bias, fmt_v, q_out, k_cache,
+                         v_cache, kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q, n_kv,
+                         (hipStream_t)stream);
+    else
+        e = vte::qkv_mm(x, wq, q_bias, fmt_q, wk, k_bias, fmt_k, wv, v_bias, fmt_v, q_out, k_cache, v_cache,
+                        kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q, n_kv, (hipStream_t)stream);
     if (e == hipErrorNotSupported) return fail("attn_in: shape does not fit the fused kernel's LDS plan");
     return hip_status(e, "vte_attn_in launch");
 }
 
 int vte_ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up, int fmt,
                void* out, int batch, int hidden, int ffn, void* stream) {
-    REQUIRE(x && norm_w && w_gate && w_up && out, "ffn_in: null pointer");
+    REQUIRE(x && w_gate && w_up && out, "ffn_in: null pointer");
     REQUIRE(fmt == 4, "ffn_in: gate/up must be Q4_K");
-    REQUIRE(batch >= 1 && batch <= 4, "ffn_in: batch %d outside 1..4", batch);
+    REQUIRE(batch >= 1 && batch <= 4096, "ffn_in: batch %d outside 1..4096", batch);
+    REQUIRE(batch <= 4 || norm_w == nullptr,
+            "ffn_in: batch %d > 4 takes RMSNorm-ed activations (norm_w must be NULL)", batch);
     REQUIRE(hidden % 256 == 0 && hidden <= 8192 && ffn >= 1, "ffn_in: bad shape");
-    REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(w_gate, 16) && aligned(w_up, 16), "ffn_in: 16-byte alignment");
-    hipError_t e = vte::ffn_in(x, norm_w, eps, w_gate, w_up, fmt, out, batch, hidden, ffn, (hipStream_t)stream);
+    REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(w_gate, 16) && aligned(w_up, 16),
+            "ffn_in: 16-byte alignment");
+    hipError_t e = batch <= 4
+                       ? vte::ffn_in(x, norm_w, eps, w_gate, w_up, fmt, out, batch, hidden, ffn, (hipStream_t)stream)
+                       : vte::gate_up_mm(x, w_gate, w_up, fmt, out, batch, hidden, ffn, (hipStream_t)stream);
     if (e == hipErrorNotSupported) return fail("ffn_in: shape does not fit the fused kernel's LDS plan");
     return hip_status(e, "vte_ffn_in launch");
 }

@@ -1,0 +1,388 @@
+// Batched (B >= 8) projections with the decode-step glue fused in, on MFMA
+// (gfx950).  One launch per group of projections that read the same
+// (already RMSNorm-ed, fp16) activations:
+//
+//   q/k/v (+bias) -> RoPE(q, k) -> K/V cache append       => one launch
+//   gate/up -> SwiGLU                                       => one launch
+//
+// (reference nodes: vte/compiler/qwen_compute.py:100-282, captured by
+// vte/core/hip_graph_executor.py:504-738), with the rounding points of those
+// nodes: projections (+bias) and rotated q/k are fp16 values computed in fp32,
+// SwiGLU is fp16(g / (1 + exp(-g)) * u) on fp16 g and u
+// (rope.hip.template:82-97, swiglu.hip.template:11-25).
+//
+// Tiles are 16 * RT weight rows; paired tiles hold 8 * RT rows and their
+// partners (RoPE: d and d + 64 of one head; SwiGLU: gate row j and up row j),
+// so a pair's two sums finish in the same block.  The A operand of each lane
+// comes from its tile row's weight row; everything else is the batched MFMA
+// GEMM (8 waves split K, partial C tiles summed through LDS), whose k-slot
+// map and dequantisation it shares (mfma_deq.h).
+#include <cstring>
+
+#include "mfma_deq.h"
+
+#define MM_MAX_SEG 3
+
+enum MmMode : int {
+    MM_STORE = 0,        // out[m][row] = fp16(acc + bias)
+    MM_ROPE_Q = 2,       // fp16(acc + bias), rotated -> out (q [m][rows])
+    MM_ROPE_KCACHE = 3,  // fp16(acc + bias), rotated -> k_cache at kv_offset[m]
+    MM_VCACHE = 4,       // fp16(acc + bias) -> v_cache at kv_offset[m]
+    MM_SWIGLU = 5,       // gate rows of w, up rows of w2: out[m][j] = fp16(silu(g) * u)
+};
+
+struct MmSeg {
+    const uint8_t* w;
+    const uint8_t* w2;   // up rows (SwiGLU)
+    __half* out;
+    const __half* bias;  // nullable
+    int fmt;             // 4 = Q4_K, 6 = Q6_K
+    int n_rows;          // output rows (SwiGLU: outputs, i.e. gate rows)
+    int mode;
+    int tiles;
+    int row_bytes;
+};
+
+struct MmPlan {
+    MmSeg seg[MM_MAX_SEG];
+    int nseg;
+    int K, M;            // activations [M][K] fp16, M <= 16 * NT in one launch
+    const __half* x;
+    const __half* rope_cos;
+    const __half* rope_sin;
+    const int* kv_offset;  // [M] positions of this launch's columns
+    __half* k_cache;       // sequence m at k_cache + m * kv_batch_stride
+    __half* v_cache;
+    int kv_batch_stride;
+    int n_kv;
+};
+
+__host__ __device__ __forceinline__ bool mm_paired(int mode) {
+    return mode == MM_ROPE_Q || mode == MM_ROPE_KCACHE || mode == MM_SWIGLU;
+}
+
+// Tile of a block: `pr` pairs (paired) or 16*RT rows starting at j0.
+struct MmTile {
+    const MmSeg* S;
+    int j0;      // first row (paired: first A row)
+    int nvalid;  // valid rows (not paired) or pairs (paired)
+};
+
+template <int RT>
+__device__ __forceinline__ MmTile mm_tile(const MmPlan& P, int g) {
+    MmTile T;
+    const int t0 = P.seg[0].tiles, t1 = P.seg[1].tiles;
+    int s = 0;
+    if (P.nseg > 1 && g >= t0) {
+        g -= t0;
+        s = 1;
+        if (P.nseg > 2 && g >= t1) {
+            g -= t1;
+            s = 2;
+        }
+    }
+    const MmSeg& S = P.seg[s];
+    T.S = &P.seg[s];
+    if (!mm_paired(S.mode)) {
+        T.j0 = g * 16 * RT;
+        T.nvalid = min(16 * RT, S.n_rows - T.j0);
+    } else if (S.mode == MM_SWIGLU) {
+        T.j0 = g * 8 * RT;
+        T.nvalid = min(8 * RT, S.n_rows - T.j0);
+    } else {  // RoPE: 8 * RT pairs (d, d + 64) of one 128-row head
+        const int tph = 64 / (8 * RT);  // tiles per head
+        T.j0 = (g / tph) * 128 + (g % tph) * 8 * RT;
+        T.nvalid = 8 * RT;
+    }
+    return T;
+}
+
+// Weight row of tile row rr (past the valid rows: a valid row, results unused).
+template <int RT>
+__device__ __forceinline__ const uint8_t* mm_row(const MmTile& T, int rr) {
+    const MmSeg& S = *T.S;
+    if (!mm_paired(S.mode)) return S.w + (size_t)(T.j0 + min(rr, T.nvalid - 1)) * S.row_bytes;
+    const int p = rr & (8 * RT - 1), pc = min(p, T.nvalid - 1);
+    if (rr < 8 * RT) return S.w + (size_t)(T.j0 + pc) * S.row_bytes;
+    if (S.mode == MM_SWIGLU) return S.w2 + (size_t)(T.j0 + pc) * S.row_bytes;
+    return S.w + (size_t)(T.j0 + 64 + pc) * S.row_bytes;
+}
+
+template <int FMT, int RT, int NT>
+__device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64],
+                                        uint8_t* stage) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int K = P.K, M = P.M, n_sb = K / QK_K;
+    const int sb0 = (n_sb * wv) / MF_WAVES, sb1 = (n_sb * (wv + 1)) / MF_WAVES;
+    const __half* x = P.x;
+
+    floatx4_t acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    const uint8_t* rowp[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) rowp[rt] = mm_row<RT>(T, rt * 16 + col);
+
+    for (int sb = sb0; sb < sb1; ++sb) {
+        half8_t bx[8][NT];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int kb = sb * QK_K + kslot_base<FMT>(t, grp);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int m = nt * 16 + col;
+                bx[t][nt] = load_x8<__half>(x + (size_t)(m < M ? m : 0) * K + kb, m < M);
+            }
+        }
+        if (FMT == 4) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint8_t* blk = rowp[rt] + (size_t)sb * Q4K_BYTES;
+                const uint4 h = *reinterpret_cast<const uint4*>(blk);
+                uint4 qc[2];
+                qc[0] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * grp);
+                qc[1] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (grp + 4));
+                Q4KLaneScale s[2];
+                s[0] = q4k_lane_scale(h, grp >> 1);
+                s[1] = q4k_lane_scale(h, 2 + (grp >> 1));
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int ci = t >> 2, part = (t >> 1) & 1, e = t & 1;
+                    const uint32_t wa = (e == 0) ? ((ci == 0) ? qc[0].x : qc[1].x) : ((ci == 0) ? qc[0].z : qc[1].z);
+                    const uint32_t wb = (e == 0) ? ((ci == 0) ? qc[0].y : qc[1].y) : ((ci == 0) ? qc[0].w : qc[1].w);
+                    const uint32_t u0 = part ? ((wa >> 4) & 0x0F0F0F0Fu) : (wa & 0x0F0F0F0Fu);
+                    const uint32_t u1 = part ? ((wb >> 4) & 0x0F0F0F0Fu) : (wb & 0x0F0F0F0Fu);
+                    const float dd = part ? s[ci].d_hi : s[ci].d_lo;
+                    const float mm = part ? s[ci].m_hi : s[ci].m_lo;
+                    const half2_t d2 = {(_Float16)dd, (_Float16)dd};
+                    const half2_t m2 = {(_Float16)mm, (_Float16)mm};
+                    const half8_t a = deq8(u0, u1, (_Float16)0.0f, d2, m2);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx[t][nt], acc[rt][nt], 0, 0, 0);
+                }
+            }
+        } else {
+            // stage the RT*16 Q6_K blocks of super-block sb (2-byte aligned)
+            // through LDS with aligned 16-byte loads
+            const int nchunk = RT * 16 * (Q6_SLOT / 16);
+            for (int i = lane; i < nchunk; i += 64) {
+                const int rr = i / (Q6_SLOT / 16), ch = i % (Q6_SLOT / 16);
+                const uintptr_t a = reinterpret_cast<uintptr_t>(mm_row<RT>(T, rr) + (size_t)sb * Q6K_BYTES);
+                const uint4* g = reinterpret_cast<const uint4*>(a & ~(uintptr_t)15);
+                reinterpret_cast<uint4*>(stage + rr * Q6_SLOT)[ch] = g[ch];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int rr = rt * 16 + col;
+                const uintptr_t a = reinterpret_cast<uintptr_t>(rowp[rt] + (size_t)sb * Q6K_BYTES);
+                const uint8_t* blk = stage + rr * Q6_SLOT + (a & 15);
+                const float d = h2f_bits(lds_u16(blk + 208));
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint8_t* ql = blk + 64 * hh + 8 * grp;
+                    const uint32_t qa0 = lds_u32_a2(ql), qa1 = lds_u32_a2(ql + 4);
+                    const uint32_t qb0 = lds_u32_a2(ql + 32), qb1 = lds_u32_a2(ql + 36);
+                    const uint8_t* qhp = blk + 128 + 32 * hh + 8 * grp;
+                    const uint32_t qh0 = lds_u32_a2(qhp), qh1 = lds_u32_a2(qhp + 4);
+                    const uint8_t* scp = blk + 192 + 8 * hh + (grp >> 1);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        uint32_t u0, u1;
+                        if (q == 0) {
+                            u0 = (qa0 & 0x0F0F0F0Fu) | ((qh0 << 4) & 0x30303030u);
+                            u1 = (qa1 & 0x0F0F0F0Fu) | ((qh1 << 4) & 0x30303030u);
+                        } else if (q == 1) {
+                            u0 = (qb0 & 0x0F0F0F0Fu) | ((qh0 << 2) & 0x30303030u);
+                            u1 = (qb1 & 0x0F0F0F0Fu) | ((qh1 << 2) & 0x30303030u);
+                        } else if (q == 2) {
+                            u0 = ((qa0 >> 4) & 0x0F0F0F0Fu) | (qh0 & 0x30303030u);
+                            u1 = ((qa1 >> 4) & 0x0F0F0F0Fu) | (qh1 & 0x30303030u);
+                        } else {
+                            u0 = ((qb0 >> 4) & 0x0F0F0F0Fu) | ((qh0 >> 2) & 0x30303030u);
+                            u1 = ((qb1 >> 4) & 0x0F0F0F0Fu) | ((qh1 >> 2) & 0x30303030u);
+                        }
+                        const float dsc = d * (float)(int8_t)scp[2 * q];
+                        const half2_t d2 = {(_Float16)dsc, (_Float16)dsc};
+                        const half2_t z2 = {(_Float16)0.0f, (_Float16)0.0f};
+                        const half8_t av = deq8(u0, u1, (_Float16)32.0f, d2, z2);
+                        const int t = 4 * hh + q;
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt)
+                            acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bx[t][nt], acc[rt][nt], 0, 0, 0);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wv][rt][nt][i][lane] = acc[rt][nt][i];
+}
+
+// Sum over the 8 waves of tile row rr, batch column mc (C layout: lane
+// (col, grp) holds rows 4*grp+i of a 16-row tile for column col).
+template <int RT, int NT>
+__device__ __forceinline__ float mm_sum(float (*red)[RT][NT][4][64], int rr, int mc) {
+    const int rt = rr >> 4, rw = rr & 15, nt = mc >> 4, cc = mc & 15;
+    const int ln = cc + 16 * (rw >> 2), i = rw & 3;
+    float s = 0.f;
+#pragma unroll
+    for (int wq = 0; wq < MF_WAVES; ++wq) s += red[wq][rt][nt][i][ln];
+    return s;
+}
+
+__device__ __forceinline__ float mm_bias(const __half* b, int row) { return b ? __half2float(b[row]) : 0.f; }
+
+template <int RT, int NT>
+__global__ __launch_bounds__(512) void fused_mm_kernel(MmPlan P) {
+    __shared__ float red[MF_WAVES][RT][NT][4][64];
+    __shared__ uint4 stage_u4[MF_WAVES * RT * 16 * Q6_SLOT / 16];
+    const MmTile T = mm_tile<RT>(P, blockIdx.x);
+    const MmSeg& S = *T.S;
+    uint8_t* stage = reinterpret_cast<uint8_t*>(stage_u4) + (size_t)(threadIdx.x >> 6) * RT * 16 * Q6_SLOT;
+    if (S.fmt == 4) mm_body<4, RT, NT>(P, T, red, stage);
+    else mm_body<6, RT, NT>(P, T, red, stage);
+    __syncthreads();
+
+    const int M = P.M;
+    if (!mm_paired(S.mode)) {
+        for (int o = threadIdx.x; o < 16 * RT * 16 * NT; o += blockDim.x) {
+            const int rr = o / (16 * NT), mc = o % (16 * NT);
+            if (rr >= T.nvalid || mc >= M) continue;
+            const int row = T.j0 + rr;
+            const __half v = __float2half(mm_sum<RT, NT>(red, rr, mc) + mm_bias(S.bias, row));
+            if (S.mode == MM_VCACHE) {
+                const int pos = P.kv_offset[mc];
+                P.v_cache[(size_t)mc * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128 + (row % 128)] = v;
+            } else {
+                S.out[(size_t)mc * S.n_rows + row] = v;
+            }
+        }
+        return;
+    }
+    for (int o = threadIdx.x; o < 8 * RT * 16 * NT; o += blockDim.x) {
+        const int p = o / (16 * NT), mc = o % (16 * NT);
+        if (p >= T.nvalid || mc >= M) continue;
+        const float a = mm_sum<RT, NT>(red, p, mc), b = mm_sum<RT, NT>(red, p + 8 * RT, mc);
+        const int row = T.j0 + p;
+        if (S.mode == MM_SWIGLU) {
+            const float g = __half2float(__float2half(a)), u = __half2float(__float2half(b));
+            S.out[(size_t)mc * S.n_rows + row] = __float2half(g / (1.0f + expf(-g)) * u);
+            continue;
+        }
+        const float x1 = __half2float(__float2half(a + mm_bias(S.bias, row)));
+        const float x2 = __half2float(__float2half(b + mm_bias(S.bias, row + 64)));
+        const int pos = P.kv_offset[mc], d = row & 127;
+        const float c = __half2float(P.rope_cos[(size_t)pos * 128 + d]);
+        const float sn = __half2float(P.rope_sin[(size_t)pos * 128 + d]);
+        const __half o1 = __float2half(x1 * c - x2 * sn), o2 = __float2half(x1 * sn + x2 * c);
+        if (S.mode == MM_ROPE_Q) {
+            S.out[(size_t)mc * S.n_rows + row] = o1;
+            S.out[(size_t)mc * S.n_rows + row + 64] = o2;
+        } else {
+            __half* kc = P.k_cache + (size_t)mc * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128;
+            kc[d] = o1;
+            kc[d + 64] = o2;
+        }
+    }
+}
+
+namespace vte {
+
+static MmSeg mm_seg(const void* w, const void* w2, void* out, const void* bias, int fmt, int n_rows, int mode, int K,
+                    int RT) {
+    MmSeg S;
+    memset(&S, 0, sizeof(S));
+    S.w = (const uint8_t*)w;
+    S.w2 = (const uint8_t*)w2;
+    S.out = (__half*)out;
+    S.bias = (const __half*)bias;
+    S.fmt = fmt;
+    S.n_rows = n_rows;
+    S.mode = mode;
+    S.row_bytes = (K / QK_K) * (fmt == 4 ? Q4K_BYTES : Q6K_BYTES);
+    if (mode == MM_SWIGLU) S.tiles = (n_rows + 8 * RT - 1) / (8 * RT);
+    else if (mode == MM_ROPE_Q || mode == MM_ROPE_KCACHE) S.tiles = n_rows / (8 * RT) / 2;
+    else S.tiles = (n_rows + 16 * RT - 1) / (16 * RT);
+    return S;
+}
+
+// Runs the plan over the batch in chunks of 32 columns (one launch each).
+static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipStream_t st) {
+    constexpr int RT = 1;
+    int total = 0;
+    for (int s = 0; s < P.nseg; ++s) total += P.seg[s].tiles;
+    const __half* x0 = P.x;
+    const int* ko0 = P.kv_offset;
+    __half* out0[MM_MAX_SEG];
+    for (int s = 0; s < P.nseg; ++s) out0[s] = P.seg[s].out;
+    __half* kc0 = P.k_cache;
+    __half* vc0 = P.v_cache;
+    for (int m0 = 0; m0 < B; m0 += 32) {
+        const int mc = B - m0 < 32 ? B - m0 : 32;
+        P.M = mc;
+        P.x = x0 + (size_t)m0 * P.K;
+        P.kv_offset = ko0 ? ko0 + m0 : nullptr;
+        for (int s = 0; s < P.nseg; ++s) P.seg[s].out = out0[s] ? out0[s] + (size_t)m0 * out_ld_elems[s] : nullptr;
+        P.k_cache = kc0 ? kc0 + (size_t)m0 * P.kv_batch_stride : nullptr;
+        P.v_cache = vc0 ? vc0 + (size_t)m0 * P.kv_batch_stride : nullptr;
+        if (mc > 16) hipLaunchKernelGGL((fused_mm_kernel<RT, 2>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
+        else hipLaunchKernelGGL((fused_mm_kernel<RT, 1>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// q/k/v projections of RMSNorm-ed fp16 activations xn [B][K] with bias, RoPE
+// on q and k, and the K/V rows written at kv_offset[b]; q_out [B][n_q*128].
+hipError_t qkv_mm(const void* xn, const void* wq, const void* q_bias, int fmt_q, const void* wk, const void* k_bias,
+                  int fmt_k, const void* wv, const void* v_bias, int fmt_v, void* q_out, void* k_cache, void* v_cache,
+                  const int* kv_offset, int kv_batch_stride, const void* rope_cos, const void* rope_sin, int B, int K,
+                  int n_q, int n_kv, hipStream_t st) {
+    constexpr int RT = 1;
+    MmPlan P;
+    memset(&P, 0, sizeof(P));
+    P.K = K;
+    P.x = (const __half*)xn;
+    P.seg[0] = mm_seg(wq, nullptr, q_out, q_bias, fmt_q, n_q * 128, MM_ROPE_Q, K, RT);
+    P.seg[1] = mm_seg(wk, nullptr, nullptr, k_bias, fmt_k, n_kv * 128, MM_ROPE_KCACHE, K, RT);
+    P.seg[2] = mm_seg(wv, nullptr, nullptr, v_bias, fmt_v, n_kv * 128, MM_VCACHE, K, RT);
+    P.nseg = 3;
+    P.rope_cos = (const __half*)rope_cos;
+    P.rope_sin = (const __half*)rope_sin;
+    P.kv_offset = kv_offset;
+    P.k_cache = (__half*)k_cache;
+    P.v_cache = (__half*)v_cache;
+    P.kv_batch_stride = kv_batch_stride;
+    P.n_kv = n_kv;
+    size_t ld[MM_MAX_SEG] = {(size_t)n_q * 128, 0, 0};
+    return mm_run(P, B, ld, st);
+}
+
+// out [B][ffn] = fp16(silu(W_gate xn) * (W_up xn)) for RMSNorm-ed fp16 xn [B][K].
+hipError_t gate_up_mm(const void* xn, const void* w_gate, const void* w_up, int fmt, void* out, int B, int K, int ffn,
+                      hipStream_t st) {
+    constexpr int RT = 1;
+    MmPlan P;
+    memset(&P, 0, sizeof(P));
+    P.K = K;
+    P.x = (const __half*)xn;
+    P.seg[0] = mm_seg(w_gate, w_up, out, nullptr, fmt, ffn, MM_SWIGLU, K, RT);
+    P.nseg = 1;
+    size_t ld[MM_MAX_SEG] = {(size_t)ffn, 0, 0};
+    return mm_run(P, B, ld, st);
+}
+
+}  // namespace vte
