@@ -109,8 +109,7 @@ __device__ __forceinline__ const uint8_t* mm_row(const MmTile& T, int rr) {
 }
 
 template <int FMT, int RT, int NT>
-__device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64],
-                                        uint8_t* stage) {
+__device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64]) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int K = P.K, M = P.M, n_sb = K / QK_K;
@@ -166,60 +165,16 @@ __device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float 
                 }
             }
         } else {
-            // stage the RT*16 Q6_K blocks of super-block sb (2-byte aligned)
-            // through LDS with aligned 16-byte loads
-            const int nchunk = RT * 16 * (Q6_SLOT / 16);
-            for (int i = lane; i < nchunk; i += 64) {
-                const int rr = i / (Q6_SLOT / 16), ch = i % (Q6_SLOT / 16);
-                const uintptr_t a = reinterpret_cast<uintptr_t>(mm_row<RT>(T, rr) + (size_t)sb * Q6K_BYTES);
-                const uint4* g = reinterpret_cast<const uint4*>(a & ~(uintptr_t)15);
-                reinterpret_cast<uint4*>(stage + rr * Q6_SLOT)[ch] = g[ch];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-            __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                const int rr = rt * 16 + col;
-                const uintptr_t a = reinterpret_cast<uintptr_t>(rowp[rt] + (size_t)sb * Q6K_BYTES);
-                const uint8_t* blk = stage + rr * Q6_SLOT + (a & 15);
-                const float d = h2f_bits(lds_u16(blk + 208));
+                half8_t av[8];
+                q6k_a_operands(rowp[rt] + (size_t)sb * Q6K_BYTES, grp, av);
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const uint8_t* ql = blk + 64 * hh + 8 * grp;
-                    const uint32_t qa0 = lds_u32_a2(ql), qa1 = lds_u32_a2(ql + 4);
-                    const uint32_t qb0 = lds_u32_a2(ql + 32), qb1 = lds_u32_a2(ql + 36);
-                    const uint8_t* qhp = blk + 128 + 32 * hh + 8 * grp;
-                    const uint32_t qh0 = lds_u32_a2(qhp), qh1 = lds_u32_a2(qhp + 4);
-                    const uint8_t* scp = blk + 192 + 8 * hh + (grp >> 1);
+                for (int t = 0; t < 8; ++t)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        uint32_t u0, u1;
-                        if (q == 0) {
-                            u0 = (qa0 & 0x0F0F0F0Fu) | ((qh0 << 4) & 0x30303030u);
-                            u1 = (qa1 & 0x0F0F0F0Fu) | ((qh1 << 4) & 0x30303030u);
-                        } else if (q == 1) {
-                            u0 = (qb0 & 0x0F0F0F0Fu) | ((qh0 << 2) & 0x30303030u);
-                            u1 = (qb1 & 0x0F0F0F0Fu) | ((qh1 << 2) & 0x30303030u);
-                        } else if (q == 2) {
-                            u0 = ((qa0 >> 4) & 0x0F0F0F0Fu) | (qh0 & 0x30303030u);
-                            u1 = ((qa1 >> 4) & 0x0F0F0F0Fu) | (qh1 & 0x30303030u);
-                        } else {
-                            u0 = ((qb0 >> 4) & 0x0F0F0F0Fu) | ((qh0 >> 2) & 0x30303030u);
-                            u1 = ((qb1 >> 4) & 0x0F0F0F0Fu) | ((qh1 >> 2) & 0x30303030u);
-                        }
-                        const float dsc = d * (float)(int8_t)scp[2 * q];
-                        const half2_t d2 = {(_Float16)dsc, (_Float16)dsc};
-                        const half2_t z2 = {(_Float16)0.0f, (_Float16)0.0f};
-                        const half8_t av = deq8(u0, u1, (_Float16)32.0f, d2, z2);
-                        const int t = 4 * hh + q;
-#pragma unroll
-                        for (int nt = 0; nt < NT; ++nt)
-                            acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bx[t][nt], acc[rt][nt], 0, 0, 0);
-                    }
-                }
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t], bx[t][nt], acc[rt][nt], 0, 0, 0);
             }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-            __builtin_amdgcn_wave_barrier();
         }
     }
 #pragma unroll
@@ -247,12 +202,10 @@ __device__ __forceinline__ float mm_bias(const __half* b, int row) { return b ? 
 template <int RT, int NT>
 __global__ __launch_bounds__(512) void fused_mm_kernel(MmPlan P) {
     __shared__ float red[MF_WAVES][RT][NT][4][64];
-    __shared__ uint4 stage_u4[MF_WAVES * RT * 16 * Q6_SLOT / 16];
     const MmTile T = mm_tile<RT>(P, blockIdx.x);
     const MmSeg& S = *T.S;
-    uint8_t* stage = reinterpret_cast<uint8_t*>(stage_u4) + (size_t)(threadIdx.x >> 6) * RT * 16 * Q6_SLOT;
-    if (S.fmt == 4) mm_body<4, RT, NT>(P, T, red, stage);
-    else mm_body<6, RT, NT>(P, T, red, stage);
+    if (S.fmt == 4) mm_body<4, RT, NT>(P, T, red);
+    else mm_body<6, RT, NT>(P, T, red);
     __syncthreads();
 
     const int M = P.M;

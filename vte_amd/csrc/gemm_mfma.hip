@@ -21,8 +21,8 @@
 //    slots are 8 contiguous elements sharing one sub-block scale:
 //      Q4_K step t, group g: qs chunk c = g + 4*(t>>2), nibble (t>>1)&1, half t&1
 //      Q6_K step t, group g: half h = t>>2, quarter q = t&3, l = 8g .. 8g+7
-//  * Q4_K rows are 16-byte aligned and load straight from HBM; Q6_K tiles are
-//    staged through LDS with aligned 16-byte loads (blocks are 2-byte aligned).
+//  * Q4_K rows are 16-byte aligned and Q6_K rows 2-byte aligned; both load
+//    straight from HBM (unaligned 8-byte loads stream at full speed).
 #include "mfma_deq.h"
 
 template <typename TI, typename TO, int FMT, int RT, int NT>
@@ -31,7 +31,6 @@ __global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x
                                                         const TO* __restrict__ bias, const TO* __restrict__ residual,
                                                         float rs) {
     __shared__ float red[MF_WAVES][RT][NT][4][64];
-    __shared__ uint4 stage_u4[(FMT == 6) ? MF_WAVES * RT * 16 * Q6_SLOT / 16 : 1];
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -48,7 +47,6 @@ __global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-    uint8_t* stage = reinterpret_cast<uint8_t*>(stage_u4) + (size_t)wv * RT * 16 * Q6_SLOT;
 
     for (int sb = sb0; sb < sb1; ++sb) {
         // ---- B operand (activations) for the 8 k-steps ----
@@ -92,61 +90,16 @@ __global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x
                 }
             }
         } else {
-            // ---- stage RT*16 Q6_K blocks (row r, super-block sb) into LDS ----
-            const int nchunk = RT * 16 * (Q6_SLOT / 16);
-            for (int i = lane; i < nchunk; i += 64) {
-                const int rr = i / (Q6_SLOT / 16), ch = i % (Q6_SLOT / 16);
-                const int r = min(row0 + rr, N - 1);
-                const uintptr_t a = reinterpret_cast<uintptr_t>(w + (size_t)r * row_bytes + (size_t)sb * Q6K_BYTES);
-                const uint4* g = reinterpret_cast<const uint4*>(a & ~(uintptr_t)15);
-                reinterpret_cast<uint4*>(stage + rr * Q6_SLOT)[ch] = g[ch];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-            __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                const int rr = rt * 16 + col;
-                const int r = min(row0 + rr, N - 1);
-                const uintptr_t a = reinterpret_cast<uintptr_t>(w + (size_t)r * row_bytes + (size_t)sb * Q6K_BYTES);
-                const uint8_t* blk = stage + rr * Q6_SLOT + (a & 15);
-                const float d = h2f_bits(lds_u16(blk + 208));
+                half8_t av[8];
+                q6k_a_operands(w + (size_t)min(row0 + rt * 16 + col, N - 1) * row_bytes + (size_t)sb * Q6K_BYTES, grp, av);
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const uint8_t* ql = blk + 64 * hh + 8 * grp;
-                    const uint32_t qa0 = lds_u32_a2(ql), qa1 = lds_u32_a2(ql + 4);
-                    const uint32_t qb0 = lds_u32_a2(ql + 32), qb1 = lds_u32_a2(ql + 36);
-                    const uint8_t* qhp = blk + 128 + 32 * hh + 8 * grp;
-                    const uint32_t qh0 = lds_u32_a2(qhp), qh1 = lds_u32_a2(qhp + 4);
-                    const uint8_t* scp = blk + 192 + 8 * hh + (grp >> 1);
+                for (int t = 0; t < 8; ++t)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        uint32_t u0, u1;
-                        if (q == 0) {
-                            u0 = (qa0 & 0x0F0F0F0Fu) | ((qh0 << 4) & 0x30303030u);
-                            u1 = (qa1 & 0x0F0F0F0Fu) | ((qh1 << 4) & 0x30303030u);
-                        } else if (q == 1) {
-                            u0 = (qb0 & 0x0F0F0F0Fu) | ((qh0 << 2) & 0x30303030u);
-                            u1 = (qb1 & 0x0F0F0F0Fu) | ((qh1 << 2) & 0x30303030u);
-                        } else if (q == 2) {
-                            u0 = ((qa0 >> 4) & 0x0F0F0F0Fu) | (qh0 & 0x30303030u);
-                            u1 = ((qa1 >> 4) & 0x0F0F0F0Fu) | (qh1 & 0x30303030u);
-                        } else {
-                            u0 = ((qb0 >> 4) & 0x0F0F0F0Fu) | ((qh0 >> 2) & 0x30303030u);
-                            u1 = ((qb1 >> 4) & 0x0F0F0F0Fu) | ((qh1 >> 2) & 0x30303030u);
-                        }
-                        const float dsc = d * (float)(int8_t)scp[2 * q];
-                        const half2_t d2 = {(_Float16)dsc, (_Float16)dsc};
-                        const half2_t z2 = {(_Float16)0.0f, (_Float16)0.0f};
-                        const half8_t av = deq8(u0, u1, (_Float16)32.0f, d2, z2);
-                        const int t = 4 * hh + q;
-#pragma unroll
-                        for (int nt = 0; nt < NT; ++nt)
-                            acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bx[t][nt], acc[rt][nt], 0, 0, 0);
-                    }
-                }
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t], bx[t][nt], acc[rt][nt], 0, 0, 0);
             }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-            __builtin_amdgcn_wave_barrier();
         }
     }
 
@@ -181,12 +134,11 @@ static void launch_tile(const TI* x, const void* w, TO* y, int M, int K, int N, 
 }
 
 // Batch columns are processed in chunks of 32 (two 16-wide MFMA N tiles).
-// Q4_K uses 32-row tiles on tall matrices; Q6_K keeps 16-row tiles so its
-// LDS staging stays small enough for several blocks per CU.
+// Tall matrices (N >= 4096) use 32-row tiles.
 template <typename TI, typename TO, int FMT>
 static hipError_t launch_mfma(const void* x, const void* w, void* y, int M, int K, int N, const void* bias,
                               const void* residual, float rs, hipStream_t st) {
-    const bool tall = (FMT == 4) && N >= 4096;
+    const bool tall = N >= 4096;
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mc = (M - m0 < 32) ? (M - m0) : 32;
         const TI* xs = (const TI*)x + (size_t)m0 * K;

@@ -26,7 +26,6 @@ union H8 {
 };
 
 #define MF_WAVES 8
-#define Q6_SLOT 224  // LDS bytes per staged Q6_K block row (14 aligned chunks)
 
 // bytes b0..b3 of `u` (each < 256, here 6-bit values) -> two fp16 pairs 1024+b.
 __device__ __forceinline__ void bytes_to_f16magic(uint32_t u, uint32_t& lo, uint32_t& hi) {
@@ -74,3 +73,46 @@ __device__ __forceinline__ int kslot_base(int t, int g) {
     }
 }
 
+
+// The eight MFMA A operands (k-steps t = 4*hh + q) of one lane for a Q6_K
+// super-block read straight from global memory: the lane's 8-byte slices of
+// ql, qh and the scales of each half.  Q6_K blocks are only 2-byte aligned;
+// the unaligned 8-byte loads stream as fast as aligned ones on gfx950.
+__device__ __forceinline__ uint2 q6_ld8(const uint8_t* p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ void q6k_a_operands(const uint8_t* blk, int grp, half8_t (&a)[8]) {
+    const float d = h2f_bits(((const __attribute__((address_space(1))) uint16_t*)(blk + 208))[0]);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const uint2 qa = q6_ld8(blk + 64 * hh + 8 * grp);
+        const uint2 qb = q6_ld8(blk + 64 * hh + 32 + 8 * grp);
+        const uint2 qh = q6_ld8(blk + 128 + 32 * hh + 8 * grp);
+        const uint2 scw = q6_ld8(blk + 192 + 8 * hh);
+        const uint64_t sc = ((uint64_t)scw.y << 32) | scw.x;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t u0, u1;
+            if (q == 0) {
+                u0 = (qa.x & 0x0F0F0F0Fu) | ((qh.x << 4) & 0x30303030u);
+                u1 = (qa.y & 0x0F0F0F0Fu) | ((qh.y << 4) & 0x30303030u);
+            } else if (q == 1) {
+                u0 = (qb.x & 0x0F0F0F0Fu) | ((qh.x << 2) & 0x30303030u);
+                u1 = (qb.y & 0x0F0F0F0Fu) | ((qh.y << 2) & 0x30303030u);
+            } else if (q == 2) {
+                u0 = ((qa.x >> 4) & 0x0F0F0F0Fu) | (qh.x & 0x30303030u);
+                u1 = ((qa.y >> 4) & 0x0F0F0F0Fu) | (qh.y & 0x30303030u);
+            } else {
+                u0 = ((qb.x >> 4) & 0x0F0F0F0Fu) | ((qh.x >> 2) & 0x30303030u);
+                u1 = ((qb.y >> 4) & 0x0F0F0F0Fu) | ((qh.y >> 2) & 0x30303030u);
+            }
+            const int8_t scq = (int8_t)((sc >> (8 * ((grp >> 1) + 2 * q))) & 0xFF);
+            const float dsc = d * (float)scq;
+            const half2_t d2 = {(_Float16)dsc, (_Float16)dsc};
+            const half2_t z2 = {(_Float16)0.0f, (_Float16)0.0f};
+            a[4 * hh + q] = deq8(u0, u1, (_Float16)32.0f, d2, z2);
+        }
+    }
+}
