@@ -71,6 +71,15 @@ int vte_gemv(int fmt, int in_dtype, int out_dtype, const void* x, const void* w,
 int vte_gemm_mfma(int fmt, int in_dtype, int out_dtype, const void* x, const void* w, void* y, int M, int K,
                   int N, const void* bias, const void* residual, float residual_scale, void* stream);
 
+/* Split-K partial sums for batched projections (M >= 8), Q4_K / Q6_K, fp16 x:
+ *   part[s][m][n] = sum over split s's super-blocks of dequant(W[n, k]) * x[m, k]
+ * (fp32, no bias / scale / residual; 1 <= splits <= 8 and splits <= K / 256).
+ * vte_add_rmsnorm adds the splits to the residual.
+ * Replaces: split_k_qkv_pass1_kernel (split_k_qkv_pass1.hip.template:29-79), the
+ *           reference's split-K pass writing per-split sums to a scratchpad. */
+int vte_gemm_mfma_splitk(int fmt, const void* x, const void* w, float* part, int M, int K, int N, int splits,
+                         void* stream);
+
 /* Dequantise n_elements (a multiple of the block size) to fp32, bit-exact with
  * the reference's NumPy dequantiser.
  * Replaces: dequantize_q4_k / dequantize_q6_k / dequantize_q8_0
@@ -107,6 +116,15 @@ int vte_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, in
 /* out = fp16(x * rsqrt(mean(x^2) + eps) * w), rows x hidden, fp16.
  * Replaces: rmsnorm_kernel (rmsnorm.hip.template:6-117). */
 int vte_rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps, void* stream);
+
+/* x_out = fp16(x + sum_s part[s]) and xn = fp16(x_out * rsqrt(mean(x_out^2) + eps) * w)
+ * for part [n_parts][rows][hidden] fp32 (1 <= n_parts <= 8), hidden % 8 == 0,
+ * hidden <= 8192; x_out may equal x.
+ * Replaces: add_kernel (add.hip.template:4-17) as the residual add of the
+ *           projection, followed by rmsnorm_kernel (rmsnorm.hip.template:6-117);
+ *           the split sum is split_k_qkv_pass2.hip.template:25-137's reduction. */
+int vte_add_rmsnorm(const void* x, const float* part, int n_parts, const void* w, void* x_out, void* xn, int rows,
+                    int hidden, float eps, void* stream);
 
 /* In-place rotary embedding of q [B][seq][n_q][hd] and k [B][seq][n_kv][hd]
  * at positions kv_offset[b] + s, fp16 cos/sin caches [max_seq][hd].

@@ -172,3 +172,24 @@ def test_batch_above_4_rejects_fused_norm(hip, K):
     rc = K.lib.vte_ffn_in(ctypes.c_void_p(x.ptr), ctypes.c_void_p(nw.ptr), ctypes.c_float(EPS), ctypes.c_void_p(w.ptr),
                           ctypes.c_void_p(w.ptr), 4, ctypes.c_void_p(out.ptr), B, k, ffn, None)
     assert rc == -1 and b"norm_w must be NULL" in K.lib.vte_last_error()
+
+
+@pytest.mark.parametrize("fmt,k,n,M,splits", [("q6_k", 8960, 1536, 16, 4), ("q4_k", 8960, 1536, 8, 4),
+                                              ("q4_k", 8960, 1536, 40, 5), ("q6_k", 1536, 1536, 16, 1),
+                                              ("q4_k", 1536, 1536, 20, 6), ("q6_k", 2304, 640, 9, 8)])
+def test_gemm_mfma_splitk(hip, K, fmt, k, n, M, splits):
+    """Each split's partial equals the GEMV over its super-block range
+    [n_sb * s // splits, n_sb * (s + 1) // splits) of every weight row."""
+    rng = np.random.default_rng(k + n + M + splits)
+    raw = _mat(fmt, n, k, 11)
+    x = _x(rng, M, k)
+    part = empty(hip, (splits, M, n), np.float32)
+    K.gemm_mfma_splitk(fmt, up(hip, x), up(hip, raw), part, M, k, n, splits, stream=hip.stream)
+    got = down(part)
+    n_sb = k // 256
+    blk = raw.reshape(n, n_sb, -1)
+    for s in range(splits):
+        a, b = n_sb * s // splits, n_sb * (s + 1) // splits
+        sub = np.ascontiguousarray(blk[:, a:b]).reshape(-1)
+        ref = dq.gemv(fmt, sub, n, (b - a) * 256, x[:, a * 256:b * 256].astype(np.float32))
+        assert rel_l2(got[s], ref) <= TOL, s

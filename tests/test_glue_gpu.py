@@ -16,9 +16,11 @@ def _ulp_close(a, b, ulps=1):
     return np.max(np.abs(a - b)) <= ulps
 
 
-def test_rmsnorm(hip, K):
+@pytest.mark.parametrize("H", [1536, 8192, 8200, 1000, 12])
+def test_rmsnorm(hip, K, H):
+    """Register path (multiples of 8 up to 8192) and element loop (8200, 1000, 12)."""
     rng = np.random.default_rng(1)
-    rows, H = 16, 1536
+    rows = 16
     x = rng.standard_normal((rows, H)).astype(np.float16)
     w = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
     out = empty(hip, (rows, H), np.float16)
@@ -85,3 +87,23 @@ def test_topk_exact(hip, K, k, vocab):
         order = np.lexsort((np.arange(vocab), -logits[r]))[:k]  # value desc, index asc
         assert np.array_equal(gi[r], order), r
         assert np.array_equal(gv[r], logits[r, order])
+
+
+@pytest.mark.parametrize("rows,H,n_parts,inplace", [(16, 1536, 4, False), (8, 1536, 1, True), (40, 1536, 8, False),
+                                                    (3, 8192, 2, False), (5, 24, 3, True)])
+def test_add_rmsnorm(hip, K, rows, H, n_parts, inplace):
+    """x_out = fp16(x + sum of split partials in split order), then RMSNorm of x_out."""
+    rng = np.random.default_rng(rows * H + n_parts)
+    x = rng.standard_normal((rows, H)).astype(np.float16)
+    part = rng.standard_normal((n_parts, rows, H)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+    s = np.zeros((rows, H), np.float32)
+    for p in part:
+        s += p
+    ref_x = (s + x.astype(np.float32)).astype(np.float16)
+    xd = up(hip, x)
+    xo = xd if inplace else empty(hip, (rows, H), np.float16)
+    xn = empty(hip, (rows, H), np.float16)
+    K.add_rmsnorm(xd, up(hip, part), n_parts, up(hip, w), xo, xn, rows, H, 1e-6, stream=hip.stream)
+    np.testing.assert_array_equal(down(xo).view(np.uint16), ref_x.view(np.uint16))
+    assert _ulp_close(down(xn), st.rmsnorm(ref_x, w, 1e-6), 2)

@@ -40,6 +40,15 @@ class GraphCaptureError(RuntimeError):
     pass
 
 
+MAX_SPLITK = 8  # split-K partial buffers of the batched o-proj / down projections
+
+
+def splitk_splits(K: int) -> int:
+    """Splits of a batched projection over K: about one super-block (256
+    elements) per wave of the 8-wave blocks."""
+    return max(1, min(MAX_SPLITK, (K // 256) // 8))
+
+
 class HIPGraphExecutor:
     def __init__(self, hip: HIPRuntime, model: SyntheticQwen2, batch_size: int = 1, max_seq: Optional[int] = None,
                  top_k: int = 40, gemm_min_batch: int = 8, split: Optional[int] = None, fused: bool = True):
@@ -53,7 +62,8 @@ class HIPGraphExecutor:
         # fused norm+QKV+RoPE+append / norm+gate+up+SwiGLU / norm+LM-head kernels (batch <= 4)
         self.fused = fused and batch_size <= 4
         # batch >= gemm_min_batch: MFMA launches with the QKV+RoPE+append and
-        # gate/up+SwiGLU glue fused in (RMSNorm stays its own launch)
+        # gate/up+SwiGLU glue fused in; o-proj and down write split-K partial
+        # sums that one launch adds to the residual and RMS-normalises
         self.mm_fused = fused and batch_size >= gemm_min_batch
         self.K = kernels()
         self.graph = None
@@ -62,6 +72,7 @@ class HIPGraphExecutor:
         B, H = batch_size, cfg.hidden
         kv_elems = B * self.max_seq * cfg.n_kv * cfg.head_dim
         act_bytes = 4 * (B * (2 * H + cfg.q_dim * 2 + cfg.kv_dim * 2 + 3 * cfg.ffn) * 2 + B * cfg.vocab * 4)
+        act_bytes += MAX_SPLITK * B * H * 4
         need = model.weight_bytes() + 2 * cfg.n_layers * kv_elems * 2 + act_bytes + (64 << 20)
         need += (cfg.n_layers * len(PROJ) + 16) * 1024  # alignment and slack per tensor
         self.slab = SlabAllocator(hip, 0, requested_pool_size=need + (256 << 20))
@@ -96,6 +107,7 @@ class HIPGraphExecutor:
         self.g = A((B, cfg.ffn), np.float16, "gate")
         self.u = A((B, cfg.ffn), np.float16, "up")
         self.a = A((B, cfg.ffn), np.float16, "swiglu")
+        self.part = A((MAX_SPLITK, B, H), np.float32, "splitk_partials")
         self.logits = A((B, cfg.vocab), np.float32, "logits")
         self.topk_val = A((B, max(top_k, 1)), np.float32, "topk_val")
         self.topk_idx = A((B, max(top_k, 1)), np.int32, "topk_idx")
@@ -213,8 +225,8 @@ class HIPGraphExecutor:
         offs = self.staging_kv_offset
         cur = 0
         K.embedding_q6k(self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
+        K.rmsnorm(self.h[cur], self.layers[0]["attn_norm"], self.xn, B, H, cfg.eps, stream=st)
         for L, lw in enumerate(self.layers):
-            K.rmsnorm(self.h[cur], lw["attn_norm"], self.xn, B, H, cfg.eps, stream=st)
             if self.mm_fused:  # q/k/v + bias + RoPE + K/V append in one MFMA launch
                 K.attn_in(self.xn, None, cfg.eps, lw["q"], lw["q_bias"], lw["q_fmt"], lw["k"], lw["k_bias"],
                           lw["k_fmt"], lw["v"], lw["v_bias"], lw["v_fmt"], self.q, self.k_cache[L], self.v_cache[L],
@@ -230,9 +242,12 @@ class HIPGraphExecutor:
                             self.kv_batch_stride, stream=st)
             self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], self.att, offs, self.kv_batch_stride,
                              dtype="f16", batch=B, stream=st)
-            self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
+            if self.mm_fused:  # o-proj split-K partials; residual add + ffn RMSNorm in one launch
+                self._proj_add_norm(lw["o_fmt"], self.att, lw["o"], cfg.q_dim, cur, lw["ffn_norm"])
+            else:
+                self._linear(lw["o_fmt"], self.att, lw["o"], self.h[1 - cur], cfg.q_dim, H, residual=self.h[cur])
+                K.rmsnorm(self.h[1 - cur], lw["ffn_norm"], self.xn, B, H, cfg.eps, stream=st)
             cur = 1 - cur
-            K.rmsnorm(self.h[cur], lw["ffn_norm"], self.xn, B, H, cfg.eps, stream=st)
             if self.mm_fused and lw["gate_fmt"] == "q4_k" and lw["up_fmt"] == "q4_k":  # gate/up + SwiGLU
                 K.ffn_in(self.xn, None, cfg.eps, lw["gate"], lw["up"], lw["gate_fmt"], self.a, B, H, cfg.ffn,
                          stream=st)
@@ -240,13 +255,29 @@ class HIPGraphExecutor:
                 self._linear(lw["gate_fmt"], self.xn, lw["gate"], self.g, H, cfg.ffn)
                 self._linear(lw["up_fmt"], self.xn, lw["up"], self.u, H, cfg.ffn)
                 K.swiglu(self.g, self.u, self.a, B * cfg.ffn, stream=st)
-            self._linear(lw["down_fmt"], self.a, lw["down"], self.h[1 - cur], cfg.ffn, H, residual=self.h[cur])
+            nxt = self.layers[L + 1]["attn_norm"] if L + 1 < len(self.layers) else self.output_norm
+            if self.mm_fused:  # down split-K partials; residual add + next RMSNorm in one launch
+                self._proj_add_norm(lw["down_fmt"], self.a, lw["down"], cfg.ffn, cur, nxt)
+            else:
+                self._linear(lw["down_fmt"], self.a, lw["down"], self.h[1 - cur], cfg.ffn, H, residual=self.h[cur])
+                K.rmsnorm(self.h[1 - cur], nxt, self.xn, B, H, cfg.eps, stream=st)
             cur = 1 - cur
         self.h_final = cur
-        K.rmsnorm(self.h[cur], self.output_norm, self.xn, B, H, cfg.eps, stream=st)
         self._linear("q6_k", self.xn, self.token_embd, self.logits, H, cfg.vocab, out_dtype="f32")
         if self.top_k > 0:
             K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st)
+
+    def _proj_add_norm(self, fmt, x, w, K_in, cur, norm_w) -> None:
+        """h[1-cur] = h[cur] + W x (split-K partials), xn = RMSNorm(h[1-cur]) * norm_w."""
+        cfg, H = self.cfg, self.cfg.hidden
+        if fmt not in ("q4_k", "q6_k"):
+            self._linear(fmt, x, w, self.h[1 - cur], K_in, H, residual=self.h[cur])
+            self.K.rmsnorm(self.h[1 - cur], norm_w, self.xn, self.B, H, cfg.eps, stream=self.hip.stream)
+            return
+        s = splitk_splits(K_in)
+        self.K.gemm_mfma_splitk(fmt, x, w, self.part, self.B, K_in, H, s, stream=self.hip.stream)
+        self.K.add_rmsnorm(self.h[cur], self.part, s, norm_w, self.h[1 - cur], self.xn, self.B, H, cfg.eps,
+                           stream=self.hip.stream)
 
     # -------------------------------------------------------------------- graph
     def build_decode_graph(self) -> None:

@@ -40,7 +40,7 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 __device__ unsigned long long att_trace[4096][8];
 __device__ unsigned long long comb_trace[4096][2];
 #define CMB_TS(k) do { if (threadIdx.x == 0) { const int bi = blockIdx.x + gridDim.x * blockIdx.y; if (bi < 4096) comb_trace[bi][k] = wall_clock64(); } } while (0)
-#define ATT_TS(k) do { if (threadIdx.x == 0) { const int bi = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); if (bi < 4096) att_trace[bi][k] = wall_clock64(); } } while (0)
+#define ATT_TS(k) do { if (threadIdx.x == 0) { const int bi = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); if (bi < 4096) { att_trace[bi][k] = wall_clock64(); if (k == 0) { att_trace[bi][4] = __builtin_amdgcn_s_getreg(4 | (31 << 11)); att_trace[bi][5] = __builtin_amdgcn_s_getreg(20 | (31 << 11)); } } } } while (0)
 #else
 #define ATT_TS(k) do { } while (0)
 #define CMB_TS(k) do { } while (0)

@@ -31,6 +31,10 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
 hipError_t kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int B, int n_kv, int head_dim,
                      const int* kv_offset, int kv_batch_stride, hipStream_t st);
 hipError_t rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps, hipStream_t st);
+hipError_t add_rmsnorm(const void* x, const float* part, int n_parts, const void* w, void* x_out, void* xn,
+                       int rows, int hidden, float eps, hipStream_t st);
+hipError_t gemm_mfma_splitk(int fmt, const void* x, const void* w, float* part, int M, int K, int N, int splits,
+                            hipStream_t st);
 hipError_t rope(void* q, void* k, const void* cosc, const void* sinc, int B, int seq_len, int n_q, int n_kv,
                 int head_dim, const int* kv_offset, int rope_type, int rotary_dim, hipStream_t st);
 hipError_t swiglu(const void* g, const void* u, void* out, int n, hipStream_t st);
@@ -141,6 +145,17 @@ int vte_gemm_mfma(int fmt, int in_dtype, int out_dtype, const void* x, const voi
                       "vte_gemm_mfma launch");
 }
 
+int vte_gemm_mfma_splitk(int fmt, const void* x, const void* w, float* part, int M, int K, int N, int splits,
+                         void* stream) {
+    int rc = check_gemv(fmt, VTE_F16, VTE_F32, x, w, part, M, K, N);
+    if (rc) return rc;
+    REQUIRE(fmt == 4 || fmt == 6, "gemm_mfma_splitk: Q4_K and Q6_K only");
+    REQUIRE(splits >= 1 && splits <= 8 && splits <= K / 256, "gemm_mfma_splitk: splits %d outside 1..min(8, K/256)",
+            splits);
+    return hip_status(vte::gemm_mfma_splitk(fmt, x, w, part, M, K, N, splits, (hipStream_t)stream),
+                      "vte_gemm_mfma_splitk launch");
+}
+
 int vte_dequantize(int fmt, const void* src, float* dst, long long n_elements, void* stream) {
     REQUIRE(fmt == 4 || fmt == 6 || fmt == 8, "dequantize: unknown format %d", fmt);
     REQUIRE(src && dst, "dequantize: null pointer");
@@ -180,6 +195,18 @@ int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void*
                                                             batch, n_q, n_kv, scale, kv_offset, kv_batch_stride,
                                                             split, max_splits, counters, st);
     return hip_status(e, "vte_attn_split_kv launch");
+}
+
+int vte_add_rmsnorm(const void* x, const float* part, int n_parts, const void* w, void* x_out, void* xn, int rows,
+                    int hidden, float eps, void* stream) {
+    REQUIRE(x && part && w && x_out && xn, "add_rmsnorm: null pointer");
+    REQUIRE(rows >= 1 && n_parts >= 1 && n_parts <= 8, "add_rmsnorm: rows %d / n_parts %d", rows, n_parts);
+    REQUIRE(hidden >= 8 && hidden % 8 == 0 && hidden <= 8192, "add_rmsnorm: hidden %d not a multiple of 8 in 8..8192",
+            hidden);
+    REQUIRE(aligned(x, 16) && aligned(part, 16) && aligned(w, 16) && aligned(x_out, 16) && aligned(xn, 16),
+            "add_rmsnorm: 16-byte alignment required");
+    return hip_status(vte::add_rmsnorm(x, part, n_parts, w, x_out, xn, rows, hidden, eps, (hipStream_t)stream),
+                      "vte_add_rmsnorm launch");
 }
 
 int vte_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int batch, int n_kv, int head_dim,

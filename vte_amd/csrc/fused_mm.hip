@@ -17,6 +17,7 @@
 // comes from its tile row's weight row; everything else is the batched MFMA
 // GEMM (8 waves split K, partial C tiles summed through LDS), whose k-slot
 // map and dequantisation it shares (mfma_deq.h).
+#include <cstdlib>
 #include <cstring>
 
 #include "mfma_deq.h"
@@ -272,8 +273,8 @@ static MmSeg mm_seg(const void* w, const void* w2, void* out, const void* bias, 
 }
 
 // Runs the plan over the batch in chunks of 32 columns (one launch each).
+template <int RT>
 static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipStream_t st) {
-    constexpr int RT = 1;
     int total = 0;
     for (int s = 0; s < P.nseg; ++s) total += P.seg[s].tiles;
     const __half* x0 = P.x;
@@ -298,13 +299,18 @@ static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipSt
     return hipSuccess;
 }
 
+static int mm_env(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
 // q/k/v projections of RMSNorm-ed fp16 activations xn [B][K] with bias, RoPE
 // on q and k, and the K/V rows written at kv_offset[b]; q_out [B][n_q*128].
 hipError_t qkv_mm(const void* xn, const void* wq, const void* q_bias, int fmt_q, const void* wk, const void* k_bias,
                   int fmt_k, const void* wv, const void* v_bias, int fmt_v, void* q_out, void* k_cache, void* v_cache,
                   const int* kv_offset, int kv_batch_stride, const void* rope_cos, const void* rope_sin, int B, int K,
                   int n_q, int n_kv, hipStream_t st) {
-    constexpr int RT = 1;
+    const int RT = mm_env("VTE_MM_RT_QKV", 1);
     MmPlan P;
     memset(&P, 0, sizeof(P));
     P.K = K;
@@ -321,13 +327,13 @@ hipError_t qkv_mm(const void* xn, const void* wq, const void* q_bias, int fmt_q,
     P.kv_batch_stride = kv_batch_stride;
     P.n_kv = n_kv;
     size_t ld[MM_MAX_SEG] = {(size_t)n_q * 128, 0, 0};
-    return mm_run(P, B, ld, st);
+    return RT == 2 ? mm_run<2>(P, B, ld, st) : mm_run<1>(P, B, ld, st);
 }
 
 // out [B][ffn] = fp16(silu(W_gate xn) * (W_up xn)) for RMSNorm-ed fp16 xn [B][K].
 hipError_t gate_up_mm(const void* xn, const void* w_gate, const void* w_up, int fmt, void* out, int B, int K, int ffn,
                       hipStream_t st) {
-    constexpr int RT = 1;
+    const int RT = mm_env("VTE_MM_RT_FFN", 2);  // 16 gate/up pairs per block: half the blocks, x read half as often
     MmPlan P;
     memset(&P, 0, sizeof(P));
     P.K = K;
@@ -335,7 +341,7 @@ hipError_t gate_up_mm(const void* xn, const void* w_gate, const void* w_up, int 
     P.seg[0] = mm_seg(w_gate, w_up, out, nullptr, fmt, ffn, MM_SWIGLU, K, RT);
     P.nseg = 1;
     size_t ld[MM_MAX_SEG] = {(size_t)ffn, 0, 0};
-    return mm_run(P, B, ld, st);
+    return RT == 2 ? mm_run<2>(P, B, ld, st) : mm_run<1>(P, B, ld, st);
 }
 
 }  // namespace vte

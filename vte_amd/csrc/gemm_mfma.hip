@@ -29,7 +29,7 @@ template <typename TI, typename TO, int FMT, int RT, int NT>
 __global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
                                                         TO* __restrict__ y, int M, int K, int N,
                                                         const TO* __restrict__ bias, const TO* __restrict__ residual,
-                                                        float rs) {
+                                                        float rs, size_t split_stride) {
     __shared__ float red[MF_WAVES][RT][NT][4][64];
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -38,8 +38,11 @@ __global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x
     const int bpr = (FMT == 4) ? Q4K_BYTES : Q6K_BYTES;
     const size_t row_bytes = (size_t)n_sb * bpr;
     const int row0 = blockIdx.x * (16 * RT);
-    // contiguous super-block range of this wave
-    const int sb0 = (n_sb * wv) / MF_WAVES, sb1 = (n_sb * (wv + 1)) / MF_WAVES;
+    // split-K over blockIdx.y: this block's super-block range, then each
+    // wave's contiguous share of it; split s writes its sums at y + s * split_stride
+    const int kb0 = (n_sb * (int)blockIdx.y) / (int)gridDim.y, kb1 = (n_sb * ((int)blockIdx.y + 1)) / (int)gridDim.y;
+    const int sb0 = kb0 + ((kb1 - kb0) * wv) / MF_WAVES, sb1 = kb0 + ((kb1 - kb0) * (wv + 1)) / MF_WAVES;
+    y += blockIdx.y * split_stride;
 
     floatx4_t acc[RT][NT];
 #pragma unroll
@@ -128,9 +131,10 @@ namespace vte {
 
 template <typename TI, typename TO, int FMT, int RT, int NT>
 static void launch_tile(const TI* x, const void* w, TO* y, int M, int K, int N, const void* bias,
-                        const TO* residual, float rs, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<TI, TO, FMT, RT, NT>), dim3((N + 16 * RT - 1) / (16 * RT)),
-                       dim3(64 * MF_WAVES), 0, st, x, (const uint8_t*)w, y, M, K, N, (const TO*)bias, residual, rs);
+                        const TO* residual, float rs, hipStream_t st, int splits = 1, size_t split_stride = 0) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<TI, TO, FMT, RT, NT>), dim3((N + 16 * RT - 1) / (16 * RT), splits),
+                       dim3(64 * MF_WAVES), 0, st, x, (const uint8_t*)w, y, M, K, N, (const TO*)bias, residual, rs,
+                       split_stride);
 }
 
 // Batch columns are processed in chunks of 32 (two 16-wide MFMA N tiles).
@@ -155,6 +159,32 @@ static hipError_t launch_mfma(const void* x, const void* w, void* y, int M, int 
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+// Split-K partial sums: part[s][m][n] (fp32) = sum over split s's share of the
+// super-blocks of dequant(W[n, k]) * x[m, k]; no bias, scale or residual (the
+// consumer adds the splits).  Splits multiply the blocks of a short-and-wide
+// problem (down projection: K = 8960, N = 1536) so the whole chip streams W.
+template <int FMT>
+static hipError_t launch_splitk(const void* x, const void* w, float* part, int M, int K, int N, int splits,
+                                hipStream_t st) {
+    const size_t ss = (size_t)M * N;
+    for (int m0 = 0; m0 < M; m0 += 32) {
+        const int mc = (M - m0 < 32) ? (M - m0) : 32;
+        const __half* xs = (const __half*)x + (size_t)m0 * K;
+        float* ps = part + (size_t)m0 * N;
+        if (mc > 16) launch_tile<__half, float, FMT, 1, 2>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
+        else launch_tile<__half, float, FMT, 1, 1>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t gemm_mfma_splitk(int fmt, const void* x, const void* w, float* part, int M, int K, int N, int splits,
+                            hipStream_t st) {
+    if (fmt == 4) return launch_splitk<4>(x, w, part, M, K, N, splits, st);
+    return launch_splitk<6>(x, w, part, M, K, N, splits, st);
 }
 
 hipError_t gemm_mfma(int fmt, int in_dt, int out_dt, const void* x, const void* w, void* y, int M, int K, int N,

@@ -12,8 +12,12 @@
 
 // ---------------------------------------------------------------------------
 // RMSNorm: out = x * rsqrt(mean(x^2) + eps) * w.  grid (rows), block (256).
-// Hidden sizes that are multiples of 8 use 16-byte loads.
+// Hidden sizes that are multiples of 8 and at most 8 * 4 * 256 keep their
+// 16-byte chunks (and the matching weight chunks, requested together) in
+// registers, so a row costs one memory round trip; other sizes take the
+// element loop.
 // ---------------------------------------------------------------------------
+#define RMS_CH 4  // 16-byte chunks per thread on the register path
 extern "C" __global__ __launch_bounds__(256) void rmsnorm_kernel(const __half* __restrict__ x,
                                                                  const __half* __restrict__ weight,
                                                                  __half* __restrict__ output, int hidden_size,
@@ -22,21 +26,33 @@ extern "C" __global__ __launch_bounds__(256) void rmsnorm_kernel(const __half* _
     const int row = blockIdx.x, tid = threadIdx.x;
     const __half* xr = x + (size_t)row * hidden_size;
     __half* orow = output + (size_t)row * hidden_size;
+    const int nv = hidden_size / 8;
+    const bool regs = hidden_size % 8 == 0 && nv <= RMS_CH * 256;
+    uint4 xv[RMS_CH], wv[RMS_CH];
     float ss = 0.f;
-    const int nv = (hidden_size % 8 == 0) ? hidden_size / 8 : 0;
-    for (int i = tid; i < nv; i += blockDim.x) {
-        const uint4 v = reinterpret_cast<const uint4*>(xr)[i];
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    if (regs) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float a = h2f_bits(w4[j]), b = h2f_bits(w4[j] >> 16);
-            ss = fmaf(a, a, ss);
-            ss = fmaf(b, b, ss);
+        for (int j = 0; j < RMS_CH; ++j) {
+            const int c = min(tid + 256 * j, nv - 1);
+            xv[j] = reinterpret_cast<const uint4*>(xr)[c];
+            wv[j] = reinterpret_cast<const uint4*>(weight)[c];
         }
-    }
-    for (int i = nv * 8 + tid; i < hidden_size; i += blockDim.x) {
-        const float a = __half2float(xr[i]);
-        ss = fmaf(a, a, ss);
+#pragma unroll
+        for (int j = 0; j < RMS_CH; ++j) {
+            if (tid + 256 * j >= nv) continue;
+            const uint32_t w4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float a = h2f_bits(w4[i]), b = h2f_bits(w4[i] >> 16);
+                ss = fmaf(a, a, ss);
+                ss = fmaf(b, b, ss);
+            }
+        }
+    } else {
+        for (int i = tid; i < hidden_size; i += blockDim.x) {
+            const float a = __half2float(xr[i]);
+            ss = fmaf(a, a, ss);
+        }
     }
     ss = wave_sum(ss);
     if ((tid & 63) == 0) part[tid >> 6] = ss;
@@ -45,8 +61,106 @@ extern "C" __global__ __launch_bounds__(256) void rmsnorm_kernel(const __half* _
     const int nw = (blockDim.x + 63) >> 6;
     for (int w = 0; w < nw; ++w) tot += part[w];
     const float inv = rsqrtf(tot / (float)hidden_size + eps);
-    for (int i = tid; i < hidden_size; i += blockDim.x)
-        orow[i] = __float2half(__half2float(xr[i]) * inv * __half2float(weight[i]));
+    if (regs) {
+#pragma unroll
+        for (int j = 0; j < RMS_CH; ++j) {
+            const int c = tid + 256 * j;
+            if (c >= nv) continue;
+            const uint32_t xa[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+            const uint32_t wa[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const __half lo = __float2half(h2f_bits(xa[i]) * inv * h2f_bits(wa[i]));
+                const __half hi = __float2half(h2f_bits(xa[i] >> 16) * inv * h2f_bits(wa[i] >> 16));
+                o[i] = (uint32_t)__half_as_ushort(lo) | ((uint32_t)__half_as_ushort(hi) << 16);
+            }
+            reinterpret_cast<uint4*>(orow)[c] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    } else {
+        for (int i = tid; i < hidden_size; i += blockDim.x)
+            orow[i] = __float2half(__half2float(xr[i]) * inv * __half2float(weight[i]));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Residual add of split-K partial sums, then RMSNorm (grid rows, block 256):
+//   x_out = fp16(x + sum_s part[s])        (the projection + residual store)
+//   xn    = fp16(x_out * rsqrt(mean(x_out^2) + eps) * w)
+// part is [n_parts][rows][hidden] fp32, summed in split order.  The sums
+// replace the residual epilogue of the projection and the following RMSNorm
+// node (reference: add_kernel, add.hip.template:4-17, then rmsnorm.hip.template:6-117),
+// one launch for both.  hidden % 8 == 0 and hidden <= 8 * RMS_CH * 256;
+// x_out may alias x (each thread reads its chunks before writing them).
+// ---------------------------------------------------------------------------
+#define ADDN_MAX_PARTS 8
+extern "C" __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const __half* x,
+                                                                     const float* __restrict__ part, int n_parts,
+                                                                     const __half* __restrict__ weight,
+                                                                     __half* x_out, __half* __restrict__ xn,
+                                                                     int rows, int hidden, float eps) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int nv = hidden / 8;
+    const size_t ro = (size_t)row * hidden;
+    const size_t ps = (size_t)rows * hidden;
+    uint4 xv[RMS_CH], wv[RMS_CH];
+    float acc[RMS_CH][8];
+#pragma unroll
+    for (int j = 0; j < RMS_CH; ++j) {
+        const int c = min(tid + 256 * j, nv - 1);
+        xv[j] = reinterpret_cast<const uint4*>(x + ro)[c];
+        wv[j] = reinterpret_cast<const uint4*>(weight)[c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+    }
+    for (int s = 0; s < n_parts; ++s) {
+        const float* pr = part + s * ps + ro;
+#pragma unroll
+        for (int j = 0; j < RMS_CH; ++j) {
+            const int c = min(tid + 256 * j, nv - 1);
+            const float4 a = reinterpret_cast<const float4*>(pr)[2 * c];
+            const float4 b = reinterpret_cast<const float4*>(pr)[2 * c + 1];
+            acc[j][0] += a.x; acc[j][1] += a.y; acc[j][2] += a.z; acc[j][3] += a.w;
+            acc[j][4] += b.x; acc[j][5] += b.y; acc[j][6] += b.z; acc[j][7] += b.w;
+        }
+    }
+    float ss = 0.f;
+    uint32_t xo[RMS_CH][4];
+#pragma unroll
+    for (int j = 0; j < RMS_CH; ++j) {
+        const uint32_t w4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const __half lo = __float2half(acc[j][2 * i] + h2f_bits(w4[i]));
+            const __half hi = __float2half(acc[j][2 * i + 1] + h2f_bits(w4[i] >> 16));
+            xo[j][i] = (uint32_t)__half_as_ushort(lo) | ((uint32_t)__half_as_ushort(hi) << 16);
+            const float a = __half2float(lo), b = __half2float(hi);
+            if (tid + 256 * j < nv) {
+                ss = fmaf(a, a, ss);
+                ss = fmaf(b, b, ss);
+            }
+        }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)hidden + eps);
+#pragma unroll
+    for (int j = 0; j < RMS_CH; ++j) {
+        const int c = tid + 256 * j;
+        if (c >= nv) continue;
+        const uint32_t wa[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const __half lo = __float2half(h2f_bits(xo[j][i]) * inv * h2f_bits(wa[i]));
+            const __half hi = __float2half(h2f_bits(xo[j][i] >> 16) * inv * h2f_bits(wa[i] >> 16));
+            o[i] = (uint32_t)__half_as_ushort(lo) | ((uint32_t)__half_as_ushort(hi) << 16);
+        }
+        reinterpret_cast<uint4*>(x_out + ro)[c] = make_uint4(xo[j][0], xo[j][1], xo[j][2], xo[j][3]);
+        reinterpret_cast<uint4*>(xn + ro)[c] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -572,6 +686,13 @@ hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, floa
 hipError_t rmsnorm(const void* x, const void* w, void* out, int rows, int hidden, float eps, hipStream_t st) {
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, (const __half*)x, (const __half*)w,
                        (__half*)out, hidden, eps);
+    return hipGetLastError();
+}
+
+hipError_t add_rmsnorm(const void* x, const float* part, int n_parts, const void* w, void* x_out, void* xn,
+                      int rows, int hidden, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(256), 0, st, (const __half*)x, part, n_parts,
+                       (const __half*)w, (__half*)x_out, (__half*)xn, rows, hidden, eps);
     return hipGetLastError();
 }
 

@@ -33,6 +33,8 @@ SIGNATURES = {
     "vte_attn_split_kv": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _i, _i, _i, _vp, _vp],
     "vte_kv_append": [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp],
     "vte_rmsnorm": [_vp, _vp, _vp, _i, _i, _f, _vp],
+    "vte_add_rmsnorm": [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _f, _vp],
+    "vte_gemm_mfma_splitk": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "vte_rope": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i, _i, _vp],
     "vte_swiglu": [_vp, _vp, _vp, _i, _vp],
     "vte_add": [_vp, _vp, _vp, _i, _f, _vp],
@@ -102,6 +104,11 @@ class VTEKernels:
         self._check(self.lib.vte_gemm_mfma(FMT[fmt], DT[in_dtype], DT[out_dtype], _p(x), _p(w), _p(y), M, K, N,
                                            _p(bias), _p(residual), residual_scale, self._st(stream)), "vte_gemm_mfma")
 
+    def gemm_mfma_splitk(self, fmt: str, x, w, part, M: int, K: int, N: int, splits: int, stream=None) -> None:
+        """part[s][M][N] (fp32) = split s's share of dequant(W[N,K]) @ x[M,K] (fp16 x)."""
+        self._check(self.lib.vte_gemm_mfma_splitk(FMT[fmt], _p(x), _p(w), _p(part), M, K, N, splits,
+                                                  self._st(stream)), "vte_gemm_mfma_splitk")
+
     def dequantize(self, fmt: str, src, dst, n_elements: int, stream=None) -> None:
         self._check(self.lib.vte_dequantize(FMT[fmt], _p(src), _p(dst), n_elements, self._st(stream)),
                     "vte_dequantize")
@@ -124,6 +131,11 @@ class VTEKernels:
 
     def rmsnorm(self, x, w, out, rows, hidden, eps, stream=None):
         self._check(self.lib.vte_rmsnorm(_p(x), _p(w), _p(out), rows, hidden, eps, self._st(stream)), "vte_rmsnorm")
+
+    def add_rmsnorm(self, x, part, n_parts, w, x_out, xn, rows, hidden, eps, stream=None):
+        """x_out = fp16(x + sum of the n_parts fp32 partials); xn = RMSNorm(x_out) * w."""
+        self._check(self.lib.vte_add_rmsnorm(_p(x), _p(part), n_parts, _p(w), _p(x_out), _p(xn), rows, hidden, eps,
+                                             self._st(stream)), "vte_add_rmsnorm")
 
     def rope(self, q, k, cos_cache, sin_cache, batch, seq_len, n_q, n_kv, head_dim, kv_offset, rope_type=0,
              rotary_dim=0, stream=None):
