@@ -65,6 +65,8 @@ class HIPGraphExecutor:
         # gate/up+SwiGLU glue fused in; o-proj and down write split-K partial
         # sums that one launch adds to the residual and RMS-normalises
         self.mm_fused = fused and batch_size >= gemm_min_batch
+        # batch <= 4: the LSE combine runs in the o-proj prologue up to this many splits
+        self.oproj_combine_max_splits = 8
         self.K = kernels()
         self.graph = None
         self.graph_exec = None
@@ -156,7 +158,7 @@ class HIPGraphExecutor:
                           cfg.n_kv, cfg.head_dim, stream=st)
             # the o-proj blocks each re-read every split's partials, so the fused
             # combine only pays off while there are few splits (short caches)
-            combine_in_oproj = self.attn.max_splits <= 8
+            combine_in_oproj = self.attn.max_splits <= self.oproj_combine_max_splits
             if on("attn"):
                 self.attn.launch(self.q, self.k_cache[L], self.v_cache[L], None if combine_in_oproj else self.att,
                                  offs, self.kv_batch_stride, dtype="f16", batch=B, stream=st)

@@ -91,17 +91,29 @@ __device__ __forceinline__ void att_load_tile(AttTile& T, const __half* kb, cons
     }
 }
 
+// Eight consecutive query elements as fp16 (16- or 32-byte loads).
+__device__ __forceinline__ half8_t att_load_q8(const __half* p) { return *reinterpret_cast<const half8_t*>(p); }
+__device__ __forceinline__ half8_t att_load_q8(const float* p) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], c = reinterpret_cast<const float4*>(p)[1];
+    return half8_t{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                   (_Float16)c.x, (_Float16)c.y, (_Float16)c.z, (_Float16)c.w};
+}
+
 // One 32-token tile of a wave: scores (MFMA), online softmax, P.V (MFMA)
 // into the running (m_run, l_run, o_acc).  `vt` is the wave's LDS tile for
-// the transposed V.
+// the transposed V.  FIRST: the wave's first tile (nothing to rescale; the
+// P.V products start from zero).
+template <bool FIRST>
 __device__ __forceinline__ void att_tile_step(AttTile& T, int t0, int t_end, const half8_t (&qb)[ATT_D / 32],
                                               float scale, float& m_run, float& l_run,
                                               floatx4_t (&o_acc)[ATT_D / 16],
                                               uint32_t (*vt)[ATT_VT_STRIDE / 2], int lane, int col, int grp) {
     // rows at or past the end contribute p = 0; zero their V so that
-    // whatever the rows hold cannot turn 0 * V into NaN
+    // whatever the rows hold cannot turn 0 * V into NaN (tail tile only)
+    if (t0 + ATT_TILE > t_end) {
 #pragma unroll
-    for (int t = 0; t < ATT_TILE; ++t) T.vv[t] = (t0 + t < t_end) ? T.vv[t] : 0u;
+        for (int t = 0; t < ATT_TILE; ++t) T.vv[t] = (t0 + t < t_end) ? T.vv[t] : 0u;
+    }
     // ---- scores for 32 tokens: two 16x16 S^T tiles ----
     floatx4_t acc[2];
 #pragma unroll
@@ -133,8 +145,8 @@ __device__ __forceinline__ void att_tile_step(AttTile& T, int t0, int t_end, con
         }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float corr = __expf(m_run - m_new);
+    const float m_new = FIRST ? tmax : fmaxf(m_run, tmax);
+    const float corr = FIRST ? 0.f : __expf(m_run - m_new);
     // A operand of P.V: P[head = col][token slots (grp, j)], j < 4 -> tile 0, j >= 4 -> tile 1
     half8_t pa;
     float psum = 0.f;
@@ -146,31 +158,30 @@ __device__ __forceinline__ void att_tile_step(AttTile& T, int t0, int t_end, con
             psum += pv;
             pa[4 * tt + i] = (_Float16)pv;
         }
-    l_run = l_run * corr + psum;
+    l_run = FIRST ? psum : l_run * corr + psum;
     m_run = m_new;
     // rescale O rows (heads 4*grp + i) by their corr, held by lanes 4*grp + i
     float cr[4];
+    if (!FIRST) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * grp + i, 64);
+        for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * grp + i, 64);
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int dt = 0; dt < ATT_D / 16; ++dt) {
+        if (!FIRST) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o_acc[dt][i] *= cr[i];
+            for (int i = 0; i < 4; ++i) o_acc[dt][i] *= cr[i];
+        }
         // B operand: V[token slots][d = 16*dt + col]
         const uint32_t* vr = &vt[16 * dt + col][0];
         const uint2 lo = *reinterpret_cast<const uint2*>(vr + 2 * grp);       // tokens 4g .. 4g+3
         const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8 + 2 * grp);   // tokens 16+4g ..
-        half8_t vb8;
-        const uint32_t w4[4] = {lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            vb8[2 * j] = __builtin_bit_cast(_Float16, (unsigned short)(w4[j] & 0xFFFFu));
-            vb8[2 * j + 1] = __builtin_bit_cast(_Float16, (unsigned short)(w4[j] >> 16));
-        }
-        o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb8, o_acc[dt], 0, 0, 0);
+        const half8_t vb8 = __builtin_bit_cast(half8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb8, FIRST ? floatx4_t{0.f, 0.f, 0.f, 0.f} : o_acc[dt],
+                                                           0, 0, 0);
     }
     __builtin_amdgcn_wave_barrier();
 }
@@ -183,7 +194,7 @@ __device__ __forceinline__ void att_tile_step(AttTile& T, int t0, int t_end, con
 // length and the first tile arrive in one memory round trip; rows at or past
 // the length are masked (scores -inf, V zero).
 template <typename TQ, typename TO, bool SPEC, int TPW>
-__global__ __launch_bounds__(256) void attn_partial_gqa(
+__global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     const TQ* __restrict__ q,            // [B][n_q][D]
     const __half* __restrict__ k_cache, const __half* __restrict__ v_cache,
     float* __restrict__ part_m, float* __restrict__ part_l, float* __restrict__ part_o,
@@ -212,17 +223,15 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
     }
 
     // B operand: Q^T for this KV head's G query heads, fp16, zero-padded to 16.
+    // Rows past G read head G-1 and are zeroed by a select (no branch).
     half8_t qb[ATT_D / 32];
     {
-        const int qh = kvh * G + col;
+        const int qh = kvh * G + min(col, G - 1);
         const TQ* qp = q + ((size_t)b * n_q + qh) * ATT_D;
 #pragma unroll
         for (int s = 0; s < ATT_D / 32; ++s) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float v = (col < G) ? ld_act<TQ>(qp + 32 * s + 8 * grp + j) : 0.f;
-                qb[s][j] = (_Float16)v;
-            }
+            const half8_t v = att_load_q8(qp + 32 * s + 8 * grp);
+            qb[s] = (col < G) ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }
 
@@ -236,7 +245,7 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
     // per-wave O rows (block combine) and the split weights (LSE combine).
     union AttnLDS {
         uint32_t vt[ATT_WAVES][ATT_D][ATT_VT_STRIDE / 2];
-        float o[ATT_WAVES][ATT_MAXG][ATT_D + 4];
+        float o[ATT_WAVES][16][ATT_D + 4];  // heads >= G hold zeros (unconditional stores)
         float w[ATT_MAXG][ATT_MAX_COMBINE];
     };
     __shared__ AttnLDS lds;
@@ -256,7 +265,7 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
         if (TPW == 2) att_load_tile(T1, kb, vb, row_stride, t0 + ATT_WAVES * ATT_TILE, t_end - 1, col, grp, lane);
     }
     ATT_TS(1);
-    if (t0 < t_end) att_tile_step(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
+    if (t0 < t_end) att_tile_step<true>(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
     if (PW) {  // the wave's split is done: its statistics and outputs are the partials
         l_run += __shfl_xor(l_run, 16, 64);
         l_run += __shfl_xor(l_run, 32, 64);
@@ -276,12 +285,12 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
     }
     t0 += ATT_WAVES * ATT_TILE;
     if (TPW == 2) {
-        if (t0 < t_end) att_tile_step(T1, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
+        if (t0 < t_end) att_tile_step<false>(T1, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
         t0 += ATT_WAVES * ATT_TILE;
     }
     for (; t0 < t_end; t0 += ATT_WAVES * ATT_TILE) {
         att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
-        att_tile_step(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
+        att_tile_step<false>(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
     }
 
     ATT_TS(2);
@@ -293,10 +302,7 @@ __global__ __launch_bounds__(256) void attn_partial_gqa(
 #pragma unroll
     for (int dt = 0; dt < ATT_D / 16; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int h = 4 * grp + i;
-            if (h < G) o_sh[wv][h][16 * dt + col] = o_acc[dt][i];
-        }
+        for (int i = 0; i < 4; ++i) o_sh[wv][4 * grp + i][16 * dt + col] = o_acc[dt][i];
     __syncthreads();
     // thread -> (head h, dim pair): 256 threads cover 2 heads x 128 dims per pass
     for (int idx = threadIdx.x; idx < G * ATT_D; idx += 256) {

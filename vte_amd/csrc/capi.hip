@@ -185,6 +185,7 @@ int vte_attn_split_kv(int dtype, const void* q, const void* k_cache, const void*
     REQUIRE(counters == nullptr || max_splits <= 512, "attn: in-kernel combine supports at most 512 splits");
     REQUIRE(counters == nullptr || split > 32, "attn: in-kernel combine needs splits of more than 32 tokens");
     REQUIRE(aligned(k_cache, 16) && aligned(v_cache, 16), "attn: KV cache must be 16-byte aligned");
+    REQUIRE(aligned(q, 16), "attn: q must be 16-byte aligned");
     REQUIRE(kv_batch_stride % 8 == 0, "attn: kv_batch_stride must keep rows 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     hipError_t e = (dtype == VTE_F32)
