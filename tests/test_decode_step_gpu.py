@@ -133,3 +133,29 @@ def test_full_shape_batch16_vs_batch1(hip, full_model):
             assert rel_l2(l16[b], l1) <= 1.5e-2, (b, rel_l2(l16[b], l1))
     finally:
         ex1.close()
+
+
+@pytest.mark.parametrize("B,fused", [(1, True), (2, False), (8, True)])
+def test_gguf_model_matches_in_memory_model(hip, tiny_model, tmp_path, B, fused):
+    """The same weights loaded from a GGUF file (memory-mapped, raw blocks
+    uploaded as they lie in the file) give bit-identical logits and top-k."""
+    from vte_amd.core.gguf_model import GGUFQwen2, export_qwen2_gguf
+    path = tmp_path / "tiny.gguf"
+    export_qwen2_gguf(tiny_model, path)
+    gm = GGUFQwen2(path)
+    rng = np.random.default_rng(40 + B)
+    toks, pos = list(rng.integers(0, TINY.vocab, B)), list(rng.integers(0, 100, B))
+    out = []
+    try:
+        for m in (tiny_model, gm):
+            ex = HIPGraphExecutor(hip, m, batch_size=B, max_seq=128, top_k=40, fused=fused)
+            try:
+                ex.fill_kv_prefix(seed=7)
+                ex.execute_decode_batch(toks, pos)
+                out.append((ex.read_logits().copy(), ex.read_topk()[1].copy()))
+            finally:
+                ex.close()
+    finally:
+        gm.close()
+    assert np.array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
+    assert np.array_equal(out[0][1], out[1][1])

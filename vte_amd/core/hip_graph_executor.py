@@ -84,6 +84,10 @@ class HIPGraphExecutor:
 
         # ---- weights ----
         self.token_embd = W(model.token_embd, "token_embd")
+        # LM head: a separate output matrix when the model has one, else the tied embedding
+        lm = getattr(model, "lm_head", None)
+        self.lm_head_fmt = getattr(model, "lm_head_fmt", "q6_k")
+        self.lm_head = self.token_embd if lm is None or lm is model.token_embd else W(lm, "lm_head")
         self.output_norm = W(model.output_norm, "output_norm")
         self.layers = []
         for L, lw in enumerate(model.layers):
@@ -178,7 +182,7 @@ class HIPGraphExecutor:
             cur = 1 - cur
         self.h_final = cur
         if on("lm_head"):
-            K.norm_gemv(self.h[cur], self.output_norm, cfg.eps, self.token_embd, "q6_k", self.logits, B, H,
+            K.norm_gemv(self.h[cur], self.output_norm, cfg.eps, self.lm_head, self.lm_head_fmt, self.logits, B, H,
                         cfg.vocab, out_dtype="f32", stream=st)
         if self.top_k > 0 and on("topk"):
             K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st)
@@ -203,7 +207,7 @@ class HIPGraphExecutor:
             out["o_proj"] += wb(lw["o_fmt"], H, qd) + B * 2 * (qd + 2 * H)
             out["ffn_in"] += wb(lw["gate_fmt"], F, H) + wb(lw["up_fmt"], F, H) + 2 * H + B * 2 * (H + F)
             out["down"] += wb(lw["down_fmt"], H, F) + B * 2 * (F + 2 * H)
-        out["lm_head"] = wb("q6_k", cfg.vocab, H) + 2 * H + B * (2 * H + 4 * cfg.vocab)
+        out["lm_head"] = wb(self.lm_head_fmt, cfg.vocab, H) + 2 * H + B * (2 * H + 4 * cfg.vocab)
         out["topk"] = B * (4 * cfg.vocab + 8 * self.top_k)
         return out
 
@@ -265,7 +269,7 @@ class HIPGraphExecutor:
                 K.rmsnorm(self.h[1 - cur], nxt, self.xn, B, H, cfg.eps, stream=st)
             cur = 1 - cur
         self.h_final = cur
-        self._linear("q6_k", self.xn, self.token_embd, self.logits, H, cfg.vocab, out_dtype="f32")
+        self._linear(self.lm_head_fmt, self.xn, self.lm_head, self.logits, H, cfg.vocab, out_dtype="f32")
         if self.top_k > 0:
             K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st)
 
