@@ -44,9 +44,11 @@ MAX_SPLITK = 8  # split-K partial buffers of the batched o-proj / down projectio
 
 
 def splitk_splits(K: int) -> int:
-    """Splits of a batched projection over K: about one super-block (256
-    elements) per wave of the 8-wave blocks."""
-    return max(1, min(MAX_SPLITK, (K // 256) // 8))
+    """Splits of a batched projection over K: at most seven super-blocks
+    (256 elements) per 8-wave block, so no wave takes two, and at least two
+    splits (measured at B=16: o-proj K=1536 -> 2, down K=8960 -> 5)."""
+    n_sb = K // 256
+    return max(1, min(MAX_SPLITK, n_sb, max(2, -(-n_sb // 7))))
 
 
 class HIPGraphExecutor:

@@ -90,11 +90,12 @@ extern "C" __global__ __launch_bounds__(256) void rmsnorm_kernel(const __half* _
 // part is [n_parts][rows][hidden] fp32, summed in split order.  The sums
 // replace the residual epilogue of the projection and the following RMSNorm
 // node (reference: add_kernel, add.hip.template:4-17, then rmsnorm.hip.template:6-117),
-// one launch for both.  hidden % 8 == 0 and hidden <= 8 * RMS_CH * 256;
+// one launch for both.  hidden % 8 == 0 and hidden <= 8 * 4 * 256;
 // x_out may alias x (each thread reads its chunks before writing them).
 // ---------------------------------------------------------------------------
 #define ADDN_MAX_PARTS 8
-extern "C" __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const __half* x,
+template <int CH>  // 16-byte chunks per thread: ceil(hidden / 8 / 256)
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const __half* x,
                                                                      const float* __restrict__ part, int n_parts,
                                                                      const __half* __restrict__ weight,
                                                                      __half* x_out, __half* __restrict__ xn,
@@ -104,31 +105,38 @@ extern "C" __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const __hal
     const int nv = hidden / 8;
     const size_t ro = (size_t)row * hidden;
     const size_t ps = (size_t)rows * hidden;
-    uint4 xv[RMS_CH], wv[RMS_CH];
-    float acc[RMS_CH][8];
+    uint4 xv[CH], wv[CH];
+    float acc[CH][8];
 #pragma unroll
-    for (int j = 0; j < RMS_CH; ++j) {
+    for (int j = 0; j < CH; ++j) {
         const int c = min(tid + 256 * j, nv - 1);
         xv[j] = reinterpret_cast<const uint4*>(x + ro)[c];
         wv[j] = reinterpret_cast<const uint4*>(weight)[c];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
     }
-    for (int s = 0; s < n_parts; ++s) {
-        const float* pr = part + s * ps + ro;
+    // CH == 1: every split's loads are issued unconditionally (clamped split
+    // index, masked add), so they all travel in one memory round trip
 #pragma unroll
-        for (int j = 0; j < RMS_CH; ++j) {
+    for (int s = 0; s < ADDN_MAX_PARTS; ++s) {
+        if (CH > 1 && s >= n_parts) break;
+        const bool use = s < n_parts;
+        const float* pr = part + min(s, n_parts - 1) * ps + ro;
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
             const int c = min(tid + 256 * j, nv - 1);
             const float4 a = reinterpret_cast<const float4*>(pr)[2 * c];
             const float4 b = reinterpret_cast<const float4*>(pr)[2 * c + 1];
-            acc[j][0] += a.x; acc[j][1] += a.y; acc[j][2] += a.z; acc[j][3] += a.w;
-            acc[j][4] += b.x; acc[j][5] += b.y; acc[j][6] += b.z; acc[j][7] += b.w;
+            acc[j][0] += use ? a.x : 0.f; acc[j][1] += use ? a.y : 0.f;
+            acc[j][2] += use ? a.z : 0.f; acc[j][3] += use ? a.w : 0.f;
+            acc[j][4] += use ? b.x : 0.f; acc[j][5] += use ? b.y : 0.f;
+            acc[j][6] += use ? b.z : 0.f; acc[j][7] += use ? b.w : 0.f;
         }
     }
     float ss = 0.f;
-    uint32_t xo[RMS_CH][4];
+    uint32_t xo[CH][4];
 #pragma unroll
-    for (int j = 0; j < RMS_CH; ++j) {
+    for (int j = 0; j < CH; ++j) {
         const uint32_t w4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -147,7 +155,7 @@ extern "C" __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const __hal
     __syncthreads();
     const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)hidden + eps);
 #pragma unroll
-    for (int j = 0; j < RMS_CH; ++j) {
+    for (int j = 0; j < CH; ++j) {
         const int c = tid + 256 * j;
         if (c >= nv) continue;
         const uint32_t wa[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
@@ -691,8 +699,15 @@ hipError_t rmsnorm(const void* x, const void* w, void* out, int rows, int hidden
 
 hipError_t add_rmsnorm(const void* x, const float* part, int n_parts, const void* w, void* x_out, void* xn,
                       int rows, int hidden, float eps, hipStream_t st) {
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(256), 0, st, (const __half*)x, part, n_parts,
-                       (const __half*)w, (__half*)x_out, (__half*)xn, rows, hidden, eps);
+    const int ch = (hidden / 8 + 255) / 256;
+#define ADDN_LAUNCH(C)                                                                                            \
+    hipLaunchKernelGGL(add_rmsnorm_kernel<C>, dim3(rows), dim3(256), 0, st, (const __half*)x, part, n_parts,     \
+                       (const __half*)w, (__half*)x_out, (__half*)xn, rows, hidden, eps)
+    if (ch == 1) ADDN_LAUNCH(1);
+    else if (ch == 2) ADDN_LAUNCH(2);
+    else if (ch == 3) ADDN_LAUNCH(3);
+    else ADDN_LAUNCH(4);
+#undef ADDN_LAUNCH
     return hipGetLastError();
 }
 
