@@ -472,9 +472,9 @@ __device__ __forceinline__ void tile_w_issue(TileW<UPT>& W, const TileGeo& T, in
         const uint8_t* rowp = lr < T.hA ? T.bA + (size_t)lr * T.rb : T.bB + (size_t)(lr - T.hA) * T.rb;
         if (FMT == 4) {
             const uint8_t* blk = rowp + sb * Q4K_BYTES;
-            W.w0[i] = ldg_stream16(blk);
-            W.w1[i] = ldg_stream16(blk + 16 + 32 * q);
-            W.w2[i] = ldg_stream16(blk + 32 + 32 * q);
+            W.w0[i] = ldg_g16(blk);
+            W.w1[i] = ldg_g16(blk + 16 + 32 * q);
+            W.w2[i] = ldg_g16(blk + 32 + 32 * q);
         } else {
             const uint8_t* blk = rowp + sb * Q6K_BYTES;
             const int h = q >> 1, l16 = (q & 1) * 16;
