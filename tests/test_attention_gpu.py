@@ -157,20 +157,22 @@ def test_reference_abi_split_kv_kernels(hip):
         assert rel_l2(got[b], ref) <= TOL
 
 
-@pytest.mark.parametrize("B,fmt", [(1, "q4_k"), (3, "q6_k")])
-def test_attn_out_gemv_combines_partials(hip, K, B, fmt):
+@pytest.mark.parametrize("B,fmt,max_seq,split", [(1, "q4_k", 1024, 128), (3, "q6_k", 1024, 128),
+                                                 (1, "q4_k", 2304, 128), (2, "q4_k", 4096, 128),
+                                                 (4, "q6_k", 2304, 64)])
+def test_attn_out_gemv_combines_partials(hip, K, B, fmt, max_seq, split):
     """o-proj with the LSE combine in its prologue equals combine-then-GEMV:
-    y = W . fp16(attention) + residual against the float64 oracle."""
+    y = W . fp16(attention) + residual against the float64 oracle.  Up to 36
+    splits (several load rounds of the combine); the split scratch starts as
+    NaN, so splits past a sequence's count must be masked."""
     from oracle import dequant as odq
     from vte_amd import synthetic as syn
-    rng = np.random.default_rng(40 + B)
-    max_seq, split = 1024, 128
+    rng = np.random.default_rng(40 + B + max_seq)
     q, kc, vc = _inputs(rng, B, max_seq)
-    offs = np.array([1023, 130, 7][:B], np.int32)
+    offs = np.array([max_seq - 1, 130, 7, 1500][:B], np.int32)
     ms = max_seq // split
-    pm = empty(hip, (B, NQ, ms), np.float32)
-    pl = empty(hip, (B, NQ, ms), np.float32)
-    po = empty(hip, (B, NQ, ms, D), np.float32)
+    nan = lambda *shape: up(hip, np.full(shape, np.nan, np.float32))
+    pm, pl, po = nan(B, NQ, ms), nan(B, NQ, ms), nan(B, NQ, ms, D)
     doffs = up(hip, offs)
     K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), pm, pl, po, None, B, NQ, NKV, D, SCALE, doffs,
                     max_seq * NKV * D, split, ms, dtype="f32", stream=hip.stream)

@@ -106,7 +106,7 @@ hipError_t fused_mv(const void* x, FmvPlan plan, hipStream_t st) {
     if ((reinterpret_cast<uintptr_t>(x) & 15) || (plan.K % QK_K) != 0) return hipErrorInvalidValue;
     if (plan.norm_w != nullptr && (reinterpret_cast<uintptr_t>(plan.norm_w) & 15)) return hipErrorInvalidValue;
     const int NC = plan.M <= 1 ? 1 : (plan.M <= 2 ? 2 : 4);
-    const int att_rows = plan.att_o != nullptr ? plan.M * plan.att_nq * plan.att_S : 0;
+    const int att_rows = plan.att_o != nullptr ? 2 * plan.M * plan.att_nq * plan.att_S : 0;
     static int upt_force = -1;  // VTE_FMV_UPT=1|2|4 pins units per thread (tuning)
     if (upt_force < 0) upt_force = env_int("VTE_FMV_UPT", 0);
     for (int upt : {4, 2, 1}) {

@@ -292,6 +292,93 @@ __device__ __forceinline__ void stage_combine(const FmvPlan& P, _Float16* xs, fl
     }
 }
 
+// The same combine with every global load of a column issued before its
+// results are needed (K = KC a multiple of 256 known at compile time): thread
+// tid owns dims tid + 256 j; the partial outputs of those dims for the
+// first CMB_SC splits, and the split statistics (one (head, split) per
+// thread, into LDS), are requested together; after a barrier one thread per
+// head turns the statistics into normalised weights; after another the
+// thread combines its dims (further rounds of CMB_SC splits if S is larger).
+// `wb` holds 2 * att_nq * att_S floats (maxima, then denominators).
+#define CMB_SC 9
+template <int NC, int KC>
+__device__ __forceinline__ void stage_combine_fast(const FmvPlan& P, _Float16* xs, float* wb, const int* pos_s,
+                                                   int tid) {
+    constexpr int DPT = KC / ROWS_THREADS;
+    const int M = NC == 1 ? 1 : P.M, nq = P.att_nq, S = P.att_S, ldx = xpad_len(KC);
+    const int per_col = nq * S;
+    float* wm = wb;
+    float* wl = wb + per_col;
+    for (int m = 0; m < M; ++m) {
+        const int ns = (pos_s[m] + 1 + P.att_split - 1) / P.att_split;
+        const float* om = P.att_o + (size_t)m * per_col * 128;
+        float ov[DPT][CMB_SC];
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) {
+            const int d = tid + ROWS_THREADS * j, h = d >> 7;
+#pragma unroll
+            for (int c = 0; c < CMB_SC; ++c)
+                ov[j][c] = om[((size_t)h * S + min(c, S - 1)) * 128 + (d & 127)];
+        }
+        for (int i = tid; i < per_col; i += ROWS_THREADS) {
+            const bool ok = i % S < ns;
+            const float mv = P.att_m[(size_t)m * per_col + i], lv = P.att_l[(size_t)m * per_col + i];
+            wm[i] = ok ? mv : -INFINITY;
+            wl[i] = ok ? lv : 0.f;
+        }
+        __syncthreads();
+        if (tid < nq) {  // head tid: w_s = exp(m_s - max) / sum_s l_s exp(m_s - max)
+            float* w = wm + tid * S;
+            const float* l = wl + tid * S;
+            float mx = -INFINITY;
+            for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, w[sp]);
+            float L = 0.f;
+            for (int sp = 0; sp < ns; ++sp) {
+                const float e = __expf(w[sp] - mx);
+                w[sp] = e;
+                L = fmaf(l[sp], e, L);
+            }
+            const float inv = 1.0f / fmaxf(L, 1e-20f);
+            for (int sp = 0; sp < ns; ++sp) w[sp] *= inv;
+        }
+        __syncthreads();
+        float acc[DPT];
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) {
+            const int h = (tid + ROWS_THREADS * j) >> 7;
+            acc[j] = 0.f;
+#pragma unroll
+            for (int c = 0; c < CMB_SC; ++c) acc[j] = c < ns ? fmaf(ov[j][c], wm[h * S + c], acc[j]) : acc[j];
+        }
+        for (int c0 = CMB_SC; c0 < ns; c0 += CMB_SC) {  // caches of more than CMB_SC splits
+#pragma unroll
+            for (int j = 0; j < DPT; ++j) {
+                const int d = tid + ROWS_THREADS * j, h = d >> 7;
+#pragma unroll
+                for (int c = 0; c < CMB_SC; ++c)
+                    ov[j][c] = om[((size_t)h * S + min(c0 + c, S - 1)) * 128 + (d & 127)];
+            }
+#pragma unroll
+            for (int j = 0; j < DPT; ++j) {
+                const int h = (tid + ROWS_THREADS * j) >> 7;
+#pragma unroll
+                for (int c = 0; c < CMB_SC; ++c)
+                    acc[j] = c0 + c < ns ? fmaf(ov[j][c], wm[h * S + min(c0 + c, S - 1)], acc[j]) : acc[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) {
+            const int e = tid + ROWS_THREADS * j;
+            xs[(size_t)m * ldx + xpad(xperm(e))] = (_Float16)acc[j];
+        }
+        if (m + 1 < M) __syncthreads();  // wm / wl are reused by the next column
+    }
+    for (int j = tid; j < (NC - M) * KC; j += ROWS_THREADS) {  // padding columns
+        const int m = M + j / KC, e = j % KC;
+        xs[(size_t)m * ldx + xpad(xperm(e))] = (_Float16)0.f;
+    }
+}
+
 // 32-bit aligned load holding element i of an fp16 (f32 = false) or fp32
 // array; returns the element's bits (0 for a null array).  The load is
 // unconditional (a null array reads `dummy`), which keeps the vector-memory
@@ -639,13 +726,13 @@ __device__ __forceinline__ FmvLDS fmv_lds(uint8_t* lds, int NC, int K, int UPT) 
 // first barrier (the activations are in), so the caller's weight loads do not
 // queue ahead of them; the normalisation then runs while those are in flight.
 // Ends with a barrier.
-template <int NC, bool F32, int KC, typename IssueFn>
+template <int NC, bool F32, int KC, bool ATT, typename IssueFn>
 __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const FmvPlan& P, const FmvLDS& L,
                                              float* wb, float (*red)[NC], int* pos_s, IssueFn issue) {
     const int K = KC > 0 ? KC : P.K, M = NC == 1 ? 1 : P.M;
     const int ldx = xpad_len(K);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const bool att_src = P.att_o != nullptr;
+    constexpr bool att_src = ATT;  // the launcher sets ATT exactly when P.att_o != nullptr
     const bool norm = P.norm_w != nullptr;
     const void* dummy = P.seg[0].w;
     const int pos_reg = (int)ld_elem_bits(P.kv_offset, dummy, min(tid, M - 1), true);
@@ -690,8 +777,9 @@ __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const F
     issue();
     TMV_M(4);
 
-    if (att_src) {
-        stage_combine<NC>(P, L.xs, wb, pos_s, tid);
+    if constexpr (att_src) {
+        if constexpr (KC > 0 && KC % ROWS_THREADS == 0) stage_combine_fast<NC, KC>(P, L.xs, wb, pos_s, tid);
+        else stage_combine<NC>(P, L.xs, wb, pos_s, tid);
         __syncthreads();
         act_sums<NC>(ActLDS{L.xs, L.s16}, K);
     } else if (norm) {
@@ -740,7 +828,7 @@ __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const F
 
 // One tile per block (grid = tiles): everything a block reads is requested
 // up front, so a block costs about one memory latency plus its arithmetic.
-template <int NC, bool F32, int UPT, int FMT, int KC, bool RO>
+template <int NC, bool F32, int UPT, int FMT, int KC, bool RO, bool ATT>
 __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPlan& P, const TileGeo& T,
                                          uint8_t* lds, float (*red)[NC], int* pos_s) {
     const int K = KC > 0 ? KC : P.K, M = NC == 1 ? 1 : P.M;
@@ -756,7 +844,7 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     tile_e_issue<NC>(E, P, T, M, dummy, tid);
     TMV_M(2);
     TileW<UPT> W;
-    fmv_prologue<NC, F32, KC>(x, P, L, wb, red, pos_s, [&]() {
+    fmv_prologue<NC, F32, KC, ATT>(x, P, L, wb, red, pos_s, [&]() {
         tile_w_issue<UPT, FMT, RO>(W, T, n_sb, per_row, tid);
         tile_e_rope(E, P, T, pos_s[E.em], dummy);  // kv offsets are in LDS after the first barrier
     });
@@ -783,15 +871,17 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
 // KC: the activation length K when fixed at compile time (0: P.K), so the
 // staging, norm and row-sum loops have constant trip counts and no divisions.
 // RO: range-owned unit mapping (see unit_pos).
-template <int NC, bool F32, int UPT, int KC, bool RO>
+// ATT: activations combined from split-KV partials (a separate instantiation:
+// the combine's registers would otherwise lower every mat-vec's occupancy).
+template <int NC, bool F32, int UPT, int KC, bool RO, bool ATT = false>
 __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const void* __restrict__ x, FmvPlan P) {
     extern __shared__ uint4 smem_fmv[];
     __shared__ float red[4][NC];
     __shared__ int pos_s[NC];
     const TileGeo T = tile_geo(P, blockIdx.x);
     uint8_t* lds = reinterpret_cast<uint8_t*>(smem_fmv);
-    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4, KC, RO>(x, P, T, lds, red, pos_s);
-    else tmv_body<NC, F32, UPT, 6, KC, RO>(x, P, T, lds, red, pos_s);
+    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4, KC, RO, ATT>(x, P, T, lds, red, pos_s);
+    else tmv_body<NC, F32, UPT, 6, KC, RO, ATT>(x, P, T, lds, red, pos_s);
 }
 
 // Range-owned mapping when a row's units fill the block's threads with at
@@ -805,6 +895,14 @@ __host__ __device__ inline bool fmv_ro(int K) {
 template <int NC, bool F32, int KC, bool RO>
 static void fmv_launch_k(int upt, int total, size_t lds, hipStream_t st, const void* x, const FmvPlan& plan) {
     const dim3 g(total), b(ROWS_THREADS);
+    if constexpr (!F32 && KC != 8960) {  // attention-output activations (o-proj): fp16 path, K = q_dim
+        if (plan.att_o != nullptr) {
+            if (upt == 4) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4, KC, RO, true>), g, b, lds, st, x, plan);
+            else if (upt == 2) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 2, KC, RO, true>), g, b, lds, st, x, plan);
+            else hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 1, KC, RO, true>), g, b, lds, st, x, plan);
+            return;
+        }
+    }
     if (upt == 4) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4, KC, RO>), g, b, lds, st, x, plan);
     else if (upt == 2) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 2, KC, RO>), g, b, lds, st, x, plan);
     else hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 1, KC, RO>), g, b, lds, st, x, plan);

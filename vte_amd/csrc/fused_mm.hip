@@ -24,6 +24,16 @@
 
 #define MM_MAX_SEG 3
 
+#ifdef MM_TRACE
+__device__ unsigned long long mm_trace[8192][8];
+#define MM_TS(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) mm_trace[blockIdx.x][k] = wall_clock64(); } while (0)
+extern "C" int vte_dbg_mm_trace_read(void* host, int blocks) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(mm_trace), (size_t)blocks * 64, 0, hipMemcpyDeviceToHost);
+}
+#else
+#define MM_TS(k) do { } while (0)
+#endif
+
 enum MmMode : int {
     MM_STORE = 0,        // out[m][row] = fp16(acc + bias)
     MM_ROPE_Q = 2,       // fp16(acc + bias), rotated -> out (q [m][rows])
@@ -109,12 +119,12 @@ __device__ __forceinline__ const uint8_t* mm_row(const MmTile& T, int rr) {
     return S.w + (size_t)(T.j0 + 64 + pc) * S.row_bytes;
 }
 
-template <int FMT, int RT, int NT>
+template <int FMT, int RT, int NT, int NW>
 __device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64]) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int K = P.K, M = P.M, n_sb = K / QK_K;
-    const int sb0 = (n_sb * wv) / MF_WAVES, sb1 = (n_sb * (wv + 1)) / MF_WAVES;
+    const int sb0 = (n_sb * wv) / NW, sb1 = (n_sb * (wv + 1)) / NW;
     const __half* x = P.x;
 
     floatx4_t acc[RT][NT];
@@ -137,6 +147,12 @@ __device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float 
                 bx[t][nt] = load_x8<__half>(x + (size_t)(m < M ? m : 0) * K + kb, m < M);
             }
         }
+#ifdef MM_TRACE
+        if (sb == sb0 && threadIdx.x == 0) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            MM_TS(1);
+        }
+#endif
         if (FMT == 4) {
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
@@ -186,28 +202,38 @@ __device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float 
             for (int i = 0; i < 4; ++i) red[wv][rt][nt][i][lane] = acc[rt][nt][i];
 }
 
-// Sum over the 8 waves of tile row rr, batch column mc (C layout: lane
+// Sum over the NW waves of tile row rr, batch column mc (C layout: lane
 // (col, grp) holds rows 4*grp+i of a 16-row tile for column col).
-template <int RT, int NT>
+template <int RT, int NT, int NW>
 __device__ __forceinline__ float mm_sum(float (*red)[RT][NT][4][64], int rr, int mc) {
     const int rt = rr >> 4, rw = rr & 15, nt = mc >> 4, cc = mc & 15;
     const int ln = cc + 16 * (rw >> 2), i = rw & 3;
     float s = 0.f;
 #pragma unroll
-    for (int wq = 0; wq < MF_WAVES; ++wq) s += red[wq][rt][nt][i][ln];
+    for (int wq = 0; wq < NW; ++wq) s += red[wq][rt][nt][i][ln];
     return s;
 }
 
 __device__ __forceinline__ float mm_bias(const __half* b, int row) { return b ? __half2float(b[row]) : 0.f; }
 
-template <int RT, int NT>
-__global__ __launch_bounds__(512) void fused_mm_kernel(MmPlan P) {
-    __shared__ float red[MF_WAVES][RT][NT][4][64];
+// NW waves per block split K (6 for K = 1536: one super-block each).
+template <int RT, int NT, int NW>
+__global__ __launch_bounds__(64 * NW) void fused_mm_kernel(MmPlan P) {
+    __shared__ float red[NW][RT][NT][4][64];
+    MM_TS(0);
     const MmTile T = mm_tile<RT>(P, blockIdx.x);
     const MmSeg& S = *T.S;
-    if (S.fmt == 4) mm_body<4, RT, NT>(P, T, red);
-    else mm_body<6, RT, NT>(P, T, red);
+    if (S.fmt == 4) mm_body<4, RT, NT, NW>(P, T, red);
+    else mm_body<6, RT, NT, NW>(P, T, red);
+    MM_TS(2);
     __syncthreads();
+    MM_TS(3);
+#ifdef MM_TRACE
+    if (threadIdx.x == 0 && blockIdx.x < 8192) {
+        mm_trace[blockIdx.x][5] = __builtin_amdgcn_s_getreg(4 | (31 << 11));
+        mm_trace[blockIdx.x][6] = __builtin_amdgcn_s_getreg(20 | (31 << 11));
+    }
+#endif
 
     const int M = P.M;
     if (!mm_paired(S.mode)) {
@@ -215,7 +241,7 @@ __global__ __launch_bounds__(512) void fused_mm_kernel(MmPlan P) {
             const int rr = o / (16 * NT), mc = o % (16 * NT);
             if (rr >= T.nvalid || mc >= M) continue;
             const int row = T.j0 + rr;
-            const __half v = __float2half(mm_sum<RT, NT>(red, rr, mc) + mm_bias(S.bias, row));
+            const __half v = __float2half(mm_sum<RT, NT, NW>(red, rr, mc) + mm_bias(S.bias, row));
             if (S.mode == MM_VCACHE) {
                 const int pos = P.kv_offset[mc];
                 P.v_cache[(size_t)mc * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128 + (row % 128)] = v;
@@ -223,12 +249,13 @@ __global__ __launch_bounds__(512) void fused_mm_kernel(MmPlan P) {
                 S.out[(size_t)mc * S.n_rows + row] = v;
             }
         }
+        MM_TS(4);
         return;
     }
     for (int o = threadIdx.x; o < 8 * RT * 16 * NT; o += blockDim.x) {
         const int p = o / (16 * NT), mc = o % (16 * NT);
         if (p >= T.nvalid || mc >= M) continue;
-        const float a = mm_sum<RT, NT>(red, p, mc), b = mm_sum<RT, NT>(red, p + 8 * RT, mc);
+        const float a = mm_sum<RT, NT, NW>(red, p, mc), b = mm_sum<RT, NT, NW>(red, p + 8 * RT, mc);
         const int row = T.j0 + p;
         if (S.mode == MM_SWIGLU) {
             const float g = __half2float(__float2half(a)), u = __half2float(__float2half(b));
@@ -250,6 +277,7 @@ __global__ __launch_bounds__(512) void fused_mm_kernel(MmPlan P) {
             kc[d + 64] = o2;
         }
     }
+    MM_TS(4);
 }
 
 namespace vte {
@@ -291,8 +319,13 @@ static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipSt
         for (int s = 0; s < P.nseg; ++s) P.seg[s].out = out0[s] ? out0[s] + (size_t)m0 * out_ld_elems[s] : nullptr;
         P.k_cache = kc0 ? kc0 + (size_t)m0 * P.kv_batch_stride : nullptr;
         P.v_cache = vc0 ? vc0 + (size_t)m0 * P.kv_batch_stride : nullptr;
-        if (mc > 16) hipLaunchKernelGGL((fused_mm_kernel<RT, 2>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
-        else hipLaunchKernelGGL((fused_mm_kernel<RT, 1>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
+        if (P.K == 6 * QK_K) {
+            if (mc > 16) hipLaunchKernelGGL((fused_mm_kernel<RT, 2, 6>), dim3(total), dim3(64 * 6), 0, st, P);
+            else hipLaunchKernelGGL((fused_mm_kernel<RT, 1, 6>), dim3(total), dim3(64 * 6), 0, st, P);
+        } else {
+            if (mc > 16) hipLaunchKernelGGL((fused_mm_kernel<RT, 2, MF_WAVES>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
+            else hipLaunchKernelGGL((fused_mm_kernel<RT, 1, MF_WAVES>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
+        }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -341,7 +374,7 @@ hipError_t gate_up_mm(const void* xn, const void* w_gate, const void* w_up, int 
     P.seg[0] = mm_seg(w_gate, w_up, out, nullptr, fmt, ffn, MM_SWIGLU, K, RT);
     P.nseg = 1;
     size_t ld[MM_MAX_SEG] = {(size_t)ffn, 0, 0};
-    return RT == 2 ? mm_run<2>(P, B, ld, st) : mm_run<1>(P, B, ld, st);
+    return RT == 4 ? mm_run<4>(P, B, ld, st) : RT == 2 ? mm_run<2>(P, B, ld, st) : mm_run<1>(P, B, ld, st);
 }
 
 }  // namespace vte
