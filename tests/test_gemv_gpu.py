@@ -121,6 +121,34 @@ def test_gemm_mfma_configs(hip, K, fmt, n, k, M):
     assert rel_l2(down(y), dq.gemv(fmt, raw, n, k, x)) <= TOL
 
 
+@pytest.mark.parametrize("fmt,n", [("q6_k", 20000), ("q4_k", 16390)])
+@pytest.mark.parametrize("M,src", [(8, "f32"), (16, "f16"), (33, "f16"), (20, "f32")])
+def test_gemm_mfma_tall_streaming(hip, K, fmt, n, M, src):
+    """K = 1536, N >= 16384 (the LM head shape at batch >= 8) takes the
+    persistent streaming kernel: ragged last row tile (n % 16 != 0), batch
+    chunks of 32 with a ragged second chunk (M = 33), fp16 activations with
+    the f16 bias/residual epilogue and fp32 activations with f32 output."""
+    k = 1536
+    rng = np.random.default_rng(n + M)
+    raw = syn.random_matrix(fmt, rng, n, k)
+    rows = np.unique(np.concatenate([rng.choice(n, 1024, replace=False), np.arange(n - 20, n), np.arange(20)]))
+    rb = raw.reshape(n, -1)[rows].reshape(-1)
+    if src == "f32":
+        x = rng.standard_normal((M, k)).astype(np.float32)
+        y = empty(hip, (M, n), np.float32)
+        K.gemm_mfma(fmt, up(hip, x), up(hip, raw), y, M, k, n, stream=hip.stream)
+        ref = dq.gemv(fmt, rb, len(rows), k, x)
+    else:
+        x = rng.standard_normal((M, k)).astype(np.float16)
+        bias = (0.1 * rng.standard_normal(n)).astype(np.float16)
+        res = rng.standard_normal((M, n)).astype(np.float16)
+        y = empty(hip, (M, n), np.float16)
+        K.gemm_mfma(fmt, up(hip, x), up(hip, raw), y, M, k, n, bias=up(hip, bias), residual=up(hip, res),
+                    residual_scale=0.5, in_dtype="f16", out_dtype="f16", stream=hip.stream)
+        ref = dq.gemv_epilogue(dq.gemv(fmt, rb, len(rows), k, x.astype(np.float32)), bias[rows], res[:, rows], 0.5)
+    assert rel_l2(down(y)[:, rows], ref) <= TOL
+
+
 def test_gemm_mfma_f16_epilogue(hip, K):
     n, k, M = 512, 1536, 16
     rng = np.random.default_rng(5)

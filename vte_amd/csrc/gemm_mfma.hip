@@ -23,14 +23,19 @@
 //      Q6_K step t, group g: half h = t>>2, quarter q = t&3, l = 8g .. 8g+7
 //  * Q4_K rows are 16-byte aligned and Q6_K rows 2-byte aligned; both load
 //    straight from HBM (unaligned 8-byte loads stream at full speed).
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
 #include "mfma_deq.h"
 
-template <typename TI, typename TO, int FMT, int RT, int NT>
-__global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
+// NW waves per block split K (6 when K = 1536: one super-block each).
+template <typename TI, typename TO, int FMT, int RT, int NT, int NW = MF_WAVES>
+__global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
                                                         TO* __restrict__ y, int M, int K, int N,
                                                         const TO* __restrict__ bias, const TO* __restrict__ residual,
                                                         float rs, size_t split_stride) {
-    __shared__ float red[MF_WAVES][RT][NT][4][64];
+    __shared__ float red[NW][RT][NT][4][64];
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -41,7 +46,7 @@ __global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x
     // split-K over blockIdx.y: this block's super-block range, then each
     // wave's contiguous share of it; split s writes its sums at y + s * split_stride
     const int kb0 = (n_sb * (int)blockIdx.y) / (int)gridDim.y, kb1 = (n_sb * ((int)blockIdx.y + 1)) / (int)gridDim.y;
-    const int sb0 = kb0 + ((kb1 - kb0) * wv) / MF_WAVES, sb1 = kb0 + ((kb1 - kb0) * (wv + 1)) / MF_WAVES;
+    const int sb0 = kb0 + ((kb1 - kb0) * wv) / NW, sb1 = kb0 + ((kb1 - kb0) * (wv + 1)) / NW;
     y += blockIdx.y * split_stride;
 
     floatx4_t acc[RT][NT];
@@ -121,9 +126,88 @@ __global__ __launch_bounds__(512) void gemm_mfma_kernel(const TI* __restrict__ x
         const int ln = cc + 16 * (rw >> 2), i = rw & 3;
         float s = 0.f;
 #pragma unroll
-        for (int wq = 0; wq < MF_WAVES; ++wq) s += red[wq][rt][nt][i][ln];
+        for (int wq = 0; wq < NW; ++wq) s += red[wq][rt][nt][i][ln];
         const int row = row0 + rr;
         if (row < N && mc < M) gemv_store<TO>(y, bias, residual, rs, row, mc, N, s);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming batched GEMM for tall matrices at K = 1536 (the LM head at batch
+// >= 8).  Persistent 8-wave blocks, two per CU; the batch's activations are staged once
+// per block in LDS as fp16 rows padded by 16 bytes (the 16 lanes of an MFMA
+// B-operand read hit distinct banks); each wave then owns whole 16-row
+// tiles: it requests the raw bytes of all six super-blocks of its rows at
+// once, dequantises them into A operands and runs the K loop with the B
+// operands read from LDS, so a tile needs no cross-wave reduction and no
+// barrier, and the waves of a CU keep their loads in flight independently
+// (three super-blocks ahead).  Its time is mostly the Q6_K dequantisation
+// VALU (measured: 85 us for 151936 x 1536 at batch 16, 44 us with the
+// dequantisation replaced by raw bits).
+// ---------------------------------------------------------------------------
+#define GS_K 1536
+#define GS_NSB (GS_K / QK_K)
+#define GS_LDX (GS_K + 8)  // halves per staged activation row
+
+template <typename TI, typename TO, int FMT, int NT, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gemm_stream_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
+                                                          TO* __restrict__ y, int M, int N, const TO* __restrict__ bias,
+                                                          const TO* __restrict__ residual, float rs) {
+    extern __shared__ uint4 gs_smem[];
+    _Float16* xs = reinterpret_cast<_Float16*>(gs_smem);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    constexpr int CPR = GS_K / 8;  // 8-element chunks per row
+    for (int i = tid; i < 16 * NT * CPR; i += 64 * WPB) {
+        const int m = i / CPR, c = i - m * CPR;
+        const half8_t v = load_x8<TI>(x + (size_t)(m < M ? m : 0) * GS_K + 8 * c, m < M);
+        *reinterpret_cast<half8_t*>(xs + m * GS_LDX + 8 * c) = v;
+    }
+    __syncthreads();
+    constexpr int BPB = FMT == 4 ? Q4K_BYTES : Q6K_BYTES;
+    const size_t row_bytes = (size_t)GS_NSB * BPB;
+    const int ntiles = (N + 15) / 16;
+    for (int tile = blockIdx.x * WPB + wv; tile < ntiles; tile += gridDim.x * WPB) {
+        const uint8_t* rowp = w + (size_t)min(tile * 16 + col, N - 1) * row_bytes;
+        using Raw = typename std::conditional<FMT == 4, Q4Raw, Q6Raw>::type;
+        auto load = [&](int sb, Raw& r) {
+            if constexpr (FMT == 4) q4_raw_load(rowp + sb * BPB, grp, r);
+            else q6_raw_load(rowp + sb * BPB, grp, r);
+        };
+        Raw cur, nxt, nx2;
+        load(0, cur);
+        load(1, nxt);
+        load(2, nx2);
+        floatx4_t acc[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        // three super-blocks in flight per wave while sb is multiplied
+#pragma unroll 1
+        for (int sb = 0; sb < GS_NSB; ++sb) {
+            half8_t a[8];
+            if constexpr (FMT == 4) q4_raw_operands(cur, grp, a);
+            else q6_raw_operands(cur, grp, a);
+            cur = nxt;
+            nxt = nx2;
+            load(min(sb + 3, GS_NSB - 1), nx2);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int kb = sb * QK_K + kslot_base<FMT>(t, grp);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const half8_t b = *reinterpret_cast<const half8_t*>(xs + (nt * 16 + col) * GS_LDX + kb);
+                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b, acc[nt], 0, 0, 0);
+                }
+            }
+        }
+        // C layout: lane (col, grp) holds weight rows 4*grp + i for batch column col
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = tile * 16 + 4 * grp + i, m = nt * 16 + col;
+                if (r < N && m < M) gemv_store<TO>(y, bias, residual, rs, r, m, N, acc[nt][i]);
+            }
     }
 }
 
@@ -132,16 +216,55 @@ namespace vte {
 template <typename TI, typename TO, int FMT, int RT, int NT>
 static void launch_tile(const TI* x, const void* w, TO* y, int M, int K, int N, const void* bias,
                         const TO* residual, float rs, hipStream_t st, int splits = 1, size_t split_stride = 0) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<TI, TO, FMT, RT, NT>), dim3((N + 16 * RT - 1) / (16 * RT), splits),
-                       dim3(64 * MF_WAVES), 0, st, x, (const uint8_t*)w, y, M, K, N, (const TO*)bias, residual, rs,
-                       split_stride);
+    const dim3 g((N + 16 * RT - 1) / (16 * RT), splits);
+    if (K == 6 * QK_K && splits == 1)
+        hipLaunchKernelGGL((gemm_mfma_kernel<TI, TO, FMT, RT, NT, 6>), g, dim3(64 * 6), 0, st, x, (const uint8_t*)w, y,
+                           M, K, N, (const TO*)bias, residual, rs, split_stride);
+    else
+        hipLaunchKernelGGL((gemm_mfma_kernel<TI, TO, FMT, RT, NT>), g, dim3(64 * MF_WAVES), 0, st, x,
+                           (const uint8_t*)w, y, M, K, N, (const TO*)bias, residual, rs, split_stride);
 }
 
 // Batch columns are processed in chunks of 32 (two 16-wide MFMA N tiles).
 // Tall matrices (N >= 4096) use 32-row tiles.
+static int gs_num_cus() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    }
+    return n;
+}
+
+// The streaming kernel for K = 1536 and N >= 16384 (one launch per 32 batch columns).
+template <typename TI, typename TO, int FMT>
+static hipError_t launch_stream(const void* x, const void* w, void* y, int M, int N, const void* bias,
+                                const void* residual, float rs, hipStream_t st) {
+    constexpr int WPB = 8;  // 8-wave blocks, two per CU
+    const int ntiles = (N + 15) / 16;
+    const int grid = std::min((ntiles + WPB - 1) / WPB, gs_num_cus() * 2);
+    for (int m0 = 0; m0 < M; m0 += 32) {
+        const int mc = (M - m0 < 32) ? (M - m0) : 32;
+        const TI* xs = (const TI*)x + (size_t)m0 * GS_K;
+        TO* ys = (TO*)y + (size_t)m0 * N;
+        const TO* rp = residual ? (const TO*)residual + (size_t)m0 * N : nullptr;
+#define GS_LAUNCH(NT_, W_)                                                                                          \
+    hipLaunchKernelGGL((gemm_stream_kernel<TI, TO, FMT, NT_, W_>), dim3(grid), dim3(64 * W_), 16 * NT_ * GS_LDX * 2, st, \
+                       xs, (const uint8_t*)w, ys, mc, N, (const TO*)bias, rp, rs)
+        if (mc > 16) GS_LAUNCH(2, WPB);
+        else GS_LAUNCH(1, WPB);
+#undef GS_LAUNCH
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 template <typename TI, typename TO, int FMT>
 static hipError_t launch_mfma(const void* x, const void* w, void* y, int M, int K, int N, const void* bias,
                               const void* residual, float rs, hipStream_t st) {
+    if (K == GS_K && N >= 16384) return launch_stream<TI, TO, FMT>(x, w, y, M, N, bias, residual, rs, st);
     const bool tall = N >= 4096;
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mc = (M - m0 < 32) ? (M - m0) : 32;

@@ -83,14 +83,27 @@ __device__ __forceinline__ uint2 q6_ld8(const uint8_t* p) {
     __builtin_memcpy(&v, p, 8);
     return v;
 }
-__device__ __forceinline__ void q6k_a_operands(const uint8_t* blk, int grp, half8_t (&a)[8]) {
-    const float d = h2f_bits(((const __attribute__((address_space(1))) uint16_t*)(blk + 208))[0]);
+// A lane's raw bytes of one Q6_K super-block (both halves), loaded ahead of
+// the dequantisation so several super-blocks can be in flight.
+struct Q6Raw {
+    uint2 qa[2], qb[2], qh[2], sc[2];
+    uint32_t d;
+};
+__device__ __forceinline__ void q6_raw_load(const uint8_t* blk, int grp, Q6Raw& r) {
+    r.d = ((const __attribute__((address_space(1))) uint16_t*)(blk + 208))[0];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-        const uint2 qa = q6_ld8(blk + 64 * hh + 8 * grp);
-        const uint2 qb = q6_ld8(blk + 64 * hh + 32 + 8 * grp);
-        const uint2 qh = q6_ld8(blk + 128 + 32 * hh + 8 * grp);
-        const uint2 scw = q6_ld8(blk + 192 + 8 * hh);
+        r.qa[hh] = q6_ld8(blk + 64 * hh + 8 * grp);
+        r.qb[hh] = q6_ld8(blk + 64 * hh + 32 + 8 * grp);
+        r.qh[hh] = q6_ld8(blk + 128 + 32 * hh + 8 * grp);
+        r.sc[hh] = q6_ld8(blk + 192 + 8 * hh);
+    }
+}
+__device__ __forceinline__ void q6_raw_operands(const Q6Raw& r, int grp, half8_t (&a)[8]) {
+    const float d = h2f_bits(r.d);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const uint2 qa = r.qa[hh], qb = r.qb[hh], qh = r.qh[hh], scw = r.sc[hh];
         const uint64_t sc = ((uint64_t)scw.y << 32) | scw.x;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -114,5 +127,40 @@ __device__ __forceinline__ void q6k_a_operands(const uint8_t* blk, int grp, half
             const half2_t z2 = {(_Float16)0.0f, (_Float16)0.0f};
             a[4 * hh + q] = deq8(u0, u1, (_Float16)32.0f, d2, z2);
         }
+    }
+}
+
+__device__ __forceinline__ void q6k_a_operands(const uint8_t* blk, int grp, half8_t (&a)[8]) {
+    Q6Raw r;
+    q6_raw_load(blk, grp, r);
+    q6_raw_operands(r, grp, a);
+}
+
+// Q4_K: the header and the lane's two 16-byte code chunks; operands for the
+// k-slot map of kslot_base<4>.
+struct Q4Raw {
+    uint4 h, q0, q1;
+};
+__device__ __forceinline__ void q4_raw_load(const uint8_t* blk, int grp, Q4Raw& r) {
+    r.h = *reinterpret_cast<const uint4*>(blk);
+    r.q0 = *reinterpret_cast<const uint4*>(blk + 16 + 16 * grp);
+    r.q1 = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (grp + 4));
+}
+__device__ __forceinline__ void q4_raw_operands(const Q4Raw& r, int grp, half8_t (&a)[8]) {
+    Q4KLaneScale s[2];
+    s[0] = q4k_lane_scale(r.h, grp >> 1);
+    s[1] = q4k_lane_scale(r.h, 2 + (grp >> 1));
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int ci = t >> 2, part = (t >> 1) & 1, e = t & 1;
+        const uint4 qc = ci == 0 ? r.q0 : r.q1;
+        const uint32_t wa = e == 0 ? qc.x : qc.z, wb = e == 0 ? qc.y : qc.w;
+        const uint32_t u0 = part ? ((wa >> 4) & 0x0F0F0F0Fu) : (wa & 0x0F0F0F0Fu);
+        const uint32_t u1 = part ? ((wb >> 4) & 0x0F0F0F0Fu) : (wb & 0x0F0F0F0Fu);
+        const float dd = part ? s[ci].d_hi : s[ci].d_lo;
+        const float mm = part ? s[ci].m_hi : s[ci].m_lo;
+        const half2_t d2 = {(_Float16)dd, (_Float16)dd};
+        const half2_t m2 = {(_Float16)mm, (_Float16)mm};
+        a[t] = deq8(u0, u1, (_Float16)0.0f, d2, m2);
     }
 }
