@@ -159,3 +159,42 @@ def test_gguf_model_matches_in_memory_model(hip, tiny_model, tmp_path, B, fused)
         gm.close()
     assert np.array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
     assert np.array_equal(out[0][1], out[1][1])
+
+
+def test_prefill_matches_token_by_token(hip, tiny_model):
+    """A 37-token prompt prefilled in chunks of 16 (the last one padded) into
+    sequence 1 of a 2-sequence executor gives the same next-token logits and
+    K/V rows as feeding the tokens one decode step at a time, and leaves
+    sequence 0's cache untouched."""
+    from vte_amd.core.prefill import PrefillRunner
+    cfg, max_seq, start, n = TINY, 128, 10, 37
+    rng = np.random.default_rng(77)
+    prompt = list(rng.integers(0, cfg.vocab, n))
+    exa = HIPGraphExecutor(hip, tiny_model, batch_size=2, max_seq=max_seq, top_k=40)
+    exb = HIPGraphExecutor(hip, tiny_model, batch_size=2, max_seq=max_seq, top_k=40)
+    runner = PrefillRunner(exa, chunk=16)
+    try:
+        exa.fill_kv_prefix(seed=5)
+        exb.fill_kv_prefix(seed=5)
+        hip.synchronize()
+        k0 = [exa.k_cache[L].numpy() for L in range(cfg.n_layers)]
+        sub = runner.prefill(prompt, seq=1, start=start)
+        got = sub.read_logits()[0]
+        got_idx = sub.read_topk()[1][0]
+        for i, t in enumerate(prompt):
+            exb.execute_decode_batch([0, t], [0, start + i])
+        ref = exb.read_logits()[1]
+        assert rel_l2(got, ref) <= TOL, rel_l2(got, ref)
+        order = np.lexsort((np.arange(cfg.vocab), -got))[:40]
+        assert np.array_equal(got_idx, order)
+        for L in range(cfg.n_layers):
+            hip.synchronize()
+            ka, kb = exa.k_cache[L].numpy(), exb.k_cache[L].numpy()
+            rows = slice(start, start + n)
+            assert rel_l2(ka[1, rows], kb[1, rows]) <= TOL, L
+            assert np.array_equal(ka[0].view(np.uint16), k0[L][0].view(np.uint16)), L
+            assert np.array_equal(ka[1, :start].view(np.uint16), k0[L][1, :start].view(np.uint16)), L
+    finally:
+        runner.close()
+        exa.close()
+        exb.close()

@@ -53,8 +53,15 @@ def splitk_splits(K: int) -> int:
 
 class HIPGraphExecutor:
     def __init__(self, hip: HIPRuntime, model: SyntheticQwen2, batch_size: int = 1, max_seq: Optional[int] = None,
-                 top_k: int = 40, gemm_min_batch: int = 8, split: Optional[int] = None, fused: bool = True):
+                 top_k: int = 40, gemm_min_batch: int = 8, split: Optional[int] = None, fused: bool = True,
+                 shared: Optional["HIPGraphExecutor"] = None, kv_seq: int = 0):
+        """``shared``: reuse that executor's weights, RoPE tables and the KV
+        cache of its sequence ``kv_seq`` (columns of this executor are tokens of
+        that one sequence: KV rows at each column's own position, stride 0),
+        with activation buffers of ``batch_size`` columns and only the last
+        column's logits (the prefill of ``PrefillRunner``)."""
         self.hip = hip
+        self.prefill_of = shared
         self.cfg: Qwen2Config = model.cfg
         cfg = self.cfg
         self.B = batch_size
@@ -74,16 +81,53 @@ class HIPGraphExecutor:
         self.graph_exec = None
 
         B, H = batch_size, cfg.hidden
-        kv_elems = B * self.max_seq * cfg.n_kv * cfg.head_dim
+        if shared is not None:
+            self.max_seq = shared.max_seq
+            if not 0 <= kv_seq < shared.B:
+                raise HIPSafetyError(f"kv_seq {kv_seq} outside the shared executor's batch of {shared.B}")
+        kv_elems = 0 if shared is not None else B * self.max_seq * cfg.n_kv * cfg.head_dim
         act_bytes = 4 * (B * (2 * H + cfg.q_dim * 2 + cfg.kv_dim * 2 + 3 * cfg.ffn) * 2 + B * cfg.vocab * 4)
         act_bytes += MAX_SPLITK * B * H * 4
-        need = model.weight_bytes() + 2 * cfg.n_layers * kv_elems * 2 + act_bytes + (64 << 20)
+        need = (0 if shared is not None else model.weight_bytes()) + 2 * cfg.n_layers * kv_elems * 2 + act_bytes + \
+            (64 << 20)
         need += (cfg.n_layers * len(PROJ) + 16) * 1024  # alignment and slack per tensor
         self.slab = SlabAllocator(hip, 0, requested_pool_size=need + (256 << 20))
         self.slab.initialize()
         A = lambda shape, dt, tag, reg=MemoryRegion.ACTIVATIONS: DeviceArray(hip, shape, dt, tag, self.slab, reg)
         W = lambda arr, tag: DeviceArray.from_numpy(hip, arr, tag, self.slab, MemoryRegion.WEIGHTS)
 
+        if shared is not None:
+            self._share(shared, kv_seq)
+        else:
+            self._upload_weights(model, W, A)
+        # ---- activations (fp16 between nodes, fp32 logits) ----
+        self.h = [A((B, H), np.float16, "hidden0"), A((B, H), np.float16, "hidden1")]
+        self.xn = A((B, H), np.float16, "normed")
+        self.q = A((B, cfg.q_dim), np.float16, "q")
+        self.k = A((B, cfg.kv_dim), np.float16, "k")
+        self.v = A((B, cfg.kv_dim), np.float16, "v")
+        self.att = A((B, cfg.q_dim), np.float16, "attn_out")
+        self.g = A((B, cfg.ffn), np.float16, "gate")
+        self.u = A((B, cfg.ffn), np.float16, "up")
+        self.a = A((B, cfg.ffn), np.float16, "swiglu")
+        self.part = A((MAX_SPLITK, B, H), np.float32, "splitk_partials")
+        self.out_rows = 1 if shared is not None else B  # prefill: only the last column's logits
+        self.logits = A((self.out_rows, cfg.vocab), np.float32, "logits")
+        self.topk_val = A((self.out_rows, max(top_k, 1)), np.float32, "topk_val")
+        self.topk_idx = A((self.out_rows, max(top_k, 1)), np.int32, "topk_idx")
+        self.topk_scratch = A(self.K.topk_scratch_bytes(self.out_rows), np.uint8, "topk_scratch")
+        self.staging_input = A(B, np.int32, "staging_tokens")
+        self.staging_kv_offset = A(B, np.int32, "staging_kv_offset")
+        if shared is None:
+            cos_c, sin_c = build_rope_cache(self.max_seq, cfg.head_dim, cfg.rope_theta)
+            self.rope_cos = W(cos_c, "rope_cos")
+            self.rope_sin = W(sin_c, "rope_sin")
+        self.attn = SplitKVAttentionDispatcher(hip, cfg.n_q, cfg.n_kv, cfg.head_dim, self.max_seq, B, split,
+                                               allocator=self.slab)
+        self.h_final = 0  # index of the hidden buffer holding the layer output
+
+    def _upload_weights(self, model, W, A) -> None:
+        cfg, B = self.cfg, self.B
         # ---- weights ----
         self.token_embd = W(model.token_embd, "token_embd")
         # LM head: a separate output matrix when the model has one, else the tied embedding
@@ -105,29 +149,15 @@ class HIPGraphExecutor:
         kv_shape = (B, self.max_seq, cfg.n_kv, cfg.head_dim)
         self.k_cache = [A(kv_shape, np.float16, f"blk.{L}.k_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
         self.v_cache = [A(kv_shape, np.float16, f"blk.{L}.v_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
-        # ---- activations (fp16 between nodes, fp32 logits) ----
-        self.h = [A((B, H), np.float16, "hidden0"), A((B, H), np.float16, "hidden1")]
-        self.xn = A((B, H), np.float16, "normed")
-        self.q = A((B, cfg.q_dim), np.float16, "q")
-        self.k = A((B, cfg.kv_dim), np.float16, "k")
-        self.v = A((B, cfg.kv_dim), np.float16, "v")
-        self.att = A((B, cfg.q_dim), np.float16, "attn_out")
-        self.g = A((B, cfg.ffn), np.float16, "gate")
-        self.u = A((B, cfg.ffn), np.float16, "up")
-        self.a = A((B, cfg.ffn), np.float16, "swiglu")
-        self.part = A((MAX_SPLITK, B, H), np.float32, "splitk_partials")
-        self.logits = A((B, cfg.vocab), np.float32, "logits")
-        self.topk_val = A((B, max(top_k, 1)), np.float32, "topk_val")
-        self.topk_idx = A((B, max(top_k, 1)), np.int32, "topk_idx")
-        self.topk_scratch = A(self.K.topk_scratch_bytes(B), np.uint8, "topk_scratch")
-        self.staging_input = A(B, np.int32, "staging_tokens")
-        self.staging_kv_offset = A(B, np.int32, "staging_kv_offset")
-        cos_c, sin_c = build_rope_cache(self.max_seq, cfg.head_dim, cfg.rope_theta)
-        self.rope_cos = W(cos_c, "rope_cos")
-        self.rope_sin = W(sin_c, "rope_sin")
-        self.attn = SplitKVAttentionDispatcher(hip, cfg.n_q, cfg.n_kv, cfg.head_dim, self.max_seq, B, split,
-                                               allocator=self.slab)
-        self.h_final = 0  # index of the hidden buffer holding the layer output
+
+    def _share(self, ex: "HIPGraphExecutor", seq: int) -> None:
+        """Weights, RoPE tables and sequence ``seq``'s KV cache of ``ex``."""
+        for name in ("token_embd", "lm_head", "lm_head_fmt", "output_norm", "layers", "rope_cos", "rope_sin"):
+            setattr(self, name, getattr(ex, name))
+        off = seq * ex.kv_batch_stride * 2  # bytes
+        self.k_cache = [c.ptr + off for c in ex.k_cache]
+        self.v_cache = [c.ptr + off for c in ex.v_cache]
+        self.kv_batch_stride = 0  # every column is a token of the one sequence
 
     # ------------------------------------------------------------------ kernels
     def _linear(self, fmt, x, w, y, K_in, N, bias=None, residual=None, out_dtype="f16"):
@@ -271,9 +301,14 @@ class HIPGraphExecutor:
                 K.rmsnorm(self.h[1 - cur], nxt, self.xn, B, H, cfg.eps, stream=st)
             cur = 1 - cur
         self.h_final = cur
-        self._linear(self.lm_head_fmt, self.xn, self.lm_head, self.logits, H, cfg.vocab, out_dtype="f32")
+        if self.prefill_of is not None:  # the last column only (the prompt's next-token logits)
+            K.gemv(self.lm_head_fmt, self.xn.ptr + (B - 1) * H * 2, self.lm_head, self.logits, 1, H, cfg.vocab,
+                   in_dtype="f16", out_dtype="f32", stream=st)
+        else:
+            self._linear(self.lm_head_fmt, self.xn, self.lm_head, self.logits, H, cfg.vocab, out_dtype="f32")
         if self.top_k > 0:
-            K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st)
+            K.topk(self.logits, self.out_rows, cfg.vocab, self.top_k, self.topk_val, self.topk_idx,
+                   self.topk_scratch, stream=st)
 
     def _proj_add_norm(self, fmt, x, w, K_in, cur, norm_w) -> None:
         """h[1-cur] = h[cur] + W x (split-K partials), xn = RMSNorm(h[1-cur]) * norm_w."""
@@ -343,20 +378,22 @@ class HIPGraphExecutor:
     # ------------------------------------------------------------------ outputs
     def read_logits(self) -> np.ndarray:
         self.hip.synchronize()
-        out = np.empty((self.B, self.cfg.vocab), np.float32)
+        out = np.empty((self.out_rows, self.cfg.vocab), np.float32)
         self.hip.safe_memcpy_device_to_host(out, ctypes.c_void_p(self.logits.ptr), "logits")
         return out
 
     def read_topk(self) -> tuple[np.ndarray, np.ndarray]:
         self.hip.synchronize()
-        v = np.empty((self.B, self.top_k), np.float32)
-        i = np.empty((self.B, self.top_k), np.int32)
+        v = np.empty((self.out_rows, self.top_k), np.float32)
+        i = np.empty((self.out_rows, self.top_k), np.int32)
         self.hip.safe_memcpy_device_to_host(v, ctypes.c_void_p(self.topk_val.ptr), "sampler_topk_val")
         self.hip.safe_memcpy_device_to_host(i, ctypes.c_void_p(self.topk_idx.ptr), "sampler_topk_idx")
         return v, i
 
     def fill_kv_prefix(self, seed: int = 0, scale: float = 0.5) -> None:
         """Fill every KV cache with scale * N(0,1) fp16 on the device (synthetic prefix)."""
+        if self.prefill_of is not None:
+            raise HIPSafetyError("a prefill executor shares its KV cache; fill the owning executor")
         n = self.B * self.max_seq * self.cfg.n_kv * self.cfg.head_dim
         for L in range(self.cfg.n_layers):
             self.K.fill_normal_f16(self.k_cache[L], n, seed * 1000 + 2 * L, scale, stream=self.hip.stream)
@@ -364,6 +401,8 @@ class HIPGraphExecutor:
         self.hip.synchronize()
 
     def upload_kv(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
+        if self.prefill_of is not None:
+            raise HIPSafetyError("a prefill executor shares its KV cache; upload through the owning executor")
         self.k_cache[layer].upload(k)
         self.v_cache[layer].upload(v)
 
