@@ -552,6 +552,7 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint64_t
                                                                     float* __restrict__ out_val,
                                                                     int* __restrict__ out_idx) {
     constexpr int NS = TOPK_P * TOPK_CAP / TOPK_THREADS;  // candidate slots per thread
+    static_assert(TOPK_THREADS == 2 * TOPK_CAP && NS <= 32, "slot map: two slices per round, <= 32 slots");
     __shared__ uint32_t keys[TOPK_P * TOPK_CAP];
     __shared__ int idx[TOPK_P * TOPK_CAP];
     __shared__ int offs[TOPK_P + 1];
@@ -562,85 +563,98 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint64_t
     __shared__ uint32_t wt[TOPK_THREADS / 64];
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     TK_TS(1, 0);
-    // every slot's candidate and the block counts requested at once
+    // every slot's candidate and its slice's count requested at once; slots
+    // past their slice's count are invalid (no compaction on the common path).
+    // Slot j of a thread: slice 2j + tid / 128, offset (tid + 37 j) mod 128,
+    // so each thread sees low offsets (the filled ones) of many slices.
     const size_t rb = (size_t)row * P * TOPK_CAP;
     uint32_t ck[NS];
     int cx[NS];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        const int sl = min(j * TOPK_THREADS + tid, P * TOPK_CAP - 1);
-        const uint64_t c = cand[rb + sl];
-        ck[j] = (uint32_t)(c >> 32);
-        cx[j] = (int)(uint32_t)c;
-    }
-    if (tid < 64) {
-        const int c = tid < P ? cand_cnt[(size_t)row * P + tid] : 0;
-        int incl = c;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
-        offs[tid] = incl - c;
-        if (tid == 63) offs[TOPK_P] = incl;
-    }
-    __syncthreads();
-    // compact the candidates: keys[0 .. n)
-    const int n = offs[TOPK_P];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        const int sl = j * TOPK_THREADS + tid, seg = sl / TOPK_CAP, off = sl % TOPK_CAP;
-        if (seg < P && off < offs[seg + 1] - offs[seg]) {
-            keys[offs[seg] + off] = ck[j];
-            idx[offs[seg] + off] = cx[j];
-        }
-    }
-    __syncthreads();
-    TK_TS(1, 1);
-    // candidate i in register i / 256 of thread i % 256
+    uint32_t cvm = 0;  // bit j: slot j valid
     uint32_t tm = 0;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const int i = j * TOPK_THREADS + tid;
-        ck[j] = i < n ? keys[i] : 0u;
-        cx[j] = i < n ? idx[i] : 0x7fffffff;
-        tm = i < n ? max(tm, ck[j]) : tm;
+        const int seg = 2 * j + (tid >> 7), off = ((tid & 127) + 37 * j) & 127;
+        const int segc = min(seg, P - 1);
+        const uint64_t c = cand[rb + (size_t)segc * TOPK_CAP + off];
+        const int cnt = cand_cnt[(size_t)row * P + segc];
+        const bool ok = seg < P && off < cnt;
+        ck[j] = ok ? (uint32_t)(c >> 32) : 0u;
+        cx[j] = ok ? (int)(uint32_t)c : 0x7fffffff;
+        cvm |= ok ? (1u << j) : 0u;
+        tm = ok ? max(tm, ck[j]) : tm;
     }
+    // total candidates (each wave sums the slice counts itself)
+    const int n = (int)wave_sum((float)(lane < P ? cand_cnt[(size_t)row * P + lane] : 0));
+    TK_TS(1, 1);
     // n > 256: every thread holds a candidate, so each wave's ceil(k/4)
     // largest maxima are candidates' keys and at least k candidates are >= T
     const uint32_t T = n > TOPK_THREADS ? tk_block_threshold(tm, k, wt) : 0u;
     TK_TS(1, 2);
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < NS; ++j) c += (j * TOPK_THREADS + tid < n && ck[j] >= T) ? 1 : 0;
+    for (int j = 0; j < NS; ++j) c += ((cvm >> j) & 1u) && ck[j] >= T ? 1 : 0;
     int total;
     int base = tk_excl_scan(c, sh.wsum, total);
     if (total <= TOPK_THREADS) {
-        // survivors -> LDS; each one's rank = survivors ordered before it
+        // survivors -> LDS; each one's rank = survivors ordered before it,
+        // counted by g = 256 / (survivor slots) threads over 1/g of them each
+        __shared__ int rk[TOPK_THREADS];
+        rk[tid] = 0;
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
-            if (j * TOPK_THREADS + tid < n && ck[j] >= T) {
+            if (((cvm >> j) & 1u) && ck[j] >= T) {
                 sk[base] = ck[j];
                 si[base] = cx[j];
                 ++base;
             }
         }
         __syncthreads();
-        if (tid < total) {
-            const uint32_t kk = sk[tid];
-            const int ix = si[tid];
+        const int per = total <= 64 ? 64 : (total <= 128 ? 128 : TOPK_THREADS);
+        const int g = TOPK_THREADS / per, sv = tid % per, q = tid / per;
+        if (sv < total) {
+            const uint32_t kk = sk[sv];
+            const int ix = si[sv];
+            const int j0 = (total * q) / g, j1 = (total * (q + 1)) / g;
             int rank = 0;
 #pragma unroll 8
-            for (int j = 0; j < total; ++j) rank += tk_before(sk[j], si[j], kk, ix) ? 1 : 0;
+            for (int j = j0; j < j1; ++j) rank += tk_before(sk[j], si[j], kk, ix) ? 1 : 0;
+            if (g > 1) atomicAdd(&rk[sv], rank);
+            else rk[sv] = rank;
+        }
+        __syncthreads();
+        if (tid < total) {
+            const int rank = rk[tid];
             if (rank < k) {
-                out_val[(size_t)row * k + rank] = tk_val(kk);
-                out_idx[(size_t)row * k + rank] = ix;
+                out_val[(size_t)row * k + rank] = tk_val(sk[tid]);
+                out_idx[(size_t)row * k + rank] = si[tid];
             }
         }
         TK_TS(1, 6);
         return;
     }
-    // many ties at the top: exact radix selection over all candidates
+    // many ties at the top: compact every candidate into keys[0 .. n) ...
+    if (tid < 64) {
+        const int cc = tid < P ? cand_cnt[(size_t)row * P + tid] : 0;
+        int incl = cc;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        offs[tid] = incl - cc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const int seg = 2 * j + (tid >> 7), off = ((tid & 127) + 37 * j) & 127;
+        if ((cvm >> j) & 1u) {
+            keys[offs[seg] + off] = ck[j];
+            idx[offs[seg] + off] = cx[j];
+        }
+    }
+    __syncthreads();
+    // ... and select exactly by radix over all of them
     int need_eq;
     const uint32_t T64 = tk_radix_select(keys, n, 64, sh, need_eq);
     const int kept = tk_compact(keys, n, T64, need_eq, pos, sh);
