@@ -11,7 +11,7 @@ sequence) and issues the launches of one layer.  MI355X choices:
   append is a separate tiny launch as in the reference;
 * the split is a token count per block (multiple of 32; 128 = one 32-token
   MFMA step per wave of the block's four), kept at 128 while a sequence has
-  at most 128 splits (see ``choose_split``; the reference's 1024/num_cus
+  at most 256 splits (see ``choose_split``; the reference's 1024/num_cus
   rule gives 4-token chunks on 256 CUs);
 * the per-sequence split count is derived on the device from kv_offset[b],
   so ragged batches inside one captured graph only touch their own splits.
@@ -25,13 +25,14 @@ from ..kernels import kernels
 
 def choose_split(max_context: int, batch: int, n_kv: int, num_cus: int) -> int:
     """Tokens per split block: 128 (one 32-token tile per wave, the most
-    blocks in flight) while that leaves at most 128 splits per sequence -- the
-    combine's one-round-trip form -- else the smallest power of two up to 1024
-    that does.  Measured on MI355X: at a 2K context 128-token splits beat
-    256-token ones both at batch 1 and 16 (the two-tile form holds more
-    registers and halves the blocks)."""
+    blocks in flight) while that leaves at most 256 splits per sequence, else
+    the smallest power of two up to 1024 that does.  Measured on MI355X: at a
+    2K context 128-token splits beat 256-token ones at batch 1 and 16 (the
+    two-tile form holds more registers and halves the blocks); at 32K,
+    128-token splits with the wide combine take 14.5 us against 15.9 us for
+    256-token splits."""
     split = 128
-    while max_context > 128 * split and split < 1024:
+    while max_context > 256 * split and split < 1024:
         split *= 2
     return split
 

@@ -402,24 +402,34 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     }
 }
 
-// LSE combine: grid (n_q, B), block 128 (one thread per dim).
+// LSE combine for many splits (> 128): grid (n_q, B, 4 dim quarters), block
+// 256 = 32 dims x 8 split groups.  Every block computes the split weights of
+// its (head, sequence) (one split per thread, block max and sum); a thread
+// then accumulates its dim over the splits g, g + 8, ... with 16 of them
+// requested per round, the first round before the weights are known; the 8
+// group sums meet in LDS.
+#define CMBW_R 16
 template <typename TO>
-__global__ __launch_bounds__(128) void attn_combine(const float* __restrict__ part_m,
-                                                    const float* __restrict__ part_l,
-                                                    const float* __restrict__ part_o, TO* __restrict__ out,
-                                                    int n_q, const int* __restrict__ kv_offset, int split,
-                                                    int max_splits) {
-    // All loads are issued before any result is needed: split statistics are
-    // read one split per thread, the partial outputs eight splits at a time.
+__global__ __launch_bounds__(256) void attn_combine_wide(const float* __restrict__ part_m,
+                                                         const float* __restrict__ part_l,
+                                                         const float* __restrict__ part_o, TO* __restrict__ out,
+                                                         int n_q, const int* __restrict__ kv_offset, int split,
+                                                         int max_splits) {
     __shared__ float w_sh[ATT_MAX_SPLITS];
-    __shared__ float red[2][2];
-    const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x, lane = d & 63, wv = d >> 6;
+    __shared__ float red[2][4];
+    __shared__ float osum[8][33];
+    const int qh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int dl = tid & 31, g = tid >> 5, d = blockIdx.z * 32 + dl;
     CMB_TS(0);
     const int len = kv_offset[b] + 1;
     const int ns = (len + split - 1) / split;
     const size_t base = ((size_t)b * n_q + qh) * max_splits;
-    float mloc = -1e30f;
-    for (int c = d; c < ns; c += 128) {
+    const float* po = part_o + base * ATT_D + d;
+    float ov[CMBW_R];
+#pragma unroll
+    for (int i = 0; i < CMBW_R; ++i) ov[i] = po[(size_t)min(g + 8 * i, ns - 1) * ATT_D];
+    float mloc = -INFINITY;
+    for (int c = tid; c < ns; c += 256) {
         const float m = part_m[base + c];
         w_sh[c] = m;
         mloc = fmaxf(mloc, m);
@@ -427,9 +437,9 @@ __global__ __launch_bounds__(128) void attn_combine(const float* __restrict__ pa
     mloc = wave_max(mloc);
     if (lane == 0) red[0][wv] = mloc;
     __syncthreads();
-    const float M = fmaxf(red[0][0], red[0][1]);
+    const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
     float lloc = 0.f;
-    for (int c = d; c < ns; c += 128) {
+    for (int c = tid; c < ns; c += 256) {
         const float w = __expf(w_sh[c] - M);
         w_sh[c] = w;
         lloc = fmaf(part_l[base + c], w, lloc);
@@ -437,19 +447,30 @@ __global__ __launch_bounds__(128) void attn_combine(const float* __restrict__ pa
     lloc = wave_sum(lloc);
     if (lane == 0) red[1][wv] = lloc;
     __syncthreads();
-    const float L = red[1][0] + red[1][1];
-    const float* po = part_o + base * ATT_D + d;
+    const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
     float O = 0.f;
-    int c = 0;
-    for (; c + 8 <= ns; c += 8) {
-        float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = po[(size_t)(c + i) * ATT_D];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) O = fmaf(v[i], w_sh[c + i], O);
+    for (int i = 0; i < CMBW_R; ++i) {
+        const int c = g + 8 * i;
+        O = c < ns ? fmaf(ov[i], w_sh[min(c, ns - 1)], O) : O;
     }
-    for (; c < ns; ++c) O = fmaf(po[(size_t)c * ATT_D], w_sh[c], O);
-    st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(L, 1e-20f));
+    for (int c0 = 8 * CMBW_R; c0 < ns; c0 += 8 * CMBW_R) {
+#pragma unroll
+        for (int i = 0; i < CMBW_R; ++i) ov[i] = po[(size_t)min(c0 + g + 8 * i, ns - 1) * ATT_D];
+#pragma unroll
+        for (int i = 0; i < CMBW_R; ++i) {
+            const int c = c0 + g + 8 * i;
+            O = c < ns ? fmaf(ov[i], w_sh[min(c, ns - 1)], O) : O;
+        }
+    }
+    osum[g][dl] = O;
+    __syncthreads();
+    if (g == 0) {
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t += osum[j][dl];
+        st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, t / fmaxf(L, 1e-20f));
+    }
     CMB_TS(1);
 }
 
@@ -626,8 +647,8 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
         hipLaunchKernelGGL((attn_combine_small<TO, 128>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q,
                            kv_offset, split, max_splits);
     else
-        hipLaunchKernelGGL((attn_combine<TO>), g2, b2, 0, st, part_m, part_l, part_o, (TO*)out, n_q, kv_offset,
-                           split, max_splits);
+        hipLaunchKernelGGL((attn_combine_wide<TO>), dim3(n_q, B, ATT_D / 32), dim3(256), 0, st, part_m, part_l, part_o,
+                           (TO*)out, n_q, kv_offset, split, max_splits);
     return hipGetLastError();
 }
 
