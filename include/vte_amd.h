@@ -162,8 +162,9 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
  * -> q to q_out [B][n_q*128], k and v appended to the caches at kv_offset[b].
  * Same rounding points as the unfused nodes.  head_dim 128, q/k Q4_K, v Q4_K
  * or Q6_K.  norm_w NULL: x is already normalised (fp16) and is used as is.
- * batch 1..4: VALU mat-vec with the norm fused in; batch 5..4096 (MFMA, in
- * launches of 32 sequences): norm_w must be NULL (RMSNorm runs before).
+ * With norm_w: batch 1..4 on the VALU mat-vec (norm fused in).  NULL norm_w:
+ * batch 1..2 on the VALU mat-vec, batch 3..4096 on MFMA (launches of 32
+ * sequences); above batch 4 norm_w must be NULL (RMSNorm runs before).
  * Replaces: the rmsnorm -> q/k/v gemv -> rope -> kv_cache_append nodes
  *           (vte/compiler/qwen_compute.py:100-282) and their fused forms
  *           FusedQKVDispatcher (vte/core/fused_qkv_dispatch.py:12-198),
@@ -176,8 +177,8 @@ int vte_attn_in(const void* x, const void* norm_w, float eps, const void* wq, co
 
 /* One launch: RMSNorm(x) -> gate and up projections -> fp16(silu(g) * u),
  * out [B][ffn], Q4_K gate/up.  norm_w NULL: x is already normalised.
- * batch 1..4: VALU mat-vec with the norm fused in; batch 5..4096 (MFMA):
- * norm_w must be NULL.
+ * With norm_w: batch 1..4 on the VALU mat-vec.  NULL norm_w: batch 1..2 on
+ * the VALU mat-vec, 3..4096 on MFMA; above batch 4 norm_w must be NULL.
  * Replaces: FusedFFNDispatcher (vte/core/fused_qkv_dispatch.py:200-270) with
  *           fused_gate_up_silu_kernel (fused_rmsnorm_gate_up_silu.hip.template:66-111). */
 int vte_ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate, const void* w_up, int fmt,

@@ -113,9 +113,9 @@ def test_attn_in(hip, K, k, n_q, n_kv, positions):
         assert not got_k[m, others].any() and not got_v[m, others].any()
 
 
-@pytest.mark.parametrize("B,fmt_v", [(8, "q6_k"), (16, "q6_k"), (40, "q4_k")])
+@pytest.mark.parametrize("B,fmt_v", [(3, "q6_k"), (4, "q4_k"), (8, "q6_k"), (16, "q6_k"), (40, "q4_k")])
 def test_attn_in_batched_mfma(hip, K, B, fmt_v):
-    """Batch > 4 (MFMA, launches of 32 sequences): pre-normalised fp16 x,
+    """Batch >= 3 with NULL norm weights (MFMA, launches of 32 sequences): pre-normalised fp16 x,
     q/k/v + bias + RoPE + K/V rows at ragged positions."""
     k, n_q, n_kv, hd, max_seq = 1536, 12, 2, 128, 320
     rng = np.random.default_rng(B)
@@ -146,9 +146,9 @@ def test_attn_in_batched_mfma(hip, K, B, fmt_v):
         assert not got_k[m, others].any() and not got_v[m, others].any()
 
 
-@pytest.mark.parametrize("B,ffn", [(8, 8960), (20, 1000), (33, 512)])
+@pytest.mark.parametrize("B,ffn", [(3, 8960), (4, 1000), (8, 8960), (20, 1000), (33, 512)])
 def test_ffn_in_batched_mfma(hip, K, B, ffn):
-    """Batch > 4 (MFMA): gate/up + SwiGLU on pre-normalised fp16 x."""
+    """Batch >= 3 with NULL norm weights (MFMA): gate/up + SwiGLU on pre-normalised fp16 x."""
     k = 1536
     rng = np.random.default_rng(ffn + B)
     wg, wu = _mat("q4_k", ffn, k, 15), _mat("q4_k", ffn, k, 16)

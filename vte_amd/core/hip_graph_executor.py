@@ -53,7 +53,7 @@ def splitk_splits(K: int) -> int:
 
 class HIPGraphExecutor:
     def __init__(self, hip: HIPRuntime, model: SyntheticQwen2, batch_size: int = 1, max_seq: Optional[int] = None,
-                 top_k: int = 40, gemm_min_batch: int = 8, split: Optional[int] = None, fused: bool = True,
+                 top_k: int = 40, gemm_min_batch: int = 3, split: Optional[int] = None, fused: bool = True,
                  shared: Optional["HIPGraphExecutor"] = None, kv_seq: int = 0):
         """``shared``: reuse that executor's weights, RoPE tables and the KV
         cache of its sequence ``kv_seq`` (columns of this executor are tokens of
@@ -68,8 +68,10 @@ class HIPGraphExecutor:
         self.max_seq = max_seq or cfg.max_seq
         self.top_k = top_k
         self.gemm_min_batch = gemm_min_batch
-        # fused norm+QKV+RoPE+append / norm+gate+up+SwiGLU / norm+LM-head kernels (batch <= 4)
-        self.fused = fused and batch_size <= 4
+        # fused norm+QKV+RoPE+append / norm+gate+up+SwiGLU / norm+LM-head mat-vec
+        # kernels below gemm_min_batch (measured: batch 2 1.07 ms vs 1.21 ms on
+        # the MFMA path; batch 3 1.51 ms vs 1.24 ms)
+        self.fused = fused and batch_size < gemm_min_batch and batch_size <= 4
         # batch >= gemm_min_batch: MFMA launches with the QKV+RoPE+append and
         # gate/up+SwiGLU glue fused in; o-proj and down write split-K partial
         # sums that one launch adds to the residual and RMS-normalises

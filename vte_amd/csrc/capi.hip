@@ -287,7 +287,7 @@ int vte_attn_in(const void* x, const void* norm_w, float eps, const void* wq, co
     REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(wq, 16) && aligned(wk, 16) && aligned(wv, 16),
             "attn_in: 16-byte alignment");
     hipError_t e;
-    if (batch <= 4)
+    if (norm_w != nullptr || batch <= 2)  // fused mat-vec; batch >= 3 on normalised activations: MFMA
         e = vte::attn_in(x, norm_w, eps, wq, q_bias, fmt_q, wk, k_bias, fmt_k, wv, v_bias, fmt_v, q_out, k_cache,
                          v_cache, kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q, n_kv,
                          (hipStream_t)stream);
@@ -308,7 +308,7 @@ int vte_ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate,
     REQUIRE(hidden % 256 == 0 && hidden <= 8192 && ffn >= 1, "ffn_in: bad shape");
     REQUIRE(aligned(x, 16) && aligned(norm_w, 16) && aligned(w_gate, 16) && aligned(w_up, 16),
             "ffn_in: 16-byte alignment");
-    hipError_t e = batch <= 4
+    hipError_t e = norm_w != nullptr || batch <= 2
                        ? vte::ffn_in(x, norm_w, eps, w_gate, w_up, fmt, out, batch, hidden, ffn, (hipStream_t)stream)
                        : vte::gate_up_mm(x, w_gate, w_up, fmt, out, batch, hidden, ffn, (hipStream_t)stream);
     if (e == hipErrorNotSupported) return fail("ffn_in: shape does not fit the fused kernel's LDS plan");

@@ -164,14 +164,15 @@ class VTEKernels:
                 v_cache, kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q, n_kv, head_dim=128,
                 stream=None):
         """Fused rmsnorm -> q/k/v (+bias) -> RoPE(q, k) -> K/V append; norm_w None: x already normalised
-        (required above batch 4, where the MFMA path runs)."""
+        (required above batch 4; from batch 3 it runs on MFMA)."""
         self._check(self.lib.vte_attn_in(_p(x), _p(norm_w), eps, _p(wq), _p(q_bias), FMT[fmt_q], _p(wk), _p(k_bias),
                                          FMT[fmt_k], _p(wv), _p(v_bias), FMT[fmt_v], _p(q_out), _p(k_cache),
                                          _p(v_cache), _p(kv_offset), kv_batch_stride, _p(rope_cos), _p(rope_sin),
                                          batch, hidden, n_q, n_kv, head_dim, self._st(stream)), "vte_attn_in")
 
     def ffn_in(self, x, norm_w, eps, w_gate, w_up, fmt, out, batch, hidden, ffn, stream=None):
-        """Fused rmsnorm -> gate/up -> SwiGLU; norm_w None: x already normalised (required above batch 4)."""
+        """Fused rmsnorm -> gate/up -> SwiGLU; norm_w None: x already normalised (required above batch 4;
+        from batch 3 it runs on MFMA)."""
         self._check(self.lib.vte_ffn_in(_p(x), _p(norm_w), eps, _p(w_gate), _p(w_up), FMT[fmt], _p(out), batch,
                                         hidden, ffn, self._st(stream)), "vte_ffn_in")
 
