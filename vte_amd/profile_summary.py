@@ -4,6 +4,7 @@ kept under profiles/.
     python -m vte_amd.profile_summary stats   <kernel_stats.csv>  <out.md> "<command>" [<kernel substring>]
     python -m vte_amd.profile_summary traffic <fetch counter_collection.csv> <write counter_collection.csv>
                                               <kernel substring> <out.json> <out.md> "<commands>"
+    python -m vte_amd.profile_summary mfma    <counter_collection.csv> <out.md> "<command>"
 
 ``traffic``: FETCH_SIZE / WRITE_SIZE are averaged per dispatch of the named
 kernel and converted to bytes with the factor that makes the run's 256 MiB
@@ -92,10 +93,48 @@ def traffic(fetch_csv, write_csv, kernel, out_json, out_md, commands):
         f.write("\n".join(lines) + "\n")
 
 
+SIMDS = 1024       # MI355X: 256 CUs x 4 SIMDs
+GRBM_INSTANCES = 8  # GRBM_GUI_ACTIVE arrives summed over the 8 XCDs
+
+
+def mfma(path, out_md, command):
+    """Per kernel: MFMA work (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 flops), its
+    rate over the dispatch's duration, and MFMA busy share
+    SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE / 8)."""
+    per = defaultdict(lambda: defaultdict(float))
+    disp = defaultdict(dict)
+    for r in _rows(path):
+        key = r["Kernel_Name"][:100]
+        did = r["Dispatch_Id"]
+        per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+        disp[key][did] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9
+    lines = ["# MFMA utilisation per kernel", "", f"Command: `{command}`", "",
+             "MFMA flops = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512; busy = SQ_VALU_MFMA_BUSY_CYCLES / "
+             f"({SIMDS} SIMDs x GRBM_GUI_ACTIVE / {GRBM_INSTANCES}); VALU = SQ_INSTS_VALU per dispatch.", "",
+             "| kernel | dispatches | avg us | MFMA GFLOP / dispatch | MFMA TFLOP/s | MFMA busy % | VALU instr / dispatch |",
+             "|---|---|---|---|---|---|---|"]
+    rows = []
+    for key, c in per.items():
+        n = len(disp[key])
+        t = sum(disp[key].values())
+        flops = c.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) * 512
+        if flops == 0:
+            continue
+        act = c.get("GRBM_GUI_ACTIVE", 0.0) / GRBM_INSTANCES
+        busy = 100.0 * c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (SIMDS * act) if act else 0.0
+        rows.append((t, f"| `{key}` | {n} | {t / n * 1e6:.2f} | {flops / n / 1e9:.3f} | {flops / t / 1e12:.1f} | "
+                        f"{busy:.1f} | {c.get('SQ_INSTS_VALU', 0.0) / n:.3g} |"))
+    lines += [r for _, r in sorted(rows, reverse=True)]
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
         stats(sys.argv[2], sys.argv[3], sys.argv[4], sys.argv[5] if len(sys.argv) > 5 else None)
     elif sys.argv[1] == "traffic":
         traffic(*sys.argv[2:8])
+    elif sys.argv[1] == "mfma":
+        mfma(sys.argv[2], sys.argv[3], sys.argv[4])
     else:
         raise SystemExit(__doc__)
