@@ -237,6 +237,19 @@ static int gs_num_cus() {
     return n;
 }
 
+// Whether the device grants the streaming kernel's dynamic LDS (staged
+// activations of up to 32 batch columns).
+static bool gs_lds_ok(int M) {
+    static int max_lds = 0;
+    if (max_lds == 0) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            max_lds = 65536;
+    }
+    return (M > 16 ? 32 : 16) * GS_LDX * 2 <= max_lds;
+}
+
 // The streaming kernel for K = 1536 and N >= 16384 (one launch per 32 batch columns).
 template <typename TI, typename TO, int FMT>
 static hipError_t launch_stream(const void* x, const void* w, void* y, int M, int N, const void* bias,
@@ -264,7 +277,7 @@ static hipError_t launch_stream(const void* x, const void* w, void* y, int M, in
 template <typename TI, typename TO, int FMT>
 static hipError_t launch_mfma(const void* x, const void* w, void* y, int M, int K, int N, const void* bias,
                               const void* residual, float rs, hipStream_t st) {
-    if (K == GS_K && N >= 16384) return launch_stream<TI, TO, FMT>(x, w, y, M, N, bias, residual, rs, st);
+    if (K == GS_K && N >= 16384 && gs_lds_ok(M)) return launch_stream<TI, TO, FMT>(x, w, y, M, N, bias, residual, rs, st);
     const bool tall = N >= 4096;
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mc = (M - m0 < 32) ? (M - m0) : 32;
