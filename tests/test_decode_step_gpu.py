@@ -161,18 +161,26 @@ def test_gguf_model_matches_in_memory_model(hip, tiny_model, tmp_path, B, fused)
     assert np.array_equal(out[0][1], out[1][1])
 
 
-def test_prefill_matches_token_by_token(hip, tiny_model):
-    """A 37-token prompt prefilled in chunks of 16 (the last one padded) into
-    sequence 1 of a 2-sequence executor gives the same next-token logits and
-    K/V rows as feeding the tokens one decode step at a time, and leaves
-    sequence 0's cache untouched."""
+@pytest.mark.parametrize("shape", ["tiny", "1.5b"])
+def test_prefill_matches_token_by_token(hip, request, shape):
+    """A 37-token prompt (tiny model, chunks of 16) or a 100-token prompt (1.5B
+    shapes, chunks of 64: the weight-stationary projection launches), the last
+    chunk padded, prefilled into sequence 1 of a 2-sequence executor gives the
+    same next-token logits and K/V rows as feeding the tokens one decode step
+    at a time, and leaves sequence 0's cache untouched."""
     from vte_amd.core.prefill import PrefillRunner
-    cfg, max_seq, start, n = TINY, 128, 10, 37
+    model = request.getfixturevalue("tiny_model" if shape == "tiny" else "full_model")
+    cfg = model.cfg
+    max_seq, start, n, chunk = (128, 10, 37, 16) if shape == "tiny" else (192, 10, 100, 64)
     rng = np.random.default_rng(77)
     prompt = list(rng.integers(0, cfg.vocab, n))
-    exa = HIPGraphExecutor(hip, tiny_model, batch_size=2, max_seq=max_seq, top_k=40)
-    exb = HIPGraphExecutor(hip, tiny_model, batch_size=2, max_seq=max_seq, top_k=40)
-    runner = PrefillRunner(exa, chunk=16)
+    exa = HIPGraphExecutor(hip, model, batch_size=2, max_seq=max_seq, top_k=40)
+    # 1.5B: the token-by-token run takes the MFMA kernels too (3 columns, the
+    # prompt in column 1), so its K/V rows must come out bit for bit the same;
+    # only the LM head (one column vs a batched GEMM) sums in another order
+    nb = 2 if shape == "tiny" else 3
+    exb = HIPGraphExecutor(hip, model, batch_size=nb, max_seq=max_seq, top_k=40)
+    runner = PrefillRunner(exa, chunk=chunk)
     try:
         exa.fill_kv_prefix(seed=5)
         exb.fill_kv_prefix(seed=5)
@@ -182,7 +190,7 @@ def test_prefill_matches_token_by_token(hip, tiny_model):
         got = sub.read_logits()[0]
         got_idx = sub.read_topk()[1][0]
         for i, t in enumerate(prompt):
-            exb.execute_decode_batch([0, t], [0, start + i])
+            exb.execute_decode_batch([0, t] + [0] * (nb - 2), [0, start + i] + [0] * (nb - 2))
         ref = exb.read_logits()[1]
         assert rel_l2(got, ref) <= TOL, rel_l2(got, ref)
         order = np.lexsort((np.arange(cfg.vocab), -got))[:40]
@@ -192,6 +200,8 @@ def test_prefill_matches_token_by_token(hip, tiny_model):
             ka, kb = exa.k_cache[L].numpy(), exb.k_cache[L].numpy()
             rows = slice(start, start + n)
             assert rel_l2(ka[1, rows], kb[1, rows]) <= TOL, L
+            if shape != "tiny":
+                assert np.array_equal(ka[1, rows].view(np.uint16), kb[1, rows].view(np.uint16)), L
             assert np.array_equal(ka[0].view(np.uint16), k0[L][0].view(np.uint16)), L
             assert np.array_equal(ka[1, :start].view(np.uint16), k0[L][1, :start].view(np.uint16)), L
     finally:

@@ -6,6 +6,9 @@ specialised for those K) and at other K (the runtime-K kernels).
 Composition under test (vte/compiler/qwen_compute.py:100-282):
 rmsnorm -> GEMV (+bias) -> RoPE -> K/V append, rmsnorm -> gate/up -> SwiGLU,
 rmsnorm -> GEMV (+bias, *scale, +residual), GEMV (+residual)."""
+import contextlib
+import os
+
 import numpy as np
 import pytest
 
@@ -18,6 +21,19 @@ from vte_amd import synthetic as syn
 pytestmark = pytest.mark.gpu
 TOL = 1e-3  # rel-L2 with fp32 accumulation
 EPS = 1e-6
+
+
+@contextlib.contextmanager
+def _env(name, value):
+    old = os.environ.get(name)
+    os.environ[name] = value
+    try:
+        yield
+    finally:
+        if old is None:
+            del os.environ[name]
+        else:
+            os.environ[name] = old
 
 
 def _mat(fmt, n, k, seed):
@@ -113,10 +129,11 @@ def test_attn_in(hip, K, k, n_q, n_kv, positions):
         assert not got_k[m, others].any() and not got_v[m, others].any()
 
 
-@pytest.mark.parametrize("B,fmt_v", [(3, "q6_k"), (4, "q4_k"), (8, "q6_k"), (16, "q6_k"), (40, "q4_k")])
+@pytest.mark.parametrize("B,fmt_v", [(3, "q6_k"), (4, "q4_k"), (8, "q6_k"), (16, "q6_k"), (40, "q4_k"),
+                                      (130, "q6_k")])
 def test_attn_in_batched_mfma(hip, K, B, fmt_v):
-    """Batch >= 3 with NULL norm weights (MFMA, launches of 32 sequences): pre-normalised fp16 x,
-    q/k/v + bias + RoPE + K/V rows at ragged positions."""
+    """Batch >= 3 with NULL norm weights (MFMA: launches of 32 sequences, one weight-stationary
+    launch above 32): pre-normalised fp16 x, q/k/v + bias + RoPE + K/V rows at ragged positions."""
     k, n_q, n_kv, hd, max_seq = 1536, 12, 2, 128, 320
     rng = np.random.default_rng(B)
     wq, wk, wv = _mat("q4_k", n_q * hd, k, 11), _mat("q4_k", n_kv * hd, k, 12), _mat(fmt_v, n_kv * hd, k, 13)
@@ -144,9 +161,16 @@ def test_attn_in_batched_mfma(hip, K, B, fmt_v):
         assert rel_l2(got_v[m, pos], v[m].reshape(n_kv, hd)) <= TOL, m
         others = np.delete(np.arange(max_seq), pos)
         assert not got_k[m, others].any() and not got_v[m, others].any()
+    if B > 32:  # the weight-stationary launch gives the bits of the 32-column launches
+        with _env("VTE_MM_WS", "0"):
+            K.attn_in(up(hip, xn), None, EPS, up(hip, wq), up(hip, bq), "q4_k", up(hip, wk), up(hip, bk), "q4_k",
+                      up(hip, wv), up(hip, bv), fmt_v, q_out, kc, vc, up(hip, positions), stride,
+                      up(hip, cos_c), up(hip, sin_c), B, k, n_q, n_kv, stream=hip.stream)
+        for a, b in ((down(q_out), got_q), (down(kc), got_k), (down(vc), got_v)):
+            assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
 
 
-@pytest.mark.parametrize("B,ffn", [(3, 8960), (4, 1000), (8, 8960), (20, 1000), (33, 512)])
+@pytest.mark.parametrize("B,ffn", [(3, 8960), (4, 1000), (8, 8960), (20, 1000), (33, 512), (200, 8960)])
 def test_ffn_in_batched_mfma(hip, K, B, ffn):
     """Batch >= 3 with NULL norm weights (MFMA): gate/up + SwiGLU on pre-normalised fp16 x."""
     k = 1536
@@ -158,7 +182,12 @@ def test_ffn_in_batched_mfma(hip, K, B, ffn):
     x32 = xn.astype(np.float32)
     g = dq.gemv("q4_k", wg, ffn, k, x32).astype(np.float16)
     u = dq.gemv("q4_k", wu, ffn, k, x32).astype(np.float16)
-    assert rel_l2(down(out), ost.swiglu(g, u)) <= TOL
+    got = down(out)
+    assert rel_l2(got, ost.swiglu(g, u)) <= TOL
+    if B > 32:  # the weight-stationary launch gives the bits of the 32-column launches
+        with _env("VTE_MM_WS", "0"):
+            K.ffn_in(up(hip, xn), None, EPS, up(hip, wg), up(hip, wu), "q4_k", out, B, k, ffn, stream=hip.stream)
+        assert np.array_equal(down(out).view(np.uint16), got.view(np.uint16))
 
 
 def test_batch_above_4_rejects_fused_norm(hip, K):
@@ -176,10 +205,14 @@ def test_batch_above_4_rejects_fused_norm(hip, K):
 
 @pytest.mark.parametrize("fmt,k,n,M,splits", [("q6_k", 8960, 1536, 16, 4), ("q4_k", 8960, 1536, 8, 4),
                                               ("q4_k", 8960, 1536, 40, 5), ("q6_k", 1536, 1536, 16, 1),
-                                              ("q4_k", 1536, 1536, 20, 6), ("q6_k", 2304, 640, 9, 8)])
+                                              ("q4_k", 1536, 1536, 20, 6), ("q6_k", 2304, 640, 9, 8),
+                                              ("q6_k", 8960, 1536, 100, 5), ("q6_k", 1536, 1536, 70, 2),
+                                              ("q4_k", 2304, 640, 33, 3), ("q4_k", 8960, 1536, 40, 2)])
 def test_gemm_mfma_splitk(hip, K, fmt, k, n, M, splits):
     """Each split's partial equals the GEMV over its super-block range
-    [n_sb * s // splits, n_sb * (s + 1) // splits) of every weight row."""
+    [n_sb * s // splits, n_sb * (s + 1) // splits) of every weight row.  Above
+    32 columns with at most 8 super-blocks per split one weight-stationary
+    launch runs; it must give the bits of the 32-column launches."""
     rng = np.random.default_rng(k + n + M + splits)
     raw = _mat(fmt, n, k, 11)
     x = _x(rng, M, k)
@@ -193,3 +226,7 @@ def test_gemm_mfma_splitk(hip, K, fmt, k, n, M, splits):
         sub = np.ascontiguousarray(blk[:, a:b]).reshape(-1)
         ref = dq.gemv(fmt, sub, n, (b - a) * 256, x[:, a * 256:b * 256].astype(np.float32))
         assert rel_l2(got[s], ref) <= TOL, s
+    if M > 32:
+        with _env("VTE_MM_WS", "0"):
+            K.gemm_mfma_splitk(fmt, up(hip, x), up(hip, raw), part, M, k, n, splits, stream=hip.stream)
+        assert np.array_equal(down(part).view(np.uint32), got.view(np.uint32))

@@ -216,6 +216,54 @@ __device__ __forceinline__ float mm_sum(float (*red)[RT][NT][4][64], int rr, int
 
 __device__ __forceinline__ float mm_bias(const __half* b, int row) { return b ? __half2float(b[row]) : 0.f; }
 
+// Epilogue of one C tile group: batch columns cb .. cb + mcount - 1 of the
+// launch (column m reads kv_offset[m] and writes row m of the outputs).
+template <int RT, int NT, int NW>
+__device__ __forceinline__ void mm_epilogue(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64], int cb,
+                                            int mcount) {
+    const MmSeg& S = *T.S;
+    if (!mm_paired(S.mode)) {
+        for (int o = threadIdx.x; o < 16 * RT * 16 * NT; o += blockDim.x) {
+            const int rr = o / (16 * NT), mc = o % (16 * NT);
+            if (rr >= T.nvalid || mc >= mcount) continue;
+            const int row = T.j0 + rr, m = cb + mc;
+            const __half v = __float2half(mm_sum<RT, NT, NW>(red, rr, mc) + mm_bias(S.bias, row));
+            if (S.mode == MM_VCACHE) {
+                const int pos = P.kv_offset[m];
+                P.v_cache[(size_t)m * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128 + (row % 128)] = v;
+            } else {
+                S.out[(size_t)m * S.n_rows + row] = v;
+            }
+        }
+        return;
+    }
+    for (int o = threadIdx.x; o < 8 * RT * 16 * NT; o += blockDim.x) {
+        const int p = o / (16 * NT), mc = o % (16 * NT);
+        if (p >= T.nvalid || mc >= mcount) continue;
+        const float a = mm_sum<RT, NT, NW>(red, p, mc), b = mm_sum<RT, NT, NW>(red, p + 8 * RT, mc);
+        const int row = T.j0 + p, m = cb + mc;
+        if (S.mode == MM_SWIGLU) {
+            const float g = __half2float(__float2half(a)), u = __half2float(__float2half(b));
+            S.out[(size_t)m * S.n_rows + row] = __float2half(g / (1.0f + expf(-g)) * u);
+            continue;
+        }
+        const float x1 = __half2float(__float2half(a + mm_bias(S.bias, row)));
+        const float x2 = __half2float(__float2half(b + mm_bias(S.bias, row + 64)));
+        const int pos = P.kv_offset[m], d = row & 127;
+        const float c = __half2float(P.rope_cos[(size_t)pos * 128 + d]);
+        const float sn = __half2float(P.rope_sin[(size_t)pos * 128 + d]);
+        const __half o1 = __float2half(x1 * c - x2 * sn), o2 = __float2half(x1 * sn + x2 * c);
+        if (S.mode == MM_ROPE_Q) {
+            S.out[(size_t)m * S.n_rows + row] = o1;
+            S.out[(size_t)m * S.n_rows + row + 64] = o2;
+        } else {
+            __half* kc = P.k_cache + (size_t)m * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128;
+            kc[d] = o1;
+            kc[d + 64] = o2;
+        }
+    }
+}
+
 // NW waves per block split K (6 for K = 1536: one super-block each).
 template <int RT, int NT, int NW>
 __global__ __launch_bounds__(64 * NW) void fused_mm_kernel(MmPlan P) {
@@ -235,49 +283,84 @@ __global__ __launch_bounds__(64 * NW) void fused_mm_kernel(MmPlan P) {
     }
 #endif
 
-    const int M = P.M;
-    if (!mm_paired(S.mode)) {
-        for (int o = threadIdx.x; o < 16 * RT * 16 * NT; o += blockDim.x) {
-            const int rr = o / (16 * NT), mc = o % (16 * NT);
-            if (rr >= T.nvalid || mc >= M) continue;
-            const int row = T.j0 + rr;
-            const __half v = __float2half(mm_sum<RT, NT, NW>(red, rr, mc) + mm_bias(S.bias, row));
-            if (S.mode == MM_VCACHE) {
-                const int pos = P.kv_offset[mc];
-                P.v_cache[(size_t)mc * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128 + (row % 128)] = v;
-            } else {
-                S.out[(size_t)mc * S.n_rows + row] = v;
+    mm_epilogue<RT, NT, NW>(P, T, red, 0, P.M);
+    MM_TS(4);
+}
+
+
+// Weight-stationary form for long batches (prefill chunks), K = 6 super-blocks:
+// wave w dequantises super-block w of its tile rows once, keeps the A
+// operands in registers and runs them against the block's columns
+// [blockIdx.y * cols, ...) 16 * NT at a time; the next columns' activations
+// are requested before the epilogue of the current ones.  Each C tile sums
+// its eight k-steps in the same order as fused_mm_kernel, so both forms give
+// the same bits.
+template <int FMT, int RT, int NT>
+__device__ __forceinline__ void mm_ws_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64], int c0,
+                                           int c1) {
+    constexpr int NW = 6;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int K = P.K;
+    half8_t av[RT][8];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const uint8_t* rowp = mm_row<RT>(T, rt * 16 + col);
+        if (FMT == 4) {
+            Q4Raw r;
+            q4_raw_load(rowp + (size_t)wv * Q4K_BYTES, grp, r);
+            q4_raw_operands(r, grp, av[rt]);
+        } else {
+            q6k_a_operands(rowp + (size_t)wv * Q6K_BYTES, grp, av[rt]);
+        }
+    }
+    half8_t bx[8][NT];
+    auto load_b = [&](int m0) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int kb = wv * QK_K + kslot_base<FMT>(t, grp);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int m = m0 + nt * 16 + col;
+                bx[t][nt] = load_x8<__half>(P.x + (size_t)(m < c1 ? m : c0) * K + kb, m < c1);
             }
         }
-        MM_TS(4);
-        return;
+    };
+    load_b(c0);
+    for (int m0 = c0; m0 < c1; m0 += 16 * NT) {
+        floatx4_t acc[RT][NT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[rt][t], bx[t][nt], acc[rt][nt], 0, 0, 0);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wv][rt][nt][i][lane] = acc[rt][nt][i];
+        if (m0 + 16 * NT < c1) load_b(m0 + 16 * NT);
+        __syncthreads();
+        mm_epilogue<RT, NT, NW>(P, T, red, m0, min(16 * NT, c1 - m0));
+        __syncthreads();
     }
-    for (int o = threadIdx.x; o < 8 * RT * 16 * NT; o += blockDim.x) {
-        const int p = o / (16 * NT), mc = o % (16 * NT);
-        if (p >= T.nvalid || mc >= M) continue;
-        const float a = mm_sum<RT, NT, NW>(red, p, mc), b = mm_sum<RT, NT, NW>(red, p + 8 * RT, mc);
-        const int row = T.j0 + p;
-        if (S.mode == MM_SWIGLU) {
-            const float g = __half2float(__float2half(a)), u = __half2float(__float2half(b));
-            S.out[(size_t)mc * S.n_rows + row] = __float2half(g / (1.0f + expf(-g)) * u);
-            continue;
-        }
-        const float x1 = __half2float(__float2half(a + mm_bias(S.bias, row)));
-        const float x2 = __half2float(__float2half(b + mm_bias(S.bias, row + 64)));
-        const int pos = P.kv_offset[mc], d = row & 127;
-        const float c = __half2float(P.rope_cos[(size_t)pos * 128 + d]);
-        const float sn = __half2float(P.rope_sin[(size_t)pos * 128 + d]);
-        const __half o1 = __float2half(x1 * c - x2 * sn), o2 = __float2half(x1 * sn + x2 * c);
-        if (S.mode == MM_ROPE_Q) {
-            S.out[(size_t)mc * S.n_rows + row] = o1;
-            S.out[(size_t)mc * S.n_rows + row + 64] = o2;
-        } else {
-            __half* kc = P.k_cache + (size_t)mc * P.kv_batch_stride + ((size_t)pos * P.n_kv + row / 128) * 128;
-            kc[d] = o1;
-            kc[d + 64] = o2;
-        }
-    }
-    MM_TS(4);
+}
+
+template <int RT, int NT>
+__global__ __launch_bounds__(64 * 6) void fused_mm_ws_kernel(MmPlan P, int cols) {
+    __shared__ float red[6][RT][NT][4][64];
+    const MmTile T = mm_tile<RT>(P, blockIdx.x);
+    const int c0 = blockIdx.y * cols, c1 = min(P.M, c0 + cols);
+    if (c0 >= c1) return;
+    if (T.S->fmt == 4) mm_ws_body<4, RT, NT>(P, T, red, c0, c1);
+    else mm_ws_body<6, RT, NT>(P, T, red, c0, c1);
 }
 
 namespace vte {
@@ -300,7 +383,13 @@ static MmSeg mm_seg(const void* w, const void* w2, void* out, const void* bias, 
     return S;
 }
 
-// Runs the plan over the batch in chunks of 32 columns (one launch each).
+static int mm_env(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
+// Runs the plan over the batch: in chunks of 32 columns (one launch each), or
+// in one weight-stationary launch when the batch is longer than 32 columns.
 template <int RT>
 static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipStream_t st) {
     int total = 0;
@@ -311,6 +400,17 @@ static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipSt
     for (int s = 0; s < P.nseg; ++s) out0[s] = P.seg[s].out;
     __half* kc0 = P.k_cache;
     __half* vc0 = P.v_cache;
+    if constexpr (RT <= 2) if (B > 32 && P.K == 6 * QK_K && mm_env("VTE_MM_WS", 1)) {
+        // column groups of a multiple of 32 so that about 512 blocks run
+        const int groups_max = (B + 31) / 32;
+        int gy = 512 / total;
+        gy = gy < 1 ? 1 : gy > groups_max ? groups_max : gy;
+        const int cols = ((B + gy - 1) / gy + 31) / 32 * 32;
+        gy = (B + cols - 1) / cols;
+        P.M = B;
+        hipLaunchKernelGGL((fused_mm_ws_kernel<RT, 2>), dim3(total, gy), dim3(64 * 6), 0, st, P, cols);
+        return hipGetLastError();
+    }
     for (int m0 = 0; m0 < B; m0 += 32) {
         const int mc = B - m0 < 32 ? B - m0 : 32;
         P.M = mc;
@@ -330,11 +430,6 @@ static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipSt
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
-}
-
-static int mm_env(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : dflt;
 }
 
 // q/k/v projections of RMSNorm-ed fp16 activations xn [B][K] with bias, RoPE

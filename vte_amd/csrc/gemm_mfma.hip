@@ -132,6 +132,89 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
     }
 }
 
+
+// Weight-stationary split-K for long batches (prefill chunks): as
+// gemm_mfma_kernel with fp16 activations and fp32 partial sums, when no wave
+// owns more than one super-block of its block's range.  Each wave dequantises
+// its super-block of the 16 tile rows once and runs it against the block's
+// columns [blockIdx.z * cols, ...), 16 * NT at a time, requesting the next
+// columns' activations before the epilogue; the k-steps and the wave sum keep
+// the order of gemm_mfma_kernel, so the partial sums have the same bits.
+template <int FMT, int NT>
+__global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __half* __restrict__ x,
+                                                                     const uint8_t* __restrict__ w,
+                                                                     float* __restrict__ part, int M, int K, int N,
+                                                                     size_t split_stride, int cols) {
+    constexpr int NW = MF_WAVES;
+    __shared__ float red[NW][NT][4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int n_sb = K / QK_K;
+    const size_t row_bytes = (size_t)n_sb * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES);
+    const int row0 = blockIdx.x * 16;
+    const int kb0 = (n_sb * (int)blockIdx.y) / (int)gridDim.y, kb1 = (n_sb * ((int)blockIdx.y + 1)) / (int)gridDim.y;
+    const int sb0 = kb0 + ((kb1 - kb0) * wv) / NW, sb1 = kb0 + ((kb1 - kb0) * (wv + 1)) / NW;
+    const bool has = sb1 > sb0;
+    const int c0 = blockIdx.z * cols, c1 = min(M, c0 + cols);
+    if (c0 >= c1) return;
+    float* y = part + blockIdx.y * split_stride;
+
+    half8_t av[8];
+    if (has) {
+        const uint8_t* blk = w + (size_t)min(row0 + col, N - 1) * row_bytes;
+        if (FMT == 4) {
+            Q4Raw r;
+            q4_raw_load(blk + (size_t)sb0 * Q4K_BYTES, grp, r);
+            q4_raw_operands(r, grp, av);
+        } else {
+            q6k_a_operands(blk + (size_t)sb0 * Q6K_BYTES, grp, av);
+        }
+    }
+    half8_t bx[8][NT];
+    auto load_b = [&](int m0) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int kb = sb0 * QK_K + kslot_base<FMT>(t, grp);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int m = m0 + nt * 16 + col;
+                bx[t][nt] = load_x8<__half>(x + (size_t)(m < c1 ? m : c0) * K + kb, has && m < c1);
+            }
+        }
+    };
+    load_b(c0);
+    for (int m0 = c0; m0 < c1; m0 += 16 * NT) {
+        floatx4_t acc[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        if (has) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t], bx[t][nt], acc[nt], 0, 0, 0);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wv][nt][i][lane] = acc[nt][i];
+        if (m0 + 16 * NT < c1) load_b(m0 + 16 * NT);
+        __syncthreads();
+        const int mcount = min(16 * NT, c1 - m0);
+        for (int o = threadIdx.x; o < 16 * NT * 16; o += blockDim.x) {
+            const int rr = o / (NT * 16), mc = o % (NT * 16);
+            const int nt = mc >> 4, cc = mc & 15;
+            const int ln = cc + 16 * (rr >> 2), i = rr & 3;
+            float s = 0.f;
+#pragma unroll
+            for (int wq = 0; wq < NW; ++wq) s += red[wq][nt][i][ln];
+            const int row = row0 + rr;
+            if (row < N && mc < mcount) y[(size_t)(m0 + mc) * N + row] = s;
+        }
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Streaming batched GEMM for tall matrices at K = 1536 (the LM head at batch
 // >= 8).  Persistent 8-wave blocks, two per CU; the batch's activations are staged once
@@ -301,10 +384,28 @@ static hipError_t launch_mfma(const void* x, const void* w, void* y, int M, int 
 // super-blocks of dequant(W[n, k]) * x[m, k]; no bias, scale or residual (the
 // consumer adds the splits).  Splits multiply the blocks of a short-and-wide
 // problem (down projection: K = 8960, N = 1536) so the whole chip streams W.
+// true when the environment variable is set to 0 (switches a launch form off)
+static bool getenv_off(const char* name) {
+    const char* v = getenv(name);
+    return v != nullptr && atoi(v) == 0;
+}
+
 template <int FMT>
 static hipError_t launch_splitk(const void* x, const void* w, float* part, int M, int K, int N, int splits,
                                 hipStream_t st) {
     const size_t ss = (size_t)M * N;
+    const int n_sb = K / QK_K;
+    if (M > 32 && (n_sb + splits - 1) / splits <= MF_WAVES && !getenv_off("VTE_MM_WS")) {
+        // one launch; column groups of a multiple of 32 so that about 512 blocks run
+        const int tiles = (N + 15) / 16, groups_max = (M + 31) / 32;
+        int gz = 512 / (tiles * splits);
+        gz = gz < 1 ? 1 : gz > groups_max ? groups_max : gz;
+        const int cols = ((M + gz - 1) / gz + 31) / 32 * 32;
+        gz = (M + cols - 1) / cols;
+        hipLaunchKernelGGL((gemm_ws_splitk_kernel<FMT, 2>), dim3(tiles, splits, gz), dim3(64 * MF_WAVES), 0, st,
+                           (const __half*)x, (const uint8_t*)w, part, M, K, N, ss, cols);
+        return hipGetLastError();
+    }
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mc = (M - m0 < 32) ? (M - m0) : 32;
         const __half* xs = (const __half*)x + (size_t)m0 * K;
