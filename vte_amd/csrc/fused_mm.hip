@@ -401,12 +401,9 @@ static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipSt
     __half* kc0 = P.k_cache;
     __half* vc0 = P.v_cache;
     if constexpr (RT <= 2) if (B > 32 && P.K == 6 * QK_K && mm_env("VTE_MM_WS", 1)) {
-        // column groups of a multiple of 32 so that about 512 blocks run
-        const int groups_max = (B + 31) / 32;
-        int gy = 512 / total;
-        gy = gy < 1 ? 1 : gy > groups_max ? groups_max : gy;
-        const int cols = ((B + gy - 1) / gy + 31) / 32 * 32;
-        gy = (B + cols - 1) / cols;
+        // two 6-wave blocks fit per CU
+        const int g = ws_column_groups(total, B, 2 * device_cus());
+        const int cols = ((B + 31) / 32 + g - 1) / g * 32, gy = (B + cols - 1) / cols;
         P.M = B;
         hipLaunchKernelGGL((fused_mm_ws_kernel<RT, 2>), dim3(total, gy), dim3(64 * 6), 0, st, P, cols);
         return hipGetLastError();

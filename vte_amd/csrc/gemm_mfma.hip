@@ -310,15 +310,7 @@ static void launch_tile(const TI* x, const void* w, TO* y, int M, int K, int N, 
 
 // Batch columns are processed in chunks of 32 (two 16-wide MFMA N tiles).
 // Tall matrices (N >= 4096) use 32-row tiles.
-static int gs_num_cus() {
-    static int n = 0;
-    if (n == 0) {
-        int dev = 0;
-        (void)hipGetDevice(&dev);
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    }
-    return n;
-}
+static int gs_num_cus() { return device_cus(); }
 
 // Whether the device grants the streaming kernel's dynamic LDS (staged
 // activations of up to 32 batch columns).
@@ -396,12 +388,10 @@ static hipError_t launch_splitk(const void* x, const void* w, float* part, int M
     const size_t ss = (size_t)M * N;
     const int n_sb = K / QK_K;
     if (M > 32 && (n_sb + splits - 1) / splits <= MF_WAVES && !getenv_off("VTE_MM_WS")) {
-        // one launch; column groups of a multiple of 32 so that about 512 blocks run
-        const int tiles = (N + 15) / 16, groups_max = (M + 31) / 32;
-        int gz = 512 / (tiles * splits);
-        gz = gz < 1 ? 1 : gz > groups_max ? groups_max : gz;
-        const int cols = ((M + gz - 1) / gz + 31) / 32 * 32;
-        gz = (M + cols - 1) / cols;
+        // one launch; two 8-wave blocks fit per CU
+        const int tiles = (N + 15) / 16;
+        const int g = ws_column_groups(tiles * splits, M, 2 * device_cus());
+        const int cols = ((M + 31) / 32 + g - 1) / g * 32, gz = (M + cols - 1) / cols;
         hipLaunchKernelGGL((gemm_ws_splitk_kernel<FMT, 2>), dim3(tiles, splits, gz), dim3(64 * MF_WAVES), 0, st,
                            (const __half*)x, (const uint8_t*)w, part, M, K, N, ss, cols);
         return hipGetLastError();

@@ -164,3 +164,37 @@ __device__ __forceinline__ void q4_raw_operands(const Q4Raw& r, int grp, half8_t
         a[t] = deq8(u0, u1, (_Float16)0.0f, d2, m2);
     }
 }
+
+// Column groups for a weight-stationary launch of `tiles` row tiles over M
+// batch columns, 32 at a time: each group re-reads and re-dequantises the
+// weights, each block walks its group's 32-column chunks one after another,
+// and `slots` blocks run at once.  Picks the group count with the least
+// (rounds of blocks) x (chunks per block), weighted by 1 + groups / 16 for
+// the repeated weight reads.
+static inline int ws_column_groups(int tiles, int M, int slots) {
+    const int chunks = (M + 31) / 32;
+    int best = 1;
+    double best_cost = 1e30;
+    for (int g = 1; g <= chunks; ++g) {
+        const int per = (chunks + g - 1) / g;
+        const int used = (chunks + per - 1) / per;  // groups that hold columns
+        const int rounds = (tiles * used + slots - 1) / slots;
+        const double cost = (double)rounds * per * (1.0 + used / 16.0);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = used;
+        }
+    }
+    return best;
+}
+
+// Compute units of the current device (cached after the first query).
+static inline int device_cus() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    }
+    return n;
+}
