@@ -170,7 +170,8 @@ def test_attn_in_batched_mfma(hip, K, B, fmt_v):
             assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
 
 
-@pytest.mark.parametrize("B,ffn", [(3, 8960), (4, 1000), (8, 8960), (20, 1000), (33, 512), (200, 8960)])
+@pytest.mark.parametrize("B,ffn", [(3, 8960), (4, 1000), (8, 8960), (20, 1000), (32, 8960), (33, 512),
+                                   (200, 8960)])
 def test_ffn_in_batched_mfma(hip, K, B, ffn):
     """Batch >= 3 with NULL norm weights (MFMA): gate/up + SwiGLU on pre-normalised fp16 x."""
     k = 1536

@@ -113,7 +113,7 @@ template <int RT>
 __device__ __forceinline__ const uint8_t* mm_row(const MmTile& T, int rr) {
     const MmSeg& S = *T.S;
     if (!mm_paired(S.mode)) return S.w + (size_t)(T.j0 + min(rr, T.nvalid - 1)) * S.row_bytes;
-    const int p = rr & (8 * RT - 1), pc = min(p, T.nvalid - 1);
+    const int p = rr % (8 * RT), pc = min(p, T.nvalid - 1);
     if (rr < 8 * RT) return S.w + (size_t)(T.j0 + pc) * S.row_bytes;
     if (S.mode == MM_SWIGLU) return S.w2 + (size_t)(T.j0 + pc) * S.row_bytes;
     return S.w + (size_t)(T.j0 + 64 + pc) * S.row_bytes;
@@ -458,7 +458,12 @@ hipError_t qkv_mm(const void* xn, const void* wq, const void* q_bias, int fmt_q,
 // out [B][ffn] = fp16(silu(W_gate xn) * (W_up xn)) for RMSNorm-ed fp16 xn [B][K].
 hipError_t gate_up_mm(const void* xn, const void* w_gate, const void* w_up, int fmt, void* out, int B, int K, int ffn,
                       hipStream_t st) {
-    const int RT = mm_env("VTE_MM_RT_FFN", 2);  // 16 gate/up pairs per block: half the blocks, x read half as often
+    // 16 gate/up pairs per block (half the blocks of 8, activations read half
+    // as often); 24 for 17-32 columns (measured: batch 32 2.26 -> 2.18 ms per
+    // step, batch 8-16 slightly slower); the weight-stationary form above 32
+    // columns takes at most 16
+    int RT = mm_env("VTE_MM_RT_FFN", B > 16 && B <= 32 ? 3 : 2);
+    if (B > 32 && RT > 2) RT = 2;
     MmPlan P;
     memset(&P, 0, sizeof(P));
     P.K = K;
@@ -466,7 +471,10 @@ hipError_t gate_up_mm(const void* xn, const void* w_gate, const void* w_up, int 
     P.seg[0] = mm_seg(w_gate, w_up, out, nullptr, fmt, ffn, MM_SWIGLU, K, RT);
     P.nseg = 1;
     size_t ld[MM_MAX_SEG] = {(size_t)ffn, 0, 0};
-    return RT == 4 ? mm_run<4>(P, B, ld, st) : RT == 2 ? mm_run<2>(P, B, ld, st) : mm_run<1>(P, B, ld, st);
+    return RT == 4   ? mm_run<4>(P, B, ld, st)
+           : RT == 3 ? mm_run<3>(P, B, ld, st)
+           : RT == 2 ? mm_run<2>(P, B, ld, st)
+                     : mm_run<1>(P, B, ld, st);
 }
 
 }  // namespace vte
