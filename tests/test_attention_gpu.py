@@ -228,3 +228,45 @@ def test_single_sequence_with_zero_batch_stride(hip, K):
     K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), pm, pl, po, out, 1, NQ, NKV, D, SCALE,
                     up(hip, np.asarray([700], np.int32)), 0, 128, max_splits, dtype="f32", stream=hip.stream)
     assert np.array_equal(down(out).view(np.uint32), a.view(np.uint32))
+
+
+@pytest.mark.parametrize("B,start,split,dtype", [(64, 100, 128, "f16"), (7, 0, 128, "f32"), (33, 1900, 128, "f16"),
+                                                 (2, 5, 512, "f32")])
+def test_prompt_columns_sharing_one_cache(hip, K, B, start, split, dtype):
+    """Prefill layout: B query columns at consecutive positions of ONE cache
+    (kv_batch_stride 0), two columns per block sharing each K/V tile; each
+    column must equal its own single-column run bit for bit and the oracle,
+    odd B included (the last block holds one column)."""
+    import os
+    rng = np.random.default_rng(B + start)
+    max_seq = 2304
+    q, kc, vc = _inputs(rng, B, max_seq)
+    kc1, vc1 = kc[:1], vc[:1]
+    offsets = np.arange(start, start + B, dtype=np.int32)
+    max_splits = (max_seq + split - 1) // split
+    pm, pl = empty(hip, (B, NQ, max_splits), np.float32), empty(hip, (B, NQ, max_splits), np.float32)
+    po = empty(hip, (B, NQ, max_splits, D), np.float32)
+    odt = np.float32 if dtype == "f32" else np.float16
+    qd, kd, vd, od = up(hip, q.astype(odt)), up(hip, kc1), up(hip, vc1), up(hip, offsets)
+
+    def run():
+        out = empty(hip, (B, NQ, D), odt)
+        K.attn_split_kv(qd, kd, vd, pm, pl, po, out, B, NQ, NKV, D, SCALE, od, 0, split, max_splits, dtype=dtype,
+                        stream=hip.stream)
+        return down(out)
+
+    got = run()
+    old = os.environ.get("VTE_ATT_QC")
+    os.environ["VTE_ATT_QC"] = "0"  # one column per block
+    try:
+        one = run()
+    finally:
+        if old is None:
+            del os.environ["VTE_ATT_QC"]
+        else:
+            os.environ["VTE_ATT_QC"] = old
+    assert np.array_equal(got.view(np.uint16 if dtype == "f16" else np.uint32),
+                          one.view(np.uint16 if dtype == "f16" else np.uint32))
+    for b in (0, B // 2, B - 1):
+        ref = attention_ref(q[b].astype(odt).astype(np.float32), kc1[0], vc1[0], int(offsets[b]) + 1, SCALE)
+        assert rel_l2(got[b].astype(np.float32), ref) <= TOL, b

@@ -23,6 +23,7 @@
 //    blocks past a sequence's last split exit at once, and the combine reads
 //    only that sequence's splits, so each sequence's result is independent of
 //    the batch it sits in.
+#include <cstdlib>
 #include "vte_common.h"
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -107,7 +108,10 @@ template <bool FIRST>
 __device__ __forceinline__ void att_tile_step(AttTile& T, int t0, int t_end, const half8_t (&qb)[ATT_D / 32],
                                               float scale, float& m_run, float& l_run,
                                               floatx4_t (&o_acc)[ATT_D / 16],
-                                              uint32_t (*vt)[ATT_VT_STRIDE / 2], int lane, int col, int grp) {
+                                              uint32_t (*vt)[ATT_VT_STRIDE / 2], int lane, int col, int grp,
+                                              int t_end_col) {
+    // t_end: end of the tokens any query slot reads (V rows past it are
+    // zeroed); t_end_col: end for this lane's query slot (scores past it -inf)
     // rows at or past the end contribute p = 0; zero their V so that
     // whatever the rows hold cannot turn 0 * V into NaN (tail tile only)
     if (t0 + ATT_TILE > t_end) {
@@ -139,7 +143,7 @@ __device__ __forceinline__ void att_tile_step(AttTile& T, int t0, int t_end, con
         for (int i = 0; i < 4; ++i) {
             const int tok = t0 + 16 * tt + 4 * grp + i;
             float sv = acc[tt][i] * scale;
-            sv = (tok < t_end) ? sv : -INFINITY;
+            sv = (tok < t_end_col) ? sv : -INFINITY;
             sc[tt][i] = sv;
             tmax = fmaxf(tmax, sv);
         }
@@ -193,17 +197,22 @@ __device__ __forceinline__ void att_tile_step(AttTile& T, int t0, int t_end, con
 // end, which the host checked lie inside the sequence's cache), so the
 // length and the first tile arrive in one memory round trip; rows at or past
 // the length are masked (scores -inf, V zero).
-template <typename TQ, typename TO, bool SPEC, int TPW>
+// QC = 2: the block serves query columns 2z and 2z + 1, which read the same
+// cache (kv_batch_stride 0: prompt tokens of one sequence), so each K/V tile
+// is loaded once for both: MFMA N slots 0..G-1 are column 2z's heads and
+// G..2G-1 column 2z + 1's, each slot masked at its own column's length.
+template <typename TQ, typename TO, bool SPEC, int TPW, int QC = 1>
 __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     const TQ* __restrict__ q,            // [B][n_q][D]
     const __half* __restrict__ k_cache, const __half* __restrict__ v_cache,
     float* __restrict__ part_m, float* __restrict__ part_l, float* __restrict__ part_o,
     int n_q, int n_kv, float scale, const int* __restrict__ kv_offset, int kv_batch_stride,
-    int split, int max_splits, int* __restrict__ counters, TO* __restrict__ out) {
+    int split, int max_splits, int* __restrict__ counters, TO* __restrict__ out, int n_cols) {
     // TPW == 0: one 32-token split per wave (split == 32), no block combine
     constexpr bool PW = TPW == 0;
+    static_assert(QC == 1 || (!PW && !SPEC), "two query columns per block: block-combined, non-speculative splits");
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int sp = PW ? blockIdx.x * ATT_WAVES + wv : blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int sp = PW ? blockIdx.x * ATT_WAVES + wv : blockIdx.x, kvh = blockIdx.y, b = QC * blockIdx.z;
     if (PW && sp >= max_splits) return;
     ATT_TS(0);
     const int t_begin = sp * split;
@@ -213,7 +222,7 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     const size_t row_stride = (size_t)n_kv * ATT_D;  // elements between consecutive positions
     const __half* kb = k_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
     const __half* vb = v_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
-    const int len_raw = kv_offset[b];
+    const int len_raw = QC == 1 ? kv_offset[b] : max(kv_offset[b], kv_offset[min(b + 1, n_cols - 1)]);
     AttTile T, T1;
     int t0 = PW ? t_begin : t_begin + wv * ATT_TILE;
     if (SPEC) {
@@ -225,19 +234,24 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     // B operand: Q^T for this KV head's G query heads, fp16, zero-padded to 16.
     // Rows past G read head G-1 and are zeroed by a select (no branch).
     half8_t qb[ATT_D / 32];
+    // this lane's query slot: column b + qc, head hs of the group
+    const int qc = QC == 1 ? 0 : min(col / G, QC - 1), hs = QC == 1 ? min(col, G - 1) : col - qc * G;
+    const int bq = QC == 1 ? b : min(b + qc, n_cols - 1);
+    const bool slot_ok = QC == 1 ? col < G : (col < QC * G && hs < G && b + qc < n_cols);
     {
-        const int qh = kvh * G + min(col, G - 1);
-        const TQ* qp = q + ((size_t)b * n_q + qh) * ATT_D;
+        const int qh = kvh * G + min(hs, G - 1);
+        const TQ* qp = q + ((size_t)bq * n_q + qh) * ATT_D;
 #pragma unroll
         for (int s = 0; s < ATT_D / 32; ++s) {
             const half8_t v = att_load_q8(qp + 32 * s + 8 * grp);
-            qb[s] = (col < G) ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            qb[s] = slot_ok ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }
 
     const int len = len_raw + 1;
     if (t_begin >= len) return;  // past this sequence's last split (PW: this wave's)
     const int t_end = min(t_begin + split, len);
+    const int t_end_col = QC == 1 ? t_end : min(t_begin + split, kv_offset[bq] + 1);
 
     // V tile of a wave, transposed: vt[d][t] (fp16, rows of 36 halves so the
     // 8-byte reads of 16 consecutive d rows hit distinct LDS banks)
@@ -265,7 +279,7 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         if (TPW == 2) att_load_tile(T1, kb, vb, row_stride, t0 + ATT_WAVES * ATT_TILE, t_end - 1, col, grp, lane);
     }
     ATT_TS(1);
-    if (t0 < t_end) att_tile_step<true>(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
+    if (t0 < t_end) att_tile_step<true>(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp, t_end_col);
     if (PW) {  // the wave's split is done: its statistics and outputs are the partials
         l_run += __shfl_xor(l_run, 16, 64);
         l_run += __shfl_xor(l_run, 32, 64);
@@ -285,12 +299,12 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     }
     t0 += ATT_WAVES * ATT_TILE;
     if (TPW == 2) {
-        if (t0 < t_end) att_tile_step<false>(T1, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
+        if (t0 < t_end) att_tile_step<false>(T1, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp, t_end_col);
         t0 += ATT_WAVES * ATT_TILE;
     }
     for (; t0 < t_end; t0 += ATT_WAVES * ATT_TILE) {
         att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
-        att_tile_step<false>(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp);
+        att_tile_step<false>(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp, t_end_col);
     }
 
     ATT_TS(2);
@@ -304,9 +318,11 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
 #pragma unroll
         for (int i = 0; i < 4; ++i) o_sh[wv][4 * grp + i][16 * dt + col] = o_acc[dt][i];
     __syncthreads();
-    // thread -> (head h, dim pair): 256 threads cover 2 heads x 128 dims per pass
-    for (int idx = threadIdx.x; idx < G * ATT_D; idx += 256) {
+    // thread -> (query slot h, dim): 256 threads cover 2 slots x 128 dims per pass
+    for (int idx = threadIdx.x; idx < QC * G * ATT_D; idx += 256) {
         const int h = idx / ATT_D, d = idx % ATT_D;
+        const int bc = b + h / G;  // the slot's query column
+        if (QC > 1 && bc >= n_cols) break;
         float M = -1e30f;
 #pragma unroll
         for (int w = 0; w < ATT_WAVES; ++w) M = fmaxf(M, m_sh[w][h]);
@@ -317,13 +333,13 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
             L = fmaf(l_sh[w][h], c, L);
             O = fmaf(o_sh[w][h][d], c, O);
         }
-        const int qh = kvh * G + h;
-        const size_t st = ((size_t)b * n_q + qh) * max_splits + sp;
+        const int qh = kvh * G + h % G;
+        const size_t st = ((size_t)bc * n_q + qh) * max_splits + sp;
         part_o[st * ATT_D + d] = O;
         if (d == 0) { part_m[st] = M; part_l[st] = L; }
     }
     ATT_TS(3);
-    if (counters == nullptr) return;  // separate combine launch
+    if (QC > 1 || counters == nullptr) return;  // separate combine launch
 
     // ---- last block of this (sequence, KV head) performs the LSE combine ----
     // Release the partials at device scope, count this split, and let the block
@@ -605,6 +621,12 @@ __global__ __launch_bounds__(128) void attn_combine_small(const float* __restric
 // ---------------------------------------------------------------------------
 namespace vte {
 
+// true when the environment variable is set to 0 (switches a launch form off)
+static bool getenv_off_att(const char* name) {
+    const char* v = getenv(name);
+    return v != nullptr && atoi(v) == 0;
+}
+
 template <typename TQ, typename TO>
 hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache, float* part_m, float* part_l,
                          float* part_o, void* out, int B, int n_q, int n_kv, float scale, const int* kv_offset,
@@ -614,12 +636,21 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
     // max_splits * split must lie inside one sequence's kv_batch_stride
     const long long rows_cap = kv_batch_stride / ((long long)n_kv * ATT_D);
     const bool spec = (long long)max_splits * split <= rows_cap;
-#define ATT_LAUNCH_P(SP, TP)                                                                                   \
-    hipLaunchKernelGGL((attn_partial_gqa<TQ, TO, SP, TP>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache,   \
+#define ATT_LAUNCH_Q(SP, TP, QC)                                                                               \
+    hipLaunchKernelGGL((attn_partial_gqa<TQ, TO, SP, TP, QC>), g1, b1, 0, st, (const TQ*)q, (const __half*)k_cache, \
                        (const __half*)v_cache, part_m, part_l, part_o, n_q, n_kv, scale, kv_offset, kv_batch_stride, \
-                       split, max_splits, counters, (TO*)out)
+                       split, max_splits, counters, (TO*)out, B)
+#define ATT_LAUNCH_P(SP, TP) ATT_LAUNCH_Q(SP, TP, 1)
     const bool two = split >= 2 * ATT_WAVES * ATT_TILE;  // two tiles per wave loaded together
-    if (split == ATT_TILE) {  // one split per wave: a block takes four consecutive splits
+    const int G = n_q / n_kv;
+    if (kv_batch_stride == 0 && B > 1 && counters == nullptr && split != ATT_TILE && 2 * G <= 16 &&
+        !getenv_off_att("VTE_ATT_QC")) {
+        // every column reads one cache (prompt tokens of one sequence): two
+        // query columns per block share each K/V tile
+        g1.z = (B + 1) / 2;
+        if (two) ATT_LAUNCH_Q(false, 2, 2);
+        else ATT_LAUNCH_Q(false, 1, 2);
+    } else if (split == ATT_TILE) {  // one split per wave: a block takes four consecutive splits
         g1.x = (max_splits + ATT_WAVES - 1) / ATT_WAVES;
         if (spec) ATT_LAUNCH_P(true, 0);
         else ATT_LAUNCH_P(false, 0);
@@ -631,6 +662,7 @@ hipError_t attn_split_kv(const void* q, const void* k_cache, const void* v_cache
         else ATT_LAUNCH_P(false, 1);
     }
 #undef ATT_LAUNCH_P
+#undef ATT_LAUNCH_Q
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || counters != nullptr || out == nullptr) return e;  // out == nullptr: partials only
     dim3 g2(n_q, B), b2(ATT_D);
