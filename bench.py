@@ -44,6 +44,39 @@ def time_graph(hip, ex, steps, warmup):
     return ms / steps, wall
 
 
+def prefill_bench(hip, model, n=2048, chunk=512, trials=3, profile_runs=0):
+    """Multi-token prefill of an n-token synthetic prompt into sequence 0 of a
+    batch-1 executor, chunks of `chunk` columns (vte_amd.core.prefill), timed
+    with HIP events around the whole prompt; median of `trials` after one
+    untimed run.  With profile_runs > 0: only that many untimed runs (for
+    rocprofv3 kernel traces)."""
+    from vte_amd.core.hip_graph_executor import HIPGraphExecutor
+    from vte_amd.core.prefill import PrefillRunner
+    ex = HIPGraphExecutor(hip, model, batch_size=1, max_seq=n + 256)
+    runner = PrefillRunner(ex, chunk=chunk)
+    prompt = [int(t) for t in np.random.default_rng(0).integers(0, model.cfg.vocab, n)]
+    try:
+        runner.prefill(prompt, seq=0, start=0)
+        if profile_runs:
+            for i in range(profile_runs):
+                runner.prefill(prompt, seq=0, start=0)
+                print(f"profile-prefill: run {i + 1}/{profile_runs}", flush=True)
+            return None
+        times = []
+        for _ in range(trials):
+            e0, e1 = _events(hip)
+            hip.event_record(e0)
+            runner.prefill(prompt, seq=0, start=0)
+            hip.event_record(e1)
+            hip.synchronize()
+            times.append(hip.event_elapsed_ms(e0, e1))
+        ms = float(np.median(times))
+        return {"prompt": n, "chunk": chunk, "ms": round(ms, 3), "tok_s": round(n / (ms * 1e-3), 1)}
+    finally:
+        runner.close()
+        ex.close()
+
+
 def time_classes(hip, ex, classes, reps=20):
     """Average time of the launches of ``classes`` in one step, measured with
     HIP events on the executor's stream around replays of a graph holding only
@@ -299,6 +332,8 @@ def main():
     ap.add_argument("--profile-step", type=int, default=0, metavar="B",
                     help="profiling run only: a 256 MiB calibration copy, then --steps replays of the batch-B "
                          "step graph (for rocprofv3 kernel traces and counters)")
+    ap.add_argument("--profile-prefill", type=int, default=0, metavar="R",
+                    help="profiling run only: R untimed 2048-token prefills (chunks of 512)")
     ap.add_argument("--profile-classes", default="", metavar="C1,C2",
                     help="with --profile-step: replay only these launch classes (e.g. attn_in,ffn_in,lm_head)")
     args = ap.parse_args()
@@ -325,6 +360,10 @@ def main():
     t_gen = time.perf_counter()
     model = SyntheticQwen2(QWEN25_1P5B, seed=0)
     t_gen = time.perf_counter() - t_gen
+    if args.profile_prefill:
+        prefill_bench(hip, model, profile_runs=args.profile_prefill)
+        hip.cleanup()
+        return
     wbytes = model.weight_bytes()
     prefix = 2048
     result = {}
@@ -359,6 +398,7 @@ def main():
         attn.append(attn_bench(hip, K, 2049))
         attn.append(attn_bench(hip, K, 2049, fused=True))
         attn.append(attn_bench(hip, K, 2049, B=16))
+    prefill = None if args.quick else prefill_bench(hip, model)
     cpu = None if args.no_cpu else cpu_baseline()
     r1 = result[1]
     line = {
@@ -384,6 +424,8 @@ def main():
         line["gemv"] = gemv
     if attn:
         line["attention"] = attn
+    if prefill:
+        line["prefill"] = prefill
     line["roofline"] = roof
     line["step_breakdown_b1"] = breakdown
     if cpu:
