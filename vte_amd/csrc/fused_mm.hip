@@ -224,7 +224,7 @@ __device__ __forceinline__ void mm_epilogue(const MmPlan& P, const MmTile& T, fl
     const MmSeg& S = *T.S;
     if (!mm_paired(S.mode)) {
         for (int o = threadIdx.x; o < 16 * RT * 16 * NT; o += blockDim.x) {
-            const int rr = o % (16 * RT), mc = o / (16 * RT);  // consecutive threads: consecutive rows
+            const int rr = o / (16 * NT), mc = o % (16 * NT);
             if (rr >= T.nvalid || mc >= mcount) continue;
             const int row = T.j0 + rr, m = cb + mc;
             const __half v = __float2half(mm_sum<RT, NT, NW>(red, rr, mc) + mm_bias(S.bias, row));
@@ -238,7 +238,7 @@ __device__ __forceinline__ void mm_epilogue(const MmPlan& P, const MmTile& T, fl
         return;
     }
     for (int o = threadIdx.x; o < 8 * RT * 16 * NT; o += blockDim.x) {
-        const int p = o % (8 * RT), mc = o / (8 * RT);  // consecutive threads: consecutive rows
+        const int p = o / (16 * NT), mc = o % (16 * NT);
         if (p >= T.nvalid || mc >= mcount) continue;
         const float a = mm_sum<RT, NT, NW>(red, p, mc), b = mm_sum<RT, NT, NW>(red, p + 8 * RT, mc);
         const int row = T.j0 + p, m = cb + mc;

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
     __syncthreads();
     // C layout: lane (col, grp) holds rows 4*grp+i of the tile, batch column col.
     for (int o = threadIdx.x; o < RT * 16 * NT * 16; o += blockDim.x) {
-        const int rr = o % (RT * 16), mc = o / (RT * 16);  // consecutive threads: consecutive rows
+        const int rr = o / (NT * 16), mc = o % (NT * 16);
         const int rt = rr >> 4, rw = rr & 15, nt = mc >> 4, cc = mc & 15;
         const int ln = cc + 16 * (rw >> 2), i = rw & 3;
         float s = 0.f;
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
         __syncthreads();
         const int mcount = min(16 * NT, c1 - m0);
         for (int o = threadIdx.x; o < 16 * NT * 16; o += blockDim.x) {
-            const int rr = o % 16, mc = o / 16;  // consecutive threads: consecutive rows
+            const int rr = o / (NT * 16), mc = o % (NT * 16);
             const int nt = mc >> 4, cc = mc & 15;
             const int ln = cc + 16 * (rr >> 2), i = rr & 3;
             float s = 0.f;
