@@ -175,10 +175,12 @@ class HIPGraphExecutor:
     FUSED_CLASSES = ("embed", "attn_in", "attn", "o_proj", "ffn_in", "down", "lm_head", "topk")
 
     def _enqueue_fused(self, only=None) -> None:
-        """Five launches per layer: norm+QKV+RoPE+append [fused_mv_kernel],
-        split-KV attention partials [attn_partial_gqa], LSE combine + o-proj
-        + residual [fused_mv_kernel], norm+gate/up+SwiGLU [fused_mv_kernel],
-        down + residual [fused_mv_kernel]; then
+        """Five or six launches per layer: norm+QKV+RoPE+append [fused_mv_kernel],
+        split-KV attention partials [attn_partial_gqa], the LSE combine (its
+        own launch [attn_combine_small] beyond ``oproj_combine_max_splits``
+        splits, else in the o-proj prologue), o-proj + residual
+        [fused_mv_kernel], norm+gate/up+SwiGLU [fused_mv_kernel], down +
+        residual [fused_mv_kernel]; then
         norm+LM head [fused_mv_kernel] and top-k.  ``only``: a set of
         FUSED_CLASSES to issue (timing of one class over the same buffers)."""
         cfg, K, st, B = self.cfg, self.K, self.hip.stream, self.B
