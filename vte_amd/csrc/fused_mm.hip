@@ -400,6 +400,14 @@ static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipSt
     for (int s = 0; s < P.nseg; ++s) out0[s] = P.seg[s].out;
     __half* kc0 = P.k_cache;
     __half* vc0 = P.v_cache;
+    if constexpr (RT == 4) if (B > 32 && P.K == 6 * QK_K && mm_env("VTE_MM_WS", 1)) {
+        // 64 rows per block, 16 columns at a time: one block per CU
+        const int g = ws_column_groups(total, B, device_cus());
+        const int cols = ((B + 31) / 32 + g - 1) / g * 32, gy = (B + cols - 1) / cols;
+        P.M = B;
+        hipLaunchKernelGGL((fused_mm_ws_kernel<RT, 1>), dim3(total, gy), dim3(64 * 6), 0, st, P, cols);
+        return hipGetLastError();
+    }
     if constexpr (RT <= 2) if (B > 32 && P.K == 6 * QK_K && mm_env("VTE_MM_WS", 1)) {
         // two 6-wave blocks fit per CU
         const int g = ws_column_groups(total, B, 2 * device_cus());
@@ -435,7 +443,9 @@ hipError_t qkv_mm(const void* xn, const void* wq, const void* q_bias, int fmt_q,
                   int fmt_k, const void* wv, const void* v_bias, int fmt_v, void* q_out, void* k_cache, void* v_cache,
                   const int* kv_offset, int kv_batch_stride, const void* rope_cos, const void* rope_sin, int B, int K,
                   int n_q, int n_kv, hipStream_t st) {
-    const int RT = mm_env("VTE_MM_RT_QKV", 1);
+    // 64 rows per block from 129 columns (2048-token prefill in chunks of 512:
+    // 38.5 -> 37.2 ms; chunks of 64-128 are faster with 16)
+    const int RT = mm_env("VTE_MM_RT_QKV", B > 128 ? 4 : 1);
     MmPlan P;
     memset(&P, 0, sizeof(P));
     P.K = K;
@@ -452,7 +462,7 @@ hipError_t qkv_mm(const void* xn, const void* wq, const void* q_bias, int fmt_q,
     P.kv_batch_stride = kv_batch_stride;
     P.n_kv = n_kv;
     size_t ld[MM_MAX_SEG] = {(size_t)n_q * 128, 0, 0};
-    return RT == 2 ? mm_run<2>(P, B, ld, st) : mm_run<1>(P, B, ld, st);
+    return RT == 4 ? mm_run<4>(P, B, ld, st) : RT == 2 ? mm_run<2>(P, B, ld, st) : mm_run<1>(P, B, ld, st);
 }
 
 // out [B][ffn] = fp16(silu(W_gate xn) * (W_up xn)) for RMSNorm-ed fp16 xn [B][K].
@@ -460,10 +470,11 @@ hipError_t gate_up_mm(const void* xn, const void* w_gate, const void* w_up, int 
                       hipStream_t st) {
     // 16 gate/up pairs per block (half the blocks of 8, activations read half
     // as often); 24 for 17-32 columns (measured: batch 32 2.26 -> 2.18 ms per
-    // step, batch 8-16 slightly slower); the weight-stationary form above 32
-    // columns takes at most 16
-    int RT = mm_env("VTE_MM_RT_FFN", B > 16 && B <= 32 ? 3 : 2);
-    if (B > 32 && RT > 2) RT = 2;
+    // step, batch 8-16 slightly slower); 32 in the weight-stationary form above
+    // 32 columns (one block per CU, but each activation chunk serves twice
+    // the rows: 2048-token prefill 51.9 -> 47.9 ms)
+    int RT = mm_env("VTE_MM_RT_FFN", B > 32 ? 4 : B > 16 ? 3 : 2);
+    if (B > 32 && RT == 3) RT = 2;
     MmPlan P;
     memset(&P, 0, sizeof(P));
     P.K = K;

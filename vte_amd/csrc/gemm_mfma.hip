@@ -140,18 +140,18 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
 // columns [blockIdx.z * cols, ...), 16 * NT at a time, requesting the next
 // columns' activations before the epilogue; the k-steps and the wave sum keep
 // the order of gemm_mfma_kernel, so the partial sums have the same bits.
-template <int FMT, int NT>
+template <int FMT, int RT, int NT>
 __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __half* __restrict__ x,
                                                                      const uint8_t* __restrict__ w,
                                                                      float* __restrict__ part, int M, int K, int N,
                                                                      size_t split_stride, int cols) {
     constexpr int NW = MF_WAVES;
-    __shared__ float red[NW][NT][4][64];
+    __shared__ float red[NW][RT][NT][4][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int n_sb = K / QK_K;
     const size_t row_bytes = (size_t)n_sb * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES);
-    const int row0 = blockIdx.x * 16;
+    const int row0 = blockIdx.x * 16 * RT;
     const int kb0 = (n_sb * (int)blockIdx.y) / (int)gridDim.y, kb1 = (n_sb * ((int)blockIdx.y + 1)) / (int)gridDim.y;
     const int sb0 = kb0 + ((kb1 - kb0) * wv) / NW, sb1 = kb0 + ((kb1 - kb0) * (wv + 1)) / NW;
     const bool has = sb1 > sb0;
@@ -159,15 +159,18 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
     if (c0 >= c1) return;
     float* y = part + blockIdx.y * split_stride;
 
-    half8_t av[8];
+    half8_t av[RT][8];
     if (has) {
-        const uint8_t* blk = w + (size_t)min(row0 + col, N - 1) * row_bytes;
-        if (FMT == 4) {
-            Q4Raw r;
-            q4_raw_load(blk + (size_t)sb0 * Q4K_BYTES, grp, r);
-            q4_raw_operands(r, grp, av);
-        } else {
-            q6k_a_operands(blk + (size_t)sb0 * Q6K_BYTES, grp, av);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const uint8_t* blk = w + (size_t)min(row0 + rt * 16 + col, N - 1) * row_bytes;
+            if (FMT == 4) {
+                Q4Raw r;
+                q4_raw_load(blk + (size_t)sb0 * Q4K_BYTES, grp, r);
+                q4_raw_operands(r, grp, av[rt]);
+            } else {
+                q6k_a_operands(blk + (size_t)sb0 * Q6K_BYTES, grp, av[rt]);
+            }
         }
     }
     half8_t bx[8][NT];
@@ -184,30 +187,36 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
     };
     load_b(c0);
     for (int m0 = c0; m0 < c1; m0 += 16 * NT) {
-        floatx4_t acc[NT];
+        floatx4_t acc[RT][NT];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
         if (has) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
+            for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t], bx[t][nt], acc[nt], 0, 0, 0);
+                for (int t = 0; t < 8; ++t)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[rt][t], bx[t][nt], acc[rt][nt], 0, 0, 0);
         }
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[wv][nt][i][lane] = acc[nt][i];
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wv][rt][nt][i][lane] = acc[rt][nt][i];
         if (m0 + 16 * NT < c1) load_b(m0 + 16 * NT);
         __syncthreads();
         const int mcount = min(16 * NT, c1 - m0);
-        for (int o = threadIdx.x; o < 16 * NT * 16; o += blockDim.x) {
+        for (int o = threadIdx.x; o < 16 * RT * NT * 16; o += blockDim.x) {
             const int rr = o / (NT * 16), mc = o % (NT * 16);
-            const int nt = mc >> 4, cc = mc & 15;
-            const int ln = cc + 16 * (rr >> 2), i = rr & 3;
+            const int rt = rr >> 4, rw = rr & 15, nt = mc >> 4, cc = mc & 15;
+            const int ln = cc + 16 * (rw >> 2), i = rw & 3;
             float s = 0.f;
 #pragma unroll
-            for (int wq = 0; wq < NW; ++wq) s += red[wq][nt][i][ln];
+            for (int wq = 0; wq < NW; ++wq) s += red[wq][rt][nt][i][ln];
             const int row = row0 + rr;
             if (row < N && mc < mcount) y[(size_t)(m0 + mc) * N + row] = s;
         }
@@ -389,11 +398,19 @@ static hipError_t launch_splitk(const void* x, const void* w, float* part, int M
     const int n_sb = K / QK_K;
     if (M > 32 && (n_sb + splits - 1) / splits <= MF_WAVES && !getenv_off("VTE_MM_WS")) {
         // one launch; two 8-wave blocks fit per CU
-        const int tiles = (N + 15) / 16;
-        const int g = ws_column_groups(tiles * splits, M, 2 * device_cus());
-        const int cols = ((M + 31) / 32 + g - 1) / g * 32, gz = (M + cols - 1) / cols;
-        hipLaunchKernelGGL((gemm_ws_splitk_kernel<FMT, 2>), dim3(tiles, splits, gz), dim3(64 * MF_WAVES), 0, st,
-                           (const __half*)x, (const uint8_t*)w, part, M, K, N, ss, cols);
+        if (getenv_off("VTE_MM_WS_RT4")) {  // 16 rows per block, 32 columns at a time
+            const int tiles = (N + 15) / 16;
+            const int g = ws_column_groups(tiles * splits, M, 2 * device_cus());
+            const int cols = ((M + 31) / 32 + g - 1) / g * 32, gz = (M + cols - 1) / cols;
+            hipLaunchKernelGGL((gemm_ws_splitk_kernel<FMT, 1, 2>), dim3(tiles, splits, gz), dim3(64 * MF_WAVES), 0,
+                               st, (const __half*)x, (const uint8_t*)w, part, M, K, N, ss, cols);
+        } else {  // 64 rows per block, 16 columns at a time: each activation chunk serves 4x the rows
+            const int tiles = (N + 63) / 64;
+            const int g = ws_column_groups(tiles * splits, M, device_cus());
+            const int cols = ((M + 31) / 32 + g - 1) / g * 32, gz = (M + cols - 1) / cols;
+            hipLaunchKernelGGL((gemm_ws_splitk_kernel<FMT, 4, 1>), dim3(tiles, splits, gz), dim3(64 * MF_WAVES), 0,
+                               st, (const __half*)x, (const uint8_t*)w, part, M, K, N, ss, cols);
+        }
         return hipGetLastError();
     }
     for (int m0 = 0; m0 < M; m0 += 32) {
