@@ -1,4 +1,4 @@
-// Batched (B >= 8) projections with the decode-step glue fused in, on MFMA
+// Batched (3 or more columns) projections with the decode-step glue fused in, on MFMA
 // (gfx950).  One launch per group of projections that read the same
 // (already RMSNorm-ed, fp16) activations:
 //

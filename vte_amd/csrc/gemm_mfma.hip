@@ -4,7 +4,8 @@
 //
 // Same contract as the GEMV (vte/compiler/templates/rdna/gemv_q4k.hip.template:56-168);
 // the reference re-reads W once per batch row (grid.y = batch), this kernel
-// reads it once per 32-column batch tile.
+// reads it once per 32-column batch tile (and the weight-stationary split-K
+// form once per column group of up to hundreds of columns).
 //
 // Design:
 //  * v_mfma_f32_16x16x32_f16: M = 16 weight rows, N = 16 batch columns,
