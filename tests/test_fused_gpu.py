@@ -208,7 +208,8 @@ def test_batch_above_4_rejects_fused_norm(hip, K):
                                               ("q4_k", 8960, 1536, 40, 5), ("q6_k", 1536, 1536, 16, 1),
                                               ("q4_k", 1536, 1536, 20, 6), ("q6_k", 2304, 640, 9, 8),
                                               ("q6_k", 8960, 1536, 100, 5), ("q6_k", 1536, 1536, 70, 2),
-                                              ("q4_k", 2304, 640, 33, 3), ("q4_k", 8960, 1536, 40, 2)])
+                                              ("q4_k", 2304, 640, 33, 3), ("q4_k", 8960, 1536, 40, 2),
+                                              ("q4_k", 1536, 1536, 100, 1)])
 def test_gemm_mfma_splitk(hip, K, fmt, k, n, M, splits):
     """Each split's partial equals the GEMV over its super-block range
     [n_sb * s // splits, n_sb * (s + 1) // splits) of every weight row.  Above
