@@ -99,7 +99,9 @@ long long vte_attn_scratch_floats(int batch, int n_q, int max_splits);
  * launch; else B*n_kv zeroed ints and the combine runs in the last partial
  * block of each (sequence, KV head) (max_splits <= 512), leaving them zero.
  * out NULL (with counters NULL): only the partials are written, for
- * vte_attn_out_gemv to combine.
+ * vte_attn_out_gemv to combine.  kv_batch_stride 0 with B > 1: every column
+ * reads the same cache (prompt tokens of one sequence, each at its own
+ * kv_offset); two columns then share each K/V tile load, same results.
  * Replaces: SplitKVAttentionDispatcher launches (vte/core/split_kv_attention.py:187-217),
  *           flash_attention_split_kv_partial_kernel (flash_attention_split_kv_partial.hip.template:31-120),
  *           flash_attention_split_kv_reduce_kernel (flash_attention_split_kv_reduce.hip.template:14-67). */
