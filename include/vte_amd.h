@@ -71,7 +71,9 @@ int vte_gemv(int fmt, int in_dtype, int out_dtype, const void* x, const void* w,
 int vte_gemm_mfma(int fmt, int in_dtype, int out_dtype, const void* x, const void* w, void* y, int M, int K,
                   int N, const void* bias, const void* residual, float residual_scale, void* stream);
 
-/* Split-K partial sums for batched projections (M >= 8), Q4_K / Q6_K, fp16 x:
+/* Split-K partial sums for batched projections (M >= 3; above 32 columns with
+ * at most 8 super-blocks per split one weight-stationary launch, same
+ * results), Q4_K / Q6_K, fp16 x:
  *   part[s][m][n] = sum over split s's super-blocks of dequant(W[n, k]) * x[m, k]
  * (fp32, no bias / scale / residual; 1 <= splits <= 8 and splits <= K / 256).
  * vte_add_rmsnorm adds the splits to the residual.
@@ -166,7 +168,8 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
  * or Q6_K.  norm_w NULL: x is already normalised (fp16) and is used as is.
  * With norm_w: batch 1..4 on the VALU mat-vec (norm fused in).  NULL norm_w:
  * batch 1..2 on the VALU mat-vec, batch 3..4096 on MFMA (launches of 32
- * sequences); above batch 4 norm_w must be NULL (RMSNorm runs before).
+ * sequences; above 32 one weight-stationary launch, same results); above
+ * batch 4 norm_w must be NULL (RMSNorm runs before).
  * Replaces: the rmsnorm -> q/k/v gemv -> rope -> kv_cache_append nodes
  *           (vte/compiler/qwen_compute.py:100-282) and their fused forms
  *           FusedQKVDispatcher (vte/core/fused_qkv_dispatch.py:12-198),
