@@ -13,6 +13,7 @@
 //      Q4_K step t, group g: qs chunk c = g + 4*(t>>2), nibble (t>>1)&1, half t&1
 //      Q6_K step t, group g: half h = t>>2, quarter q = t&3, l = 8g .. 8g+7
 #pragma once
+#include <cstdlib>
 #include "quant.h"
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -173,6 +174,10 @@ __device__ __forceinline__ void q4_raw_operands(const Q4Raw& r, int grp, half8_t
 // the repeated weight reads.
 static inline int ws_column_groups(int tiles, int M, int slots) {
     const int chunks = (M + 31) / 32;
+    if (const char* v = getenv("VTE_WS_GROUPS")) {  // tuning: pin the group count
+        const int g = atoi(v);
+        if (g >= 1) return g < chunks ? g : chunks;
+    }
     int best = 1;
     double best_cost = 1e30;
     for (int g = 1; g <= chunks; ++g) {
