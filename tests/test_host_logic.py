@@ -1,0 +1,46 @@
+"""Host-side planning logic of the decode path (no GPU): prefill chunk
+widths, split-K split counts and the split-KV split size."""
+from types import SimpleNamespace
+
+import pytest
+
+from vte_amd.core.hip_graph_executor import MAX_SPLITK, splitk_splits
+from vte_amd.core.prefill import PrefillRunner
+
+
+def _runner(chunk, gemm_min_batch=3):
+    return PrefillRunner(SimpleNamespace(gemm_min_batch=gemm_min_batch), chunk=chunk)
+
+
+@pytest.mark.parametrize("chunk,n,width", [(512, 512, 512), (512, 37, 64), (512, 1, 4), (512, 5, 8),
+                                           (16, 5, 8), (16, 16, 16), (100, 70, 100), (100, 3, 4)])
+def test_prefill_chunk_width(chunk, n, width):
+    """A chunk of n tokens runs at the smallest power of two >= max(4, n),
+    capped at the configured chunk."""
+    assert _runner(chunk)._width(n) == width
+
+
+def test_prefill_chunk_below_batched_minimum_is_rejected():
+    from vte_amd.bridge.hip_runtime import HIPSafetyError
+    with pytest.raises(HIPSafetyError):
+        _runner(2)
+
+
+@pytest.mark.parametrize("K,splits", [(1536, 2), (8960, 5), (256, 1), (512, 2), (2304, 2), (4096, 3)])
+def test_splitk_splits(K, splits):
+    """At most seven super-blocks per split (one per wave of an 8-wave
+    block), at least two splits where K allows, at most MAX_SPLITK."""
+    s = splitk_splits(K)
+    assert s == splits
+    n_sb = K // 256
+    assert 1 <= s <= min(MAX_SPLITK, n_sb)
+    assert -(-n_sb // s) <= 8
+
+
+@pytest.mark.parametrize("ctx,split", [(1, 128), (2304, 128), (32768, 128), (32769, 256), (65536, 256),
+                                       (131072, 512), (10 ** 6, 1024)])
+def test_choose_split(ctx, split):
+    """128-token splits while they leave at most 256 splits per sequence,
+    then the smallest power of two (up to 1024) that does."""
+    from vte_amd.core.split_kv_attention import choose_split
+    assert choose_split(ctx, 1, 2, 256) == split
