@@ -41,33 +41,34 @@ def _blocks(raw, n_blocks: int, block_bytes: int) -> np.ndarray:
     return np.frombuffer(raw, dtype=np.uint8, count=n_blocks * block_bytes).reshape(n_blocks, block_bytes)
 
 
+def _q4k_scale_min_all(scales: np.ndarray):
+    """All eight (scale, min) pairs of each block, [n_blocks, 8] float32 each,
+    by q4k_scale_min (vte/compiler/dequantizer.py:6-23)."""
+    pairs = [q4k_scale_min(scales, j) for j in range(8)]
+    return (np.stack([p[0] for p in pairs], 1), np.stack([p[1] for p in pairs], 1))
+
+
 def dequantize_q4_k(raw, n_elements: int) -> np.ndarray:
     """Q4_K super-blocks -> fp32.  Follows vte/compiler/dequantizer.py:26-70.
 
     Block: [d f16][dmin f16][12 B packed scales][128 B qs].  Group mblk of
     64 outputs uses qs[32*mblk:32*mblk+32]: low nibbles -> outputs
     64*mblk+i with sub-block 2*mblk, high nibbles -> 64*mblk+32+i with
-    sub-block 2*mblk+1.
+    sub-block 2*mblk+1.  Each output is ``(d*sc)*q - (dmin*m)``, three fp32
+    operations rounded separately (all sub-blocks at once, same operations).
     """
     n_blocks = n_elements // QK_K
     blocks = _blocks(raw, n_blocks, Q4K_BLOCK_BYTES)
     d = blocks[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
     dmin = blocks[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
-    scales = blocks[:, 4:16].astype(np.int32)
-    qs = blocks[:, 16:144]
-    out = np.empty((n_blocks, QK_K), dtype=np.float32)
-    for mblk in range(4):
-        sc0, mn0 = q4k_scale_min(scales, 2 * mblk)
-        sc1, mn1 = q4k_scale_min(scales, 2 * mblk + 1)
-        d1 = d * sc0
-        m1 = dmin * mn0
-        d2 = d * sc1
-        m2 = dmin * mn1
-        q = qs[:, 32 * mblk:32 * mblk + 32]
-        lo = (q & 0x0F).astype(np.float32)
-        hi = (q >> 4).astype(np.float32)
-        out[:, 64 * mblk:64 * mblk + 32] = d1[:, None] * lo - m1[:, None]
-        out[:, 64 * mblk + 32:64 * mblk + 64] = d2[:, None] * hi - m2[:, None]
+    sc, mn = _q4k_scale_min_all(blocks[:, 4:16].astype(np.int32))
+    dsc = d[:, None] * sc                       # [nb, 8]   d*sc, sub-block j = 2*mblk + (0 lo | 1 hi)
+    mmn = dmin[:, None] * mn                    # [nb, 8]   dmin*m
+    qs = np.ascontiguousarray(blocks[:, 16:144]).reshape(n_blocks, 4, 1, 32)
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=2).astype(np.float32)     # [nb, mblk, lo/hi, 32]
+    dsc = np.repeat(dsc.reshape(n_blocks, 4, 2, 1), 32, axis=3)
+    mmn = np.repeat(mmn.reshape(n_blocks, 4, 2, 1), 32, axis=3)
+    out = dsc * q - mmn
     return out.reshape(-1)[:n_elements]
 
 
@@ -77,30 +78,22 @@ def dequantize_q6_k(raw, n_elements: int) -> np.ndarray:
     Block: [128 B ql][64 B qh][16 x int8 scales][d f16].  For half h and
     l<32 the four 6-bit values at 128h+l+{0,32,64,96} are built from the
     low/high nibbles of ql[64h+l] / ql[64h+l+32] and the 2-bit fields of
-    qh[32h+l], minus 32, scaled by d*sc[8h + l//16 + {0,2,4,6}].
+    qh[32h+l], minus 32, scaled by d*sc[8h + l//16 + {0,2,4,6}], computed
+    as ``(d*sc)*q`` in fp32 (all positions at once, same operations).
     """
     n_blocks = n_elements // QK_K
     blocks = _blocks(raw, n_blocks, Q6K_BLOCK_BYTES)
-    ql_all = blocks[:, 0:128]
-    qh_all = blocks[:, 128:192]
-    sc_all = blocks[:, 192:208].copy().view(np.int8)
+    ql = np.ascontiguousarray(blocks[:, 0:128]).reshape(n_blocks, 2, 2, 32)    # [nb, half, l / l+32, l]
+    qh = np.ascontiguousarray(blocks[:, 128:192]).reshape(n_blocks, 2, 1, 32)  # [nb, half, 1, l]
+    sc = blocks[:, 192:208].copy().view(np.int8).astype(np.float32).reshape(n_blocks, 2, 4, 2)  # [nb, half, k, l//16]
     d = blocks[:, 208:210].copy().view(np.float16).astype(np.float32)[:, 0]
-    out = np.empty((n_blocks, QK_K), dtype=np.float32)
-    for half in range(2):
-        ql = ql_all[:, half * 64:half * 64 + 64]
-        qh = qh_all[:, half * 32:half * 32 + 32]
-        sc = sc_all[:, half * 8:half * 8 + 8]
-        base = half * 128
-        for l in range(32):
-            is_ = l // 16
-            q1 = ((ql[:, l] & 0x0F) | (((qh[:, l] >> 0) & 3) << 4)).astype(np.int32) - 32
-            q2 = ((ql[:, l + 32] & 0x0F) | (((qh[:, l] >> 2) & 3) << 4)).astype(np.int32) - 32
-            q3 = ((ql[:, l] >> 4) | (((qh[:, l] >> 4) & 3) << 4)).astype(np.int32) - 32
-            q4 = ((ql[:, l + 32] >> 4) | (((qh[:, l] >> 6) & 3) << 4)).astype(np.int32) - 32
-            out[:, base + l] = d * sc[:, is_ + 0].astype(np.float32) * q1.astype(np.float32)
-            out[:, base + l + 32] = d * sc[:, is_ + 2].astype(np.float32) * q2.astype(np.float32)
-            out[:, base + l + 64] = d * sc[:, is_ + 4].astype(np.float32) * q3.astype(np.float32)
-            out[:, base + l + 96] = d * sc[:, is_ + 6].astype(np.float32) * q4.astype(np.float32)
+    # k = 0..3 -> q1..q4 at offsets 32k: low nibble of ql[l] / ql[l+32], then high nibbles;
+    # qh supplies bits 4-5 from its 2-bit field k
+    lo4 = np.concatenate([ql & 0x0F, ql >> 4], axis=2)        # [nb, half, 4, l]  (q1, q2, q3, q4)
+    hi2 = np.concatenate([(qh >> (2 * k)) & 3 for k in range(4)], axis=2)
+    q = ((lo4 | (hi2 << 4)).astype(np.int32) - 32).astype(np.float32).reshape(n_blocks, 2, 4, 2, 16)
+    dsc = d[:, None, None, None] * sc                          # d*sc[8h + l//16 + 2k]
+    out = np.repeat(dsc[..., None], 16, axis=4) * q
     return out.reshape(-1)[:n_elements]
 
 

@@ -57,15 +57,20 @@ def embedding_q6k(raw_table: np.ndarray, token: int, hidden: int) -> np.ndarray:
     return dq.dequantize_q6_k(raw_table[token * rb:(token + 1) * rb].tobytes(), hidden).astype(np.float16)
 
 
-def _lin(fmt, raw, n, k, x, bias=None, residual=None, cache=None, key=None):
-    """fp16-out GEMV with the reference epilogue; dequantised weights may be cached."""
+def _weights(fmt, raw, n, k, cache, key):
+    """Dequantised [n, k] fp32 matrix, optionally kept in ``cache``."""
     if cache is not None and key in cache:
-        w = cache[key]
-    else:
-        w = dq.dequantize_matrix(fmt, raw, n, k)
-        if cache is not None:
-            cache[key] = w
-    y = w @ x.astype(np.float32)
+        return cache[key]
+    w = dq.dequantize_matrix(fmt, raw, n, k)
+    if cache is not None:
+        cache[key] = w
+    return w
+
+
+def _lin(w, x, bias=None, residual=None):
+    """fp16-out GEMV with the reference epilogue (gemv_q4k.hip.template:155-166):
+    fp32 sum, + bias, + residual, rounded to fp16.  ``x`` [B, K] fp16."""
+    y = x.astype(np.float32) @ w.T
     if bias is not None:
         y = y + bias.astype(np.float32)
     if residual is not None:
@@ -76,42 +81,99 @@ def _lin(fmt, raw, n, k, x, bias=None, residual=None, cache=None, key=None):
 def decode_step(model, tokens, positions, k_cache, v_cache, cache=None):
     """One decode step for B sequences.
 
-    ``model``: vte_amd.core.model.SyntheticQwen2 (host copies of the weights).
+    ``model``: vte_amd.core.weights.SyntheticQwen2 (host copies of the weights).
     ``tokens`` [B], ``positions`` [B]; ``k_cache``/``v_cache`` per layer
     [B, max_seq, n_kv, hd] fp16, updated in place.  Returns fp32 logits [B, vocab].
+    The layer loop is outermost, so each layer's weights are dequantised once per
+    call for all B sequences (``cache`` optionally keeps them across calls).
+    Per layer (qwen_compute.py:100-282): attn_norm -> q/k/v (+bias) -> RoPE on q
+    and k -> K/V append -> attention (query head h reads KV head h // (n_q/n_kv))
+    -> o-proj + residual -> ffn_norm -> gate, up -> silu(gate) * up -> down +
+    residual; then output_norm and the tied Q6_K LM head.
     """
     cfg = model.cfg
     H, hd, nq, nkv = cfg.hidden, cfg.head_dim, cfg.n_q, cfg.n_kv
     scale = 1.0 / np.sqrt(hd)
     cos_c, sin_c = rope_cache(cfg.max_seq, hd, cfg.rope_theta)
     B = len(tokens)
-    logits = np.empty((B, cfg.vocab), np.float32)
-    for b in range(B):
-        pos = int(positions[b])
-        h = embedding_q6k(model.token_embd, int(tokens[b]), H)
-        for L, lw in enumerate(model.layers):
-            xn = rmsnorm(h, lw["attn_norm"], cfg.eps)
-            q = _lin(lw["q_fmt"], lw["q"], nq * hd, H, xn, lw["q_bias"], cache=cache, key=(L, "q"))
-            k = _lin(lw["k_fmt"], lw["k"], nkv * hd, H, xn, lw["k_bias"], cache=cache, key=(L, "k"))
-            v = _lin(lw["v_fmt"], lw["v"], nkv * hd, H, xn, lw["v_bias"], cache=cache, key=(L, "v"))
-            q = rope_neox(q.reshape(nq, hd), pos, cos_c, sin_c)
-            k = rope_neox(k.reshape(nkv, hd), pos, cos_c, sin_c)
-            k_cache[L][b, pos] = k
-            v_cache[L][b, pos] = v.reshape(nkv, hd)
-            att = attention_ref(q.astype(np.float32), k_cache[L][b], v_cache[L][b], pos + 1, scale)
-            att = att.astype(np.float16).reshape(-1)
-            h = _lin(lw["o_fmt"], lw["o"], H, nq * hd, att, residual=h, cache=cache, key=(L, "o"))
-            xn = rmsnorm(h, lw["ffn_norm"], cfg.eps)
-            g = _lin(lw["gate_fmt"], lw["gate"], cfg.ffn, H, xn, cache=cache, key=(L, "gate"))
-            u = _lin(lw["up_fmt"], lw["up"], cfg.ffn, H, xn, cache=cache, key=(L, "up"))
-            a = swiglu(g, u)
-            h = _lin(lw["down_fmt"], lw["down"], H, cfg.ffn, a, residual=h, cache=cache, key=(L, "down"))
-        hn = rmsnorm(h, model.output_norm, cfg.eps)
-        if cache is not None and "lm" in cache:
-            wl = cache["lm"]
-        else:
-            wl = dq.dequantize_matrix("q6_k", model.token_embd, cfg.vocab, H)
-            if cache is not None:
-                cache["lm"] = wl
-        logits[b] = wl @ hn.astype(np.float32)
-    return logits
+    pos = [int(p) for p in positions]
+    h = np.stack([embedding_q6k(model.token_embd, int(t), H) for t in tokens])      # [B, H] fp16
+    for L, lw in enumerate(model.layers):
+        w = {p: _weights(lw[p + "_fmt"], lw[p], *_shape(cfg, p), cache, (L, p))
+             for p in ("q", "k", "v", "o", "gate", "up", "down")}
+        xn = rmsnorm(h, lw["attn_norm"], cfg.eps)
+        q = _lin(w["q"], xn, lw["q_bias"])
+        k = _lin(w["k"], xn, lw["k_bias"])
+        v = _lin(w["v"], xn, lw["v_bias"])
+        att = np.empty((B, nq * hd), np.float16)
+        for b in range(B):
+            qb = rope_neox(q[b].reshape(nq, hd), pos[b], cos_c, sin_c)
+            k_cache[L][b, pos[b]] = rope_neox(k[b].reshape(nkv, hd), pos[b], cos_c, sin_c)
+            v_cache[L][b, pos[b]] = v[b].reshape(nkv, hd)
+            att[b] = attention_ref(qb.astype(np.float32), k_cache[L][b], v_cache[L][b], pos[b] + 1,
+                                   scale).astype(np.float16).reshape(-1)
+        h = _lin(w["o"], att, residual=h)
+        xn = rmsnorm(h, lw["ffn_norm"], cfg.eps)
+        a = swiglu(_lin(w["gate"], xn), _lin(w["up"], xn))
+        h = _lin(w["down"], a, residual=h)
+        del w
+    hn = rmsnorm(h, model.output_norm, cfg.eps)
+    wl = _weights("q6_k", model.token_embd, cfg.vocab, H, cache, "lm")
+    return (hn.astype(np.float32) @ wl.T).astype(np.float32)
+
+
+def _shape(cfg, p):
+    """(out_features, in_features) of projection ``p``."""
+    H = cfg.hidden
+    return {"q": (cfg.q_dim, H), "k": (cfg.kv_dim, H), "v": (cfg.kv_dim, H), "o": (H, cfg.q_dim),
+            "gate": (cfg.ffn, H), "up": (cfg.ffn, H), "down": (H, cfg.ffn)}[p]
+
+
+def prefill(model, tokens, start, k_cache, v_cache, cache=None):
+    """Prompt tokens of ONE sequence at positions start .. start+n-1, layer by layer.
+
+    Token-by-token decoding (the reference's only prefill, vte/core/model.py:969-973)
+    computed with the layer loop outermost: at each layer every prompt token's
+    q/k/v is formed, all K/V rows are appended, then token i attends rows
+    0 .. start+i (causal).  Each token's result is the one ``decode_step`` gives
+    when fed the tokens one at a time.  ``k_cache``/``v_cache`` per layer
+    [max_seq, n_kv, hd] fp16, updated in place.  Returns fp32 logits [n, vocab].
+    """
+    cfg = model.cfg
+    H, hd, nq, nkv = cfg.hidden, cfg.head_dim, cfg.n_q, cfg.n_kv
+    grp = nq // nkv
+    scale = 1.0 / np.sqrt(hd)
+    cos_c, sin_c = rope_cache(cfg.max_seq, hd, cfg.rope_theta)
+    n = len(tokens)
+    pos = np.arange(start, start + n)
+    h = np.stack([embedding_q6k(model.token_embd, int(t), H) for t in tokens])
+    for L, lw in enumerate(model.layers):
+        w = {p: _weights(lw[p + "_fmt"], lw[p], *_shape(cfg, p), cache, (L, p))
+             for p in ("q", "k", "v", "o", "gate", "up", "down")}
+        xn = rmsnorm(h, lw["attn_norm"], cfg.eps)
+        q = _lin(w["q"], xn, lw["q_bias"])
+        k = _lin(w["k"], xn, lw["k_bias"])
+        v = _lin(w["v"], xn, lw["v_bias"])
+        qr = np.stack([rope_neox(q[i].reshape(nq, hd), int(pos[i]), cos_c, sin_c) for i in range(n)])
+        for i in range(n):
+            k_cache[L][pos[i]] = rope_neox(k[i].reshape(nkv, hd), int(pos[i]), cos_c, sin_c)
+            v_cache[L][pos[i]] = v[i].reshape(nkv, hd)
+        ctx = start + n
+        causal = np.arange(ctx)[None, :] <= pos[:, None]                    # [n, ctx]
+        att = np.empty((n, nq, hd))
+        for hh in range(nq):
+            kk = k_cache[L][:ctx, hh // grp].astype(np.float64)
+            vv = v_cache[L][:ctx, hh // grp].astype(np.float64)
+            s = (qr[:, hh].astype(np.float64) @ kk.T) * scale
+            s = np.where(causal, s, -np.inf)
+            s -= s.max(1, keepdims=True)
+            p = np.exp(s)
+            att[:, hh] = (p / p.sum(1, keepdims=True)) @ vv
+        h = _lin(w["o"], att.astype(np.float16).reshape(n, -1), residual=h)
+        xn = rmsnorm(h, lw["ffn_norm"], cfg.eps)
+        a = swiglu(_lin(w["gate"], xn), _lin(w["up"], xn))
+        h = _lin(w["down"], a, residual=h)
+        del w
+    hn = rmsnorm(h, model.output_norm, cfg.eps)
+    wl = _weights("q6_k", model.token_embd, cfg.vocab, H, cache, "lm")
+    return (hn.astype(np.float32) @ wl.T).astype(np.float32)

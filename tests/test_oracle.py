@@ -251,3 +251,30 @@ def test_decode_step_residual_path_and_tied_lm_head():
         for L in range(cfg.n_layers):
             assert not ks[L][b, pos[b]].any() and not vs[L][b, pos[b]].any()
             assert (ks[L][b, pos[b] + 1] == 7).all()
+
+
+def test_prefill_oracle_equals_token_by_token_decode():
+    """oracle.step.prefill (layer-outer, causal over the prompt) gives each
+    token's logits and K/V rows as decode_step fed the tokens one at a time."""
+    from vte_amd.core.model_config import TINY
+    from vte_amd.core.weights import SyntheticQwen2
+    m = SyntheticQwen2(TINY, seed=8)
+    cfg = m.cfg
+    rng = np.random.default_rng(3)
+    start, n, max_seq = 5, 9, 32
+    ks = [np.zeros((1, max_seq, cfg.n_kv, cfg.head_dim), np.float16) for _ in range(cfg.n_layers)]
+    for k in ks:
+        k[0, :start] = (0.5 * rng.standard_normal((start, cfg.n_kv, cfg.head_dim))).astype(np.float16)
+    vs = [k.copy() * np.float16(-0.5) for k in ks]
+    toks = rng.integers(0, cfg.vocab, n)
+    kp, vp = [k[0].copy() for k in ks], [v[0].copy() for v in vs]
+    lp = ost.prefill(m, toks, start, kp, vp)
+    cache = {}
+    for i, t in enumerate(toks):
+        ld = ost.decode_step(m, [t], [start + i], ks, vs, cache)
+        # fp16 rounding flips between a batched and a single-row product: ~1e-3
+        assert np.linalg.norm(lp[i] - ld[0]) <= 3e-3 * np.linalg.norm(ld[0]), i
+    for L in range(cfg.n_layers):
+        for a, b in ((kp[L], ks[L][0]), (vp[L], vs[L][0])):
+            a, b = a.astype(np.float64), b.astype(np.float64)
+            assert np.linalg.norm(a - b) <= 3e-3 * np.linalg.norm(b), L
