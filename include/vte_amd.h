@@ -162,6 +162,21 @@ long long vte_topk_scratch_bytes(int rows);
 int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
              void* stream);
 
+/* vte_topk over the tokens NOT in each row's exclusion list, plus the exact
+ * logits of the excluded tokens.  excl_ids [rows][max_excl]: sorted token ids
+ * (the repetition window of the sampler, max_excl <= 4096; the reference uses
+ * 512); excl_cnt [rows]: how many of them are valid.  Both are read on the
+ * device, so a captured graph sees the values staged before each replay.
+ * gathered [rows][max_excl]: logits[row][excl_ids[row][i]] for i < excl_cnt[row].
+ * Since the repetition penalty only lowers logits, the top-k of the penalised
+ * row is contained in the k returned candidates plus the penalised gathered
+ * values.  Needs vocab - max_excl >= k.
+ * Replaces: topk_reduce_greedy_kernel's exclusion and gather
+ *           (topk_reduce_greedy.hip.template:40-83) and the buffers of
+ *           TopKLogitsReducer (vte/core/topk_logits_reducer.py:79-125). */
+int vte_topk_exclude(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
+                     const int* excl_ids, const int* excl_cnt, int max_excl, float* gathered, void* stream);
+
 /* One launch: RMSNorm(x) -> q/k/v projections (+bias) -> NEOX RoPE on q and k
  * -> q to q_out [B][n_q*128], k and v appended to the caches at kv_offset[b].
  * Same rounding points as the unfused nodes.  head_dim 128, q/k Q4_K, v Q4_K

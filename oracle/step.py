@@ -67,18 +67,25 @@ def _weights(fmt, raw, n, k, cache, key):
     return w
 
 
-def _lin(w, x, bias=None, residual=None):
+_ACC = {"f32": np.float32, "f64": np.float64}
+
+
+def _lin(w, x, bias=None, residual=None, accum="f32"):
     """fp16-out GEMV with the reference epilogue (gemv_q4k.hip.template:155-166):
-    fp32 sum, + bias, + residual, rounded to fp16.  ``x`` [B, K] fp16."""
-    y = x.astype(np.float32) @ w.T
+    sum, + bias, + residual, rounded to fp16.  ``x`` [B, K] fp16.  ``accum``:
+    the sum's precision ("f32" as the reference kernels; "f64" gives a second,
+    equally valid rounding history, whose distance from the first measures how
+    far two correct fp16-storage implementations drift apart)."""
+    t = _ACC[accum]
+    y = x.astype(t) @ w.T.astype(t, copy=False)
     if bias is not None:
-        y = y + bias.astype(np.float32)
+        y = y + bias.astype(t)
     if residual is not None:
-        y = y + residual.astype(np.float32)
+        y = y + residual.astype(t)
     return y.astype(np.float16)
 
 
-def decode_step(model, tokens, positions, k_cache, v_cache, cache=None):
+def decode_step(model, tokens, positions, k_cache, v_cache, cache=None, accum="f32"):
     """One decode step for B sequences.
 
     ``model``: vte_amd.core.weights.SyntheticQwen2 (host copies of the weights).
@@ -102,9 +109,9 @@ def decode_step(model, tokens, positions, k_cache, v_cache, cache=None):
         w = {p: _weights(lw[p + "_fmt"], lw[p], *_shape(cfg, p), cache, (L, p))
              for p in ("q", "k", "v", "o", "gate", "up", "down")}
         xn = rmsnorm(h, lw["attn_norm"], cfg.eps)
-        q = _lin(w["q"], xn, lw["q_bias"])
-        k = _lin(w["k"], xn, lw["k_bias"])
-        v = _lin(w["v"], xn, lw["v_bias"])
+        q = _lin(w["q"], xn, lw["q_bias"], accum=accum)
+        k = _lin(w["k"], xn, lw["k_bias"], accum=accum)
+        v = _lin(w["v"], xn, lw["v_bias"], accum=accum)
         att = np.empty((B, nq * hd), np.float16)
         for b in range(B):
             qb = rope_neox(q[b].reshape(nq, hd), pos[b], cos_c, sin_c)
@@ -112,14 +119,14 @@ def decode_step(model, tokens, positions, k_cache, v_cache, cache=None):
             v_cache[L][b, pos[b]] = v[b].reshape(nkv, hd)
             att[b] = attention_ref(qb.astype(np.float32), k_cache[L][b], v_cache[L][b], pos[b] + 1,
                                    scale).astype(np.float16).reshape(-1)
-        h = _lin(w["o"], att, residual=h)
+        h = _lin(w["o"], att, residual=h, accum=accum)
         xn = rmsnorm(h, lw["ffn_norm"], cfg.eps)
-        a = swiglu(_lin(w["gate"], xn), _lin(w["up"], xn))
-        h = _lin(w["down"], a, residual=h)
+        a = swiglu(_lin(w["gate"], xn, accum=accum), _lin(w["up"], xn, accum=accum))
+        h = _lin(w["down"], a, residual=h, accum=accum)
         del w
     hn = rmsnorm(h, model.output_norm, cfg.eps)
     wl = _weights("q6_k", model.token_embd, cfg.vocab, H, cache, "lm")
-    return (hn.astype(np.float32) @ wl.T).astype(np.float32)
+    return (hn.astype(_ACC[accum]) @ wl.T.astype(_ACC[accum], copy=False)).astype(np.float32)
 
 
 def _shape(cfg, p):
@@ -129,7 +136,7 @@ def _shape(cfg, p):
             "gate": (cfg.ffn, H), "up": (cfg.ffn, H), "down": (H, cfg.ffn)}[p]
 
 
-def prefill(model, tokens, start, k_cache, v_cache, cache=None):
+def prefill(model, tokens, start, k_cache, v_cache, cache=None, accum="f32"):
     """Prompt tokens of ONE sequence at positions start .. start+n-1, layer by layer.
 
     Token-by-token decoding (the reference's only prefill, vte/core/model.py:969-973)
@@ -151,9 +158,9 @@ def prefill(model, tokens, start, k_cache, v_cache, cache=None):
         w = {p: _weights(lw[p + "_fmt"], lw[p], *_shape(cfg, p), cache, (L, p))
              for p in ("q", "k", "v", "o", "gate", "up", "down")}
         xn = rmsnorm(h, lw["attn_norm"], cfg.eps)
-        q = _lin(w["q"], xn, lw["q_bias"])
-        k = _lin(w["k"], xn, lw["k_bias"])
-        v = _lin(w["v"], xn, lw["v_bias"])
+        q = _lin(w["q"], xn, lw["q_bias"], accum=accum)
+        k = _lin(w["k"], xn, lw["k_bias"], accum=accum)
+        v = _lin(w["v"], xn, lw["v_bias"], accum=accum)
         qr = np.stack([rope_neox(q[i].reshape(nq, hd), int(pos[i]), cos_c, sin_c) for i in range(n)])
         for i in range(n):
             k_cache[L][pos[i]] = rope_neox(k[i].reshape(nkv, hd), int(pos[i]), cos_c, sin_c)
@@ -169,11 +176,11 @@ def prefill(model, tokens, start, k_cache, v_cache, cache=None):
             s -= s.max(1, keepdims=True)
             p = np.exp(s)
             att[:, hh] = (p / p.sum(1, keepdims=True)) @ vv
-        h = _lin(w["o"], att.astype(np.float16).reshape(n, -1), residual=h)
+        h = _lin(w["o"], att.astype(np.float16).reshape(n, -1), residual=h, accum=accum)
         xn = rmsnorm(h, lw["ffn_norm"], cfg.eps)
-        a = swiglu(_lin(w["gate"], xn), _lin(w["up"], xn))
-        h = _lin(w["down"], a, residual=h)
+        a = swiglu(_lin(w["gate"], xn, accum=accum), _lin(w["up"], xn, accum=accum))
+        h = _lin(w["down"], a, residual=h, accum=accum)
         del w
     hn = rmsnorm(h, model.output_norm, cfg.eps)
     wl = _weights("q6_k", model.token_embd, cfg.vocab, H, cache, "lm")
-    return (hn.astype(np.float32) @ wl.T).astype(np.float32)
+    return (hn.astype(_ACC[accum]) @ wl.T.astype(_ACC[accum], copy=False)).astype(np.float32)

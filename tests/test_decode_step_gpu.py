@@ -252,38 +252,70 @@ def _topk_agrees(got, ref, k, err):
     return all(abs(ref[i] - kth) <= err for i in g ^ r)
 
 
-@pytest.mark.parametrize("B,check", [(1, (0,)), (16, (0, 7, 15))])
-def test_full_shape_step_vs_oracle(hip, full_model, B, check):
-    """Config 4: the 28-layer Qwen2.5-1.5B-shaped step with a 2048-token fp16 KV
-    prefix, as one hipGraph at batch 1 (fused mat-vec kernels) and batch 16
-    (MFMA kernels), against oracle.decode_step on the same caches (weights
-    dequantised per layer on the host, not cached): logits within rel-L2 5e-3
-    and the top-40 sets equal up to ties inside the measured error."""
-    cfg = full_model.cfg
+class _Truncated:
+    """The first ``n`` layers of a model (same weights, same tensors)."""
+
+    def __init__(self, model, n):
+        self.cfg = model.cfg.with_(n_layers=n)
+        self.layers = model.layers[:n]
+        self.token_embd, self.output_norm = model.token_embd, model.output_norm
+
+    def weight_bytes(self):
+        return int(sum(lw[p].nbytes for lw in self.layers for p in ("q", "k", "v", "o", "gate", "up", "down"))
+                   + self.token_embd.nbytes)
+
+
+# Step-level bound, self-calibrated: the oracle is run twice, summing in fp32 (as
+# the reference kernels) and in float64, both rounding to fp16 at the same
+# nodes.  Their distance is the drift between two correct implementations that
+# differ only in summation order (measured 4.1e-3 rel-L2 on the logits after 28
+# layers: fp16 rounding flips compound layer by layer), so no correct kernel
+# can be held much tighter than it.  The GPU must stay within FLOOR_FACTOR times
+# that drift.
+FLOOR_FACTOR = 3.5
+
+
+@pytest.mark.parametrize("n_layers,B,check", [(2, 1, (0,)), (2, 16, (0, 7, 15)), (28, 1, (0,)),
+                                              (28, 16, (0, 7, 15))])
+def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check):
+    """Config 4: the Qwen2.5-1.5B-shaped step (all widths; the first 2 or all 28
+    layers) with a 2048-token fp16 KV prefix, as one hipGraph at batch 1 (fused
+    mat-vec kernels) and batch 16 (MFMA kernels), against oracle.decode_step on
+    the same caches (weights dequantised per layer on the host, not cached):
+    logits within FLOOR_FACTOR x the fp32/f64 oracle drift, the top-40 sets
+    equal up to ties inside the measured error, appended K rows within 5e-3."""
+    model = _Truncated(full_model, n_layers)
+    cfg = model.cfg
     max_seq = 2304
     rng = np.random.default_rng(100 + B)
     toks = rng.integers(0, cfg.vocab, B)
     pos = np.full(B, 2048)
-    ex = HIPGraphExecutor(hip, full_model, batch_size=B, max_seq=max_seq, top_k=40)
+    chk = list(check)
+    ex = HIPGraphExecutor(hip, model, batch_size=B, max_seq=max_seq, top_k=40)
     try:
         ex.fill_kv_prefix(seed=11)
-        ks = [ex.k_cache[L].numpy()[list(check)] for L in range(cfg.n_layers)]
-        vs = [ex.v_cache[L].numpy()[list(check)] for L in range(cfg.n_layers)]
+        ks = [ex.k_cache[L].numpy()[chk] for L in range(cfg.n_layers)]
+        vs = [ex.v_cache[L].numpy()[chk] for L in range(cfg.n_layers)]
         ex.execute_decode_batch(list(toks), list(pos))
         got = ex.read_logits()
         _, idx = ex.read_topk()
-        kg = [ex.k_cache[L].numpy()[list(check)] for L in (0, cfg.n_layers - 1)]
+        last = cfg.n_layers - 1
+        kg = [ex.k_cache[L].numpy()[chk] for L in (0, last)]
     finally:
         ex.close()
-    print(f"oracle step B={B} sequences {check}", flush=True)
-    ref = ost.decode_step(full_model, toks[list(check)], pos[list(check)], ks, vs)
+    print(f"oracle step layers={n_layers} B={B} sequences {check}", flush=True)
+    ref = ost.decode_step(model, toks[chk], pos[chk], ks, vs)
+    ref64 = ost.decode_step(model, toks[chk], pos[chk], [k.copy() for k in ks], [v.copy() for v in vs],
+                            accum="f64")
     for i, b in enumerate(check):
-        r = rel_l2(got[b], ref[i])
-        assert r <= TOL, (b, r)
+        r, floor = rel_l2(got[b], ref[i]), rel_l2(ref64[i], ref[i])
+        print(f"  seq {b}: GPU vs oracle {r:.3e}, oracle f32 vs f64 drift {floor:.3e}", flush=True)
+        assert r <= FLOOR_FACTOR * floor, (b, r, floor)
         err = 4 * float(np.abs(got[b] - ref[i]).max())
         assert _topk_agrees(got[b], ref[i], 40, err), b
-        assert set(idx[b].tolist()) == set(np.argsort(-got[b], kind="stable")[:40].tolist())
-        for j, L in enumerate((0, cfg.n_layers - 1)):        # appended K rows of the first and last layer
+        order = np.lexsort((np.arange(cfg.vocab), -got[b]))[:40]
+        assert np.array_equal(idx[b], order)
+        for j, L in enumerate((0, last)):        # appended K rows of the first and last layer
             assert rel_l2(kg[j][i, 2048], ks[L][i, 2048]) <= TOL, (b, L)
 
 
@@ -294,7 +326,8 @@ def test_prefill_vs_oracle(hip, request, shape, n, chunk):
     """A prompt prefilled in chunks into sequence 1 of a 2-sequence executor
     against oracle.step.prefill (the token-by-token decode of the reference,
     vte/core/model.py:969-973, computed layer by layer) on the same cache: the
-    next-token logits within rel-L2 5e-3 and every written K/V row within 5e-3.
+    next-token logits and every layer's written K/V rows within FLOOR_FACTOR x
+    the oracle's fp32/f64 drift (at least 1e-3).
     Widths 33, 36 and 63 are tails that run padded at 64 columns; 600 tokens
     at chunk 512 run the default chunk (weight-stationary launches with
     several column groups) plus an 88-token tail."""
@@ -319,9 +352,53 @@ def test_prefill_vs_oracle(hip, request, shape, n, chunk):
         runner.close()
         ex.close()
     print(f"oracle prefill {shape} n={n}", flush=True)
+    k64, v64 = [k.copy() for k in kh], [v.copy() for v in vh]
     ref = ost.prefill(model, prompt, start, kh, vh)[-1]
-    assert rel_l2(got, ref) <= TOL, rel_l2(got, ref)
+    ref64 = ost.prefill(model, prompt, start, k64, v64, accum="f64")[-1]
+    r, floor = rel_l2(got, ref), rel_l2(ref64, ref)
+    print(f"  logits: GPU vs oracle {r:.3e}, oracle f32 vs f64 drift {floor:.3e}", flush=True)
+    assert r <= max(FLOOR_FACTOR * floor, 1e-3), (r, floor)
     rows = slice(start, start + n)
     for L in range(cfg.n_layers):
-        assert rel_l2(kg[L][rows], kh[L][rows]) <= TOL, L
-        assert rel_l2(vg[L][rows], vh[L][rows]) <= TOL, L
+        for g_, o_, o64 in ((kg, kh, k64), (vg, vh, v64)):
+            r, floor = rel_l2(g_[L][rows], o_[L][rows]), rel_l2(o64[L][rows], o_[L][rows])
+            assert r <= max(FLOOR_FACTOR * floor, 1e-3), (L, r, floor)
+
+
+def test_repetition_window_candidates_reproduce_full_row_sampling(hip, tiny_model):
+    """The step's top-k with a staged repetition window (512-token history,
+    penalty 1.1): sampling from the k candidates plus the gathered window
+    logits gives the token Sampler.sample draws from the full logits row
+    (same NumPy seed, 0 < top_p < 1), and the greedy pick its argmax."""
+    from vte_amd.core.sampler import Sampler
+    B = 3
+    cfg = tiny_model.cfg
+    ex = HIPGraphExecutor(hip, tiny_model, batch_size=B, max_seq=128, top_k=40)
+    rng = np.random.default_rng(21)
+    try:
+        ex.fill_kv_prefix(seed=3)
+        hist = [list(rng.integers(0, cfg.vocab, 600)) for _ in range(B)]
+        toks, pos = [5, 77, 901], [40, 60, 80]
+        ex.execute_decode_batch(toks, pos)
+        full = ex.read_logits()
+        for b in range(B):                 # put each row's 10 best tokens into its window
+            hist[b] += list(np.argsort(-full[b])[:10])
+        win = [Sampler.compute_repetition_ids(h, cfg.vocab) for h in hist]
+        ex.set_repetition_window([w[0] for w in win])
+        ex.execute_decode_batch(toks, pos)
+        vals, idx, gath = ex.read_candidates()
+        assert np.array_equal(ex.read_logits(), full)
+        for b in range(B):
+            ids, counts = win[b]
+            for seed in range(5):
+                np.random.seed(seed)
+                want = Sampler.sample(full[b], temperature=0.8, top_p=0.9, top_k=40, repetition_penalty=1.1,
+                                      generated_tokens=hist[b])
+                np.random.seed(seed)
+                got = Sampler.sample_candidates(vals[b], idx[b], 0.8, 0.9, top_k=40, repetition_penalty=1.1,
+                                                unique_ids=ids, counts=counts, gathered=gath[b])
+                assert got == want, (b, seed)
+            want = Sampler.sample(full[b], temperature=0.0, repetition_penalty=1.1, generated_tokens=hist[b])
+            assert Sampler.pick_greedy_from_gpu_candidates(vals[b], idx[b], gath[b], ids, counts, 1.1) == want
+    finally:
+        ex.close()

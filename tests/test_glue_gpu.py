@@ -89,6 +89,43 @@ def test_topk_exact(hip, K, k, vocab):
         assert np.array_equal(gv[r], logits[r, order])
 
 
+@pytest.mark.parametrize("k,vocab,n_ex", [(40, 151936, 512), (64, 151936, 300), (40, 151936, 0), (8, 1000, 512),
+                                          (40, 4096, 1)])
+def test_topk_exclude_exact(hip, K, k, vocab, n_ex):
+    """Top-k over the tokens outside each row's exclusion list (value desc,
+    index asc) and the exact logits of the excluded tokens.  Row 1 excludes
+    the row's best tokens, row 2 has ties straddling excluded entries, row 3
+    excludes nothing (count 0)."""
+    rng = np.random.default_rng(9 + n_ex)
+    rows, max_ex = 4, 512
+    logits = rng.standard_normal((rows, vocab)).astype(np.float32)
+    logits[2, :] = rng.integers(0, 6, vocab)
+    ids = np.zeros((rows, max_ex), np.int32)
+    cnt = np.zeros(rows, np.int32)
+    for r in range(rows):
+        n = 0 if r == 3 else n_ex
+        if r == 1 and n:
+            sel = np.argsort(-logits[r], kind="stable")[:n]          # the best tokens themselves
+        else:
+            sel = rng.choice(vocab, n, replace=False)
+        sel = np.sort(sel)
+        ids[r, :n], cnt[r] = sel, n
+    vals, idx = empty(hip, (rows, k), np.float32), empty(hip, (rows, k), np.int32)
+    gath = up(hip, np.full((rows, max_ex), np.nan, np.float32))
+    scratch = empty(hip, K.topk_scratch_bytes(rows), np.uint8)
+    K.topk(up(hip, logits), rows, vocab, k, vals, idx, scratch, stream=hip.stream,
+           exclude=(up(hip, ids), up(hip, cnt), max_ex, gath))
+    gv, gi, gg = down(vals), down(idx), down(gath)
+    for r in range(rows):
+        keep = np.ones(vocab, bool)
+        keep[ids[r, :cnt[r]]] = False
+        cand = np.nonzero(keep)[0]
+        order = cand[np.lexsort((cand, -logits[r, cand]))][:k]
+        assert np.array_equal(gi[r], order), r
+        assert np.array_equal(gv[r], logits[r, order]), r
+        assert np.array_equal(gg[r, :cnt[r]], logits[r, ids[r, :cnt[r]]]), r
+
+
 @pytest.mark.parametrize("rows,H,n_parts,inplace", [(16, 1536, 4, False), (8, 1536, 1, True), (40, 1536, 8, False),
                                                     (3, 8192, 2, False), (5, 24, 3, True)])
 def test_add_rmsnorm(hip, K, rows, H, n_parts, inplace):

@@ -49,3 +49,60 @@ def test_sampler_draws_match_reference():
         assert got == int(g["chosen"][i]), (i, got, int(g["chosen"][i]))
     ids, counts = Sampler.compute_repetition_ids(list(g["hist"][0]), g["logits"].shape[1], ignore)
     assert np.array_equal(ids, g["rep_ids"]) and np.array_equal(counts, g["rep_counts"])
+
+
+def _gpu_candidates(row, ids, k):
+    """What vte_topk_exclude returns for one row: the k best non-window tokens
+    (value desc, index asc) and the window tokens' exact logits."""
+    keep = np.ones(row.size, bool)
+    keep[ids] = False
+    cand = np.nonzero(keep)[0]
+    order = cand[np.lexsort((cand, -row[cand]))][:k]
+    return row[order], order, row[ids]
+
+
+def test_candidate_sampling_matches_reference_draws():
+    """The reference's own draws (tests/golden/sampler.npz, Sampler.sample over
+    full 1000-token rows with a 700-token history, penalties 1.0-1.5) are
+    reproduced from k = 64 on-device candidates plus the gathered window:
+    every case with 0 < top_p < 1 and 0 < top_k <= 64 gives the same token for
+    the same NumPy seed, and every greedy case the same argmax."""
+    g = _npz("sampler.npz")
+    ignore = set(int(v) for v in g["ignore_every_third"])
+    checked = 0
+    for i, (t, p, k, rp) in enumerate(g["params"]):
+        row = g["logits"][i].astype(np.float32)
+        ids, counts = Sampler.compute_repetition_ids(list(g["hist"][i]), row.size,
+                                                     ignore if i % 3 == 0 else None)
+        vals, idx, gathered = _gpu_candidates(row, ids, 64)
+        if t <= 0.0:
+            got = Sampler.pick_greedy_from_gpu_candidates(vals, idx, gathered, ids, counts, float(rp))
+        elif 0.0 < p < 1.0 and 0 < k <= 64:
+            np.random.seed(int(g["np_seeds"][i]))
+            got = Sampler.sample_candidates(vals, idx, float(t), float(p), top_k=int(k),
+                                            repetition_penalty=float(rp), unique_ids=ids, counts=counts,
+                                            gathered=gathered)
+        else:
+            continue
+        assert got == int(g["chosen"][i]), (i, got, int(g["chosen"][i]))
+        checked += 1
+    assert checked == 8
+
+
+def test_greedy_candidates_tie_break_by_lowest_index():
+    """fp16-rounded logits tie often (sampler.py:190-205): a tie between a
+    window token after the penalty and a non-window candidate goes to the
+    lower index, as np.argmax over the full penalised row."""
+    row = np.zeros(300, np.float32)
+    row[[7, 40, 200]] = [2.0, 2.2, 2.0]
+    ids, counts = np.array([40]), np.array([1.0])
+    vals, idx, gathered = _gpu_candidates(row, ids, 8)
+    full = Sampler.sample(row, temperature=0.0, repetition_penalty=1.1, generated_tokens=[40])
+    got = Sampler.pick_greedy_from_gpu_candidates(vals, idx, gathered, ids, counts, 1.1)
+    assert got == full == 7
+    row[40] = 2.2                                     # 2.2 / 1.1 == 2.0 in fp32
+    assert np.float32(np.float32(2.2) / 1.1) == np.float32(2.0)
+    row[7] = np.float32(np.float32(2.2) / 1.1)
+    vals, idx, gathered = _gpu_candidates(row, ids, 8)
+    assert Sampler.pick_greedy_from_gpu_candidates(vals, idx, gathered, ids, counts, 1.1) == \
+        Sampler.sample(row, temperature=0.0, repetition_penalty=1.1, generated_tokens=[40])

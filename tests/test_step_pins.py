@@ -83,8 +83,8 @@ def _mutants():
     def no_rope_on_q(x, pos, c, s_):
         return x if x.shape[0] == PIN.n_q else orig_rope(x, pos, c, s_)
 
-    def no_residual(w, x, bias=None, residual=None):
-        return orig_lin(w, x, bias)
+    def no_residual(w, x, bias=None, residual=None, accum="f32"):
+        return orig_lin(w, x, bias, accum=accum)
 
     state = {}
 

@@ -32,7 +32,7 @@ from ..bridge.memory import DeviceArray, MemoryRegion, SlabAllocator
 from ..kernels import kernels
 from .model_config import Qwen2Config
 from .rope_cache import build_rope_cache
-from .split_kv_attention import SplitKVAttentionDispatcher
+from .split_kv_attention import SplitKVAttentionDispatcher, choose_split
 from .weights import PROJ, SyntheticQwen2, proj_shape
 
 
@@ -41,6 +41,7 @@ class GraphCaptureError(RuntimeError):
 
 
 MAX_SPLITK = 8  # split-K partial buffers of the batched o-proj / down projections
+MAX_EXCLUDE = 512  # repetition-window tokens excluded from the top-k and gathered (sampler.py REPETITION_WINDOW)
 
 
 def splitk_splits(K: int) -> int:
@@ -61,6 +62,8 @@ class HIPGraphExecutor:
         with activation buffers of ``batch_size`` columns and only the last
         column's logits (the prefill of ``PrefillRunner``)."""
         self.hip = hip
+        self.closed = False
+        self._dependents = []  # objects holding pointers into this executor's slab (closed with it)
         self.prefill_of = shared
         self.cfg: Qwen2Config = model.cfg
         cfg = self.cfg
@@ -88,12 +91,19 @@ class HIPGraphExecutor:
             if not 0 <= kv_seq < shared.B:
                 raise HIPSafetyError(f"kv_seq {kv_seq} outside the shared executor's batch of {shared.B}")
         kv_elems = 0 if shared is not None else B * self.max_seq * cfg.n_kv * cfg.head_dim
-        act_bytes = 4 * (B * (2 * H + cfg.q_dim * 2 + cfg.kv_dim * 2 + 3 * cfg.ffn) * 2 + B * cfg.vocab * 4)
+        out_rows = 1 if shared is not None else B  # prefill: only the last column's logits
+        # activations (fp16) with 4x headroom, logits + top-k/exclusion buffers of the output rows,
+        # split-K partials
+        act_bytes = 4 * B * (2 * H + cfg.q_dim * 2 + cfg.kv_dim * 2 + 3 * cfg.ffn) * 2
+        act_bytes += out_rows * (cfg.vocab * 4 + MAX_EXCLUDE * 8 + 1024) + 2 * self._topk_scratch_estimate(out_rows)
         act_bytes += MAX_SPLITK * B * H * 4
         need = (0 if shared is not None else model.weight_bytes()) + 2 * cfg.n_layers * kv_elems * 2 + act_bytes + \
             (64 << 20)
         need += (cfg.n_layers * len(PROJ) + 16) * 1024  # alignment and slack per tensor
-        self.slab = SlabAllocator(hip, 0, requested_pool_size=need + (256 << 20))
+        # split-KV scratch: [B][n_q][splits] stats and [B][n_q][splits][hd] partial outputs
+        sp = split or choose_split(self.max_seq, B, cfg.n_kv, 256)
+        need += B * cfg.n_q * (-(-self.max_seq // sp) + 1) * (cfg.head_dim + 2) * 4 + B * cfg.n_kv * 4
+        self.slab = SlabAllocator(hip, 0, requested_pool_size=need + (32 << 20))
         self.slab.initialize()
         A = lambda shape, dt, tag, reg=MemoryRegion.ACTIVATIONS: DeviceArray(hip, shape, dt, tag, self.slab, reg)
         W = lambda arr, tag: DeviceArray.from_numpy(hip, arr, tag, self.slab, MemoryRegion.WEIGHTS)
@@ -113,11 +123,19 @@ class HIPGraphExecutor:
         self.u = A((B, cfg.ffn), np.float16, "up")
         self.a = A((B, cfg.ffn), np.float16, "swiglu")
         self.part = A((MAX_SPLITK, B, H), np.float32, "splitk_partials")
-        self.out_rows = 1 if shared is not None else B  # prefill: only the last column's logits
+        self.out_rows = out_rows
         self.logits = A((self.out_rows, cfg.vocab), np.float32, "logits")
         self.topk_val = A((self.out_rows, max(top_k, 1)), np.float32, "topk_val")
         self.topk_idx = A((self.out_rows, max(top_k, 1)), np.int32, "topk_idx")
         self.topk_scratch = A(self.K.topk_scratch_bytes(self.out_rows), np.uint8, "topk_scratch")
+        # repetition window per output row (sorted ids, count): the top-k skips
+        # these tokens and gathers their exact logits, so the sampler can apply
+        # the repetition penalty to k + window candidates instead of the full
+        # row (topk_reduce_greedy.hip.template:40-83, topk_logits_reducer.py:79-125)
+        self.excl_ids = A((self.out_rows, MAX_EXCLUDE), np.int32, "topk_exclude_ids")
+        self.excl_cnt = A(self.out_rows, np.int32, "topk_exclude_count")
+        self.excl_gathered = A((self.out_rows, MAX_EXCLUDE), np.float32, "topk_exclude_gathered")
+        self.excl_cnt.zero()
         self.staging_input = A(B, np.int32, "staging_tokens")
         self.staging_kv_offset = A(B, np.int32, "staging_kv_offset")
         if shared is None:
@@ -221,7 +239,8 @@ class HIPGraphExecutor:
             K.norm_gemv(self.h[cur], self.output_norm, cfg.eps, self.lm_head, self.lm_head_fmt, self.logits, B, H,
                         cfg.vocab, out_dtype="f32", stream=st)
         if self.top_k > 0 and on("topk"):
-            K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st)
+            K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch, stream=st,
+                   exclude=self._exclude())
 
     def class_algorithmic_bytes(self) -> dict:
         """Algorithmic HBM bytes of one step per launch class of the fused path
@@ -312,7 +331,39 @@ class HIPGraphExecutor:
             self._linear(self.lm_head_fmt, self.xn, self.lm_head, self.logits, H, cfg.vocab, out_dtype="f32")
         if self.top_k > 0:
             K.topk(self.logits, self.out_rows, cfg.vocab, self.top_k, self.topk_val, self.topk_idx,
-                   self.topk_scratch, stream=st)
+                   self.topk_scratch, stream=st, exclude=self._exclude())
+
+    def _topk_scratch_estimate(self, rows: int) -> int:
+        return int(self.K.topk_scratch_bytes(rows))
+
+    def _exclude(self):
+        """Exclusion buffers for the top-k when the vocabulary leaves room for them."""
+        if self.cfg.vocab - MAX_EXCLUDE < self.top_k:
+            return None
+        return (self.excl_ids, self.excl_cnt, MAX_EXCLUDE, self.excl_gathered)
+
+    def set_repetition_window(self, unique_ids: Sequence[Sequence[int]]) -> None:
+        """Stage each output row's repetition window (sorted unique token ids,
+        at most 512, as Sampler.compute_repetition_ids returns them) for the
+        next replay: the top-k then leaves them out and gathers their logits
+        (``read_candidates``).  TopKLogitsReducer.upload_exclude
+        (vte/core/topk_logits_reducer.py:79-110) stages the same buffers."""
+        if len(unique_ids) != self.out_rows:
+            raise HIPSafetyError(f"expected {self.out_rows} windows, got {len(unique_ids)}")
+        if self._exclude() is None:
+            raise HIPSafetyError("vocabulary too small for the exclusion list")
+        ids = np.zeros((self.out_rows, MAX_EXCLUDE), np.int32)
+        cnt = np.zeros(self.out_rows, np.int32)
+        for r, u in enumerate(unique_ids):
+            u = np.asarray(u, np.int64)
+            if u.size > MAX_EXCLUDE:
+                raise HIPSafetyError(f"exclusion list of {u.size} exceeds {MAX_EXCLUDE}")
+            if u.size and (u.min() < 0 or u.max() >= self.cfg.vocab or np.any(np.diff(u) <= 0)):
+                raise HIPSafetyError("exclusion ids must be sorted, unique and inside the vocabulary")
+            ids[r, :u.size] = u
+            cnt[r] = u.size
+        self.excl_ids.upload(ids)
+        self.excl_cnt.upload(cnt)
 
     def _proj_add_norm(self, fmt, x, w, K_in, cur, norm_w) -> None:
         """h[1-cur] = h[cur] + W x (split-K partials), xn = RMSNorm(h[1-cur]) * norm_w."""
@@ -394,6 +445,14 @@ class HIPGraphExecutor:
         self.hip.safe_memcpy_device_to_host(i, ctypes.c_void_p(self.topk_idx.ptr), "sampler_topk_idx")
         return v, i
 
+    def read_candidates(self) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """(top-k values, top-k indices, gathered logits of the staged
+        repetition windows) of the last replay, per output row."""
+        v, i = self.read_topk()
+        g = np.empty((self.out_rows, MAX_EXCLUDE), np.float32)
+        self.hip.safe_memcpy_device_to_host(g, ctypes.c_void_p(self.excl_gathered.ptr), "sampler_gathered")
+        return v, i, g
+
     def fill_kv_prefix(self, seed: int = 0, scale: float = 0.5) -> None:
         """Fill every KV cache with scale * N(0,1) fp16 on the device (synthetic prefix)."""
         if self.prefill_of is not None:
@@ -411,6 +470,11 @@ class HIPGraphExecutor:
         self.v_cache[layer].upload(v)
 
     def close(self) -> None:
+        # executors and runners that hold pointers into this slab go first
+        for dep in list(getattr(self, "_dependents", [])):
+            dep.close()
+        self._dependents = []
+        self.closed = True
         if self.graph_exec is not None:
             self.hip.graph_exec_destroy(self.graph_exec)
             self.hip.graph_destroy(self.graph)

@@ -36,6 +36,9 @@ class PrefillRunner:
         self.ex = ex
         self.chunk = chunk
         self._subs: dict[tuple[int, int], HIPGraphExecutor] = {}
+        deps = getattr(ex, "_dependents", None)
+        if deps is not None:
+            deps.append(self)  # closing the owner closes these executors first
 
     def _width(self, n: int) -> int:
         """Batch width for a chunk of n <= chunk tokens."""
@@ -58,6 +61,8 @@ class PrefillRunner:
         of sequence ``seq`` and compute the logits (and top-k) that follow the
         last token.  Returns the executor holding them (``read_logits`` /
         ``read_topk`` give one row)."""
+        if getattr(self.ex, "closed", False):
+            raise HIPSafetyError("prefill: the owning executor has been closed")
         n = len(tokens)
         if n < 1:
             raise HIPSafetyError("prefill needs at least one token")
@@ -80,3 +85,6 @@ class PrefillRunner:
         for sub in self._subs.values():
             sub.close()
         self._subs.clear()
+        deps = getattr(self.ex, "_dependents", None)
+        if deps is not None and self in deps:
+            deps.remove(self)

@@ -43,7 +43,7 @@ hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_
                          hipStream_t st);
 size_t topk_scratch_bytes(int rows);
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
-                hipStream_t st);
+                hipStream_t st, const int* excl_ids, const int* excl_cnt, int max_excl, float* gathered);
 hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, hipStream_t st);
 hipError_t attn_in(const void* x, const void* norm_w, float eps, const void* wq, const void* q_bias, int fmt_q,
                    const void* wk, const void* k_bias, int fmt_k, const void* wv, const void* v_bias, int fmt_v,
@@ -266,8 +266,23 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
     REQUIRE(rows <= 65535, "topk: rows %d out of range", rows);
     REQUIRE(vocab <= 262144, "topk: vocab %d above 262144", vocab);
     REQUIRE(aligned(scratch, 8), "topk: scratch must be 8-byte aligned");
-    return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream),
+    return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream, nullptr,
+                                nullptr, 0, nullptr),
                       "vte_topk launch");
+}
+
+int vte_topk_exclude(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
+                     const int* excl_ids, const int* excl_cnt, int max_excl, float* gathered, void* stream) {
+    REQUIRE(logits && out_val && out_idx && scratch && excl_ids && excl_cnt && gathered, "topk_exclude: null pointer");
+    REQUIRE(rows >= 1 && k >= 1 && k <= 64 && vocab >= k, "topk_exclude: need 1 <= k <= min(64, vocab)");
+    REQUIRE(rows <= 65535, "topk_exclude: rows %d out of range", rows);
+    REQUIRE(vocab <= 262144, "topk_exclude: vocab %d above 262144", vocab);
+    REQUIRE(max_excl >= 1 && max_excl <= 4096, "topk_exclude: max_excl %d outside 1..4096", max_excl);
+    REQUIRE(vocab - max_excl >= k, "topk_exclude: vocab %d leaves fewer than k outside %d exclusions", vocab, max_excl);
+    REQUIRE(aligned(scratch, 8), "topk_exclude: scratch must be 8-byte aligned");
+    return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream, excl_ids,
+                                excl_cnt, max_excl, gathered),
+                      "vte_topk_exclude launch");
 }
 
 int vte_attn_in(const void* x, const void* norm_w, float eps, const void* wq, const void* q_bias, int fmt_q,

@@ -465,14 +465,30 @@ __device__ __forceinline__ uint32_t tk_block_threshold(uint32_t tm, int kth, uin
 
 #define TKR (TOPK_SLICE / TOPK_THREADS)  // slice entries per thread
 
+// Exclusion list of a row (sorted token ids, the repetition window of the
+// sampler): ids [rows][max_excl], counts [rows] in device memory so a captured
+// graph reads the values staged before each replay.  Excluded entries take key
+// 0 (below every finite and infinite logit) in the selection, and the block
+// whose slice holds an excluded id writes that id's exact logit to
+// gathered[row][i] (topk_reduce_greedy.hip.template:52-83 does the same for its
+// per-thread maxima: the penalty only lowers logits, so the best tokens after
+// it are the best non-excluded ones or excluded ones at their exact values).
+struct TkExclude {
+    const int* ids;
+    const int* cnt;   // null: no exclusion
+    int max_excl;
+    float* gathered;
+};
+
 __global__ __launch_bounds__(TOPK_THREADS) void topk_partial_kernel(const float* __restrict__ logits, int vocab,
                                                                       int slice, int k,
                                                                       uint64_t* __restrict__ cand,
-                                                                      int* __restrict__ cand_cnt) {
+                                                                      int* __restrict__ cand_cnt, TkExclude ex) {
     __shared__ uint32_t keys[TOPK_SLICE];
     __shared__ int pos[64];
     __shared__ TkShared sh;
     __shared__ uint32_t wt[TOPK_THREADS / 64];
+    __shared__ uint32_t xmask[TOPK_SLICE / 32];
     const int row = blockIdx.y, p = blockIdx.x, tid = threadIdx.x;
     TK_TS(0, 0);
     const int lo = p * slice, n = max(0, min(slice, vocab - lo));
@@ -485,11 +501,27 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_partial_kernel(const float*
         const int i = j * TOPK_THREADS + tid;
         v[j] = r[i < n ? i : 0];
     }
+    const int n_ex = ex.cnt != nullptr ? min(ex.cnt[row], ex.max_excl) : 0;
+    if (n_ex > 0) {  // uniform per block: mark the slice's excluded entries, gather their logits
+        for (int w = tid; w < TOPK_SLICE / 32; w += TOPK_THREADS) xmask[w] = 0u;
+        __syncthreads();
+        const int* ids = ex.ids + (size_t)row * ex.max_excl;
+        for (int i = tid; i < n_ex; i += TOPK_THREADS) {
+            const int id = ids[i];
+            if (id >= lo && id < lo + n) {
+                atomicOr(&xmask[(id - lo) >> 5], 1u << ((id - lo) & 31));
+                ex.gathered[(size_t)row * ex.max_excl + i] = r[id - lo];
+            }
+        }
+        __syncthreads();
+    }
     uint32_t tm = 0;
 #pragma unroll
     for (int j = 0; j < TKR; ++j) {
-        const bool ok = j * TOPK_THREADS + tid < n;
-        kr[j] = ok ? tk_key(v[j]) : 0u;
+        const int i = j * TOPK_THREADS + tid;
+        const bool xd = n_ex > 0 && ((xmask[i >> 5] >> (i & 31)) & 1u);
+        const bool ok = i < n;
+        kr[j] = ok && !xd ? tk_key(v[j]) : 0u;
         tm = ok ? max(tm, kr[j]) : tm;
     }
     TK_TS(0, 1);
@@ -757,7 +789,7 @@ hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_
 size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_P * (TOPK_CAP * 8 + 4); }
 
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
-                hipStream_t st) {
+                hipStream_t st, const int* excl_ids, const int* excl_cnt, int max_excl, float* gathered) {
     if (vocab > TOPK_P * TOPK_SLICE) return hipErrorInvalidValue;
     // as many slices as needed, each at most TOPK_SLICE, at most TOPK_P of them
     int P = (vocab + 2047) / 2048;
@@ -765,8 +797,9 @@ hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val,
     const int slice = (vocab + P - 1) / P;
     uint64_t* cand = (uint64_t*)scratch;
     int* cc = (int*)((char*)scratch + (size_t)rows * TOPK_P * TOPK_CAP * 8);
+    const TkExclude ex{excl_ids, excl_cnt, max_excl, gathered};
     hipLaunchKernelGGL(topk_partial_kernel, dim3(P, rows), dim3(TOPK_THREADS), 0, st, logits, vocab, slice, k, cand,
-                       cc);
+                       cc, ex);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(TOPK_THREADS), 0, st, cand, cc, P, k, out_val, out_idx);

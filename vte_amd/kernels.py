@@ -41,6 +41,7 @@ SIGNATURES = {
     "vte_embedding_q6k": [_vp, _vp, _vp, _i, _i, _f, _vp],
     "vte_topk_scratch_bytes": [_i],
     "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
+    "vte_topk_exclude": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp],
     "vte_fill_normal_f16": [_vp, _ll, ctypes.c_ulonglong, _f, _vp],
     "vte_attn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp,
                     _i, _i, _i, _i, _i, _vp],
@@ -155,10 +156,18 @@ class VTEKernels:
     def topk_scratch_bytes(self, rows: int) -> int:
         return int(self.lib.vte_topk_scratch_bytes(rows))
 
-    def topk(self, logits, rows, vocab, k, out_val, out_idx, scratch, stream=None):
-        """Top-k (k <= 64) per row, (value desc, index asc); scratch of topk_scratch_bytes(rows)."""
-        self._check(self.lib.vte_topk(_p(logits), rows, vocab, k, _p(out_val), _p(out_idx), _p(scratch),
-                                      self._st(stream)), "vte_topk")
+    def topk(self, logits, rows, vocab, k, out_val, out_idx, scratch, stream=None, exclude=None):
+        """Top-k (k <= 64) per row, (value desc, index asc); scratch of topk_scratch_bytes(rows).
+        ``exclude``: (ids [rows][max_excl], counts [rows], max_excl, gathered [rows][max_excl])
+        device buffers: top-k over the non-excluded tokens plus the excluded tokens' logits."""
+        if exclude is None:
+            self._check(self.lib.vte_topk(_p(logits), rows, vocab, k, _p(out_val), _p(out_idx), _p(scratch),
+                                          self._st(stream)), "vte_topk")
+            return
+        ids, cnt, max_excl, gathered = exclude
+        self._check(self.lib.vte_topk_exclude(_p(logits), rows, vocab, k, _p(out_val), _p(out_idx), _p(scratch),
+                                              _p(ids), _p(cnt), max_excl, _p(gathered), self._st(stream)),
+                    "vte_topk_exclude")
 
     def attn_in(self, x, norm_w, eps, wq, q_bias, fmt_q, wk, k_bias, fmt_k, wv, v_bias, fmt_v, q_out, k_cache,
                 v_cache, kv_offset, kv_batch_stride, rope_cos, rope_sin, batch, hidden, n_q, n_kv, head_dim=128,
