@@ -322,6 +322,43 @@ def profile_step(B, steps, prefix=2048, classes=None):
     hip.cleanup()
 
 
+GEMV_CONFIGS = [("q4_k", 8960, 1536, 0), ("q6_k", 1536, 8960, 0), ("q6_k", 151936, 1536, 0),
+                ("q8_0", 2048, 2048, 0), ("q4_k", 8960, 1536, 16)]
+
+
+def gemv_configs(hip, K, launches=200):
+    """Quant-GEMV configs 0/1 and the batch-16 MFMA GEMM (config 3a), cold pools."""
+    out = []
+    for fmt, n, k, mb in GEMV_CONFIGS:
+        big = n * k > 50_000_000
+        out.append(gemv_bench(hip, K, fmt, n, k, launches=50 if big else launches,
+                              pool_bytes=(600 << 20) if big else (768 << 20), mfma_batch=mb))
+    return out
+
+
+def profile_configs():
+    """rocprofv3 workload: calibration copy, GEMV configs, attention configs."""
+    from vte_amd.bridge import DeviceArray, HIPRuntime
+    from vte_amd.kernels import kernels
+    hip = HIPRuntime()
+    if not hip.initialize():
+        raise SystemExit("HIP initialisation failed")
+    a = DeviceArray(hip, 256 << 20, np.uint8, "calib_src")
+    b = DeviceArray(hip, 256 << 20, np.uint8, "calib_dst")
+    a.zero()
+    hip.synchronize()
+    hip.memcpy_device_to_device(b.ptr, a.ptr, 256 << 20)
+    hip.synchronize()
+    a.free()
+    b.free()
+    K = kernels()
+    for r in gemv_configs(hip, K, launches=100):
+        print("profile-gemv:", json.dumps(r), flush=True)
+    for ctx, B in ((512, 1), (4096, 1), (32768, 1), (2049, 1), (2049, 16)):
+        print("profile-attn:", json.dumps(attn_bench(hip, K, ctx, B=B)), flush=True)
+    hip.cleanup()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -334,6 +371,10 @@ def main():
                          "step graph (for rocprofv3 kernel traces and counters)")
     ap.add_argument("--profile-prefill", type=int, default=0, metavar="R",
                     help="profiling run only: R untimed 2048-token prefills (chunks of 512)")
+    ap.add_argument("--profile-gemv", action="store_true",
+                    help="profiling run only: a 256 MiB calibration copy, then the quant-GEMV configs 0/1 "
+                         "(Q4_K 8960x1536, Q6_K 1536x8960 and 151936x1536, Q8_0 2048x2048) and the batch-16 "
+                         "MFMA GEMM over cold rotating pools, and the split-KV attention configs 2/3b")
     ap.add_argument("--profile-classes", default="", metavar="C1,C2",
                     help="with --profile-step: replay only these launch classes (e.g. attn_in,ffn_in,lm_head)")
     args = ap.parse_args()
@@ -341,6 +382,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only (no multi-GPU path is built); "
                                    "--gpus must be 1"}))
         sys.exit(2)
+    if args.profile_gemv:
+        profile_configs()
+        return
     if args.profile_step:
         profile_step(args.profile_step, args.steps,
                      classes=[c for c in args.profile_classes.split(",") if c] or None)
@@ -384,13 +428,7 @@ def main():
                      "step_bytes": step_bytes, "step_GBps": step_bytes / (ms * 1e-3) / 1e9}
         ex.close()
 
-    gemv = []
-    if not args.quick:
-        gemv.append(gemv_bench(hip, K, "q4_k", 8960, 1536))
-        gemv.append(gemv_bench(hip, K, "q6_k", 1536, 8960))
-        gemv.append(gemv_bench(hip, K, "q6_k", 151936, 1536, launches=50, pool_bytes=600 << 20))
-        gemv.append(gemv_bench(hip, K, "q8_0", 2048, 2048))
-        gemv.append(gemv_bench(hip, K, "q4_k", 8960, 1536, mfma_batch=16))
+    gemv = [] if args.quick else gemv_configs(hip, K)
     attn = []
     if not args.quick:
         for ctx in (512, 4096, 32768):

@@ -271,8 +271,9 @@ class _Truncated:
 # differ only in summation order (measured 4.1e-3 rel-L2 on the logits after 28
 # layers: fp16 rounding flips compound layer by layer), so no correct kernel
 # can be held much tighter than it.  The GPU must stay within FLOOR_FACTOR times
-# that drift.
-FLOOR_FACTOR = 3.5
+# that drift (measured: 1.2x on the batch-1 mat-vec path, 1.4-1.8x on the
+# batched MFMA path and prefill, whose fp32 sums run in another order).
+FLOOR_FACTOR = 2.5
 
 
 @pytest.mark.parametrize("n_layers,B,check", [(2, 1, (0,)), (2, 16, (0, 7, 15)), (28, 1, (0,)),
@@ -283,7 +284,8 @@ def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check):
     mat-vec kernels) and batch 16 (MFMA kernels), against oracle.decode_step on
     the same caches (weights dequantised per layer on the host, not cached):
     logits within FLOOR_FACTOR x the fp32/f64 oracle drift, the top-40 sets
-    equal up to ties inside the measured error, appended K rows within 5e-3."""
+    equal up to ties inside the measured error, and the appended K rows of the
+    first and last layer within FLOOR_FACTOR x their own drift (at least 1e-3)."""
     model = _Truncated(full_model, n_layers)
     cfg = model.cfg
     max_seq = 2304
@@ -304,9 +306,9 @@ def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check):
     finally:
         ex.close()
     print(f"oracle step layers={n_layers} B={B} sequences {check}", flush=True)
+    k64 = [k.copy() for k in ks]
     ref = ost.decode_step(model, toks[chk], pos[chk], ks, vs)
-    ref64 = ost.decode_step(model, toks[chk], pos[chk], [k.copy() for k in ks], [v.copy() for v in vs],
-                            accum="f64")
+    ref64 = ost.decode_step(model, toks[chk], pos[chk], k64, [v.copy() for v in vs], accum="f64")
     for i, b in enumerate(check):
         r, floor = rel_l2(got[b], ref[i]), rel_l2(ref64[i], ref[i])
         print(f"  seq {b}: GPU vs oracle {r:.3e}, oracle f32 vs f64 drift {floor:.3e}", flush=True)
@@ -316,7 +318,8 @@ def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check):
         order = np.lexsort((np.arange(cfg.vocab), -got[b]))[:40]
         assert np.array_equal(idx[b], order)
         for j, L in enumerate((0, last)):        # appended K rows of the first and last layer
-            assert rel_l2(kg[j][i, 2048], ks[L][i, 2048]) <= TOL, (b, L)
+            r, floor = rel_l2(kg[j][i, 2048], ks[L][i, 2048]), rel_l2(k64[L][i, 2048], ks[L][i, 2048])
+            assert r <= max(FLOOR_FACTOR * floor, 1e-3), (b, L, r, floor)
 
 
 # ---------------------------------------------------------------- prefill vs the oracle

@@ -78,9 +78,10 @@ static hipError_t fmv_complete(const FmvPlan& plan, int upt, FmvPlan& P) {
     int total = 0;
     for (int s = 0; s < P.nseg; ++s) {
         FmvSeg& S = P.seg[s];
-        if (S.fmt != 4 && S.fmt != 6) return hipErrorInvalidValue;
+        if (S.fmt != 4 && S.fmt != 6 && S.fmt != 8) return hipErrorInvalidValue;
         if (fmv_paired(S.mode) && S.fmt != 4) return hipErrorInvalidValue;
-        S.row_bytes = n_sb * (S.fmt == 4 ? Q4K_BYTES : Q6K_BYTES);
+        if (S.fmt == 8 && P.att_o != nullptr) return hipErrorNotSupported;
+        S.row_bytes = S.fmt == 8 ? (P.K / QK8_0) * Q80_BYTES : n_sb * (S.fmt == 4 ? Q4K_BYTES : Q6K_BYTES);
         S.R = fmv_rows_per_tile(S.mode, P.K, upt);
         if (S.R <= 0 || P.M * S.R > ROWS_THREADS) return hipErrorNotSupported;
         if (S.mode == FMV_SWIGLU) {
@@ -109,6 +110,8 @@ hipError_t fused_mv(const void* x, FmvPlan plan, hipStream_t st) {
     const int att_rows = plan.att_o != nullptr ? 2 * plan.M * plan.att_nq * plan.att_S : 0;
     static int upt_force = -1;  // VTE_FMV_UPT=1|2|4 pins units per thread (tuning)
     if (upt_force < 0) upt_force = env_int("VTE_FMV_UPT", 0);
+    static int wfirst = -2;     // VTE_FMV_WFIRST=0|1 forces the weights-first form off / on (tuning)
+    if (wfirst == -2) wfirst = env_int("VTE_FMV_WFIRST", -1);
     for (int upt : {4, 2, 1}) {
         if (upt_force > 0 && upt != upt_force) continue;
         FmvPlan P;
@@ -118,6 +121,12 @@ hipError_t fused_mv(const void* x, FmvPlan plan, hipStream_t st) {
         if (upt_force <= 0 && upt > 1 && P.total < 2 * fmv_num_cus()) continue;
         const size_t lds = fmv_lds_bytes(NC, P.K, upt, att_rows);
         if (lds + 64 > fmv_max_lds()) continue;
+        // weights first when the launch has many rounds of tiles (measured: Q6_K
+        // LM head 151936 x 1536 46.7 -> 41.6 us; the decode step's launches of
+        // at most a few tiles per CU are faster with the activations first)
+        P.wfirst = wfirst >= 0 ? wfirst : (P.total >= 8 * fmv_num_cus() ? 1 : 0);
+        for (int s = 0; s < P.nseg; ++s)
+            if (P.seg[s].fmt == 8) P.wfirst = 0;  // the weights-first form has no Q8_0 instantiation
         if (P.x_f32) {
             fmv_launch_x32(NC, upt, P.total, lds, st, x, P);
         } else {
@@ -218,8 +227,8 @@ hipError_t attn_out_mv(const float* part_m, const float* part_l, const float* pa
 // launched) when the shape does not fit: rows longer than 256 units (K > 16384).
 hipError_t stream_mv(int fmt, bool in_f32, bool out_f32, const void* x, const void* w, void* y, int M, int K, int N,
                      const void* bias, const void* residual, float rs, hipStream_t st) {
-    if (fmt != 4 && fmt != 6) return hipErrorNotSupported;
-    if (M > 4) return hipErrorNotSupported;
+    if (fmt != 4 && fmt != 6 && fmt != 8) return hipErrorNotSupported;
+    if (M > 4 || K % QK_K != 0) return hipErrorNotSupported;
     FmvPlan P = plan_base(M, K, nullptr, 0.f);
     P.x_f32 = in_f32 ? 1 : 0;
     P.rs = rs;

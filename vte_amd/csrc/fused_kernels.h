@@ -94,6 +94,7 @@ struct FmvPlan {
     const float* att_l;      // [M][att_nq][att_S] denominators
     const float* att_o;      // [M][att_nq][att_S][128] unnormalised outputs
     int att_nq, att_S, att_split;
+    int wfirst;              // launch the weights-first form (fused_mv_kernel WF) when it exists
 };
 
 __host__ __device__ __forceinline__ bool fmv_paired(int mode) {
@@ -196,6 +197,29 @@ __device__ __forceinline__ float q6k_unit_dot_x(const uint4& la4, const uint4& l
         r = fmaf(d * (float)sc, fmaf(-1056.f, X[g], S), r);
     }
     return r;
+}
+
+// Q8_0 unit: two 32-weight blocks (codes qa / qb, fp16 scales in the low /
+// high half of dbits) against the 64 activations x (xperm layout) with
+// per-16 sums s16.  Signed codes become 128 + q by flipping the sign bit, so
+//   sum_i q_i x_i = S - 1152 X,   S = sum (1152 + q_i) x_i (fp16 1024 + (128 + q)),
+// and the unit's value is d_a (S_a - 1152 X_a) + d_b (S_b - 1152 X_b), the
+// reference's w = d * q (vte/compiler/dequantizer.py:172-196) summed in fp32.
+__device__ __forceinline__ float q80_unit_dot_x(const uint4& a0, const uint4& a1, const uint4& b0, const uint4& b1,
+                                                uint32_t dbits, const uint4 (&x)[8], const float (&s16)[4]) {
+    const uint32_t qa[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const uint32_t qb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    float Sa[2] = {0.f, 0.f}, Sb[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // code word j: elements 4j .. 4j+3 of each block
+        const uint4 xa = x[j >> 1], xb = x[4 + (j >> 1)];
+        const uint32_t xa02 = (j & 1) ? xa.z : xa.x, xa13 = (j & 1) ? xa.w : xa.y;
+        const uint32_t xb02 = (j & 1) ? xb.z : xb.x, xb13 = (j & 1) ? xb.w : xb.y;
+        Sa[j & 1] = dot4_codes(qa[j] ^ 0x80808080u, xa02, xa13, Sa[j & 1]);
+        Sb[j & 1] = dot4_codes(qb[j] ^ 0x80808080u, xb02, xb13, Sb[j & 1]);
+    }
+    const float r = h2f_bits(dbits) * fmaf(-1152.f, s16[0] + s16[1], Sa[0] + Sa[1]);
+    return fmaf(h2f_bits(dbits >> 16), fmaf(-1152.f, s16[2] + s16[3], Sb[0] + Sb[1]), r);
 }
 
 // Activations of a Q6_K unit (h, l16) from LDS: xsb -> the super-block's x
@@ -515,7 +539,7 @@ __device__ __forceinline__ void xr_store(int K, int c0, const XChunks<F32, XR>& 
 // This thread's UPT work units of a tile, loaded straight into registers.
 template <int UPT>
 struct TileW {
-    uint4 w0[UPT], w1[UPT], w2[UPT];
+    uint4 w0[UPT], w1[UPT], w2[UPT], w3[UPT];  // w3: Q8_0 only
     uint2 sc8[UPT];
     uint32_t dbits[UPT];
     int usb[UPT];
@@ -562,6 +586,13 @@ __device__ __forceinline__ void tile_w_issue(TileW<UPT>& W, const TileGeo& T, in
             W.w0[i] = ldg_g16(blk);
             W.w1[i] = ldg_g16(blk + 16 + 32 * q);
             W.w2[i] = ldg_g16(blk + 32 + 32 * q);
+        } else if (FMT == 8) {  // unit = Q8_0 blocks 2 kr, 2 kr + 1 (68 bytes, 2-byte aligned)
+            const uint8_t* blk = rowp + (size_t)up.kr * (2 * Q80_BYTES);
+            W.w0[i] = ldg_u16b(blk + 2);
+            W.w1[i] = ldg_u16b(blk + 18);
+            W.w2[i] = ldg_u16b(blk + Q80_BYTES + 2);
+            W.w3[i] = ldg_u16b(blk + Q80_BYTES + 18);
+            W.dbits[i] = ldg_b16(blk, 0) | (ldg_b16(blk + Q80_BYTES, 0) << 16);
         } else {
             const uint8_t* blk = rowp + sb * Q6K_BYTES;
             const int h = q >> 1, l16 = (q & 1) * 16;
@@ -622,7 +653,7 @@ __device__ __forceinline__ void tile_dot(const TileW<UPT>& W, int nr, int per_ro
         if (!RO || i == 0) {  // range-owned: the unit range, hence x, is the same for every i
 #pragma unroll
             for (int m = 0; m < NC; ++m) {
-                if (FMT == 4)
+                if (FMT == 4 || FMT == 8)
                     q4k_unit_x(xs + (size_t)m * ldx + xpad(sb * QK_K + 64 * q), s16 + m * (K / 16) + sb * 16 + 4 * q,
                                x[m], xs16[m]);
                 else
@@ -643,6 +674,11 @@ __device__ __forceinline__ void tile_dot(const TileW<UPT>& W, int nr, int per_ro
                 const Q4KUnitData d{W.w0[i], W.w1[i], W.w2[i]};
 #pragma unroll
                 for (int m = 0; m < NC; ++m) part[m * pstride + u] = q4k_unit_dot_x(d, q, x[m], xs16[m]);
+            } else if (FMT == 8) {
+#pragma unroll
+                for (int m = 0; m < NC; ++m)
+                    part[m * pstride + u] = q80_unit_dot_x(W.w0[i], W.w1[i], W.w2[i], W.w3[i], W.dbits[i], x[m],
+                                                           xs16[m]);
             } else {
 #pragma unroll
                 for (int m = 0; m < NC; ++m)
@@ -828,7 +864,7 @@ __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const F
 
 // One tile per block (grid = tiles): everything a block reads is requested
 // up front, so a block costs about one memory latency plus its arithmetic.
-template <int NC, bool F32, int UPT, int FMT, int KC, bool RO, bool ATT>
+template <int NC, bool F32, int UPT, int FMT, int KC, bool RO, bool ATT, bool WF>
 __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPlan& P, const TileGeo& T,
                                          uint8_t* lds, float (*red)[NC], int* pos_s) {
     const int K = KC > 0 ? KC : P.K, M = NC == 1 ? 1 : P.M;
@@ -844,8 +880,9 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     tile_e_issue<NC>(E, P, T, M, dummy, tid);
     TMV_M(2);
     TileW<UPT> W;
+    if constexpr (WF) tile_w_issue<UPT, FMT, RO>(W, T, n_sb, per_row, tid);
     fmv_prologue<NC, F32, KC, ATT>(x, P, L, wb, red, pos_s, [&]() {
-        tile_w_issue<UPT, FMT, RO>(W, T, n_sb, per_row, tid);
+        if constexpr (!WF) tile_w_issue<UPT, FMT, RO>(W, T, n_sb, per_row, tid);
         tile_e_rope(E, P, T, pos_s[E.em], dummy);  // kv offsets are in LDS after the first barrier
     });
     TMV_M(5);
@@ -873,15 +910,20 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
 // RO: range-owned unit mapping (see unit_pos).
 // ATT: activations combined from split-KV partials (a separate instantiation:
 // the combine's registers would otherwise lower every mat-vec's occupancy).
-template <int NC, bool F32, int UPT, int KC, bool RO, bool ATT = false>
+// WF: the tile's weight loads are issued before the activation loads (one
+// memory round trip per block instead of two, but the activations then queue
+// behind the weights): faster for launches of many tiles (the LM head),
+// slower for the short launches of the decode step.
+template <int NC, bool F32, int UPT, int KC, bool RO, bool ATT = false, bool WF = false>
 __global__ __launch_bounds__(ROWS_THREADS) void fused_mv_kernel(const void* __restrict__ x, FmvPlan P) {
     extern __shared__ uint4 smem_fmv[];
     __shared__ float red[4][NC];
     __shared__ int pos_s[NC];
     const TileGeo T = tile_geo(P, blockIdx.x);
     uint8_t* lds = reinterpret_cast<uint8_t*>(smem_fmv);
-    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4, KC, RO, ATT>(x, P, T, lds, red, pos_s);
-    else tmv_body<NC, F32, UPT, 6, KC, RO, ATT>(x, P, T, lds, red, pos_s);
+    if (T.fmt == 4) tmv_body<NC, F32, UPT, 4, KC, RO, ATT, WF>(x, P, T, lds, red, pos_s);
+    else if (ATT || WF || T.fmt == 6) tmv_body<NC, F32, UPT, 6, KC, RO, ATT, WF>(x, P, T, lds, red, pos_s);
+    else tmv_body<NC, F32, UPT, 8, KC, RO, ATT, WF>(x, P, T, lds, red, pos_s);
 }
 
 // Range-owned mapping when a row's units fill the block's threads with at
@@ -900,6 +942,12 @@ static void fmv_launch_k(int upt, int total, size_t lds, hipStream_t st, const v
             if (upt == 4) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4, KC, RO, true>), g, b, lds, st, x, plan);
             else if (upt == 2) hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 2, KC, RO, true>), g, b, lds, st, x, plan);
             else hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 1, KC, RO, true>), g, b, lds, st, x, plan);
+            return;
+        }
+    }
+    if constexpr (KC == 1536 && RO) {  // weights-first form for launches of many tiles
+        if (upt == 4 && plan.wfirst) {
+            hipLaunchKernelGGL((fused_mv_kernel<NC, F32, 4, KC, RO, false, true>), g, b, lds, st, x, plan);
             return;
         }
     }

@@ -13,10 +13,10 @@
 //
 // Tiles are 16 * RT weight rows; paired tiles hold 8 * RT rows and their
 // partners (RoPE: d and d + 64 of one head; SwiGLU: gate row j and up row j),
-// so a pair's two sums finish in the same block.  The A operand of each lane
-// comes from its tile row's weight row; everything else is the batched MFMA
-// GEMM (8 waves split K, partial C tiles summed through LDS), whose k-slot
-// map and dequantisation it shares (mfma_deq.h).
+// so a pair's two sums finish in the same block.  The weight operand of each
+// lane comes from its tile row's weight row; everything else is the batched
+// MFMA GEMM (waves split K, partial C tiles summed through LDS), whose k-slot
+// map, exact operands and per-super-block scaling it shares (mfma_deq.h).
 #include <cstdlib>
 #include <cstring>
 
@@ -153,45 +153,13 @@ __device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float 
             MM_TS(1);
         }
 #endif
-        if (FMT == 4) {
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                const uint8_t* blk = rowp[rt] + (size_t)sb * Q4K_BYTES;
-                const uint4 h = *reinterpret_cast<const uint4*>(blk);
-                uint4 qc[2];
-                qc[0] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * grp);
-                qc[1] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (grp + 4));
-                Q4KLaneScale s[2];
-                s[0] = q4k_lane_scale(h, grp >> 1);
-                s[1] = q4k_lane_scale(h, 2 + (grp >> 1));
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int ci = t >> 2, part = (t >> 1) & 1, e = t & 1;
-                    const uint32_t wa = (e == 0) ? ((ci == 0) ? qc[0].x : qc[1].x) : ((ci == 0) ? qc[0].z : qc[1].z);
-                    const uint32_t wb = (e == 0) ? ((ci == 0) ? qc[0].y : qc[1].y) : ((ci == 0) ? qc[0].w : qc[1].w);
-                    const uint32_t u0 = part ? ((wa >> 4) & 0x0F0F0F0Fu) : (wa & 0x0F0F0F0Fu);
-                    const uint32_t u1 = part ? ((wb >> 4) & 0x0F0F0F0Fu) : (wb & 0x0F0F0F0Fu);
-                    const float dd = part ? s[ci].d_hi : s[ci].d_lo;
-                    const float mm = part ? s[ci].m_hi : s[ci].m_lo;
-                    const half2_t d2 = {(_Float16)dd, (_Float16)dd};
-                    const half2_t m2 = {(_Float16)mm, (_Float16)mm};
-                    const half8_t a = deq8(u0, u1, (_Float16)0.0f, d2, m2);
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx[t][nt], acc[rt][nt], 0, 0, 0);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                half8_t av[8];
-                q6k_a_operands(rowp[rt] + (size_t)sb * Q6K_BYTES, grp, av);
-#pragma unroll
-                for (int t = 0; t < 8; ++t)
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t], bx[t][nt], acc[rt][nt], 0, 0, 0);
-            }
+        for (int rt = 0; rt < RT; ++rt) {
+            typename SbRaw<FMT>::Raw raw;
+            sb_load(rowp[rt] + (size_t)sb * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES), grp, raw);
+            typename SbRaw<FMT>::Ops ops;
+            sb_ops(raw, grp, ops);
+            sb_mfma<NT>(ops, bx, acc[rt]);
         }
     }
 #pragma unroll
@@ -203,11 +171,11 @@ __device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float 
 }
 
 // Sum over the NW waves of tile row rr, batch column mc (C layout: lane
-// (col, grp) holds rows 4*grp+i of a 16-row tile for column col).
+// (row rw, grp) holds batch columns 4*grp+i of a 16-column tile).
 template <int RT, int NT, int NW>
 __device__ __forceinline__ float mm_sum(float (*red)[RT][NT][4][64], int rr, int mc) {
     const int rt = rr >> 4, rw = rr & 15, nt = mc >> 4, cc = mc & 15;
-    const int ln = cc + 16 * (rw >> 2), i = rw & 3;
+    const int ln = c_lane(rw, cc), i = c_reg(cc);
     float s = 0.f;
 #pragma unroll
     for (int wq = 0; wq < NW; ++wq) s += red[wq][rt][nt][i][ln];
@@ -289,7 +257,7 @@ __global__ __launch_bounds__(64 * NW) void fused_mm_kernel(MmPlan P) {
 
 
 // Weight-stationary form for long batches (prefill chunks), K = 6 super-blocks:
-// wave w dequantises super-block w of its tile rows once, keeps the A
+// wave w decodes super-block w of its tile rows once, keeps the weight
 // operands in registers and runs them against the block's columns
 // [blockIdx.y * cols, ...) 16 * NT at a time; the next columns' activations
 // are requested before the epilogue of the current ones.  Each C tile sums
@@ -302,17 +270,13 @@ __device__ __forceinline__ void mm_ws_body(const MmPlan& P, const MmTile& T, flo
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int K = P.K;
-    half8_t av[RT][8];
+    typename SbRaw<FMT>::Ops ops[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const uint8_t* rowp = mm_row<RT>(T, rt * 16 + col);
-        if (FMT == 4) {
-            Q4Raw r;
-            q4_raw_load(rowp + (size_t)wv * Q4K_BYTES, grp, r);
-            q4_raw_operands(r, grp, av[rt]);
-        } else {
-            q6k_a_operands(rowp + (size_t)wv * Q6K_BYTES, grp, av[rt]);
-        }
+        typename SbRaw<FMT>::Raw raw;
+        sb_load(rowp + (size_t)wv * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES), grp, raw);
+        sb_ops(raw, grp, ops[rt]);
     }
     half8_t bx[8][NT];
     auto load_b = [&](int m0) {
@@ -334,12 +298,7 @@ __device__ __forceinline__ void mm_ws_body(const MmPlan& P, const MmTile& T, flo
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[rt][t], bx[t][nt], acc[rt][nt], 0, 0, 0);
+        for (int rt = 0; rt < RT; ++rt) sb_mfma<NT>(ops[rt], bx, acc[rt]);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll

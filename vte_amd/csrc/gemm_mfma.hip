@@ -8,20 +8,11 @@
 // form once per column group of up to hundreds of columns).
 //
 // Design:
-//  * v_mfma_f32_16x16x32_f16: M = 16 weight rows, N = 16 batch columns,
-//    K = 32.  A block of 8 waves owns RT x 16 rows; each wave takes a
+//  * v_mfma_f32_16x16x32_f16 with exact integer weight operands and the
+//    super-block scales applied in fp32 once per super-block (mfma_deq.h:
+//    sb_mfma).  A block of 8 waves owns RT x 16 rows; each wave takes a
 //    contiguous range of super-blocks (split-K inside the block) and the
-//    partial C tiles are summed through LDS before the epilogue.
-//  * Weights are dequantised in registers to fp16 with packed fp16 math
-//    (nibble -> 0x64xx magic -> exact subtract -> v_pk_fma_f16), so only the
-//    final weight carries an fp16 rounding; activations go to fp16; the MFMA
-//    accumulates in fp32.
-//  * K-slot permutation: MFMA pairs A and B by (lane group, slot), so any
-//    bijection of super-block elements to (k-step, group, slot) is valid as
-//    long as A and B use the same one.  The map is chosen so each lane's 8
-//    slots are 8 contiguous elements sharing one sub-block scale:
-//      Q4_K step t, group g: qs chunk c = g + 4*(t>>2), nibble (t>>1)&1, half t&1
-//      Q6_K step t, group g: half h = t>>2, quarter q = t&3, l = 8g .. 8g+7
+//    partial C tiles are summed through LDS in wave order before the epilogue.
 //  * Q4_K rows are 16-byte aligned and Q6_K rows 2-byte aligned; both load
 //    straight from HBM (unaligned 8-byte loads stream at full speed).
 #include <algorithm>
@@ -56,9 +47,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-
     for (int sb = sb0; sb < sb1; ++sb) {
-        // ---- B operand (activations) for the 8 k-steps ----
+        // ---- A operands (activations) for the 8 k-steps ----
         half8_t bx[8][NT];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -69,46 +59,14 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
                 bx[t][nt] = load_x8<TI>(x + (size_t)(m < M ? m : 0) * K + kb, m < M);
             }
         }
-        if (FMT == 4) {
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                const int r = min(row0 + rt * 16 + col, N - 1);
-                const uint8_t* blk = w + (size_t)r * row_bytes + (size_t)sb * Q4K_BYTES;
-                const uint4 h = *reinterpret_cast<const uint4*>(blk);
-                uint4 qc[2];
-                qc[0] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * grp);
-                qc[1] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (grp + 4));
-                Q4KLaneScale s[2];
-                s[0] = q4k_lane_scale(h, grp >> 1);
-                s[1] = q4k_lane_scale(h, 2 + (grp >> 1));
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int ci = t >> 2, part = (t >> 1) & 1, e = t & 1;
-                    const uint32_t wa = (e == 0) ? ((ci == 0) ? qc[0].x : qc[1].x) : ((ci == 0) ? qc[0].z : qc[1].z);
-                    const uint32_t wb = (e == 0) ? ((ci == 0) ? qc[0].y : qc[1].y) : ((ci == 0) ? qc[0].w : qc[1].w);
-                    const uint32_t u0 = part ? ((wa >> 4) & 0x0F0F0F0Fu) : (wa & 0x0F0F0F0Fu);
-                    const uint32_t u1 = part ? ((wb >> 4) & 0x0F0F0F0Fu) : (wb & 0x0F0F0F0Fu);
-                    const float dd = part ? s[ci].d_hi : s[ci].d_lo;
-                    const float mm = part ? s[ci].m_hi : s[ci].m_lo;
-                    const half2_t d2 = {(_Float16)dd, (_Float16)dd};
-                    const half2_t m2 = {(_Float16)mm, (_Float16)mm};
-                    const half8_t a = deq8(u0, u1, (_Float16)0.0f, d2, m2);
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx[t][nt], acc[rt][nt], 0, 0, 0);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                half8_t av[8];
-                q6k_a_operands(w + (size_t)min(row0 + rt * 16 + col, N - 1) * row_bytes + (size_t)sb * Q6K_BYTES, grp, av);
-#pragma unroll
-                for (int t = 0; t < 8; ++t)
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[t], bx[t][nt], acc[rt][nt], 0, 0, 0);
-            }
+        for (int rt = 0; rt < RT; ++rt) {
+            const int r = min(row0 + rt * 16 + col, N - 1);
+            typename SbRaw<FMT>::Raw raw;
+            sb_load(w + (size_t)r * row_bytes + (size_t)sb * bpr, grp, raw);
+            typename SbRaw<FMT>::Ops ops;
+            sb_ops(raw, grp, ops);
+            sb_mfma<NT>(ops, bx, acc[rt]);
         }
     }
 
@@ -120,11 +78,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
 #pragma unroll
             for (int i = 0; i < 4; ++i) red[wv][rt][nt][i][lane] = acc[rt][nt][i];
     __syncthreads();
-    // C layout: lane (col, grp) holds rows 4*grp+i of the tile, batch column col.
+    // C layout: lane (row rw, grp) holds batch columns 4*grp + i of the tile.
     for (int o = threadIdx.x; o < RT * 16 * NT * 16; o += blockDim.x) {
         const int rr = o / (NT * 16), mc = o % (NT * 16);
         const int rt = rr >> 4, rw = rr & 15, nt = mc >> 4, cc = mc & 15;
-        const int ln = cc + 16 * (rw >> 2), i = rw & 3;
+        const int ln = c_lane(rw, cc), i = c_reg(cc);
         float s = 0.f;
 #pragma unroll
         for (int wq = 0; wq < NW; ++wq) s += red[wq][rt][nt][i][ln];
@@ -160,18 +118,14 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
     if (c0 >= c1) return;
     float* y = part + blockIdx.y * split_stride;
 
-    half8_t av[RT][8];
+    typename SbRaw<FMT>::Ops ops[RT];
     if (has) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const uint8_t* blk = w + (size_t)min(row0 + rt * 16 + col, N - 1) * row_bytes;
-            if (FMT == 4) {
-                Q4Raw r;
-                q4_raw_load(blk + (size_t)sb0 * Q4K_BYTES, grp, r);
-                q4_raw_operands(r, grp, av[rt]);
-            } else {
-                q6k_a_operands(blk + (size_t)sb0 * Q6K_BYTES, grp, av[rt]);
-            }
+            typename SbRaw<FMT>::Raw raw;
+            sb_load(blk + (size_t)sb0 * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES), grp, raw);
+            sb_ops(raw, grp, ops[rt]);
         }
     }
     half8_t bx[8][NT];
@@ -195,12 +149,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
             for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
         if (has) {
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-                for (int t = 0; t < 8; ++t)
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-                        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[rt][t], bx[t][nt], acc[rt][nt], 0, 0, 0);
+            for (int rt = 0; rt < RT; ++rt) sb_mfma<NT>(ops[rt], bx, acc[rt]);
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
@@ -214,7 +163,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
         for (int o = threadIdx.x; o < 16 * RT * NT * 16; o += blockDim.x) {
             const int rr = o / (NT * 16), mc = o % (NT * 16);
             const int rt = rr >> 4, rw = rr & 15, nt = mc >> 4, cc = mc & 15;
-            const int ln = cc + 16 * (rw >> 2), i = rw & 3;
+            const int ln = c_lane(rw, cc), i = c_reg(cc);
             float s = 0.f;
 #pragma unroll
             for (int wq = 0; wq < NW; ++wq) s += red[wq][rt][nt][i][ln];
@@ -262,11 +211,8 @@ __global__ __launch_bounds__(64 * WPB) void gemm_stream_kernel(const TI* __restr
     const int ntiles = (N + 15) / 16;
     for (int tile = blockIdx.x * WPB + wv; tile < ntiles; tile += gridDim.x * WPB) {
         const uint8_t* rowp = w + (size_t)min(tile * 16 + col, N - 1) * row_bytes;
-        using Raw = typename std::conditional<FMT == 4, Q4Raw, Q6Raw>::type;
-        auto load = [&](int sb, Raw& r) {
-            if constexpr (FMT == 4) q4_raw_load(rowp + sb * BPB, grp, r);
-            else q6_raw_load(rowp + sb * BPB, grp, r);
-        };
+        using Raw = typename SbRaw<FMT>::Raw;
+        auto load = [&](int sb, Raw& r) { sb_load(rowp + sb * BPB, grp, r); };
         Raw cur, nxt, nx2;
         load(0, cur);
         load(1, nxt);
@@ -277,28 +223,27 @@ __global__ __launch_bounds__(64 * WPB) void gemm_stream_kernel(const TI* __restr
         // three super-blocks in flight per wave while sb is multiplied
 #pragma unroll 1
         for (int sb = 0; sb < GS_NSB; ++sb) {
-            half8_t a[8];
-            if constexpr (FMT == 4) q4_raw_operands(cur, grp, a);
-            else q6_raw_operands(cur, grp, a);
+            typename SbRaw<FMT>::Ops ops;
+            sb_ops(cur, grp, ops);
             cur = nxt;
             nxt = nx2;
             load(min(sb + 3, GS_NSB - 1), nx2);
+            half8_t bx[8][NT];
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const int kb = sb * QK_K + kslot_base<FMT>(t, grp);
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    const half8_t b = *reinterpret_cast<const half8_t*>(xs + (nt * 16 + col) * GS_LDX + kb);
-                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b, acc[nt], 0, 0, 0);
-                }
+                for (int nt = 0; nt < NT; ++nt)
+                    bx[t][nt] = *reinterpret_cast<const half8_t*>(xs + (nt * 16 + col) * GS_LDX + kb);
             }
+            sb_mfma<NT>(ops, bx, acc);
         }
-        // C layout: lane (col, grp) holds weight rows 4*grp + i for batch column col
+        // C layout: lane (col, grp) holds batch columns 4*grp + i of weight row col
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int r = tile * 16 + 4 * grp + i, m = nt * 16 + col;
+                const int r = tile * 16 + col, m = nt * 16 + 4 * grp + i;
                 if (r < N && m < M) gemv_store<TO>(y, bias, residual, rs, r, m, N, acc[nt][i]);
             }
     }

@@ -1,17 +1,31 @@
-// Weight dequantisation into MFMA A operands (Q4_K / Q6_K super-blocks to
-// fp16) and the k-slot map shared by the batched MFMA kernels, gfx950.
+// Quantised weights as exact MFMA operands (Q4_K / Q6_K super-blocks) and the
+// k-slot map shared by the batched MFMA kernels, gfx950.
 //
-//  * v_mfma_f32_16x16x32_f16: M = 16 weight rows, N = 16 batch columns, K = 32.
-//  * Weights are dequantised in registers to fp16 with packed fp16 math
-//    (nibble -> 0x64xx magic -> exact subtract -> v_pk_fma_f16), so only the
-//    final weight carries an fp16 rounding; activations go to fp16; the MFMA
-//    accumulates in fp32.
+//  * v_mfma_f32_16x16x32_f16 with the activations as the A operand (M = 16
+//    batch columns) and the weights as the B operand (N = 16 weight rows),
+//    K = 32: C[m][n] lands in lane (n, g) as batch columns 4g .. 4g+3 of
+//    weight row n, the lane that loaded row n's super-block, so the
+//    super-block scales apply lane-locally.
+//  * Exact weight operands: a super-block's weights are d * (sc_j * q) -
+//    dmin * m_j (Q4_K) or d * (sc_j * (q - 32)) (Q6_K), with 4/6-bit codes
+//    q and 6/8-bit sub-block scales sc_j, m_j.  The operands are the integer
+//    products sc_j * q (<= 945) and sc_j * (q - 32) (exact in fp16 while
+//    |sc_j| <= 64, one rounding of an integer product beyond), made with
+//    packed fp16 math from the code bytes (nibble -> 0x64xx magic = 1024 + q);
+//    the Q4_K minimum term is a second MFMA of the same activations against
+//    the splat 6-bit m_j.  The MFMA sums a super-block in fp32 and the fp32
+//    scales d, dmin are applied once per super-block (sb_mfma).  The weights
+//    therefore enter the sums exactly as the reference's fp32 dequantisation
+//    defines them (vte/compiler/dequantizer.py:26-70, 129-169); only the fp16
+//    activations and the fp32 sums round.
 //  * K-slot permutation: MFMA pairs A and B by (lane group, slot), so any
 //    bijection of super-block elements to (k-step, group, slot) is valid as
 //    long as A and B use the same one.  The map is chosen so each lane's 8
 //    slots are 8 contiguous elements sharing one sub-block scale:
 //      Q4_K step t, group g: qs chunk c = g + 4*(t>>2), nibble (t>>1)&1, half t&1
+//           (sub-block 2 * ((g>>1) + 2*(t>>2)) + ((t>>1)&1); steps 2s, 2s+1 share one)
 //      Q6_K step t, group g: half h = t>>2, quarter q = t&3, l = 8g .. 8g+7
+//           (16-element sub-block 8h + 2q + (g>>1))
 #pragma once
 #include <cstdlib>
 #include "quant.h"
@@ -28,22 +42,24 @@ union H8 {
 
 #define MF_WAVES 8
 
-// bytes b0..b3 of `u` (each < 256, here 6-bit values) -> two fp16 pairs 1024+b.
+// bytes b0..b3 of `u` (each < 256) -> two fp16 pairs 1024+b.
 __device__ __forceinline__ void bytes_to_f16magic(uint32_t u, uint32_t& lo, uint32_t& hi) {
     lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
     hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
 }
 
-// 8 nibble/6-bit values in the bytes of (u0, u1) -> 8 fp16 weights (q - bias) * d - m.
-__device__ __forceinline__ half8_t deq8(uint32_t u0, uint32_t u1, _Float16 sub, half2_t d2, half2_t m2) {
+// 8 codes in the bytes of (u0, u1) -> 8 fp16 values (1024 + q) * s + c: with
+// c = -1024 s the exact integer q * s, with c = -1056 s the integer (q - 32) * s.
+__device__ __forceinline__ half8_t codes8(uint32_t u0, uint32_t u1, half2_t s2, half2_t c2) {
     H8 r;
     bytes_to_f16magic(u0, r.u[0], r.u[1]);
     bytes_to_f16magic(u1, r.u[2], r.u[3]);
-    const half2_t off = {(_Float16)(1024.0f) + sub, (_Float16)(1024.0f) + sub};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.h2[i] = (r.h2[i] - off) * d2 - m2;
+    for (int i = 0; i < 4; ++i) r.h2[i] = __builtin_elementwise_fma(r.h2[i], s2, c2);  // one rounding: exact
     return r.v;
 }
+
+__device__ __forceinline__ half2_t splat2(float v) { return half2_t{(_Float16)v, (_Float16)v}; }
 
 template <typename TI>
 __device__ __forceinline__ half8_t load_x8(const TI* p, bool valid);
@@ -100,8 +116,20 @@ __device__ __forceinline__ void q6_raw_load(const uint8_t* blk, int grp, Q6Raw& 
         r.sc[hh] = q6_ld8(blk + 192 + 8 * hh);
     }
 }
-__device__ __forceinline__ void q6_raw_operands(const Q6Raw& r, int grp, half8_t (&a)[8]) {
-    const float d = h2f_bits(r.d);
+// Exact operands of one super-block for one lane: the 8 k-steps' weight
+// operands and the fp32 scales (Q4_K: also the 4 sub-block minima, splat).
+struct Q6Ops {
+    half8_t w[8];
+    float d;
+};
+struct Q4Ops {
+    half8_t w[8];
+    uint32_t mnb;   // byte s: m_j of the lane's sub-block of steps 2s, 2s+1
+    float d, dmin;
+};
+
+__device__ __forceinline__ void q6_exact_operands(const Q6Raw& r, int grp, Q6Ops& o) {
+    o.d = h2f_bits(r.d);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
         const uint2 qa = r.qa[hh], qb = r.qb[hh], qh = r.qh[hh], scw = r.sc[hh];
@@ -122,19 +150,17 @@ __device__ __forceinline__ void q6_raw_operands(const Q6Raw& r, int grp, half8_t
                 u0 = ((qb.x >> 4) & 0x0F0F0F0Fu) | ((qh.x >> 2) & 0x30303030u);
                 u1 = ((qb.y >> 4) & 0x0F0F0F0Fu) | ((qh.y >> 2) & 0x30303030u);
             }
-            const int8_t scq = (int8_t)((sc >> (8 * ((grp >> 1) + 2 * q))) & 0xFF);
-            const float dsc = d * (float)scq;
-            const half2_t d2 = {(_Float16)dsc, (_Float16)dsc};
-            const half2_t z2 = {(_Float16)0.0f, (_Float16)0.0f};
-            a[4 * hh + q] = deq8(u0, u1, (_Float16)32.0f, d2, z2);
+            const float scq = (float)(int8_t)((sc >> (8 * ((grp >> 1) + 2 * q))) & 0xFF);
+            // (1024 + u) - 1056 = u - 32 exactly, then one multiply by the integer scale
+            H8 v;
+            bytes_to_f16magic(u0, v.u[0], v.u[1]);
+            bytes_to_f16magic(u1, v.u[2], v.u[3]);
+            const half2_t off = splat2(-1056.0f), s2 = splat2(scq);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v.h2[i] = (v.h2[i] + off) * s2;
+            o.w[4 * hh + q] = v.v;
         }
     }
-}
-
-__device__ __forceinline__ void q6k_a_operands(const uint8_t* blk, int grp, half8_t (&a)[8]) {
-    Q6Raw r;
-    q6_raw_load(blk, grp, r);
-    q6_raw_operands(r, grp, a);
 }
 
 // Q4_K: the header and the lane's two 16-byte code chunks; operands for the
@@ -147,10 +173,13 @@ __device__ __forceinline__ void q4_raw_load(const uint8_t* blk, int grp, Q4Raw& 
     r.q0 = *reinterpret_cast<const uint4*>(blk + 16 + 16 * grp);
     r.q1 = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (grp + 4));
 }
-__device__ __forceinline__ void q4_raw_operands(const Q4Raw& r, int grp, half8_t (&a)[8]) {
-    Q4KLaneScale s[2];
-    s[0] = q4k_lane_scale(r.h, grp >> 1);
-    s[1] = q4k_lane_scale(r.h, 2 + (grp >> 1));
+__device__ __forceinline__ void q4_exact_operands(const Q4Raw& r, int grp, Q4Ops& o) {
+    o.d = h2f_bits(r.h.x);
+    o.dmin = h2f_bits(r.h.x >> 16);
+    Q4KLaneInts s[2];
+    s[0] = q4k_lane_ints(r.h, grp >> 1);
+    s[1] = q4k_lane_ints(r.h, 2 + (grp >> 1));
+    o.mnb = s[0].mn0 | (s[0].mn1 << 8) | (s[1].mn0 << 16) | (s[1].mn1 << 24);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         const int ci = t >> 2, part = (t >> 1) & 1, e = t & 1;
@@ -158,13 +187,66 @@ __device__ __forceinline__ void q4_raw_operands(const Q4Raw& r, int grp, half8_t
         const uint32_t wa = e == 0 ? qc.x : qc.z, wb = e == 0 ? qc.y : qc.w;
         const uint32_t u0 = part ? ((wa >> 4) & 0x0F0F0F0Fu) : (wa & 0x0F0F0F0Fu);
         const uint32_t u1 = part ? ((wb >> 4) & 0x0F0F0F0Fu) : (wb & 0x0F0F0F0Fu);
-        const float dd = part ? s[ci].d_hi : s[ci].d_lo;
-        const float mm = part ? s[ci].m_hi : s[ci].m_lo;
-        const half2_t d2 = {(_Float16)dd, (_Float16)dd};
-        const half2_t m2 = {(_Float16)mm, (_Float16)mm};
-        a[t] = deq8(u0, u1, (_Float16)0.0f, d2, m2);
+        const float sc = (float)(part ? s[ci].sc1 : s[ci].sc0);
+        o.w[t] = codes8(u0, u1, splat2(sc), splat2(-1024.0f * sc));
     }
 }
+
+// One super-block of MFMA work for NT 16-column activation tiles bx[t][nt]
+// (A operands, k-slot map of the format) against one lane's exact weight
+// operands: acc[nt] += d * sum(w x) [- dmin * sum(m x)], the sums in fp32 over
+// the super-block's 8 k-steps in order.  Every batched kernel goes through
+// this function, so a weight row's result depends only on which super-blocks
+// a wave sums (and the order the waves' partials are added), not on the
+// kernel or the number of columns.
+template <int NT>
+__device__ __forceinline__ void sb_mfma(const Q6Ops& o, const half8_t (&bx)[8][NT], floatx4_t (&acc)[NT]) {
+    floatx4_t aw[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) aw[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) aw[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[t][nt], o.w[t], aw[nt], 0, 0, 0);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[nt][i] = fmaf(o.d, aw[nt][i], acc[nt][i]);
+}
+template <int NT>
+__device__ __forceinline__ void sb_mfma(const Q4Ops& o, const half8_t (&bx)[8][NT], floatx4_t (&acc)[NT]) {
+    floatx4_t aw[NT], am[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) aw[nt] = am[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const _Float16 m = (_Float16)(float)((o.mnb >> (8 * (t >> 1))) & 0xFFu);
+        const half8_t mv = {m, m, m, m, m, m, m, m};
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            aw[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[t][nt], o.w[t], aw[nt], 0, 0, 0);
+            am[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[t][nt], mv, am[nt], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[nt][i] = fmaf(-o.dmin, am[nt][i], fmaf(o.d, aw[nt][i], acc[nt][i]));
+}
+
+// Raw bytes -> operands for either format.
+template <int FMT> struct SbRaw;
+template <> struct SbRaw<4> { using Raw = Q4Raw; using Ops = Q4Ops; };
+template <> struct SbRaw<6> { using Raw = Q6Raw; using Ops = Q6Ops; };
+__device__ __forceinline__ void sb_load(const uint8_t* blk, int grp, Q4Raw& r) { q4_raw_load(blk, grp, r); }
+__device__ __forceinline__ void sb_load(const uint8_t* blk, int grp, Q6Raw& r) { q6_raw_load(blk, grp, r); }
+__device__ __forceinline__ void sb_ops(const Q4Raw& r, int grp, Q4Ops& o) { q4_exact_operands(r, grp, o); }
+__device__ __forceinline__ void sb_ops(const Q6Raw& r, int grp, Q6Ops& o) { q6_exact_operands(r, grp, o); }
+
+// C tile element of weight row rw (0..15) and batch column cc (0..15): lane
+// rw + 16 * (cc / 4), register cc % 4.
+__device__ __forceinline__ int c_lane(int rw, int cc) { return rw + 16 * (cc >> 2); }
+__device__ __forceinline__ int c_reg(int cc) { return cc & 3; }
 
 // Column groups for a weight-stationary launch of `tiles` row tiles over M
 // batch columns, 32 at a time: each group re-reads and re-dequantises the

@@ -7,10 +7,10 @@
 // 2*mblk+1.  Branch-free restatement of get_scale_min_k4
 // (vte/compiler/dequantizer.py:6-23) on the three scale words.
 struct Q4KLaneScale { float d_lo, m_lo, d_hi, m_hi; };
+// The same four 6-bit values as integers: scales and mins of sub-blocks 2*mblk, 2*mblk+1.
+struct Q4KLaneInts { uint32_t sc0, mn0, sc1, mn1; };
 
-__device__ __forceinline__ Q4KLaneScale q4k_lane_scale(uint4 h, int mblk) {
-    const float d = h2f_bits(h.x);
-    const float dmin = h2f_bits(h.x >> 16);
+__device__ __forceinline__ Q4KLaneInts q4k_lane_ints(uint4 h, int mblk) {
     const int sh = (mblk & 1) * 16;
     const uint32_t a = h.y >> sh;  // bytes j, j+1        (j = 2*(mblk&1))
     const uint32_t b = h.z >> sh;  // bytes j+4, j+5
@@ -25,9 +25,16 @@ __device__ __forceinline__ Q4KLaneScale q4k_lane_scale(uint4 h, int mblk) {
         mn0 = ((c >> 4) & 15) | (((b >> 6) & 3) << 4);
         mn1 = ((c >> 12) & 15) | (((b >> 14) & 3) << 4);
     }
+    return Q4KLaneInts{sc0, mn0, sc1, mn1};
+}
+
+__device__ __forceinline__ Q4KLaneScale q4k_lane_scale(uint4 h, int mblk) {
+    const float d = h2f_bits(h.x);
+    const float dmin = h2f_bits(h.x >> 16);
+    const Q4KLaneInts i = q4k_lane_ints(h, mblk);
     Q4KLaneScale s;
-    s.d_lo = d * (float)sc0; s.m_lo = dmin * (float)mn0;
-    s.d_hi = d * (float)sc1; s.m_hi = dmin * (float)mn1;
+    s.d_lo = d * (float)i.sc0; s.m_lo = dmin * (float)i.mn0;
+    s.d_hi = d * (float)i.sc1; s.m_hi = dmin * (float)i.mn1;
     return s;
 }
 
