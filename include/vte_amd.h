@@ -162,6 +162,14 @@ long long vte_topk_scratch_bytes(int rows);
 int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
              void* stream);
 
+/* vte_topk without a workspace argument and without allocating: the
+ * candidate buffer is a fixed device array inside the library (one per GPU,
+ * 64 rows = 4.2 MB, held until the process ends).  rows must be <= 64 (else
+ * -1 and a message).  Calls that overlap on one GPU race on that array.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops). */
+int vte_topk_noalloc(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* stream);
+
 /* vte_topk over the tokens NOT in each row's exclusion list, plus the exact
  * logits of the excluded tokens.  excl_ids [rows][max_excl]: sorted token ids
  * (the repetition window of the sampler, max_excl <= 4096; the reference uses

@@ -44,6 +44,9 @@ hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_
 size_t topk_scratch_bytes(int rows);
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
                 hipStream_t st, const int* excl_ids, const int* excl_cnt, int max_excl, float* gathered);
+int topk_noalloc_max_rows();
+hipError_t topk_noalloc(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx,
+                        hipStream_t st);
 hipError_t fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, hipStream_t st);
 hipError_t attn_in(const void* x, const void* norm_w, float eps, const void* wq, const void* q_bias, int fmt_q,
                    const void* wk, const void* k_bias, int fmt_k, const void* wv, const void* v_bias, int fmt_v,
@@ -269,6 +272,17 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
     return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream, nullptr,
                                 nullptr, 0, nullptr),
                       "vte_topk launch");
+}
+
+int vte_topk_noalloc(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* stream) {
+    REQUIRE(logits && out_val && out_idx, "topk_noalloc: null pointer");
+    REQUIRE(rows >= 1 && k >= 1 && k <= 64 && vocab >= k, "topk_noalloc: need 1 <= k <= min(64, vocab)");
+    REQUIRE(rows <= vte::topk_noalloc_max_rows(),
+            "topk_noalloc: %d rows exceed the library's fixed scratch of %d rows (use vte_topk with a workspace)",
+            rows, vte::topk_noalloc_max_rows());
+    REQUIRE(vocab <= 262144, "topk_noalloc: vocab %d above 262144", vocab);
+    return hip_status(vte::topk_noalloc(logits, rows, vocab, k, out_val, out_idx, (hipStream_t)stream),
+                      "vte_topk_noalloc launch");
 }
 
 int vte_topk_exclude(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,

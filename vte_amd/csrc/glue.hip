@@ -8,6 +8,8 @@
 //   add_kernel                   vte/compiler/templates/rdna/add.hip.template:4-17
 //   embedding_lookup_q6k_kernel  vte/compiler/templates/rdna/embedding_lookup_q6k.hip.template:17-58
 // plus a top-k selector over fp32 logits for on-device sampling candidates.
+#include <mutex>
+
 #include "vte_common.h"
 
 // ---------------------------------------------------------------------------
@@ -788,15 +790,15 @@ hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_
 
 size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_P * (TOPK_CAP * 8 + 4); }
 
-hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
+hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* work,
                 hipStream_t st, const int* excl_ids, const int* excl_cnt, int max_excl, float* gathered) {
     if (vocab > TOPK_P * TOPK_SLICE) return hipErrorInvalidValue;
     // as many slices as needed, each at most TOPK_SLICE, at most TOPK_P of them
     int P = (vocab + 2047) / 2048;
     if (P > TOPK_P) P = TOPK_P;
     const int slice = (vocab + P - 1) / P;
-    uint64_t* cand = (uint64_t*)scratch;
-    int* cc = (int*)((char*)scratch + (size_t)rows * TOPK_P * TOPK_CAP * 8);
+    uint64_t* cand = (uint64_t*)work;
+    int* cc = (int*)((char*)work + (size_t)rows * TOPK_P * TOPK_CAP * 8);
     const TkExclude ex{excl_ids, excl_cnt, max_excl, gathered};
     hipLaunchKernelGGL(topk_partial_kernel, dim3(P, rows), dim3(TOPK_THREADS), 0, st, logits, vocab, slice, k, cand,
                        cc, ex);
@@ -804,6 +806,54 @@ hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val,
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(TOPK_THREADS), 0, st, cand, cc, P, k, out_val, out_idx);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free top-k: the candidate buffer lives in a file-scope device
+// array of TOPK_NOALLOC_MAX_ROWS rows (4.2 MB, held by every GPU the library
+// runs on until the process ends).  Host code never passes `scratch` itself
+// (its name is a host-side stand-in, not a device address): the device
+// address is looked up once per device with hipGetSymbolAddress and kept.
+// Every call on one GPU shares that GPU's array, so calls that overlap on one
+// GPU (two streams, two threads) race.  The kernels need no clearing: every
+// slice writes its candidate count before the final pass reads it.
+// ---------------------------------------------------------------------------
+#define TOPK_NOALLOC_MAX_ROWS 64
+#define TOPK_NOALLOC_BYTES ((size_t)TOPK_NOALLOC_MAX_ROWS * TOPK_P * (TOPK_CAP * 8 + 4))
+static __device__ __align__(256) uint8_t scratch[TOPK_NOALLOC_BYTES];
+
+#define TOPK_NOALLOC_MAX_DEVICES 64
+static void* g_scratch_ptr[TOPK_NOALLOC_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+int topk_noalloc_max_rows() { return TOPK_NOALLOC_MAX_ROWS; }
+
+// Device address of this device's `scratch` (looked up on the first call
+// per device, with that device current).
+hipError_t topk_noalloc_scratch(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= TOPK_NOALLOC_MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+hipError_t topk_noalloc(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx,
+                        hipStream_t st) {
+    if (rows > TOPK_NOALLOC_MAX_ROWS) return hipErrorInvalidValue;
+    void* work = nullptr;
+    const hipError_t e = topk_noalloc_scratch(&work);
+    if (e != hipSuccess) return e;
+    return topk(logits, rows, vocab, k, out_val, out_idx, work, st, nullptr, nullptr, 0, nullptr);
 }
 
 }  // namespace vte

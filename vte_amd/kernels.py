@@ -41,6 +41,7 @@ SIGNATURES = {
     "vte_embedding_q6k": [_vp, _vp, _vp, _i, _i, _f, _vp],
     "vte_topk_scratch_bytes": [_i],
     "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
+    "vte_topk_noalloc": [_vp, _i, _i, _i, _vp, _vp, _vp],
     "vte_topk_exclude": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp],
     "vte_fill_normal_f16": [_vp, _ll, ctypes.c_ulonglong, _f, _vp],
     "vte_attn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp,
