@@ -240,40 +240,135 @@ def attn_bench(hip, K, ctx, split=None, B=1, fused=False, launches=40):
             "kv_bytes": algo, "GBps": round(algo / (ms * 1e-3) / 1e9, 1)}
 
 
-def cpu_baseline(seconds_budget=20.0):
-    """NumPy restatement of the decode step on the host cores: 2 of 28 layers
-    (one Q6_K-down, one Q4_K-down) plus the LM head, dequantised weights cached
-    outside the timed region, per-layer time scaled to 28 layers."""
+def _host_info():
+    """CPU model, core count and the NumPy BLAS backend with its thread count."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    blas, threads = "unknown", int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    try:
+        from threadpoolctl import threadpool_info
+        for pool in threadpool_info():
+            if pool.get("user_api") == "blas":
+                blas = f"{pool.get('internal_api')} {pool.get('version')}"
+                threads = int(pool.get("num_threads", threads))
+                break
+    except Exception:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "blas": blas, "blas_threads": threads}
+
+
+def _stats(ts):
+    ts = sorted(ts)
+    return {"median": round(float(np.median(ts)), 6), "min": round(ts[0], 6), "max": round(ts[-1], 6),
+            "trials": len(ts)}
+
+
+def cpu_baseline(trials=5):
+    """The NumPy oracle (the reference's CPU arithmetic restated, oracle/) on the
+    host cores, bounded samples of the same workloads, >= 5 trials each:
+
+    * decode step: 2 of the 28 layers (one Q6_K-down, one Q4_K-down) and the LM
+      head at position 2048, dequantised weights cached outside the timed region
+      (vte/compiler/dequantizer.py), per-layer time x 28 + LM head -> tok/s at
+      batch 1 (``value``) and 16;
+    * quant GEMV configs 0/1: dequantisation and the fp32 mat-vec timed
+      separately (the pattern of tools/validate_gemv_q6k_header_fix.py:63-64);
+    * split-KV attention config 2: textbook softmax(q K^T / sqrt(128)) V per head.
+    """
+    from oracle import dequant as odq
     from oracle import step as ost
+    from oracle.attention import attention_ref
+    from vte_amd import synthetic as syn
     from vte_amd.core.model_config import QWEN25_1P5B
     from vte_amd.core.weights import SyntheticQwen2
+    info = _host_info()
+    t_start = time.perf_counter()
     cfg = QWEN25_1P5B.with_(n_layers=2, max_seq=2304)
     model = SyntheticQwen2(cfg, seed=0)
     rng = np.random.default_rng(0)
-    ks = [(0.5 * rng.standard_normal((1, 2304, 2, 128))).astype(np.float16) for _ in range(2)]
-    vs = [(0.5 * rng.standard_normal((1, 2304, 2, 128))).astype(np.float16) for _ in range(2)]
-    cache = {}
-    ost.decode_step(model, [1], [2048], ks, vs, cache)  # warm: dequantise once
-    t_all, n = 0.0, 0
-    t0 = time.perf_counter()
-    while n < 3 or (time.perf_counter() - t0 < seconds_budget and n < 20):
-        s = time.perf_counter()
-        ost.decode_step(model, [1], [2048], ks, vs, cache)
-        t_all += time.perf_counter() - s
-        n += 1
-    step2 = t_all / n
-    # split: LM head alone
-    hn = np.ones(cfg.hidden, np.float16)
-    s = time.perf_counter()
-    for _ in range(3):
-        cache["lm"] @ hn.astype(np.float32)
-    lm = (time.perf_counter() - s) / 3
-    per_layer = max(step2 - lm, 1e-9) / 2
-    est = per_layer * 28 + lm
-    threads = os.environ.get("OMP_NUM_THREADS") or str(os.cpu_count())
-    return {"value": round(1.0 / est, 3), "unit": "tok/s", "cores": int(threads), "kind": "port",
-            "sample": f"NumPy oracle decode step, batch 1, 2 of 28 layers + LM head at position 2048 "
-                      f"(dequant cached), {n} trials, per-layer time x28 + LM head"}
+    out = {}
+    for B in (1, 16):
+        ks = [(0.5 * rng.standard_normal((B, 2304, 2, 128))).astype(np.float16) for _ in range(2)]
+        vs = [(0.5 * rng.standard_normal((B, 2304, 2, 128))).astype(np.float16) for _ in range(2)]
+        toks, pos = list(range(1, B + 1)), [2048] * B
+        cache = {}
+        ost.decode_step(model, toks, pos, ks, vs, cache)  # warm: dequantise once
+        steps, lms = [], []
+        hn = np.ones((B, cfg.hidden), np.float32)
+        for _ in range(trials):
+            s = time.perf_counter()
+            ost.decode_step(model, toks, pos, ks, vs, cache)
+            steps.append(time.perf_counter() - s)
+            s = time.perf_counter()
+            hn @ cache["lm"].T
+            lms.append(time.perf_counter() - s)
+        lm = float(np.median(lms))
+        per_step = [lm + (t - lm) / 2 * 28 for t in steps]  # 2 layers -> 28
+        out[B] = {"tok_s": _stats([B / t for t in per_step]), "step_s": _stats(per_step)}
+        del cache
+    gemv = []
+    for fmt, n, k, _ in GEMV_CONFIGS[:4]:
+        raw = syn.random_matrix(fmt, np.random.default_rng(42), n, k)
+        x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
+        nt = trials if n * k < 50_000_000 else max(3, trials - 2)
+        td, tm = [], []
+        for _ in range(nt):
+            s = time.perf_counter()
+            w = odq.dequantize_matrix(fmt, raw, n, k)
+            td.append(time.perf_counter() - s)
+            s = time.perf_counter()
+            w @ x
+            tm.append(time.perf_counter() - s)
+        del w
+        algo = raw.nbytes + 4 * (n + k)
+        gemv.append({"shape": f"{n}x{k}", "fmt": fmt, "dequant_ms": _stats([1e3 * t for t in td]),
+                     "matvec_ms": _stats([1e3 * t for t in tm]),
+                     "total_ms_median": round(1e3 * (float(np.median(td)) + float(np.median(tm))), 3),
+                     "GBps_median": round(algo / (float(np.median(td)) + float(np.median(tm))) / 1e9, 2)})
+    attn = []
+    for ctx in (512, 4096, 32768):
+        q = rng.standard_normal((12, 128)).astype(np.float32)
+        kc = (0.5 * rng.standard_normal((ctx, 2, 128))).astype(np.float16)
+        vc = (0.5 * rng.standard_normal((ctx, 2, 128))).astype(np.float16)
+        ts = []
+        for _ in range(trials):
+            s = time.perf_counter()
+            attention_ref(q, kc, vc, ctx, 1 / np.sqrt(128))
+            ts.append(time.perf_counter() - s)
+        attn.append({"ctx": ctx, "ms": _stats([1e3 * t for t in ts])})
+    return {"value": out[1]["tok_s"]["median"], "unit": "tok/s", "cores": info["blas_threads"], "kind": "port",
+            "sample": "NumPy oracle (oracle/) on the host: decode step = 2 of 28 layers + LM head at position "
+                      f"2048, dequant cached, x28; {trials} trials each (median); GEMV configs 0/1 dequant and "
+                      "mat-vec separately; attention config 2",
+            "tok_s_b1": out[1]["tok_s"], "tok_s_b16": out[16]["tok_s"], "gemv": gemv, "attention": attn,
+            "host": info, "wall_s": round(time.perf_counter() - t_start, 1)}
+
+
+def hbm_copy_bandwidth(hip, nbytes=1 << 30, reps=10):
+    """Device-to-device copy of nbytes (read + write), median GB/s of (2 x nbytes) / time."""
+    from vte_amd.bridge import DeviceArray
+    a = DeviceArray(hip, nbytes, np.uint8, "copy_src")
+    b = DeviceArray(hip, nbytes, np.uint8, "copy_dst")
+    a.zero()
+    hip.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = _events(hip)
+        hip.event_record(e0)
+        hip.memcpy_device_to_device(b.ptr, a.ptr, nbytes)
+        hip.event_record(e1)
+        hip.synchronize()
+        ts.append(hip.event_elapsed_ms(e0, e1))
+    a.free()
+    b.free()
+    return round(2 * nbytes / (float(np.median(ts)) * 1e-3) / 1e9, 1)
 
 
 def profile_step(B, steps, prefix=2048, classes=None):
@@ -464,6 +559,8 @@ def main():
         line["attention"] = attn
     if prefill:
         line["prefill"] = prefill
+    line["hbm_copy_GBps"] = hbm_copy_bandwidth(hip)
+    line["hbm_peak_GBps"] = HBM_PEAK_GBPS
     line["roofline"] = roof
     line["step_breakdown_b1"] = breakdown
     if cpu:

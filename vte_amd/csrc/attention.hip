@@ -37,15 +37,6 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 #define ATT_MAX_SPLITS 4096  // splits per sequence the separate combine handles
 #define ATT_VT_STRIDE 36     // halves per row of the transposed V tile (32 tokens + pad)
 
-#ifdef ATT_TRACE
-__device__ unsigned long long att_trace[4096][8];
-__device__ unsigned long long comb_trace[4096][2];
-#define CMB_TS(k) do { if (threadIdx.x == 0) { const int bi = blockIdx.x + gridDim.x * blockIdx.y; if (bi < 4096) comb_trace[bi][k] = wall_clock64(); } } while (0)
-#define ATT_TS(k) do { if (threadIdx.x == 0) { const int bi = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); if (bi < 4096) { att_trace[bi][k] = wall_clock64(); if (k == 0) { att_trace[bi][4] = __builtin_amdgcn_s_getreg(4 | (31 << 11)); att_trace[bi][5] = __builtin_amdgcn_s_getreg(20 | (31 << 11)); } } } } while (0)
-#else
-#define ATT_TS(k) do { } while (0)
-#define CMB_TS(k) do { } while (0)
-#endif
 
 // ---------------------------------------------------------------------------
 // KV append (reference ABI, vte/compiler/templates/rdna/kv_cache_append.hip.template:13-39)
@@ -214,7 +205,6 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int sp = PW ? blockIdx.x * ATT_WAVES + wv : blockIdx.x, kvh = blockIdx.y, b = QC * blockIdx.z;
     if (PW && sp >= max_splits) return;
-    ATT_TS(0);
     const int t_begin = sp * split;
     const int G = n_q / n_kv;
     const int col = lane & 15;   // head (MFMA N index) / token row (A operand)
@@ -278,7 +268,6 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);
         if (TPW == 2) att_load_tile(T1, kb, vb, row_stride, t0 + ATT_WAVES * ATT_TILE, t_end - 1, col, grp, lane);
     }
-    ATT_TS(1);
     if (t0 < t_end) att_tile_step<true>(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp, t_end_col);
     if (PW) {  // the wave's split is done: its statistics and outputs are the partials
         l_run += __shfl_xor(l_run, 16, 64);
@@ -307,7 +296,6 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         att_tile_step<false>(T, t0, t_end, qb, scale, m_run, l_run, o_acc, vt_sh[wv], lane, col, grp, t_end_col);
     }
 
-    ATT_TS(2);
     // ---- combine the four waves of this block ----
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
@@ -338,7 +326,6 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         part_o[st * ATT_D + d] = O;
         if (d == 0) { part_m[st] = M; part_l[st] = L; }
     }
-    ATT_TS(3);
     if (QC > 1 || counters == nullptr) return;  // separate combine launch
 
     // ---- last block of this (sequence, KV head) performs the LSE combine ----
@@ -436,7 +423,6 @@ __global__ __launch_bounds__(256) void attn_combine_wide(const float* __restrict
     __shared__ float osum[8][33];
     const int qh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int dl = tid & 31, g = tid >> 5, d = blockIdx.z * 32 + dl;
-    CMB_TS(0);
     const int len = kv_offset[b] + 1;
     const int ns = (len + split - 1) / split;
     const size_t base = ((size_t)b * n_q + qh) * max_splits;
@@ -487,7 +473,6 @@ __global__ __launch_bounds__(256) void attn_combine_wide(const float* __restrict
         for (int j = 0; j < 8; ++j) t += osum[j][dl];
         st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, t / fmaxf(L, 1e-20f));
     }
-    CMB_TS(1);
 }
 
 // ---------------------------------------------------------------------------
@@ -577,7 +562,6 @@ __global__ __launch_bounds__(128) void attn_combine_small(const float* __restric
                                                           int max_splits) {
     constexpr int PL = NSMAX > 64 ? 2 : 1;  // splits per lane
     const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x, lane = d & 63;
-    CMB_TS(0);
     const size_t base = ((size_t)b * n_q + qh) * max_splits;
     const int len_raw = kv_offset[b];
     float m_l[PL], l_l[PL];
@@ -613,7 +597,6 @@ __global__ __launch_bounds__(128) void attn_combine_small(const float* __restric
         O = c < ns ? fmaf(o[c], wc, O) : O;
     }
     st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(L, 1e-20f));
-    CMB_TS(1);
 }
 
 // ---------------------------------------------------------------------------
@@ -701,11 +684,3 @@ hipError_t kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
 
 }  // namespace vte
 
-#ifdef ATT_TRACE
-extern "C" int vte_dbg_comb_trace_read(void* host, int blocks) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(comb_trace), (size_t)blocks * 16, 0, hipMemcpyDeviceToHost);
-}
-extern "C" int vte_dbg_att_trace_read(void* host, int blocks) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(att_trace), (size_t)blocks * 64, 0, hipMemcpyDeviceToHost);
-}
-#endif

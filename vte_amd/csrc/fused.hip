@@ -239,8 +239,3 @@ hipError_t stream_mv(int fmt, bool in_f32, bool out_f32, const void* x, const vo
 
 }  // namespace vte
 
-#ifdef TMV_TRACE
-extern "C" int vte_dbg_trace_read(void* host, int blocks) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(tmv_trace), (size_t)blocks * 64, 0, hipMemcpyDeviceToHost);
-}
-#endif

@@ -37,17 +37,6 @@
 #define TMV_MAX_SEG 3
 #define TMV_MAX_R 64
 
-#ifdef TMV_MARK
-#define TMV_M(n) asm volatile("; TMVMARK " #n)
-#else
-#define TMV_M(n) do { } while (0)
-#endif
-#ifdef TMV_TRACE
-__device__ unsigned long long tmv_trace[8192][8];
-#define TMV_TS(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) tmv_trace[blockIdx.x][k] = wall_clock64(); } while (0)
-#else
-#define TMV_TS(k) do { } while (0)
-#endif
 
 enum FmvMode : int {
     FMV_STORE_F16 = 0,   // out[m][row] = fp16((acc + bias) * rs + residual)
@@ -663,13 +652,6 @@ __device__ __forceinline__ void tile_dot(const TileW<UPT>& W, int nr, int per_ro
         }
         if (up.lr < nr) {
             const int u = up.lr * per_row + up.kr;
-#ifdef TMV_ABL_DOT
-            if (true) {
-                part[u] = __uint_as_float((W.w0[i].x ^ W.w1[i].y ^ W.w2[i].z ^ W.w0[i].w ^ W.w1[i].x ^ W.w2[i].w ^
-                                           W.dbits[i] ^ W.sc8[i].x) & 0x3fffffffu) + __uint_as_float(x[0][0].x) +
-                          xs16[0][0];
-            } else
-#endif
             if (FMT == 4) {
                 const Q4KUnitData d{W.w0[i], W.w1[i], W.w2[i]};
 #pragma unroll
@@ -808,10 +790,7 @@ __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const F
     }
     if (tid < M) pos_s[tid] = pos_reg;
     __syncthreads();
-    TMV_TS(1);
-    TMV_M(3);
     issue();
-    TMV_M(4);
 
     if constexpr (att_src) {
         if constexpr (KC > 0 && KC % ROWS_THREADS == 0) stage_combine_fast<NC, KC>(P, L.xs, wb, pos_s, tid);
@@ -859,7 +838,6 @@ __device__ __forceinline__ void fmv_prologue(const void* __restrict__ x, const F
         }
     }
     __syncthreads();
-    TMV_TS(2);
 }
 
 // One tile per block (grid = tiles): everything a block reads is requested
@@ -873,36 +851,18 @@ __device__ __forceinline__ void tmv_body(const void* __restrict__ x, const FmvPl
     const int pstride = UPT * ROWS_THREADS;
     float* wb = L.part + (size_t)NC * pstride;
     const int tid = threadIdx.x;
-    TMV_TS(0);
-    TMV_M(1);
     const void* dummy = P.seg[0].w;
     TileE E;
     tile_e_issue<NC>(E, P, T, M, dummy, tid);
-    TMV_M(2);
     TileW<UPT> W;
     if constexpr (WF) tile_w_issue<UPT, FMT, RO>(W, T, n_sb, per_row, tid);
     fmv_prologue<NC, F32, KC, ATT>(x, P, L, wb, red, pos_s, [&]() {
         if constexpr (!WF) tile_w_issue<UPT, FMT, RO>(W, T, n_sb, per_row, tid);
         tile_e_rope(E, P, T, pos_s[E.em], dummy);  // kv offsets are in LDS after the first barrier
     });
-    TMV_M(5);
     tile_dot<NC, UPT, FMT, RO>(W, T.nr, per_row, K, L.xs, L.s16, L.part, pstride, tid);
-    TMV_M(6);
     __syncthreads();
-    TMV_TS(3);
-#ifdef TMV_TRACE
-    if (tid == 0 && blockIdx.x < 8192) {
-        unsigned hw;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
-        unsigned xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        tmv_trace[blockIdx.x][5] = ((unsigned long long)xcc << 32) | hw;
-        tmv_trace[blockIdx.x][4] = wall_clock64();
-    }
-#endif
-    TMV_M(7);
     tile_epilogue<NC>(P, T, E, L.part, pstride, per_row, pos_s);
-    TMV_M(8);
 }
 
 // KC: the activation length K when fixed at compile time (0: P.K), so the

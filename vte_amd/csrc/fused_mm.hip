@@ -24,15 +24,6 @@
 
 #define MM_MAX_SEG 3
 
-#ifdef MM_TRACE
-__device__ unsigned long long mm_trace[8192][8];
-#define MM_TS(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) mm_trace[blockIdx.x][k] = wall_clock64(); } while (0)
-extern "C" int vte_dbg_mm_trace_read(void* host, int blocks) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(mm_trace), (size_t)blocks * 64, 0, hipMemcpyDeviceToHost);
-}
-#else
-#define MM_TS(k) do { } while (0)
-#endif
 
 enum MmMode : int {
     MM_STORE = 0,        // out[m][row] = fp16(acc + bias)
@@ -147,12 +138,6 @@ __device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float 
                 bx[t][nt] = load_x8<__half>(x + (size_t)(m < M ? m : 0) * K + kb, m < M);
             }
         }
-#ifdef MM_TRACE
-        if (sb == sb0 && threadIdx.x == 0) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            MM_TS(1);
-        }
-#endif
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             typename SbRaw<FMT>::Raw raw;
@@ -236,23 +221,13 @@ __device__ __forceinline__ void mm_epilogue(const MmPlan& P, const MmTile& T, fl
 template <int RT, int NT, int NW>
 __global__ __launch_bounds__(64 * NW) void fused_mm_kernel(MmPlan P) {
     __shared__ float red[NW][RT][NT][4][64];
-    MM_TS(0);
     const MmTile T = mm_tile<RT>(P, blockIdx.x);
     const MmSeg& S = *T.S;
     if (S.fmt == 4) mm_body<4, RT, NT, NW>(P, T, red);
     else mm_body<6, RT, NT, NW>(P, T, red);
-    MM_TS(2);
     __syncthreads();
-    MM_TS(3);
-#ifdef MM_TRACE
-    if (threadIdx.x == 0 && blockIdx.x < 8192) {
-        mm_trace[blockIdx.x][5] = __builtin_amdgcn_s_getreg(4 | (31 << 11));
-        mm_trace[blockIdx.x][6] = __builtin_amdgcn_s_getreg(20 | (31 << 11));
-    }
-#endif
 
     mm_epilogue<RT, NT, NW>(P, T, red, 0, P.M);
-    MM_TS(4);
 }
 
 

@@ -300,15 +300,6 @@ extern "C" __global__ __launch_bounds__(256) void embedding_lookup_q6k_kernel(
 #define TOPK_P 64
 #define TOPK_SLICE 4096
 #define TOPK_CAP 128  // candidate slots per slice
-#ifdef TK_TRACE
-__device__ unsigned long long tk_trace[2][128][8];
-#define TK_TS(kern, k) do { if (threadIdx.x == 0) tk_trace[kern][blockIdx.x & 127][k] = wall_clock64(); } while (0)
-extern "C" int vte_dbg_tk_trace_read(void* host) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(tk_trace), sizeof(tk_trace), 0, hipMemcpyDeviceToHost);
-}
-#else
-#define TK_TS(kern, k) do { } while (0)
-#endif
 #define TOPK_THREADS 256
 #define TOPK_BINS 2048
 
@@ -397,7 +388,6 @@ __device__ uint32_t tk_radix_select(const uint32_t* keys, int n, int need, TkSha
         mask |= (uint32_t)(nb - 1) << shift;
         need = sh.sel_need;
         __syncthreads();
-        TK_TS(gridDim.y > 1 ? 0 : (gridDim.x > 1 ? 0 : 1), 2 + r);
     }
     need_eq = need;
     return prefix;
@@ -492,7 +482,6 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_partial_kernel(const float*
     __shared__ uint32_t wt[TOPK_THREADS / 64];
     __shared__ uint32_t xmask[TOPK_SLICE / 32];
     const int row = blockIdx.y, p = blockIdx.x, tid = threadIdx.x;
-    TK_TS(0, 0);
     const int lo = p * slice, n = max(0, min(slice, vocab - lo));
     const float* r = logits + (size_t)row * vocab + lo;
     // entry j * 256 + tid of the slice in register j (all loads issued at once)
@@ -526,7 +515,6 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_partial_kernel(const float*
         kr[j] = ok && !xd ? tk_key(v[j]) : 0u;
         tm = ok ? max(tm, kr[j]) : tm;
     }
-    TK_TS(0, 1);
     const size_t o = ((size_t)row * gridDim.x + p) * TOPK_CAP;
     if (n <= 64) {
         if (tid < n) cand[o + tid] = tk_pack(kr[0], lo + tid);
@@ -535,7 +523,6 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_partial_kernel(const float*
     }
     // n > 64 >= k: every wave's ceil(k/4) largest maxima are entries' keys
     const uint32_t T = tk_block_threshold(tm, k, wt);
-    TK_TS(0, 2);
     int c = 0;
 #pragma unroll
     for (int j = 0; j < TKR; ++j) c += (j * TOPK_THREADS + tid < n && kr[j] >= T) ? 1 : 0;
@@ -551,7 +538,6 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_partial_kernel(const float*
             }
         }
         if (tid == 0) cand_cnt[(size_t)row * gridDim.x + p] = total;
-        TK_TS(0, 5);
         return;
     }
     // many entries tie at the top: exact selection of the slice's best 64
@@ -596,7 +582,6 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint64_t
     __shared__ int si[TOPK_THREADS];
     __shared__ uint32_t wt[TOPK_THREADS / 64];
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-    TK_TS(1, 0);
     // every slot's candidate and its slice's count requested at once; slots
     // past their slice's count are invalid (no compaction on the common path).
     // Slot j of a thread: slice 2j + tid / 128, offset (tid + 37 j) mod 128,
@@ -620,11 +605,9 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint64_t
     }
     // total candidates (each wave sums the slice counts itself)
     const int n = (int)wave_sum((float)(lane < P ? cand_cnt[(size_t)row * P + lane] : 0));
-    TK_TS(1, 1);
     // n > 256: every thread holds a candidate, so each wave's ceil(k/4)
     // largest maxima are candidates' keys and at least k candidates are >= T
     const uint32_t T = n > TOPK_THREADS ? tk_block_threshold(tm, k, wt) : 0u;
-    TK_TS(1, 2);
     int c = 0;
 #pragma unroll
     for (int j = 0; j < NS; ++j) c += ((cvm >> j) & 1u) && ck[j] >= T ? 1 : 0;
@@ -664,7 +647,6 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint64_t
                 out_idx[(size_t)row * k + rank] = si[tid];
             }
         }
-        TK_TS(1, 6);
         return;
     }
     // many ties at the top: compact every candidate into keys[0 .. n) ...
@@ -692,7 +674,6 @@ __global__ __launch_bounds__(TOPK_THREADS) void topk_final_kernel(const uint64_t
     int need_eq;
     const uint32_t T64 = tk_radix_select(keys, n, 64, sh, need_eq);
     const int kept = tk_compact(keys, n, T64, need_eq, pos, sh);
-    TK_TS(1, 5);
     if (tid < 64) {
         uint32_t kk = 0;
         int ix = 0x7fffffff;
