@@ -151,8 +151,10 @@ def time_e2e(hip, ex, steps, start_pos):
     return (time.perf_counter() - t0) / steps
 
 
-def gemv_bench(hip, K, fmt, n, k, launches=200, pool_bytes=768 << 20, mfma_batch=0):
-    """Average kernel time over a rotating cold pool; returns dict with GB/s."""
+def gemv_bench(hip, K, fmt, n, k, launches=200, pool_bytes=768 << 20, mfma_batch=0, in_dtype="f32"):
+    """Average kernel time over a rotating cold pool; returns dict with GB/s.
+    Activations fp32 (the BASELINE configs) or fp16 (as inside the decode step);
+    the output is fp32."""
     from vte_amd import synthetic as syn
     from vte_amd.bridge import DeviceArray
     raw = syn.random_matrix(fmt, np.random.default_rng(42), n, k)
@@ -163,10 +165,11 @@ def gemv_bench(hip, K, fmt, n, k, launches=200, pool_bytes=768 << 20, mfma_batch
     for c in range(copies):
         hip.memcpy_device_to_device(pool.ptr + c * stride, first.ptr, stride)
     M = max(1, mfma_batch)
-    x = DeviceArray.from_numpy(hip, np.random.default_rng(1).standard_normal((M, k)).astype(np.float32), "x")
+    xdt = np.float32 if in_dtype == "f32" else np.float16
+    x = DeviceArray.from_numpy(hip, np.random.default_rng(1).standard_normal((M, k)).astype(xdt), "x")
     y = DeviceArray(hip, (M, n), np.float32, "y")
-    run = (lambda w: K.gemm_mfma(fmt, x, w, y, M, k, n, stream=hip.stream)) if mfma_batch else \
-          (lambda w: K.gemv(fmt, x, w, y, M, k, n, stream=hip.stream))
+    run = (lambda w: K.gemm_mfma(fmt, x, w, y, M, k, n, in_dtype=in_dtype, stream=hip.stream)) if mfma_batch else \
+          (lambda w: K.gemv(fmt, x, w, y, M, k, n, in_dtype=in_dtype, stream=hip.stream))
     # launches captured into one graph (as inside the decode step), each on the
     # next cold copy of the weights
     hip.synchronize()
@@ -184,10 +187,10 @@ def gemv_bench(hip, K, fmt, n, k, launches=200, pool_bytes=768 << 20, mfma_batch
     ms = hip.event_elapsed_ms(e0, e1) / launches
     hip.graph_exec_destroy(gexec)
     hip.graph_destroy(graph)
-    algo = raw.nbytes + M * k * 4 + M * n * 4
+    algo = raw.nbytes + M * k * np.dtype(xdt).itemsize + M * n * 4
     for d in (pool, first, x, y):
         d.free()
-    return {"shape": f"{n}x{k}", "fmt": fmt, "batch": M, "us": round(ms * 1e3, 3),
+    return {"shape": f"{n}x{k}", "fmt": fmt, "batch": M, "x": in_dtype, "us": round(ms * 1e3, 3),
             "algo_bytes": int(algo), "GBps": round(algo / (ms * 1e-3) / 1e9, 1),
             "frac_hbm_peak": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
 
