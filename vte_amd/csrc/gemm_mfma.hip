@@ -179,13 +179,12 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
 // >= 8).  Persistent 8-wave blocks, two per CU; the batch's activations are staged once
 // per block in LDS as fp16 rows padded by 16 bytes (the 16 lanes of an MFMA
 // B-operand read hit distinct banks); each wave then owns whole 16-row
-// tiles: it requests the raw bytes of all six super-blocks of its rows at
-// once, dequantises them into A operands and runs the K loop with the B
-// operands read from LDS, so a tile needs no cross-wave reduction and no
+// tiles: it requests the raw bytes of its rows' super-blocks (16-byte loads),
+// turns them into exact weight operands and runs the K loop with the
+// activation operands read from LDS, so a tile needs no cross-wave reduction and no
 // barrier, and the waves of a CU keep their loads in flight independently
-// (three super-blocks ahead).  Its time is mostly the Q6_K dequantisation
-// VALU (measured: 85 us for 151936 x 1536 at batch 16, 44 us with the
-// dequantisation replaced by raw bits).
+// (three super-blocks ahead).  Measured at batch 16 on 151936 x 1536 Q6_K:
+// 71 us, its waves waiting on memory for more than half of their cycles.
 // ---------------------------------------------------------------------------
 #define GS_K 1536
 #define GS_NSB (GS_K / QK_K)

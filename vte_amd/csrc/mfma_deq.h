@@ -24,8 +24,9 @@
 //    slots are 8 contiguous elements sharing one sub-block scale:
 //      Q4_K step t, group g: qs chunk c = g + 4*(t>>2), nibble (t>>1)&1, half t&1
 //           (sub-block 2 * ((g>>1) + 2*(t>>2)) + ((t>>1)&1); steps 2s, 2s+1 share one)
-//      Q6_K step t, group g: half h = t>>2, quarter q = t&3, l = 8g .. 8g+7
-//           (16-element sub-block 8h + 2q + (g>>1))
+//      Q6_K step t, group g: half h = g>>1, quarter q = t>>1, l = 16 (g&1) + 8 (t&1) .. +7
+//           (16-element sub-block 8h + 2q + (g&1)); a lane's codes for all 8
+//           steps come from three 16-byte runs of its row's block (ql, ql + 32, qh)
 #pragma once
 #include <cstdlib>
 #include "quant.h"
@@ -86,7 +87,7 @@ __device__ __forceinline__ int kslot_base(int t, int g) {
         const int c = g + 4 * (t >> 2);
         return 64 * (c >> 1) + 16 * (c & 1) + 32 * ((t >> 1) & 1) + 8 * (t & 1);
     } else {
-        return 128 * (t >> 2) + 32 * (t & 3) + 8 * g;
+        return 128 * (g >> 1) + 32 * (t >> 1) + 16 * (g & 1) + 8 * (t & 1);
     }
 }
 
@@ -103,18 +104,22 @@ __device__ __forceinline__ uint2 q6_ld8(const uint8_t* p) {
 // A lane's raw bytes of one Q6_K super-block (both halves), loaded ahead of
 // the dequantisation so several super-blocks can be in flight.
 struct Q6Raw {
-    uint2 qa[2], qb[2], qh[2], sc[2];
+    uint4 la, lb, hq;  // ql[64h + 16j ..], ql[64h + 32 + 16j ..], qh[32h + 16j ..] (h = g>>1, j = g&1)
+    uint2 sc;          // scales 8h .. 8h+7
     uint32_t d;
 };
+__device__ __forceinline__ uint4 q6_ld16(const uint8_t* p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
 __device__ __forceinline__ void q6_raw_load(const uint8_t* blk, int grp, Q6Raw& r) {
+    const int h = grp >> 1, j = grp & 1;
+    r.la = q6_ld16(blk + 64 * h + 16 * j);
+    r.lb = q6_ld16(blk + 64 * h + 32 + 16 * j);
+    r.hq = q6_ld16(blk + 128 + 32 * h + 16 * j);
+    r.sc = q6_ld8(blk + 192 + 8 * h);
     r.d = ((const __attribute__((address_space(1))) uint16_t*)(blk + 208))[0];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        r.qa[hh] = q6_ld8(blk + 64 * hh + 8 * grp);
-        r.qb[hh] = q6_ld8(blk + 64 * hh + 32 + 8 * grp);
-        r.qh[hh] = q6_ld8(blk + 128 + 32 * hh + 8 * grp);
-        r.sc[hh] = q6_ld8(blk + 192 + 8 * hh);
-    }
 }
 // Exact operands of one super-block for one lane: the 8 k-steps' weight
 // operands and the fp32 scales (Q4_K: also the 4 sub-block minima, splat).
@@ -130,36 +135,30 @@ struct Q4Ops {
 
 __device__ __forceinline__ void q6_exact_operands(const Q6Raw& r, int grp, Q6Ops& o) {
     o.d = h2f_bits(r.d);
+    const uint32_t la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
+    const uint32_t lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+    const uint32_t hq[4] = {r.hq.x, r.hq.y, r.hq.z, r.hq.w};
+    const uint64_t sc = ((uint64_t)r.sc.y << 32) | r.sc.x;
+    const int j = grp & 1;
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const uint2 qa = r.qa[hh], qb = r.qb[hh], qh = r.qh[hh], scw = r.sc[hh];
-        const uint64_t sc = ((uint64_t)scw.y << 32) | scw.x;
+    for (int t = 0; t < 8; ++t) {
+        const int q = t >> 1, w0 = 2 * (t & 1);  // quarter; first code word of the step's 8 codes
+        uint32_t u[2];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint32_t u0, u1;
-            if (q == 0) {
-                u0 = (qa.x & 0x0F0F0F0Fu) | ((qh.x << 4) & 0x30303030u);
-                u1 = (qa.y & 0x0F0F0F0Fu) | ((qh.y << 4) & 0x30303030u);
-            } else if (q == 1) {
-                u0 = (qb.x & 0x0F0F0F0Fu) | ((qh.x << 2) & 0x30303030u);
-                u1 = (qb.y & 0x0F0F0F0Fu) | ((qh.y << 2) & 0x30303030u);
-            } else if (q == 2) {
-                u0 = ((qa.x >> 4) & 0x0F0F0F0Fu) | (qh.x & 0x30303030u);
-                u1 = ((qa.y >> 4) & 0x0F0F0F0Fu) | (qh.y & 0x30303030u);
-            } else {
-                u0 = ((qb.x >> 4) & 0x0F0F0F0Fu) | ((qh.x >> 2) & 0x30303030u);
-                u1 = ((qb.y >> 4) & 0x0F0F0F0Fu) | ((qh.y >> 2) & 0x30303030u);
-            }
-            const float scq = (float)(int8_t)((sc >> (8 * ((grp >> 1) + 2 * q))) & 0xFF);
-            // (1024 + u) - 1056 = u - 32 exactly, then one multiply by the integer scale
-            H8 v;
-            bytes_to_f16magic(u0, v.u[0], v.u[1]);
-            bytes_to_f16magic(u1, v.u[2], v.u[3]);
-            const half2_t off = splat2(-1056.0f), s2 = splat2(scq);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v.h2[i] = (v.h2[i] + off) * s2;
-            o.w[4 * hh + q] = v.v;
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t l = (q & 1) ? lb[w0 + e] : la[w0 + e];
+            const uint32_t nib = (q < 2) ? (l & 0x0F0F0F0Fu) : ((l >> 4) & 0x0F0F0F0Fu);
+            u[e] = nib | (((hq[w0 + e] >> (2 * q)) & 0x03030303u) << 4);
         }
+        const float scq = (float)(int8_t)((sc >> (8 * (2 * q + j))) & 0xFF);
+        // (1024 + u) - 1056 = u - 32 exactly, then one multiply by the integer scale
+        H8 v;
+        bytes_to_f16magic(u[0], v.u[0], v.u[1]);
+        bytes_to_f16magic(u[1], v.u[2], v.u[3]);
+        const half2_t off = splat2(-1056.0f), s2 = splat2(scq);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v.h2[i] = (v.h2[i] + off) * s2;
+        o.w[t] = v.v;
     }
 }
 
