@@ -111,7 +111,9 @@ __device__ __forceinline__ const uint8_t* mm_row(const MmTile& T, int rr) {
 }
 
 template <int FMT, int RT, int NT, int NW>
-__device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64]) {
+__device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64],
+                                        float (*xl)[NT * 128]) {
+    constexpr bool XM = NT > 1;  // minimum-term form (q4_xmin)
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int K = P.K, M = P.M, n_sb = K / QK_K;
@@ -138,13 +140,19 @@ __device__ __forceinline__ void mm_body(const MmPlan& P, const MmTile& T, float 
                 bx[t][nt] = load_x8<__half>(x + (size_t)(m < M ? m : 0) * K + kb, m < M);
             }
         }
+        // weights requested before the minimum-term LDS round trip, whose
+        // memory clobber would otherwise hold them back
+        typename SbRaw<FMT>::Raw raw[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            sb_load(rowp[rt] + (size_t)sb * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES), grp, raw[rt]);
+        XMin<NT, XM> xm;
+        sb_xmin<FMT, NT, XM>(bx, xl[wv], xm);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-            typename SbRaw<FMT>::Raw raw;
-            sb_load(rowp[rt] + (size_t)sb * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES), grp, raw);
             typename SbRaw<FMT>::Ops ops;
-            sb_ops(raw, grp, ops);
-            sb_mfma<NT>(ops, bx, acc[rt]);
+            sb_ops<XM>(raw[rt], grp, ops);
+            sb_mfma<NT>(ops, bx, xm, acc[rt]);
         }
     }
 #pragma unroll
@@ -221,10 +229,11 @@ __device__ __forceinline__ void mm_epilogue(const MmPlan& P, const MmTile& T, fl
 template <int RT, int NT, int NW>
 __global__ __launch_bounds__(64 * NW) void fused_mm_kernel(MmPlan P) {
     __shared__ float red[NW][RT][NT][4][64];
+    __shared__ float xl[NW][NT * 128];  // minimum-term scratch per wave (q4_xmin)
     const MmTile T = mm_tile<RT>(P, blockIdx.x);
     const MmSeg& S = *T.S;
-    if (S.fmt == 4) mm_body<4, RT, NT, NW>(P, T, red);
-    else mm_body<6, RT, NT, NW>(P, T, red);
+    if (S.fmt == 4) mm_body<4, RT, NT, NW>(P, T, red, xl);
+    else mm_body<6, RT, NT, NW>(P, T, red, xl);
     __syncthreads();
 
     mm_epilogue<RT, NT, NW>(P, T, red, 0, P.M);
@@ -239,8 +248,10 @@ __global__ __launch_bounds__(64 * NW) void fused_mm_kernel(MmPlan P) {
 // its eight k-steps in the same order as fused_mm_kernel, so both forms give
 // the same bits.
 template <int FMT, int RT, int NT>
-__device__ __forceinline__ void mm_ws_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64], int c0,
+__device__ __forceinline__ void mm_ws_body(const MmPlan& P, const MmTile& T, float (*red)[RT][NT][4][64],
+                                           float (*xl)[NT * 128], int c0,
                                            int c1) {
+    constexpr bool XM = true;  // minimum-term form (q4_xmin)
     constexpr int NW = 6;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -251,7 +262,7 @@ __device__ __forceinline__ void mm_ws_body(const MmPlan& P, const MmTile& T, flo
         const uint8_t* rowp = mm_row<RT>(T, rt * 16 + col);
         typename SbRaw<FMT>::Raw raw;
         sb_load(rowp + (size_t)wv * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES), grp, raw);
-        sb_ops(raw, grp, ops[rt]);
+        sb_ops<XM>(raw, grp, ops[rt]);
     }
     half8_t bx[8][NT];
     auto load_b = [&](int m0) {
@@ -272,8 +283,10 @@ __device__ __forceinline__ void mm_ws_body(const MmPlan& P, const MmTile& T, flo
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        XMin<NT, XM> xm;
+        sb_xmin<FMT, NT, XM>(bx, xl[wv], xm);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) sb_mfma<NT>(ops[rt], bx, acc[rt]);
+        for (int rt = 0; rt < RT; ++rt) sb_mfma<NT>(ops[rt], bx, xm, acc[rt]);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -290,11 +303,12 @@ __device__ __forceinline__ void mm_ws_body(const MmPlan& P, const MmTile& T, flo
 template <int RT, int NT>
 __global__ __launch_bounds__(64 * 6) void fused_mm_ws_kernel(MmPlan P, int cols) {
     __shared__ float red[6][RT][NT][4][64];
+    __shared__ float xl[6][NT * 128];
     const MmTile T = mm_tile<RT>(P, blockIdx.x);
     const int c0 = blockIdx.y * cols, c1 = min(P.M, c0 + cols);
     if (c0 >= c1) return;
-    if (T.S->fmt == 4) mm_ws_body<4, RT, NT>(P, T, red, c0, c1);
-    else mm_ws_body<6, RT, NT>(P, T, red, c0, c1);
+    if (T.S->fmt == 4) mm_ws_body<4, RT, NT>(P, T, red, xl, c0, c1);
+    else mm_ws_body<6, RT, NT>(P, T, red, xl, c0, c1);
 }
 
 namespace vte {
@@ -358,11 +372,14 @@ static hipError_t mm_run(MmPlan P, int B, size_t out_ld_elems[MM_MAX_SEG], hipSt
         for (int s = 0; s < P.nseg; ++s) P.seg[s].out = out0[s] ? out0[s] + (size_t)m0 * out_ld_elems[s] : nullptr;
         P.k_cache = kc0 ? kc0 + (size_t)m0 * P.kv_batch_stride : nullptr;
         P.v_cache = vc0 ? vc0 + (size_t)m0 * P.kv_batch_stride : nullptr;
+        // batches above 16 columns take the two-tile form for every chunk, a
+        // short tail included, so all their columns share the minimum-term
+        // form (and the bits) of the weight-stationary launch
         if (P.K == 6 * QK_K) {
-            if (mc > 16) hipLaunchKernelGGL((fused_mm_kernel<RT, 2, 6>), dim3(total), dim3(64 * 6), 0, st, P);
+            if (B > 16) hipLaunchKernelGGL((fused_mm_kernel<RT, 2, 6>), dim3(total), dim3(64 * 6), 0, st, P);
             else hipLaunchKernelGGL((fused_mm_kernel<RT, 1, 6>), dim3(total), dim3(64 * 6), 0, st, P);
         } else {
-            if (mc > 16) hipLaunchKernelGGL((fused_mm_kernel<RT, 2, MF_WAVES>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
+            if (B > 16) hipLaunchKernelGGL((fused_mm_kernel<RT, 2, MF_WAVES>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
             else hipLaunchKernelGGL((fused_mm_kernel<RT, 1, MF_WAVES>), dim3(total), dim3(64 * MF_WAVES), 0, st, P);
         }
         const hipError_t e = hipGetLastError();

@@ -27,7 +27,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
                                                         TO* __restrict__ y, int M, int K, int N,
                                                         const TO* __restrict__ bias, const TO* __restrict__ residual,
                                                         float rs, size_t split_stride) {
+    constexpr bool XM = NT > 1;  // minimum-term form (q4_xmin)
     __shared__ float red[NW][RT][NT][4][64];
+    __shared__ float xl[NW][NT * 128];  // minimum-term scratch per wave (q4_xmin)
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -59,14 +61,21 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
                 bx[t][nt] = load_x8<TI>(x + (size_t)(m < M ? m : 0) * K + kb, m < M);
             }
         }
+        // weights requested before the minimum-term LDS round trip, whose
+        // memory clobber would otherwise hold them back
+        typename SbRaw<FMT>::Raw raw[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const int r = min(row0 + rt * 16 + col, N - 1);
-            typename SbRaw<FMT>::Raw raw;
-            sb_load(w + (size_t)r * row_bytes + (size_t)sb * bpr, grp, raw);
+            sb_load(w + (size_t)r * row_bytes + (size_t)sb * bpr, grp, raw[rt]);
+        }
+        XMin<NT, XM> xm;
+        sb_xmin<FMT, NT, XM>(bx, xl[wv], xm);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
             typename SbRaw<FMT>::Ops ops;
-            sb_ops(raw, grp, ops);
-            sb_mfma<NT>(ops, bx, acc[rt]);
+            sb_ops<XM>(raw[rt], grp, ops);
+            sb_mfma<NT>(ops, bx, xm, acc[rt]);
         }
     }
 
@@ -104,8 +113,10 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
                                                                      const uint8_t* __restrict__ w,
                                                                      float* __restrict__ part, int M, int K, int N,
                                                                      size_t split_stride, int cols) {
+    constexpr bool XM = true;  // minimum-term form (q4_xmin)
     constexpr int NW = MF_WAVES;
     __shared__ float red[NW][RT][NT][4][64];
+    __shared__ float xl[NW][NT * 128];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int n_sb = K / QK_K;
@@ -125,7 +136,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
             const uint8_t* blk = w + (size_t)min(row0 + rt * 16 + col, N - 1) * row_bytes;
             typename SbRaw<FMT>::Raw raw;
             sb_load(blk + (size_t)sb0 * (FMT == 4 ? Q4K_BYTES : Q6K_BYTES), grp, raw);
-            sb_ops(raw, grp, ops[rt]);
+            sb_ops<XM>(raw, grp, ops[rt]);
         }
     }
     half8_t bx[8][NT];
@@ -148,8 +159,10 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
         if (has) {
+            XMin<NT, XM> xm;
+            sb_xmin<FMT, NT, XM>(bx, xl[wv], xm);
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) sb_mfma<NT>(ops[rt], bx, acc[rt]);
+            for (int rt = 0; rt < RT; ++rt) sb_mfma<NT>(ops[rt], bx, xm, acc[rt]);
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
@@ -194,7 +207,9 @@ template <typename TI, typename TO, int FMT, int NT, int WPB>
 __global__ __launch_bounds__(64 * WPB) void gemm_stream_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
                                                           TO* __restrict__ y, int M, int N, const TO* __restrict__ bias,
                                                           const TO* __restrict__ residual, float rs) {
+    constexpr bool XM = NT > 1;  // minimum-term form (q4_xmin)
     extern __shared__ uint4 gs_smem[];
+    __shared__ float xl[WPB][NT * 128];
     _Float16* xs = reinterpret_cast<_Float16*>(gs_smem);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -223,7 +238,7 @@ __global__ __launch_bounds__(64 * WPB) void gemm_stream_kernel(const TI* __restr
 #pragma unroll 1
         for (int sb = 0; sb < GS_NSB; ++sb) {
             typename SbRaw<FMT>::Ops ops;
-            sb_ops(cur, grp, ops);
+            sb_ops<XM>(cur, grp, ops);
             cur = nxt;
             nxt = nx2;
             load(min(sb + 3, GS_NSB - 1), nx2);
@@ -235,7 +250,9 @@ __global__ __launch_bounds__(64 * WPB) void gemm_stream_kernel(const TI* __restr
                 for (int nt = 0; nt < NT; ++nt)
                     bx[t][nt] = *reinterpret_cast<const half8_t*>(xs + (nt * 16 + col) * GS_LDX + kb);
             }
-            sb_mfma<NT>(ops, bx, acc);
+            XMin<NT, XM> xm;
+            sb_xmin<FMT, NT, XM>(bx, xl[wv], xm);
+            sb_mfma<NT>(ops, bx, xm, acc);
         }
         // C layout: lane (col, grp) holds batch columns 4*grp + i of weight row col
 #pragma unroll
@@ -294,7 +311,7 @@ static hipError_t launch_stream(const void* x, const void* w, void* y, int M, in
 #define GS_LAUNCH(NT_, W_)                                                                                          \
     hipLaunchKernelGGL((gemm_stream_kernel<TI, TO, FMT, NT_, W_>), dim3(grid), dim3(64 * W_), 16 * NT_ * GS_LDX * 2, st, \
                        xs, (const uint8_t*)w, ys, mc, N, (const TO*)bias, rp, rs)
-        if (mc > 16) GS_LAUNCH(2, WPB);
+        if (M > 16) GS_LAUNCH(2, WPB);  // a 16-column tail of a longer batch too (one minimum-term form)
         else GS_LAUNCH(1, WPB);
 #undef GS_LAUNCH
         const hipError_t e = hipGetLastError();
@@ -313,7 +330,7 @@ static hipError_t launch_mfma(const void* x, const void* w, void* y, int M, int 
         const TI* xs = (const TI*)x + (size_t)m0 * K;
         TO* ys = (TO*)y + (size_t)m0 * N;
         const TO* rp = residual ? (const TO*)residual + (size_t)m0 * N : nullptr;
-        if (mc > 16) {
+        if (M > 16) {  // also a tail of 16 or fewer: every column of a batch gets one minimum-term form
             if (tall) launch_tile<TI, TO, FMT, 2, 2>(xs, w, ys, mc, K, N, bias, rp, rs, st);
             else launch_tile<TI, TO, FMT, 1, 2>(xs, w, ys, mc, K, N, bias, rp, rs, st);
         } else {
@@ -367,12 +384,12 @@ static hipError_t launch_splitk(const void* x, const void* w, float* part, int M
         static const int rt_env = [] { const char* v = getenv("VTE_SPLITK_RT"); return v ? atoi(v) : 0; }();
         const int rt = rt_env > 0 ? rt_env : (mc > 8 ? 2 : 1);
         if (rt == 4) {
-            if (mc > 16) launch_tile<__half, float, FMT, 4, 2>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
+            if (M > 16) launch_tile<__half, float, FMT, 4, 2>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
             else launch_tile<__half, float, FMT, 4, 1>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
         } else if (rt == 2) {
-            if (mc > 16) launch_tile<__half, float, FMT, 2, 2>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
+            if (M > 16) launch_tile<__half, float, FMT, 2, 2>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
             else launch_tile<__half, float, FMT, 2, 1>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
-        } else if (mc > 16) launch_tile<__half, float, FMT, 1, 2>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
+        } else if (M > 16) launch_tile<__half, float, FMT, 1, 2>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
         else launch_tile<__half, float, FMT, 1, 1>(xs, w, ps, mc, K, N, nullptr, nullptr, 1.f, st, splits, ss);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

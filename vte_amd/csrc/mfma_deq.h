@@ -12,8 +12,10 @@
 //    products sc_j * q (<= 945) and sc_j * (q - 32) (exact in fp16 while
 //    |sc_j| <= 64, one rounding of an integer product beyond), made with
 //    packed fp16 math from the code bytes (nibble -> 0x64xx magic = 1024 + q);
-//    the Q4_K minimum term is a second MFMA of the same activations against
-//    the splat 6-bit m_j.  The MFMA sums a super-block in fp32 and the fp32
+//    the Q4_K minimum term is either one MFMA per k-step of the activations
+//    against the splat 6-bit minimum (launches of at most 16 columns) or one
+//    MFMA of the activations' sub-block sums (formed once per super-block and
+//    wave, q4_xmin) against the row's eight minima (longer batches).  The MFMA sums a super-block in fp32 and the fp32
 //    scales d, dmin are applied once per super-block (sb_mfma).  The weights
 //    therefore enter the sums exactly as the reference's fp32 dequantisation
 //    defines them (vte/compiler/dequantizer.py:26-70, 129-169); only the fp16
@@ -129,7 +131,8 @@ struct Q6Ops {
 };
 struct Q4Ops {
     half8_t w[8];
-    uint32_t mnb;   // byte s: m_j of the lane's sub-block of steps 2s, 2s+1
+    half8_t mins;   // XM: lane groups 0-1 the row's eight sub-block minima m_0..m_7, groups 2-3 zero
+    uint32_t mnb;   // !XM: byte s = m_j of the lane's sub-block of steps 2s, 2s+1
     float d, dmin;
 };
 
@@ -172,13 +175,25 @@ __device__ __forceinline__ void q4_raw_load(const uint8_t* blk, int grp, Q4Raw& 
     r.q0 = *reinterpret_cast<const uint4*>(blk + 16 + 16 * grp);
     r.q1 = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (grp + 4));
 }
+template <bool XM>
 __device__ __forceinline__ void q4_exact_operands(const Q4Raw& r, int grp, Q4Ops& o) {
     o.d = h2f_bits(r.h.x);
     o.dmin = h2f_bits(r.h.x >> 16);
     Q4KLaneInts s[2];
     s[0] = q4k_lane_ints(r.h, grp >> 1);
     s[1] = q4k_lane_ints(r.h, 2 + (grp >> 1));
-    o.mnb = s[0].mn0 | (s[0].mn1 << 8) | (s[1].mn0 << 16) | (s[1].mn1 << 24);
+    if constexpr (!XM) {
+        o.mnb = s[0].mn0 | (s[0].mn1 << 8) | (s[1].mn0 << 16) | (s[1].mn1 << 24);
+    } else {
+        half8_t mv;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const Q4KLaneInts v = q4k_lane_ints(r.h, mb);
+            mv[2 * mb] = grp < 2 ? (_Float16)(float)v.mn0 : (_Float16)0.0f;
+            mv[2 * mb + 1] = grp < 2 ? (_Float16)(float)v.mn1 : (_Float16)0.0f;
+        }
+        o.mins = mv;
+    }
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         const int ci = t >> 2, part = (t >> 1) & 1, e = t & 1;
@@ -191,15 +206,78 @@ __device__ __forceinline__ void q4_exact_operands(const Q4Raw& r, int grp, Q4Ops
     }
 }
 
+// Sub-block sums of the activations of one super-block, X[m][j] = sum of
+// x[m][k] over sub-block j (Q4_K: 8 sub-blocks of 32), for the minimum term
+// dmin * sum_j m_j X[m][j], which is the same for every weight row of the
+// tile and so is formed once per super-block and wave: eight MFMAs of the
+// activation operands against 0/1 sub-block indicators (exact fp32 sums),
+// then, through the wave's LDS scratch `xl` [NT][16][8], the A-operand layout
+// with X split into fp16 hi (lane group 0) and lo (group 1) parts, so the
+// single MFMA against the row minima (Q4Ops::mins) sums hi + lo to ~2^-22.
+// This form (XM) pays off where several row tiles or column tiles share the
+// sums (weight-stationary and multi-tile launches).  With one row tile and
+// one column tile per super-block and wave (the batched decode launches) its
+// serial chain (indicator MFMAs, LDS round trip) lies on the critical path,
+// and the !XM form instead adds one MFMA per k-step of the activations
+// against the splat minimum of the step's sub-block, independent of the
+// weight MFMAs.  The two forms round the minimum term differently (both sum
+// in fp32; results agree to fp32 rounding, not bit for bit).
+template <int NT, bool XM>
+struct XMin {
+    half8_t xa[NT];
+};
+template <int NT>
+struct XMin<NT, false> {};
+template <int NT>
+__device__ __forceinline__ void q4_xmin(const half8_t (&bx)[8][NT], float* xl, XMin<NT, true>& xm) {
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    floatx4_t cx[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) cx[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int sub = 2 * ((grp >> 1) + 2 * (t >> 2)) + ((t >> 1) & 1);  // sub-block of step t, group grp
+        const _Float16 one = col == sub ? (_Float16)1.0f : (_Float16)0.0f;
+        const half8_t ind = {one, one, one, one, one, one, one, one};
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) cx[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[t][nt], ind, cx[nt], 0, 0, 0);
+    }
+    // C layout: lane (j, grp) holds X[4 grp + i][j]
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (col < 8) xl[(nt * 16 + 4 * grp + i) * 8 + col] = cx[nt][i];
+    // a wave's LDS operations complete in order: wait for the stores (LDS
+    // counter only, the weight prefetches stay in flight) before the reads
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const float4 a = *reinterpret_cast<const float4*>(xl + (nt * 16 + col) * 8);
+        const float4 b = *reinterpret_cast<const float4*>(xl + (nt * 16 + col) * 8 + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        half8_t h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const _Float16 hi = (_Float16)v[j];
+            const _Float16 lo = (_Float16)(v[j] - (float)hi);
+            h[j] = grp == 0 ? hi : (grp == 1 ? lo : (_Float16)0.0f);
+        }
+        xm.xa[nt] = h;
+    }
+    asm volatile("" ::: "memory");  // xl is rewritten by the next call
+}
+
 // One super-block of MFMA work for NT 16-column activation tiles bx[t][nt]
 // (A operands, k-slot map of the format) against one lane's exact weight
-// operands: acc[nt] += d * sum(w x) [- dmin * sum(m x)], the sums in fp32 over
-// the super-block's 8 k-steps in order.  Every batched kernel goes through
-// this function, so a weight row's result depends only on which super-blocks
-// a wave sums (and the order the waves' partials are added), not on the
-// kernel or the number of columns.
-template <int NT>
-__device__ __forceinline__ void sb_mfma(const Q6Ops& o, const half8_t (&bx)[8][NT], floatx4_t (&acc)[NT]) {
+// operands: acc[nt] += d * sum(w x) [- dmin * sum_j m_j X_j], the sums in fp32
+// over the super-block's 8 k-steps in order.  Every batched kernel goes
+// through these functions, so for a given minimum-term form (XM) a weight
+// row's result depends only on which super-blocks a wave sums (and the order
+// the waves' partials are added), not on the kernel or the number of columns.
+template <int NT, bool XM>
+__device__ __forceinline__ void sb_mfma(const Q6Ops& o, const half8_t (&bx)[8][NT], const XMin<NT, XM>&,
+                                        floatx4_t (&acc)[NT]) {
     floatx4_t aw[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) aw[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
@@ -213,7 +291,27 @@ __device__ __forceinline__ void sb_mfma(const Q6Ops& o, const half8_t (&bx)[8][N
         for (int i = 0; i < 4; ++i) acc[nt][i] = fmaf(o.d, aw[nt][i], acc[nt][i]);
 }
 template <int NT>
-__device__ __forceinline__ void sb_mfma(const Q4Ops& o, const half8_t (&bx)[8][NT], floatx4_t (&acc)[NT]) {
+__device__ __forceinline__ void sb_mfma(const Q4Ops& o, const half8_t (&bx)[8][NT], const XMin<NT, true>& xm,
+                                        floatx4_t (&acc)[NT]) {
+    floatx4_t aw[NT], am[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        aw[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        am[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xm.xa[nt], o.mins, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) aw[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bx[t][nt], o.w[t], aw[nt], 0, 0, 0);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[nt][i] = fmaf(-o.dmin, am[nt][i], fmaf(o.d, aw[nt][i], acc[nt][i]));
+}
+
+template <int NT>
+__device__ __forceinline__ void sb_mfma(const Q4Ops& o, const half8_t (&bx)[8][NT], const XMin<NT, false>&,
+                                        floatx4_t (&acc)[NT]) {
     floatx4_t aw[NT], am[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) aw[nt] = am[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
@@ -233,13 +331,21 @@ __device__ __forceinline__ void sb_mfma(const Q4Ops& o, const half8_t (&bx)[8][N
         for (int i = 0; i < 4; ++i) acc[nt][i] = fmaf(-o.dmin, am[nt][i], fmaf(o.d, aw[nt][i], acc[nt][i]));
 }
 
+// The minimum-term sums where the format has one (Q4_K), else nothing.
+template <int FMT, int NT, bool XM>
+__device__ __forceinline__ void sb_xmin(const half8_t (&bx)[8][NT], float* xl, XMin<NT, XM>& xm) {
+    if constexpr (FMT == 4 && XM) q4_xmin<NT>(bx, xl, xm);
+}
+
 // Raw bytes -> operands for either format.
 template <int FMT> struct SbRaw;
 template <> struct SbRaw<4> { using Raw = Q4Raw; using Ops = Q4Ops; };
 template <> struct SbRaw<6> { using Raw = Q6Raw; using Ops = Q6Ops; };
 __device__ __forceinline__ void sb_load(const uint8_t* blk, int grp, Q4Raw& r) { q4_raw_load(blk, grp, r); }
 __device__ __forceinline__ void sb_load(const uint8_t* blk, int grp, Q6Raw& r) { q6_raw_load(blk, grp, r); }
-__device__ __forceinline__ void sb_ops(const Q4Raw& r, int grp, Q4Ops& o) { q4_exact_operands(r, grp, o); }
+template <bool XM>
+__device__ __forceinline__ void sb_ops(const Q4Raw& r, int grp, Q4Ops& o) { q4_exact_operands<XM>(r, grp, o); }
+template <bool XM>
 __device__ __forceinline__ void sb_ops(const Q6Raw& r, int grp, Q6Ops& o) { q6_exact_operands(r, grp, o); }
 
 // C tile element of weight row rw (0..15) and batch column cc (0..15): lane
