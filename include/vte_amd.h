@@ -151,6 +151,18 @@ int vte_add(const void* residual, const void* input, void* out, int n, float sca
 int vte_embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
                       void* stream);
 
+/* The same from a Q4_K table [vocab][hidden] (hidden a multiple of 256; the
+ * untied embedding of Qwen2.5-7B).
+ * Replaces: embedding_lookup_q4k_kernel (embedding_lookup_q4k.hip.template:26-75). */
+int vte_embedding_q4k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
+                      void* stream);
+
+/* The same from a Q8_0 table [vocab][hidden] (hidden a multiple of 32; tied
+ * Q8_0 embeddings, scale 12 for Granite).
+ * Replaces: embedding_lookup_q8_0_kernel (embedding_lookup_q8_0.hip.template:15-46). */
+int vte_embedding_q8_0(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
+                       void* stream);
+
 /* Bytes of device scratch (8-byte aligned) vte_topk needs for `rows` rows. */
 long long vte_topk_scratch_bytes(int rows);
 
@@ -213,7 +225,7 @@ int vte_ffn_in(const void* x, const void* norm_w, float eps, const void* w_gate,
                void* out, int batch, int hidden, int ffn, void* stream);
 
 /* One launch: RMSNorm(x) followed by the vte_gemv contract (the LM head with
- * out_dtype f32).  batch 1..4.
+ * out_dtype f32).  batch 1..4; Q4_K, Q6_K or Q8_0 (tied Q8_0 tables).
  * Replaces: the output_norm + LM-head capture (vte/core/hip_graph_executor.py:429-474). */
 int vte_norm_gemv(const void* x, const void* norm_w, float eps, const void* w, int fmt, void* out, int out_dtype,
                   const void* bias, const void* residual, float residual_scale, int batch, int K, int N,

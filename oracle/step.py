@@ -5,7 +5,8 @@ Node order per layer follows vte/compiler/qwen_compute.py:100-282 and the
 captured graph of vte/core/hip_graph_executor.py:504-738:
   rmsnorm -> q/k/v GEMV (+bias) -> RoPE(q,k) -> KV append -> attention
   -> o GEMV (+residual) -> rmsnorm -> gate/up GEMV -> SwiGLU -> down GEMV (+residual)
-then the final rmsnorm and the LM-head GEMV over the tied Q6_K embedding.
+then the final rmsnorm and the LM-head GEMV (the tied embedding table, Q6_K in
+Qwen2.5-1.5B, or a separate output matrix).
 """
 from __future__ import annotations
 
@@ -51,10 +52,34 @@ def rope_neox(x: np.ndarray, pos: int, cos_c: np.ndarray, sin_c: np.ndarray) -> 
     return np.concatenate([a * c - b * s, a * s + b * c], -1).astype(np.float16)
 
 
+def embedding_row(fmt: str, raw_table: np.ndarray, token: int, hidden: int, scale: float = 1.0) -> np.ndarray:
+    """Dequantised row `token` of a q4_k / q6_k / q8_0 table times `scale`, as
+    fp16 (embedding_lookup_q4k.hip.template:26-75, embedding_lookup_q6k
+    .hip.template:17-58, embedding_lookup_q8_0.hip.template:15-46: the
+    dequantiser's fp32 value, one fp32 multiply by the scale, fp16)."""
+    rb = {"q4_k": hidden // 256 * 144, "q6_k": hidden // 256 * 210, "q8_0": hidden // 32 * 34}[fmt]
+    w = dq.dequantize_matrix(fmt, raw_table[token * rb:(token + 1) * rb], 1, hidden)[0]
+    return (w * np.float32(scale)).astype(np.float16)
+
+
 def embedding_q6k(raw_table: np.ndarray, token: int, hidden: int) -> np.ndarray:
     """Dequantised row `token` of a Q6_K table as fp16 (embedding_lookup_q6k.hip.template:17-58)."""
-    rb = (hidden // 256) * 210
-    return dq.dequantize_q6_k(raw_table[token * rb:(token + 1) * rb].tobytes(), hidden).astype(np.float16)
+    return embedding_row("q6_k", raw_table, token, hidden)
+
+
+def _embed(model, token: int) -> np.ndarray:
+    return embedding_row(getattr(model, "token_embd_fmt", "q6_k"), model.token_embd, int(token), model.cfg.hidden)
+
+
+def _lm_head(model, cache):
+    """Dequantised LM head: ``model.lm_head`` (format ``lm_head_fmt``) when the
+    model has a separate output matrix, else the tied embedding table."""
+    lm = getattr(model, "lm_head", None)
+    if lm is None or lm is model.token_embd:
+        lm, fmt = model.token_embd, getattr(model, "token_embd_fmt", "q6_k")
+    else:
+        fmt = model.lm_head_fmt
+    return _weights(fmt, lm, model.cfg.vocab, model.cfg.hidden, cache, "lm")
 
 
 def _weights(fmt, raw, n, k, cache, key):
@@ -96,7 +121,8 @@ def decode_step(model, tokens, positions, k_cache, v_cache, cache=None, accum="f
     Per layer (qwen_compute.py:100-282): attn_norm -> q/k/v (+bias) -> RoPE on q
     and k -> K/V append -> attention (query head h reads KV head h // (n_q/n_kv))
     -> o-proj + residual -> ffn_norm -> gate, up -> silu(gate) * up -> down +
-    residual; then output_norm and the tied Q6_K LM head.
+    residual; then output_norm and the LM head (the tied embedding table unless
+    the model has a separate output matrix).
     """
     cfg = model.cfg
     H, hd, nq, nkv = cfg.hidden, cfg.head_dim, cfg.n_q, cfg.n_kv
@@ -104,7 +130,7 @@ def decode_step(model, tokens, positions, k_cache, v_cache, cache=None, accum="f
     cos_c, sin_c = rope_cache(cfg.max_seq, hd, cfg.rope_theta)
     B = len(tokens)
     pos = [int(p) for p in positions]
-    h = np.stack([embedding_q6k(model.token_embd, int(t), H) for t in tokens])      # [B, H] fp16
+    h = np.stack([_embed(model, t) for t in tokens])      # [B, H] fp16
     for L, lw in enumerate(model.layers):
         w = {p: _weights(lw[p + "_fmt"], lw[p], *_shape(cfg, p), cache, (L, p))
              for p in ("q", "k", "v", "o", "gate", "up", "down")}
@@ -125,7 +151,7 @@ def decode_step(model, tokens, positions, k_cache, v_cache, cache=None, accum="f
         h = _lin(w["down"], a, residual=h, accum=accum)
         del w
     hn = rmsnorm(h, model.output_norm, cfg.eps)
-    wl = _weights("q6_k", model.token_embd, cfg.vocab, H, cache, "lm")
+    wl = _lm_head(model, cache)
     return (hn.astype(_ACC[accum]) @ wl.T.astype(_ACC[accum], copy=False)).astype(np.float32)
 
 
@@ -153,7 +179,7 @@ def prefill(model, tokens, start, k_cache, v_cache, cache=None, accum="f32"):
     cos_c, sin_c = rope_cache(cfg.max_seq, hd, cfg.rope_theta)
     n = len(tokens)
     pos = np.arange(start, start + n)
-    h = np.stack([embedding_q6k(model.token_embd, int(t), H) for t in tokens])
+    h = np.stack([_embed(model, t) for t in tokens])
     for L, lw in enumerate(model.layers):
         w = {p: _weights(lw[p + "_fmt"], lw[p], *_shape(cfg, p), cache, (L, p))
              for p in ("q", "k", "v", "o", "gate", "up", "down")}
@@ -182,5 +208,5 @@ def prefill(model, tokens, start, k_cache, v_cache, cache=None, accum="f32"):
         h = _lin(w["down"], a, residual=h, accum=accum)
         del w
     hn = rmsnorm(h, model.output_norm, cfg.eps)
-    wl = _weights("q6_k", model.token_embd, cfg.vocab, H, cache, "lm")
+    wl = _lm_head(model, cache)
     return (hn.astype(_ACC[accum]) @ wl.T.astype(_ACC[accum], copy=False)).astype(np.float32)

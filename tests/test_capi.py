@@ -64,3 +64,9 @@ def test_host_side_queries_and_validation():
                                  None, None) == -1
     assert b"head_dim" in lib.vte_last_error()
     assert lib.vte_dequantize(6, 16, 16, 100, None) == -1
+    # embedding tables: hidden must hold whole blocks of the table's format
+    assert lib.vte_embedding_q4k(16, 16, 16, 2, 1000, ctypes.c_float(1.0), None) == -1
+    assert b"multiple of 256" in lib.vte_last_error()
+    assert lib.vte_embedding_q8_0(16, 16, 16, 2, 1000, ctypes.c_float(1.0), None) == -1
+    assert b"multiple of 32" in lib.vte_last_error()
+    assert lib.vte_embedding_q6k(None, 16, 16, 2, 1536, ctypes.c_float(1.0), None) == -1

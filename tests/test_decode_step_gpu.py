@@ -36,6 +36,19 @@ def _host_kv(cfg, B, max_seq, prefix, rng):
 
 @pytest.mark.parametrize("B", [1, 3, 8, 16])
 def test_tiny_step_matches_oracle(hip, tiny_model, B):
+    _step_vs_oracle(hip, tiny_model, B)
+
+
+@pytest.mark.parametrize("embd,lm", [("q4_k", "q6_k"), ("q8_0", None)])
+@pytest.mark.parametrize("B", [1, 4])
+def test_embedding_formats_step_matches_oracle(hip, embd, lm, B):
+    """A Q4_K embedding table with a separate Q6_K LM head (the Qwen2.5-7B
+    layout) and a tied Q8_0 table (embedding and LM head from the same Q8_0
+    blocks), on the mat-vec path (batch 1) and the MFMA path (batch 4)."""
+    _step_vs_oracle(hip, SyntheticQwen2(TINY, seed=8, embd_fmt=embd, lm_head_fmt=lm), B)
+
+
+def _step_vs_oracle(hip, tiny_model, B):
     cfg = tiny_model.cfg
     max_seq = 256
     rng = np.random.default_rng(10 + B)

@@ -166,6 +166,29 @@ def test_qwen2_export_load_round_trip(tmp_path, tiny):
         m.close()
 
 
+@pytest.mark.parametrize("embd,lm", [("q4_k", "q6_k"), ("q8_0", None), ("q4_k", None)])
+def test_qwen2_round_trip_embedding_formats(tmp_path, embd, lm):
+    """Q4_K embedding with a separate Q6_K output matrix (the Qwen2.5-7B
+    layout, qwen_mapper.py:92-104) and tied Q8_0 / Q4_K tables: the loader
+    keeps the table in its blocks and routes the LM head to the output
+    matrix or, when there is none, to the table in its own format."""
+    m0 = SyntheticQwen2(TINY, seed=6, embd_fmt=embd, lm_head_fmt=lm)
+    p = tmp_path / "e.gguf"
+    export_qwen2_gguf(m0, p)
+    m = GGUFQwen2(p)
+    try:
+        assert m.token_embd_fmt == embd
+        assert np.array_equal(m.token_embd.reshape(-1), m0.token_embd.reshape(-1))
+        if lm is None:
+            assert m.lm_head is m.token_embd and m.lm_head_fmt == embd
+        else:
+            assert m.lm_head is not m.token_embd and m.lm_head_fmt == lm
+            assert np.array_equal(m.lm_head.reshape(-1), m0.lm_head.reshape(-1))
+        assert m.weight_bytes() == m0.weight_bytes()
+    finally:
+        m.close()
+
+
 def test_qwen2_loader_errors(tmp_path, tiny):
     p = tmp_path / "bad.gguf"
     write_gguf(p, {"general.architecture": "llama"}, [])

@@ -2,6 +2,7 @@
 import numpy as np
 import pytest
 
+from oracle import dequant as dq
 from oracle import step as st
 from tests._dev import down, empty, up
 from vte_amd import synthetic as syn
@@ -58,16 +59,26 @@ def test_rope_neox_batched(hip, K):
     assert np.array_equal(gq[0], q[0])
 
 
-def test_embedding_q6k_bit_exact(hip, K):
+@pytest.mark.parametrize("fmt,H,scale", [("q6_k", 1536, 1.0), ("q4_k", 1536, 1.0), ("q4_k", 3584, 1.0),
+                                         ("q8_0", 2048, 12.0), ("q8_0", 2080, 1.0), ("q6_k", 256, 0.5)])
+def test_embedding_bit_exact(hip, K, fmt, H, scale):
+    """Rows of a Q4_K / Q6_K / Q8_0 table (first, last and repeated tokens)
+    equal the exact dequantiser's fp32 values times the scale, rounded to fp16
+    (embedding_lookup_q{4k,6k,8_0}.hip.template)."""
     rng = np.random.default_rng(4)
-    vocab, H = 1000, 1536
-    table = syn.random_q6_k(rng, vocab, H)
+    vocab = 1000
+    table = syn.random_matrix(fmt, rng, vocab, H)
     toks = np.array([0, 5, 999, 5, 123], np.int32)
     out = empty(hip, (len(toks), H), np.float16)
-    K.embedding_q6k(up(hip, toks), up(hip, table), out, len(toks), H, stream=hip.stream)
+    K.embedding(fmt, up(hip, toks), up(hip, table), out, len(toks), H, scale, stream=hip.stream)
     got = down(out)
+    full = dq.dequantize_matrix(fmt, table, vocab, H)
     for i, t in enumerate(toks):
-        assert np.array_equal(got[i], st.embedding_q6k(table, int(t), H))
+        ref = st.embedding_row(fmt, table, int(t), H, scale)
+        bad = np.flatnonzero(got[i].view(np.uint16) != ref.view(np.uint16))
+        assert bad.size == 0, (int(t), [(int(j), hex(got[i].view(np.uint16)[j]), hex(ref.view(np.uint16)[j]),
+                                         float(full[t][j])) for j in bad[:6]])
+        assert np.array_equal(got[i], (full[t] * np.float32(scale)).astype(np.float16))
 
 
 @pytest.mark.parametrize("k,vocab", [(1, 151936), (40, 151936), (64, 151936), (40, 64), (40, 1000), (7, 300)])

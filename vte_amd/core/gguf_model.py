@@ -26,7 +26,8 @@ from .weights import PROJ, proj_shape
 # projection -> GGUF tensor suffix (Qwen2 naming in llama.cpp files)
 GGUF_PROJ = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
              "up": "ffn_up", "down": "ffn_down"}
-KERNEL_FORMATS = ("q4_k", "q6_k")
+KERNEL_FORMATS = ("q4_k", "q6_k")          # projections (mat-vec and MFMA kernels)
+TABLE_FORMATS = ("q4_k", "q6_k", "q8_0")   # embedding table / LM head (embedding kernels, mat-vec / GEMV)
 
 
 def config_from_metadata(meta: dict, vocab: int, max_seq: int | None = None) -> Qwen2Config:
@@ -68,14 +69,13 @@ class GGUFQwen2:
         self.cfg = cfg = config_from_metadata(r.metadata, vocab=emb.shape[0], max_seq=max_seq)
         if cfg.head_dim != 128:
             raise HIPSafetyError(f"GGUF: head_dim {cfg.head_dim} unsupported (the attention kernels take 128)")
-        if emb.type_name != "q6_k":
-            raise HIPSafetyError(f"GGUF: token_embd is {emb.type_name}; the embedding kernel reads Q6_K")
-        self.token_embd = self._matrix("token_embd.weight", (cfg.vocab, cfg.hidden))
+        self.token_embd = self._matrix("token_embd.weight", (cfg.vocab, cfg.hidden), TABLE_FORMATS)
+        self.token_embd_fmt = emb.type_name
         out = r.tensors.get("output.weight")
         if out is None or out.is_tied:
-            self.lm_head, self.lm_head_fmt = self.token_embd, "q6_k"
+            self.lm_head, self.lm_head_fmt = self.token_embd, emb.type_name
         else:
-            self.lm_head = self._matrix("output.weight", (cfg.vocab, cfg.hidden))
+            self.lm_head = self._matrix("output.weight", (cfg.vocab, cfg.hidden), TABLE_FORMATS)
             self.lm_head_fmt = out.type_name
         self.output_norm = self._vector("output_norm.weight", cfg.hidden)
         self.layers = []
@@ -101,12 +101,13 @@ class GGUFQwen2:
             raise HIPSafetyError(f"GGUF: tensor {name} is missing")
         return t
 
-    def _matrix(self, name, shape):
+    def _matrix(self, name, shape, formats=KERNEL_FORMATS):
         t = self._info(name)
         if t.shape != tuple(shape):
             raise HIPSafetyError(f"GGUF: {name} has shape {t.shape}, expected {tuple(shape)}")
-        if t.type_name not in KERNEL_FORMATS:
-            raise HIPSafetyError(f"GGUF: {name} is {t.type_name}; the decode kernels read Q4_K and Q6_K")
+        if t.type_name not in formats:
+            raise HIPSafetyError(f"GGUF: {name} is {t.type_name}; the kernels for it read "
+                                 + ", ".join(f.upper() for f in formats))
         return self.reader.tensor(name)
 
     def _vector(self, name, n):
@@ -121,8 +122,8 @@ class GGUFQwen2:
         return v.astype(np.float16)
 
     def weight_bytes(self) -> int:
-        lm = 0 if self.lm_head is self.token_embd else self.lm_head.nbytes
-        return int(sum(lw[p].nbytes for lw in self.layers for p in PROJ) + self.token_embd.nbytes + lm)
+        """Bytes of quantised weights read by one decode step (projections + LM head)."""
+        return int(sum(lw[p].nbytes for lw in self.layers for p in PROJ) + self.lm_head.nbytes)
 
     def close(self) -> None:
         self.reader.close()
@@ -130,8 +131,9 @@ class GGUFQwen2:
 
 def export_qwen2_gguf(model, path, alignment: int = 32) -> None:
     """Write a model with the ``SyntheticQwen2`` attributes as a llama.cpp-style
-    Qwen2 GGUF (norms and biases as F32, projections as their raw blocks,
-    tied embeddings: no ``output.weight``)."""
+    Qwen2 GGUF (norms and biases as F32, projections and the embedding table
+    as their raw blocks; ``output.weight`` only for a model with a separate
+    LM head)."""
     cfg = model.cfg
     meta = {"general.architecture": "qwen2", "general.name": "vte_amd synthetic",
             "qwen2.block_count": cfg.n_layers, "qwen2.context_length": cfg.max_seq,
@@ -139,8 +141,11 @@ def export_qwen2_gguf(model, path, alignment: int = 32) -> None:
             "qwen2.attention.head_count": cfg.n_q, "qwen2.attention.head_count_kv": cfg.n_kv,
             "qwen2.attention.layer_norm_rms_epsilon": float(cfg.eps), "qwen2.rope.freq_base": float(cfg.rope_theta)}
     f32 = lambda a: np.asarray(a, np.float32)
-    ts = [("token_embd.weight", "q6_k", (cfg.vocab, cfg.hidden), model.token_embd),
+    ts = [("token_embd.weight", getattr(model, "token_embd_fmt", "q6_k"), (cfg.vocab, cfg.hidden), model.token_embd),
           ("output_norm.weight", "f32", (cfg.hidden,), f32(model.output_norm))]
+    lm = getattr(model, "lm_head", None)
+    if lm is not None and lm is not model.token_embd:
+        ts.append(("output.weight", model.lm_head_fmt, (cfg.vocab, cfg.hidden), lm))
     for i, lw in enumerate(model.layers):
         ts.append((f"blk.{i}.attn_norm.weight", "f32", (cfg.hidden,), f32(lw["attn_norm"])))
         for p in PROJ:

@@ -150,10 +150,12 @@ class HIPGraphExecutor:
         cfg, B = self.cfg, self.B
         # ---- weights ----
         self.token_embd = W(model.token_embd, "token_embd")
+        self.token_embd_fmt = getattr(model, "token_embd_fmt", "q6_k")
         # LM head: a separate output matrix when the model has one, else the tied embedding
         lm = getattr(model, "lm_head", None)
-        self.lm_head_fmt = getattr(model, "lm_head_fmt", "q6_k")
-        self.lm_head = self.token_embd if lm is None or lm is model.token_embd else W(lm, "lm_head")
+        tied = lm is None or lm is model.token_embd
+        self.lm_head_fmt = self.token_embd_fmt if tied else getattr(model, "lm_head_fmt", "q6_k")
+        self.lm_head = self.token_embd if tied else W(lm, "lm_head")
         self.output_norm = W(model.output_norm, "output_norm")
         self.layers = []
         for L, lw in enumerate(model.layers):
@@ -172,7 +174,8 @@ class HIPGraphExecutor:
 
     def _share(self, ex: "HIPGraphExecutor", seq: int) -> None:
         """Weights, RoPE tables and sequence ``seq``'s KV cache of ``ex``."""
-        for name in ("token_embd", "lm_head", "lm_head_fmt", "output_norm", "layers", "rope_cos", "rope_sin"):
+        for name in ("token_embd", "token_embd_fmt", "lm_head", "lm_head_fmt", "output_norm", "layers", "rope_cos",
+                     "rope_sin"):
             setattr(self, name, getattr(ex, name))
         off = seq * ex.kv_batch_stride * 2  # bytes
         self.k_cache = [c.ptr + off for c in ex.k_cache]
@@ -207,7 +210,7 @@ class HIPGraphExecutor:
         on = (lambda c: True) if only is None else (lambda c: c in only)
         cur = 0
         if on("embed"):
-            K.embedding_q6k(self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
+            K.embedding(self.token_embd_fmt, self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
         for L, lw in enumerate(self.layers):
             if on("attn_in"):
                 K.attn_in(self.h[cur], lw["attn_norm"], cfg.eps, lw["q"], lw["q_bias"], lw["q_fmt"], lw["k"],
@@ -285,7 +288,7 @@ class HIPGraphExecutor:
         H = cfg.hidden
         offs = self.staging_kv_offset
         cur = 0
-        K.embedding_q6k(self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
+        K.embedding(self.token_embd_fmt, self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
         K.rmsnorm(self.h[cur], self.layers[0]["attn_norm"], self.xn, B, H, cfg.eps, stream=st)
         for L, lw in enumerate(self.layers):
             if self.mm_fused:  # q/k/v + bias + RoPE + K/V append in one MFMA launch

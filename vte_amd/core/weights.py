@@ -34,11 +34,15 @@ def proj_shape(cfg: Qwen2Config, name: str) -> tuple[int, int]:
 class SyntheticQwen2:
     """Host copies of every weight (raw GGUF blocks as uint8, fp16 vectors)."""
 
-    def __init__(self, cfg: Qwen2Config, seed: int = 0):
+    def __init__(self, cfg: Qwen2Config, seed: int = 0, embd_fmt: str = "q6_k", lm_head_fmt: str | None = None):
+        """``embd_fmt``: format of the token embedding table (tied to the LM
+        head unless ``lm_head_fmt`` asks for a separate output matrix, as the
+        Qwen2.5-7B files have: Q4_K embedding, Q6_K output)."""
         self.cfg = cfg
         rng = np.random.default_rng(seed)
         H = cfg.hidden
-        self.token_embd = syn.random_q6_k(rng, cfg.vocab, H, balanced=True)
+        self.token_embd = syn.random_matrix(embd_fmt, rng, cfg.vocab, H, balanced=True)
+        self.token_embd_fmt = embd_fmt
         self.output_norm = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
         self.layers = []
         for L in range(cfg.n_layers):
@@ -54,7 +58,12 @@ class SyntheticQwen2:
             lw["attn_norm"] = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
             lw["ffn_norm"] = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
             self.layers.append(lw)
+        if lm_head_fmt is None:
+            self.lm_head, self.lm_head_fmt = self.token_embd, embd_fmt
+        else:
+            self.lm_head = syn.random_matrix(lm_head_fmt, rng, cfg.vocab, H, balanced=True)
+            self.lm_head_fmt = lm_head_fmt
 
     def weight_bytes(self) -> int:
         """Bytes of quantised weights read by one decode step (projections + LM head)."""
-        return int(sum(lw[p].nbytes for lw in self.layers for p in PROJ) + self.token_embd.nbytes)
+        return int(sum(lw[p].nbytes for lw in self.layers for p in PROJ) + self.lm_head.nbytes)

@@ -39,8 +39,8 @@ hipError_t rope(void* q, void* k, const void* cosc, const void* sinc, int B, int
                 int head_dim, const int* kv_offset, int rope_type, int rotary_dim, hipStream_t st);
 hipError_t swiglu(const void* g, const void* u, void* out, int n, hipStream_t st);
 hipError_t add(const void* r, const void* in, void* out, int n, float scale, hipStream_t st);
-hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
-                         hipStream_t st);
+hipError_t embedding(int fmt, const int* tokens, const void* table, void* out, int n_tokens, int hidden,
+                     float scale, hipStream_t st);
 size_t topk_scratch_bytes(int rows);
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
                 hipStream_t st, const int* excl_ids, const int* excl_cnt, int max_excl, float* gathered);
@@ -252,12 +252,28 @@ int vte_add(const void* residual, const void* input, void* out, int n, float sca
     return hip_status(vte::add(residual, input, out, n, scale, (hipStream_t)stream), "vte_add launch");
 }
 
+static int embedding_call(int fmt, const char* name, const int* tokens, const void* table, void* out, int n_tokens,
+                          int hidden, float scale, void* stream) {
+    const int qb = fmt == 8 ? 32 : 256;
+    REQUIRE(tokens && table && out && n_tokens >= 1 && hidden >= 1, "%s: bad arguments", name);
+    REQUIRE(hidden % qb == 0, "%s: hidden %d not a multiple of %d", name, hidden, qb);
+    REQUIRE((long long)n_tokens * hidden <= 0x7fffffffLL, "%s: %d tokens x %d too large", name, n_tokens, hidden);
+    return hip_status(vte::embedding(fmt, tokens, table, out, n_tokens, hidden, scale, (hipStream_t)stream), name);
+}
+
 int vte_embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
                       void* stream) {
-    REQUIRE(tokens && table && out && n_tokens >= 1, "embedding: bad arguments");
-    REQUIRE(hidden % 256 == 0, "embedding: hidden %d not a multiple of 256", hidden);
-    return hip_status(vte::embedding_q6k(tokens, table, out, n_tokens, hidden, scale, (hipStream_t)stream),
-                      "vte_embedding_q6k launch");
+    return embedding_call(6, "vte_embedding_q6k", tokens, table, out, n_tokens, hidden, scale, stream);
+}
+
+int vte_embedding_q4k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
+                      void* stream) {
+    return embedding_call(4, "vte_embedding_q4k", tokens, table, out, n_tokens, hidden, scale, stream);
+}
+
+int vte_embedding_q8_0(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
+                       void* stream) {
+    return embedding_call(8, "vte_embedding_q8_0", tokens, table, out, n_tokens, hidden, scale, stream);
 }
 
 long long vte_topk_scratch_bytes(int rows) { return (long long)vte::topk_scratch_bytes(rows); }
@@ -348,7 +364,7 @@ int vte_norm_gemv(const void* x, const void* norm_w, float eps, const void* w, i
                   const void* bias, const void* residual, float residual_scale, int batch, int K, int N,
                   void* stream) {
     REQUIRE(x && norm_w && w && out, "norm_gemv: null pointer");
-    REQUIRE(fmt == 4 || fmt == 6, "norm_gemv: Q4_K or Q6_K");
+    REQUIRE(fmt == 4 || fmt == 6 || fmt == 8, "norm_gemv: Q4_K, Q6_K or Q8_0");
     REQUIRE(out_dtype == VTE_F32 || out_dtype == VTE_F16, "norm_gemv: bad out dtype");
     REQUIRE(batch >= 1 && batch <= 4, "norm_gemv: batch %d outside 1..4", batch);
     REQUIRE(K % 256 == 0 && K <= 8192 && N >= 1, "norm_gemv: bad shape");

@@ -309,27 +309,7 @@ extern "C" __global__ __launch_bounds__(256) void dequantize_q4k_kernel(const vo
                                                                         long long n_blocks) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n_blocks * QK_K) return;
-    const long long b = idx >> 8;
-    const int e = (int)(idx & 255);
-    const uint8_t* blk = (const uint8_t*)src + b * Q4K_BYTES;
-    const float d = h2f_bits(blk[0] | (blk[1] << 8));
-    const float dmin = h2f_bits(blk[2] | (blk[3] << 8));
-    const uint8_t* s = blk + 4;
-    const int mblk = e >> 6;
-    const int hi = (e >> 5) & 1;
-    const int i = e & 31;
-    const int j = 2 * mblk + hi;
-    int sc, mn;
-    if (j < 4) { sc = s[j] & 63; mn = s[j + 4] & 63; }
-    else {
-        sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
-        mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-    }
-    const uint8_t q = blk[16 + 32 * mblk + i];
-    const int nib = hi ? (q >> 4) : (q & 0x0F);
-    const float dd = __fmul_rn(d, (float)sc);
-    const float mm = __fmul_rn(dmin, (float)mn);
-    dst[idx] = __fsub_rn(__fmul_rn(dd, (float)nib), mm);
+    dst[idx] = q4k_elem_exact((const uint8_t*)src + (idx >> 8) * Q4K_BYTES, (int)(idx & 255));
 }
 
 extern "C" __global__ __launch_bounds__(256) void dequantize_q6k_kernel(const void* __restrict__ src,
@@ -337,20 +317,7 @@ extern "C" __global__ __launch_bounds__(256) void dequantize_q6k_kernel(const vo
                                                                         long long n_blocks) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n_blocks * QK_K) return;
-    const long long b = idx >> 8;
-    const int e = (int)(idx & 255);
-    const uint8_t* blk = (const uint8_t*)src + b * Q6K_BYTES;
-    const int half = e >> 7;
-    const int g = (e >> 5) & 3;
-    const int l = e & 31;
-    const uint8_t* ql = blk + 64 * half;
-    const uint8_t qhb = blk[128 + 32 * half + l];
-    const int8_t sc = (int8_t)blk[192 + 8 * half + (l >> 4) + 2 * g];
-    const float d = h2f_bits(blk[208] | (blk[209] << 8));
-    const uint8_t qlb = ql[l + ((g & 1) ? 32 : 0)];
-    const int nib = (g < 2) ? (qlb & 0x0F) : (qlb >> 4);
-    const int q = (nib | (((qhb >> (2 * g)) & 3) << 4)) - 32;
-    dst[idx] = __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+    dst[idx] = q6k_elem_exact((const uint8_t*)src + (idx >> 8) * Q6K_BYTES, (int)(idx & 255));
 }
 
 extern "C" __global__ __launch_bounds__(256) void dequantize_q8_0_kernel(const void* __restrict__ src,
@@ -358,10 +325,7 @@ extern "C" __global__ __launch_bounds__(256) void dequantize_q8_0_kernel(const v
                                                                          long long n_blocks) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n_blocks * QK8_0) return;
-    const long long b = idx >> 5;
-    const uint8_t* blk = (const uint8_t*)src + b * Q80_BYTES;
-    const float d = h2f_bits(blk[0] | (blk[1] << 8));
-    dst[idx] = __fmul_rn(d, (float)(int8_t)blk[2 + (idx & 31)]);
+    dst[idx] = q80_elem_exact((const uint8_t*)src + (idx >> 5) * Q80_BYTES, (int)(idx & 31));
 }
 
 // ---------------------------------------------------------------------------

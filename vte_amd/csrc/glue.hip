@@ -7,10 +7,12 @@
 //   swiglu_kernel                vte/compiler/templates/rdna/swiglu.hip.template:4-26
 //   add_kernel                   vte/compiler/templates/rdna/add.hip.template:4-17
 //   embedding_lookup_q6k_kernel  vte/compiler/templates/rdna/embedding_lookup_q6k.hip.template:17-58
+//   embedding_lookup_q4k_kernel  vte/compiler/templates/rdna/embedding_lookup_q4k.hip.template:26-75
+//   embedding_lookup_q8_0_kernel vte/compiler/templates/rdna/embedding_lookup_q8_0.hip.template:15-46
 // plus a top-k selector over fp32 logits for on-device sampling candidates.
 #include <mutex>
 
-#include "vte_common.h"
+#include "quant.h"
 
 // ---------------------------------------------------------------------------
 // RMSNorm: out = x * rsqrt(mean(x^2) + eps) * w.  grid (rows), block (256).
@@ -257,26 +259,48 @@ extern "C" __global__ __launch_bounds__(256) void add_kernel(const __half* __res
 }
 
 // ---------------------------------------------------------------------------
-// Embedding lookup from a raw Q6_K table: out[s][d] = fp16(dequant(W[tok[s]])[d] * scale).
-// grid ceil(seq*hidden/256), block 256.  Same rounding as the Q6_K dequantiser.
+// Embedding lookup from a raw quantised table (the weights stay in their GGUF
+// blocks; only the looked-up rows are dequantised):
+//   out[s][d] = fp16(dequant(W[tok[s]])[d] * scale),
+// dequant with the exact dequantiser's rounding.  grid ceil(seq*hidden/256),
+// block 256, one element per thread (a few KB per token: off the hot path).
 // ---------------------------------------------------------------------------
+template <int FMT>
+__device__ __forceinline__ void embedding_elem(const int* __restrict__ token_ids, const void* __restrict__ table,
+                                               __half* __restrict__ output, int seq_len, int hidden, float scale) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= seq_len * hidden) return;
+    const int s = idx / hidden, dcol = idx % hidden;
+    const size_t tok = (size_t)token_ids[s];
+    constexpr int QB = FMT == 8 ? QK8_0 : QK_K;
+    constexpr int BYTES = FMT == 4 ? Q4K_BYTES : FMT == 6 ? Q6K_BYTES : Q80_BYTES;
+    const uint8_t* blk = (const uint8_t*)table + (tok * (hidden / QB) + dcol / QB) * BYTES;
+    const int e = dcol % QB;
+    const float w = FMT == 4 ? q4k_elem_exact(blk, e) : FMT == 6 ? q6k_elem_exact(blk, e) : q80_elem_exact(blk, e);
+    float v = __fmul_rn(w, scale);
+    // keep the product and the fp16 rounding apart: fused into one mixed
+    // fma with a +0 addend they would turn a -0 product into +0
+    asm volatile("" : "+v"(v));
+    output[idx] = __float2half(v);
+}
+
+// embedding_lookup_q6k.hip.template:17-58 (Qwen2.5-1.5B: tied to the LM head)
 extern "C" __global__ __launch_bounds__(256) void embedding_lookup_q6k_kernel(
     const int* __restrict__ token_ids, const void* __restrict__ embed_weight, __half* __restrict__ output,
     int seq_len, int hidden_size, float embedding_scale) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= seq_len * hidden_size) return;
-    const int s = idx / hidden_size, dcol = idx % hidden_size;
-    const int tok = token_ids[s];
-    const uint8_t* blk = (const uint8_t*)embed_weight + ((size_t)tok * (hidden_size / QK_K) + dcol / QK_K) * Q6K_BYTES;
-    const int e = dcol % QK_K;
-    const int half = e >> 7, g = (e >> 5) & 3, l = e & 31;
-    const uint8_t qlb = blk[64 * half + l + ((g & 1) ? 32 : 0)];
-    const int nib = (g < 2) ? (qlb & 0x0F) : (qlb >> 4);
-    const int q = (nib | (((blk[128 + 32 * half + l] >> (2 * g)) & 3) << 4)) - 32;
-    const int8_t sc = (int8_t)blk[192 + 8 * half + (l >> 4) + 2 * g];
-    const float d = h2f_bits(blk[208] | (blk[209] << 8));
-    const float w = __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
-    output[idx] = __float2half(w * embedding_scale);
+    embedding_elem<6>(token_ids, embed_weight, output, seq_len, hidden_size, embedding_scale);
+}
+// embedding_lookup_q4k.hip.template:26-75 (Qwen2.5-7B: untied, Q4_K table)
+extern "C" __global__ __launch_bounds__(256) void embedding_lookup_q4k_kernel(
+    const int* __restrict__ token_ids, const void* __restrict__ embed_weight, __half* __restrict__ output,
+    int seq_len, int hidden_size, float embedding_scale) {
+    embedding_elem<4>(token_ids, embed_weight, output, seq_len, hidden_size, embedding_scale);
+}
+// embedding_lookup_q8_0.hip.template:15-46 (tied Q8_0 tables; scale 12 for Granite)
+extern "C" __global__ __launch_bounds__(256) void embedding_lookup_q8_0_kernel(
+    const int* __restrict__ token_ids, const void* __restrict__ embed_weight, __half* __restrict__ output,
+    int seq_len, int hidden_size, float embedding_scale) {
+    embedding_elem<8>(token_ids, embed_weight, output, seq_len, hidden_size, embedding_scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -761,11 +785,13 @@ hipError_t add(const void* r, const void* in, void* out, int n, float scale, hip
     return hipGetLastError();
 }
 
-hipError_t embedding_q6k(const int* tokens, const void* table, void* out, int n_tokens, int hidden, float scale,
-                         hipStream_t st) {
+hipError_t embedding(int fmt, const int* tokens, const void* table, void* out, int n_tokens, int hidden,
+                     float scale, hipStream_t st) {
     const int n = n_tokens * hidden;
-    hipLaunchKernelGGL(embedding_lookup_q6k_kernel, dim3((n + 255) / 256), dim3(256), 0, st, tokens, table,
-                       (__half*)out, n_tokens, hidden, scale);
+    auto* k = fmt == 4 ? embedding_lookup_q4k_kernel : fmt == 6 ? embedding_lookup_q6k_kernel
+                                                                 : embedding_lookup_q8_0_kernel;
+    hipLaunchKernelGGL(k, dim3((n + 255) / 256), dim3(256), 0, st, tokens, table, (__half*)out, n_tokens, hidden,
+                       scale);
     return hipGetLastError();
 }
 

@@ -47,3 +47,38 @@ __device__ __forceinline__ uint32_t lds_u16(const uint8_t* p) {
     return *reinterpret_cast<const uint16_t*>(p);
 }
 
+
+// Element e of one block, dequantised exactly as the NumPy dequantiser
+// computes it (fp32, every product and difference rounded on its own: no
+// FMA contraction).  vte/compiler/dequantizer.py:6-70 (Q4_K), 129-169 (Q6_K),
+// 172-196 (Q8_0).
+__device__ __forceinline__ float q4k_elem_exact(const uint8_t* blk, int e) {
+    const float d = h2f_bits(blk[0] | (blk[1] << 8));
+    const float dmin = h2f_bits(blk[2] | (blk[3] << 8));
+    const uint8_t* s = blk + 4;
+    const int mblk = e >> 6, hi = (e >> 5) & 1, i = e & 31;
+    const int j = 2 * mblk + hi;  // sub-block: low nibbles 2*mblk, high nibbles 2*mblk+1
+    int sc, mn;
+    if (j < 4) {
+        sc = s[j] & 63;
+        mn = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
+        mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+    const uint8_t q = blk[16 + 32 * mblk + i];
+    const int nib = hi ? (q >> 4) : (q & 0x0F);
+    return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)nib), __fmul_rn(dmin, (float)mn));
+}
+__device__ __forceinline__ float q6k_elem_exact(const uint8_t* blk, int e) {
+    const int half = e >> 7, g = (e >> 5) & 3, l = e & 31;
+    const uint8_t qlb = blk[64 * half + l + ((g & 1) ? 32 : 0)];
+    const int nib = (g < 2) ? (qlb & 0x0F) : (qlb >> 4);
+    const int q = (nib | (((blk[128 + 32 * half + l] >> (2 * g)) & 3) << 4)) - 32;
+    const int8_t sc = (int8_t)blk[192 + 8 * half + (l >> 4) + 2 * g];
+    const float d = h2f_bits(blk[208] | (blk[209] << 8));
+    return __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+}
+__device__ __forceinline__ float q80_elem_exact(const uint8_t* blk, int i) {
+    return __fmul_rn(h2f_bits(blk[0] | (blk[1] << 8)), (float)(int8_t)blk[2 + i]);
+}

@@ -39,6 +39,8 @@ SIGNATURES = {
     "vte_swiglu": [_vp, _vp, _vp, _i, _vp],
     "vte_add": [_vp, _vp, _vp, _i, _f, _vp],
     "vte_embedding_q6k": [_vp, _vp, _vp, _i, _i, _f, _vp],
+    "vte_embedding_q4k": [_vp, _vp, _vp, _i, _i, _f, _vp],
+    "vte_embedding_q8_0": [_vp, _vp, _vp, _i, _i, _f, _vp],
     "vte_topk_scratch_bytes": [_i],
     "vte_topk": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
     "vte_topk_noalloc": [_vp, _i, _i, _i, _vp, _vp, _vp],
@@ -150,9 +152,14 @@ class VTEKernels:
     def add(self, residual, inp, out, n, scale=1.0, stream=None):
         self._check(self.lib.vte_add(_p(residual), _p(inp), _p(out), n, scale, self._st(stream)), "vte_add")
 
+    def embedding(self, fmt, tokens, table, out, n_tokens, hidden, scale=1.0, stream=None):
+        """out [n_tokens][hidden] fp16 = rows ``tokens`` of a q4_k / q6_k / q8_0 table, times ``scale``."""
+        name = {"q4_k": "vte_embedding_q4k", "q6_k": "vte_embedding_q6k", "q8_0": "vte_embedding_q8_0"}[fmt]
+        self._check(getattr(self.lib, name)(_p(tokens), _p(table), _p(out), n_tokens, hidden, scale,
+                                            self._st(stream)), name)
+
     def embedding_q6k(self, tokens, table, out, n_tokens, hidden, scale=1.0, stream=None):
-        self._check(self.lib.vte_embedding_q6k(_p(tokens), _p(table), _p(out), n_tokens, hidden, scale,
-                                               self._st(stream)), "vte_embedding_q6k")
+        self.embedding("q6_k", tokens, table, out, n_tokens, hidden, scale, stream)
 
     def topk_scratch_bytes(self, rows: int) -> int:
         return int(self.lib.vte_topk_scratch_bytes(rows))
