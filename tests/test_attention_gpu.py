@@ -64,6 +64,21 @@ def test_in_kernel_combine_matches_separate(hip, K, ctx, split):
         assert rel_l2(b[i], attention_ref(q[i], kc[i], vc[i], o + 1, SCALE)) <= TOL
 
 
+@pytest.mark.parametrize("B,split", [(1, 128), (9, 128), (16, 256)])
+def test_in_kernel_combine_ragged_batches(hip, K, B, split):
+    """The in-kernel (last-block) combine on ragged batches: equal to the
+    separate combine up to summation order, and to the float64 oracle."""
+    rng = np.random.default_rng(77 + B)
+    lens = rng.integers(1, 2600, B)
+    lens[0] = 2049
+    q, kc, vc = _inputs(rng, B, 2600)
+    a = _run(hip, K, q, kc, vc, lens - 1, split)
+    b = _run(hip, K, q, kc, vc, lens - 1, split, fused=True)
+    assert rel_l2(b, a) <= 1e-5
+    for i in range(min(B, 3)):
+        assert rel_l2(b[i], attention_ref(q[i], kc[i], vc[i], int(lens[i]), SCALE)) <= TOL
+
+
 @pytest.mark.parametrize("B,split", [(8, 512), (16, 512), (32, 512), (8, 32)])
 def test_config3b_ragged_matches_batch1_exactly(hip, K, B, split):
     rng = np.random.default_rng(1000 + B)

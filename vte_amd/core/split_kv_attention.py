@@ -19,6 +19,7 @@ sequence) and issues the launches of one layer.  MI355X choices:
 from __future__ import annotations
 
 import math
+import os
 
 from ..kernels import kernels
 
@@ -39,7 +40,7 @@ def choose_split(max_context: int, batch: int, n_kv: int, num_cus: int) -> int:
 
 class SplitKVAttentionDispatcher:
     def __init__(self, hip, n_q: int, n_kv: int, head_dim: int, max_context: int, batch_size: int = 1,
-                 split: int | None = None, allocator=None, fuse_combine: bool = False):
+                 split: int | None = None, allocator=None, fuse_combine: bool | None = None):
         self.hip = hip
         self.n_q, self.n_kv, self.head_dim = n_q, n_kv, head_dim
         self.batch = batch_size
@@ -47,9 +48,14 @@ class SplitKVAttentionDispatcher:
         self.split = split or choose_split(max_context, batch_size, n_kv, hip.get_num_cus() if hip else 256)
         self.max_splits = math.ceil(max_context / self.split)
         self.scale = 1.0 / math.sqrt(head_dim)
-        # In-kernel (last-block) combine saves a launch but pays a device-scope
-        # fence per block; measured slower than the separate combine launch at
-        # 2K context on MI355X, so it is opt-in.
+        # In-kernel (last-block) combine: saves a launch but chains three
+        # device-coherent memory round trips (partial stores complete, count,
+        # read back), about 1 us each on MI355X, so at a 2K context it costs
+        # more than the separate combine launch (attention 282 vs 210 us per
+        # 28-layer step, also with every split of a group on one XCD); opt-in
+        # (VTE_ATT_FUSE=1 or fuse_combine=True).
+        if fuse_combine is None:
+            fuse_combine = os.environ.get("VTE_ATT_FUSE", "0") == "1"
         self.fuse_combine = fuse_combine
         self.K = kernels()
         from ..bridge.memory import DeviceArray, MemoryRegion

@@ -59,6 +59,17 @@ extern "C" __global__ void kv_cache_append_kernel(const __half* __restrict__ k, 
 // ---------------------------------------------------------------------------
 // Native partial pass
 // ---------------------------------------------------------------------------
+// Device-coherent float store / load (relaxed device-scope atomics: on this
+// multi-XCD part they write through / read past the XCD's L2), and a wait for
+// this wave's outstanding stores to complete.
+__device__ __forceinline__ void st_coh(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // One wave's 32-token tile: K rows (MFMA A operands, two 16-token halves) and
 // V rows (two fp16 per lane: d = 2 lane, 2 lane + 1).  Rows past `rmax` read
 // row `rmax` instead (results for them are masked).
@@ -323,35 +334,44 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         }
         const int qh = kvh * G + h % G;
         const size_t st = ((size_t)bc * n_q + qh) * max_splits + sp;
-        part_o[st * ATT_D + d] = O;
-        if (d == 0) { part_m[st] = M; part_l[st] = L; }
+        if (counters != nullptr) {  // read back by another block: write-through stores
+            st_coh(part_o + st * ATT_D + d, O);
+            if (d == 0) { st_coh(part_m + st, M); st_coh(part_l + st, L); }
+        } else {
+            part_o[st * ATT_D + d] = O;
+            if (d == 0) { part_m[st] = M; part_l[st] = L; }
+        }
     }
     if (QC > 1 || counters == nullptr) return;  // separate combine launch
 
     // ---- last block of this (sequence, KV head) performs the LSE combine ----
-    // Release the partials at device scope, count this split, and let the block
-    // that completes the count read every split back (acquire) and combine.
+    // The partials were written with device-coherent (write-through) stores;
+    // once every wave's stores have completed, thread 0 counts this split, and
+    // the block that completes the count reads every split back with
+    // device-coherent loads and combines.  Only coherent accesses cross blocks,
+    // so no L2 writeback or invalidate is needed (a device-scope release /
+    // acquire fence writes back and invalidates the XCD's whole L2, which per
+    // block costs more than a separate combine launch on this 8-XCD part).
     // The counter is reset by that block, so a captured graph can be replayed.
     __shared__ int s_last;
-    __threadfence();
+    wait_stores();
     __syncthreads();
     const int ns = (len + split - 1) / split;
     if (threadIdx.x == 0) {
         int* ctr = counters + (size_t)b * n_kv + kvh;
-        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (prev == ns - 1);
         if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     // per-split weights w[h][c] = exp(m_c - M_h) and L_h in LDS (parallel loads),
     // then each thread combines its (head, dim) outputs with unrolled loads.
     auto& wsh = lds.w;  // o_sh is dead once the partials are in global memory
     __shared__ float Msh[ATT_MAXG], Lsh[ATT_MAXG];
     for (int i = threadIdx.x; i < G * ns; i += 256) {
         const int h = i / ns, c = i - h * ns;
-        wsh[h][c] = part_m[((size_t)b * n_q + kvh * G + h) * max_splits + c];
+        wsh[h][c] = ld_coh(part_m + ((size_t)b * n_q + kvh * G + h) * max_splits + c);
     }
     __syncthreads();
     if (wv < G) {  // wave h: max and denominator of head h
@@ -364,7 +384,7 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         for (int c = lane; c < ns; c += 64) {
             const float wgt = __expf(wsh[h][c] - M);
             wsh[h][c] = wgt;
-            L = fmaf(part_l[base + c], wgt, L);
+            L = fmaf(ld_coh(part_l + base + c), wgt, L);
         }
         L = wave_sum(L);
         if (lane == 0) { Msh[h] = M; Lsh[h] = L; }
@@ -380,7 +400,7 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
             for (int c = lane; c < ns; c += 64) {
                 const float wgt = __expf(wsh[h][c] - M);
                 wsh[h][c] = wgt;
-                L = fmaf(part_l[base + c], wgt, L);
+                L = fmaf(ld_coh(part_l + base + c), wgt, L);
             }
             L = wave_sum(L);
             if (lane == 0) { Msh[h] = M; Lsh[h] = L; }
@@ -396,11 +416,11 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         for (; c + 8 <= ns; c += 8) {
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = po[(size_t)(c + j) * ATT_D];
+            for (int j = 0; j < 8; ++j) v[j] = ld_coh(po + (size_t)(c + j) * ATT_D);
 #pragma unroll
             for (int j = 0; j < 8; ++j) O = fmaf(v[j], wsh[h][c + j], O);
         }
-        for (; c < ns; ++c) O = fmaf(po[(size_t)c * ATT_D], wsh[h][c], O);
+        for (; c < ns; ++c) O = fmaf(ld_coh(po + (size_t)c * ATT_D), wsh[h][c], O);
         st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(Lsh[h], 1e-20f));
     }
 }

@@ -203,8 +203,11 @@ __global__ __launch_bounds__(64 * MF_WAVES) void gemm_ws_splitk_kernel(const __h
 #define GS_NSB (GS_K / QK_K)
 #define GS_LDX (GS_K + 8)  // halves per staged activation row
 
-template <typename TI, typename TO, int FMT, int NT, int WPB>
-__global__ __launch_bounds__(64 * WPB) void gemm_stream_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
+// OT (one tile): a wave owns exactly one 16-row tile (grid = tiles / WPB,
+// the hardware balances the blocks) and requests all six of its super-blocks
+// at once.
+template <typename TI, typename TO, int FMT, int NT, int WPB, bool OT = false>
+__global__ __launch_bounds__(64 * WPB, (OT && NT == 1) ? 4 : 2) void gemm_stream_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
                                                           TO* __restrict__ y, int M, int N, const TO* __restrict__ bias,
                                                           const TO* __restrict__ residual, float rs) {
     constexpr bool XM = NT > 1;  // minimum-term form (q4_xmin)
@@ -214,18 +217,74 @@ __global__ __launch_bounds__(64 * WPB) void gemm_stream_kernel(const TI* __restr
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
     constexpr int CPR = GS_K / 8;  // 8-element chunks per row
-    for (int i = tid; i < 16 * NT * CPR; i += 64 * WPB) {
+    constexpr int BPB = FMT == 4 ? Q4K_BYTES : Q6K_BYTES;
+    const size_t row_bytes = (size_t)GS_NSB * BPB;
+    const int ntiles = (N + 15) / 16;
+    using Raw = typename SbRaw<FMT>::Raw;
+    Raw r[OT ? GS_NSB : 1];
+    const int ot_tile = blockIdx.x * WPB + wv;
+    if constexpr (OT) {
+        // The block's activation chunks, then the tile's weights, all requested
+        // at once; the chunks (requested first: the load counter is in order)
+        // go to LDS as soon as they arrive, while the weights are in flight.
+        constexpr int XPT = 16 * NT * CPR / (64 * WPB);  // chunks per thread
+        static_assert(XPT * 64 * WPB == 16 * NT * CPR, "activation chunks fill the block");
+        half8_t xv[XPT];
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int i = tid + j * 64 * WPB, m = i / CPR, c = i - m * CPR;
+            xv[j] = load_x8<TI>(x + (size_t)(m < M ? m : 0) * GS_K + 8 * c, m < M);
+        }
+        const uint8_t* rowp = w + (size_t)min(min(ot_tile, ntiles - 1) * 16 + col, N - 1) * row_bytes;
+#pragma unroll
+        for (int sb = 0; sb < GS_NSB; ++sb) sb_load(rowp + sb * BPB, grp, r[sb]);
+        __builtin_amdgcn_sched_barrier(0);  // every load issued before the LDS stores (not sunk into the K loop)
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int i = tid + j * 64 * WPB, m = i / CPR, c = i - m * CPR;
+            *reinterpret_cast<half8_t*>(xs + m * GS_LDX + 8 * c) = xv[j];
+        }
+    }
+    for (int i = tid; i < (OT ? 0 : 16 * NT * CPR); i += 64 * WPB) {
         const int m = i / CPR, c = i - m * CPR;
         const half8_t v = load_x8<TI>(x + (size_t)(m < M ? m : 0) * GS_K + 8 * c, m < M);
         *reinterpret_cast<half8_t*>(xs + m * GS_LDX + 8 * c) = v;
     }
     __syncthreads();
-    constexpr int BPB = FMT == 4 ? Q4K_BYTES : Q6K_BYTES;
-    const size_t row_bytes = (size_t)GS_NSB * BPB;
-    const int ntiles = (N + 15) / 16;
+    if constexpr (OT) {
+        // no early exit for waves past the last tile (they recompute it and
+        // store nothing), so the weight loads above stay where they are
+        const int tile = ot_tile;
+        floatx4_t acc[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[nt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int sb = 0; sb < GS_NSB; ++sb) {
+            typename SbRaw<FMT>::Ops ops;
+            sb_ops<XM>(r[sb], grp, ops);
+            half8_t bx[8][NT];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int kb = sb * QK_K + kslot_base<FMT>(t, grp);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    bx[t][nt] = *reinterpret_cast<const half8_t*>(xs + (nt * 16 + col) * GS_LDX + kb);
+            }
+            XMin<NT, XM> xm;
+            sb_xmin<FMT, NT, XM>(bx, xl[wv], xm);
+            sb_mfma<NT>(ops, bx, xm, acc);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rr = tile * 16 + col, m = nt * 16 + 4 * grp + i;
+                if (tile < ntiles && rr < N && m < M) gemv_store<TO>(y, bias, residual, rs, rr, m, N, acc[nt][i]);
+            }
+        return;
+    }
     for (int tile = blockIdx.x * WPB + wv; tile < ntiles; tile += gridDim.x * WPB) {
         const uint8_t* rowp = w + (size_t)min(tile * 16 + col, N - 1) * row_bytes;
-        using Raw = typename SbRaw<FMT>::Raw;
         auto load = [&](int sb, Raw& r) { sb_load(rowp + sb * BPB, grp, r); };
         Raw cur, nxt, nx2;
         load(0, cur);
@@ -301,18 +360,26 @@ template <typename TI, typename TO, int FMT>
 static hipError_t launch_stream(const void* x, const void* w, void* y, int M, int N, const void* bias,
                                 const void* residual, float rs, hipStream_t st) {
     constexpr int WPB = 8;  // 8-wave blocks, two per CU
+    static const int bpc = getenv("VTE_GS_BPC") ? atoi(getenv("VTE_GS_BPC")) : 2;
+    static const bool gs_ot = getenv("VTE_GS_OT") ? atoi(getenv("VTE_GS_OT")) != 0 : true;
     const int ntiles = (N + 15) / 16;
-    const int grid = std::min((ntiles + WPB - 1) / WPB, gs_num_cus() * 2);
+    const int grid = std::min((ntiles + WPB - 1) / WPB, gs_num_cus() * bpc);
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mc = (M - m0 < 32) ? (M - m0) : 32;
         const TI* xs = (const TI*)x + (size_t)m0 * GS_K;
         TO* ys = (TO*)y + (size_t)m0 * N;
         const TO* rp = residual ? (const TO*)residual + (size_t)m0 * N : nullptr;
-#define GS_LAUNCH(NT_, W_)                                                                                          \
-    hipLaunchKernelGGL((gemm_stream_kernel<TI, TO, FMT, NT_, W_>), dim3(grid), dim3(64 * W_), 16 * NT_ * GS_LDX * 2, st, \
-                       xs, (const uint8_t*)w, ys, mc, N, (const TO*)bias, rp, rs)
-        if (M > 16) GS_LAUNCH(2, WPB);  // a 16-column tail of a longer batch too (one minimum-term form)
-        else GS_LAUNCH(1, WPB);
+#define GS_LAUNCH(NT_, W_, OT_, G_)                                                                                \
+    hipLaunchKernelGGL((gemm_stream_kernel<TI, TO, FMT, NT_, W_, OT_>), dim3(G_), dim3(64 * W_), 16 * NT_ * GS_LDX * 2, \
+                       st, xs, (const uint8_t*)w, ys, mc, N, (const TO*)bias, rp, rs)
+        const int ot = (ntiles + WPB - 1) / WPB;
+        if (gs_ot) {
+            if (M > 16) GS_LAUNCH(2, WPB, true, ot);
+            else GS_LAUNCH(1, WPB, true, ot);
+        } else {
+            if (M > 16) GS_LAUNCH(2, WPB, false, grid);  // a 16-column tail of a longer batch too (one minimum-term form)
+            else GS_LAUNCH(1, WPB, false, grid);
+        }
 #undef GS_LAUNCH
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
