@@ -246,6 +246,56 @@ int vte_attn_out_gemv(const float* part_m, const float* part_l, const float* par
  * prefixes); no reference counterpart (test and benchmark input). */
 int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float scale, void* stream);
 
+/* ---- Persistent decode step (batch 1) ----
+ * The whole Qwen2-shaped decode step of one sequence (every layer's
+ * RMSNorm, q/k/v + bias + RoPE + K/V append, split-KV attention, o-proj +
+ * residual, RMSNorm, gate/up + SwiGLU, down + residual; then the output norm
+ * and the LM head) as ONE kernel launch of one block per CU, so it can be
+ * captured as a single graph node.  Blocks hand activations to each other
+ * through flagged words in the workspace instead of kernel boundaries.
+ * Limits: head_dim 128, n_q / n_kv <= 8, hidden, ffn and n_q * 128 multiples
+ * of 256 and <= 10240; q/k/o/gate/up Q4_K, v and down Q4_K or Q6_K, LM head
+ * Q4_K or Q6_K; the KV cache of one sequence [max_seq][n_kv][128] fp16 per
+ * layer.  Replaces: the batch-1 capture of vte/core/hip_graph_executor.py:504-738
+ * (nodes of vte/compiler/qwen_compute.py:100-282) up to the LM-head logits. */
+typedef struct vte_decode_layer {
+    const void *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down; /* raw GGUF rows */
+    const void *q_bias, *k_bias, *v_bias;                    /* fp16, nullable */
+    const void *attn_norm, *ffn_norm;                        /* fp16 [hidden] */
+    void *k_cache, *v_cache;                                 /* fp16 [max_seq][n_kv][128] */
+    int fmt_q, fmt_k, fmt_v, fmt_o, fmt_gate_up, fmt_down;
+} vte_decode_layer;
+
+typedef struct vte_decode_model {
+    int n_layers, hidden, ffn, n_q, n_kv, head_dim, vocab, max_seq;
+    float eps;
+    const void *rope_cos, *rope_sin; /* fp16 [max_seq][128] (rope_cache_builder.py layout) */
+    const void *output_norm;         /* fp16 [hidden] */
+    const void *lm_head;             /* raw GGUF rows [vocab][hidden] */
+    int fmt_lm;
+} vte_decode_model;
+
+/* Device workspace bytes the step needs (flagged activation buffers,
+ * attention partials, the layer table and a control word block). */
+long long vte_decode_workspace_bytes(const vte_decode_model* m);
+
+/* Validate the model, copy the layer table into the workspace and clear its
+ * control words (synchronous on `stream`; not capturable).  Once per
+ * workspace, before the first vte_decode_step. */
+int vte_decode_setup(const vte_decode_model* m, const vte_decode_layer* layers, void* workspace,
+                     long long workspace_bytes, void* stream);
+
+/* One step: x = the token's embedding (fp16 [hidden]), kv_offset[0] = its
+ * position (read on the device; rows 0..kv_offset-1 of every cache hold the
+ * prefix, row kv_offset is written), logits fp32 [vocab].  Capturable.
+ * Steps on one workspace must not overlap. */
+int vte_decode_step(const vte_decode_model* m, void* workspace, const int* kv_offset, const void* x, float* logits,
+                    void* stream);
+
+/* Synchronous read of the workspace's error flags: bit 0 = a block waited
+ * past its deadline (a step whose blocks could not all be resident). */
+int vte_decode_status(void* workspace, int* flags);
+
 #ifdef __cplusplus
 }
 #endif

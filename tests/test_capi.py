@@ -70,3 +70,29 @@ def test_host_side_queries_and_validation():
     assert lib.vte_embedding_q8_0(16, 16, 16, 2, 1000, ctypes.c_float(1.0), None) == -1
     assert b"multiple of 32" in lib.vte_last_error()
     assert lib.vte_embedding_q6k(None, 16, 16, 2, 1536, ctypes.c_float(1.0), None) == -1
+
+
+def test_decode_workspace_and_rejections_on_host():
+    """Workspace size of the persistent step for the 1.5B shape, and shapes
+    the kernel does not support rejected before any device call."""
+    from vte_amd.bridge.hip_runtime import HIPSafetyError
+    from vte_amd.kernels import DecodeModel, kernels
+    K = kernels()
+    m = DecodeModel()
+    m.n_layers, m.hidden, m.ffn, m.n_q, m.n_kv, m.head_dim, m.vocab, m.max_seq = 28, 1536, 8960, 12, 2, 128, 151936, 4096
+    m.eps = 1e-6
+    n = K.decode_workspace_bytes(m)
+    # control + layer table + flagged buffers + attention records (12 heads x 128 splits x 130 x 8 B)
+    assert 12 * 128 * 130 * 8 < n < 12 * 128 * 130 * 8 + (1 << 20)
+    for field, bad in (("head_dim", 64), ("n_kv", 5), ("hidden", 1000), ("ffn", 12288)):
+        mm = DecodeModel.from_buffer_copy(m)
+        setattr(mm, field, bad)
+        with pytest.raises(HIPSafetyError):
+            K.decode_workspace_bytes(mm)
+    mm = DecodeModel.from_buffer_copy(m)
+    mm.n_q, mm.n_kv = 24, 2  # 12 query heads per KV head: more than a block's MFMA slots serve
+    with pytest.raises(HIPSafetyError):
+        K.decode_workspace_bytes(mm)
+    # the step itself rejects a model without its pointers before launching
+    with pytest.raises(HIPSafetyError):
+        K.decode_step(m, 256, 256, 256, 256)

@@ -23,13 +23,14 @@ MI355X-specific structure:
 from __future__ import annotations
 
 import ctypes
+import os
 from typing import Optional, Sequence
 
 import numpy as np
 
 from ..bridge.hip_runtime import HIPRuntime, HIPSafetyError
 from ..bridge.memory import DeviceArray, MemoryRegion, SlabAllocator
-from ..kernels import kernels
+from ..kernels import DecodeLayer, DecodeModel, FMT, kernels
 from .model_config import Qwen2Config
 from .rope_cache import build_rope_cache
 from .split_kv_attention import SplitKVAttentionDispatcher, choose_split
@@ -55,12 +56,17 @@ def splitk_splits(K: int) -> int:
 class HIPGraphExecutor:
     def __init__(self, hip: HIPRuntime, model: SyntheticQwen2, batch_size: int = 1, max_seq: Optional[int] = None,
                  top_k: int = 40, gemm_min_batch: int = 3, split: Optional[int] = None, fused: bool = True,
-                 shared: Optional["HIPGraphExecutor"] = None, kv_seq: int = 0):
+                 shared: Optional["HIPGraphExecutor"] = None, kv_seq: int = 0, persistent: Optional[bool] = None):
         """``shared``: reuse that executor's weights, RoPE tables and the KV
         cache of its sequence ``kv_seq`` (columns of this executor are tokens of
         that one sequence: KV rows at each column's own position, stride 0),
         with activation buffers of ``batch_size`` columns and only the last
-        column's logits (the prefill of ``PrefillRunner``)."""
+        column's logits (the prefill of ``PrefillRunner``).  ``persistent``
+        (batch 1; opt-in, or VTE_PERSISTENT=1): the layers and the LM head run
+        as one persistent launch instead of six launches per layer (measured
+        slower than the graph of per-node launches on MI355X: 1.18 vs 0.89 ms)."""
+        if persistent is None:
+            persistent = os.environ.get("VTE_PERSISTENT", "0") == "1"
         self.hip = hip
         self.closed = False
         self._dependents = []  # objects holding pointers into this executor's slab (closed with it)
@@ -82,6 +88,9 @@ class HIPGraphExecutor:
         # batch <= 4: the LSE combine runs in the o-proj prologue up to this many splits
         self.oproj_combine_max_splits = 8
         self.K = kernels()
+        # batch 1: the whole step as one persistent launch (decode_persistent.hip)
+        self.persistent = (self.fused and batch_size == 1 and shared is None and persistent
+                           and self._persistent_supported(model))
         self.graph = None
         self.graph_exec = None
 
@@ -103,6 +112,10 @@ class HIPGraphExecutor:
         # split-KV scratch: [B][n_q][splits] stats and [B][n_q][splits][hd] partial outputs
         sp = split or choose_split(self.max_seq, B, cfg.n_kv, 256)
         need += B * cfg.n_q * (-(-self.max_seq // sp) + 1) * (cfg.head_dim + 2) * 4 + B * cfg.n_kv * 4
+        if self.persistent:
+            self._pd_model = self._decode_model_struct(model)
+            self._pd_ws_bytes = self.K.decode_workspace_bytes(self._pd_model)
+            need += self._pd_ws_bytes + 4096
         self.slab = SlabAllocator(hip, 0, requested_pool_size=need + (32 << 20))
         self.slab.initialize()
         A = lambda shape, dt, tag, reg=MemoryRegion.ACTIVATIONS: DeviceArray(hip, shape, dt, tag, self.slab, reg)
@@ -145,6 +158,8 @@ class HIPGraphExecutor:
         self.attn = SplitKVAttentionDispatcher(hip, cfg.n_q, cfg.n_kv, cfg.head_dim, self.max_seq, B, split,
                                                allocator=self.slab)
         self.h_final = 0  # index of the hidden buffer holding the layer output
+        if self.persistent:
+            self._setup_persistent()
 
     def _upload_weights(self, model, W, A) -> None:
         cfg, B = self.cfg, self.B
@@ -172,6 +187,57 @@ class HIPGraphExecutor:
         self.k_cache = [A(kv_shape, np.float16, f"blk.{L}.k_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
         self.v_cache = [A(kv_shape, np.float16, f"blk.{L}.v_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
 
+    @staticmethod
+    def _persistent_supported(model) -> bool:
+        cfg = model.cfg
+        if cfg.head_dim != 128 or cfg.n_q % cfg.n_kv or cfg.n_q // cfg.n_kv > 8:
+            return False
+        if any(d % 256 or d > 10240 for d in (cfg.hidden, cfg.ffn, cfg.q_dim)):
+            return False
+        lm = getattr(model, "lm_head", None)
+        lm_fmt = getattr(model, "token_embd_fmt", "q6_k") if lm is None or lm is model.token_embd else \
+            getattr(model, "lm_head_fmt", "q6_k")
+        if lm_fmt not in ("q4_k", "q6_k"):
+            return False
+        for lw in model.layers:
+            if any(lw[p + "_fmt"] != "q4_k" for p in ("q", "k", "o", "gate", "up")):
+                return False
+            if lw["v_fmt"] not in ("q4_k", "q6_k") or lw["down_fmt"] not in ("q4_k", "q6_k"):
+                return False
+        return True
+
+    def _decode_model_struct(self, model) -> DecodeModel:
+        cfg = self.cfg
+        m = DecodeModel()
+        m.n_layers, m.hidden, m.ffn, m.n_q, m.n_kv = cfg.n_layers, cfg.hidden, cfg.ffn, cfg.n_q, cfg.n_kv
+        m.head_dim, m.vocab, m.max_seq, m.eps = cfg.head_dim, cfg.vocab, self.max_seq, cfg.eps
+        return m
+
+    def _setup_persistent(self) -> None:
+        """Workspace and layer table of the persistent step (pointers into this slab)."""
+        m = self._pd_model
+        m.rope_cos, m.rope_sin = self.rope_cos.ptr, self.rope_sin.ptr
+        m.output_norm, m.lm_head, m.fmt_lm = self.output_norm.ptr, self.lm_head.ptr, FMT[self.lm_head_fmt]
+        self.pd_ws = DeviceArray(self.hip, self._pd_ws_bytes, np.uint8, "decode_workspace", self.slab,
+                                 MemoryRegion.ACTIVATIONS)
+        arr = (DecodeLayer * self.cfg.n_layers)()
+        for L, lw in enumerate(self.layers):
+            y = arr[L]
+            y.wq, y.wk, y.wv, y.wo = lw["q"].ptr, lw["k"].ptr, lw["v"].ptr, lw["o"].ptr
+            y.w_gate, y.w_up, y.w_down = lw["gate"].ptr, lw["up"].ptr, lw["down"].ptr
+            y.q_bias, y.k_bias, y.v_bias = lw["q_bias"].ptr, lw["k_bias"].ptr, lw["v_bias"].ptr
+            y.attn_norm, y.ffn_norm = lw["attn_norm"].ptr, lw["ffn_norm"].ptr
+            y.k_cache, y.v_cache = self.k_cache[L].ptr, self.v_cache[L].ptr
+            y.fmt_q, y.fmt_k, y.fmt_v = FMT[lw["q_fmt"]], FMT[lw["k_fmt"]], FMT[lw["v_fmt"]]
+            y.fmt_o, y.fmt_gate_up, y.fmt_down = FMT[lw["o_fmt"]], FMT[lw["gate_fmt"]], FMT[lw["down_fmt"]]
+        self._pd_layers = arr
+        self.K.decode_setup(m, ctypes.cast(arr, ctypes.c_void_p), self.pd_ws, self._pd_ws_bytes,
+                            stream=self.hip.stream)
+
+    def decode_status(self) -> int:
+        """Error flags of the persistent step (0: every wait completed in time)."""
+        return self.K.decode_status(self.pd_ws) if self.persistent else 0
+
     def _share(self, ex: "HIPGraphExecutor", seq: int) -> None:
         """Weights, RoPE tables and sequence ``seq``'s KV cache of ``ex``."""
         for name in ("token_embd", "token_embd_fmt", "lm_head", "lm_head_fmt", "output_norm", "layers", "rope_cos",
@@ -194,6 +260,7 @@ class HIPGraphExecutor:
 
     # launch classes of the fused step (kernel symbol in brackets)
     FUSED_CLASSES = ("embed", "attn_in", "attn", "o_proj", "ffn_in", "down", "lm_head", "topk")
+    PERSISTENT_CLASSES = ("embed", "decode", "topk")
 
     def _enqueue_fused(self, only=None) -> None:
         """Five or six launches per layer: norm+QKV+RoPE+append [fused_mv_kernel],
@@ -211,6 +278,13 @@ class HIPGraphExecutor:
         cur = 0
         if on("embed"):
             K.embedding(self.token_embd_fmt, self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
+        if self.persistent:  # every layer and the LM head: one launch
+            if on("decode"):
+                K.decode_step(self._pd_model, self.pd_ws, offs, self.h[cur], self.logits, stream=st)
+            if self.top_k > 0 and on("topk"):
+                K.topk(self.logits, B, cfg.vocab, self.top_k, self.topk_val, self.topk_idx, self.topk_scratch,
+                       stream=st, exclude=self._exclude())
+            return
         for L, lw in enumerate(self.layers):
             if on("attn_in"):
                 K.attn_in(self.h[cur], lw["attn_norm"], cfg.eps, lw["q"], lw["q_bias"], lw["q_fmt"], lw["k"],

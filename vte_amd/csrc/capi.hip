@@ -11,6 +11,11 @@
 
 #include "../../include/vte_amd.h"
 #include "vte_common.h"
+#include "fused_kernels.h"
+#include "decode_persistent.h"
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
 
 namespace vte {
 template <typename TI, typename TO>
@@ -397,3 +402,168 @@ int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float s
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------ persistent decode step
+
+namespace {
+struct PdLayout {
+    size_t ctrl, layers, ll_h, ll_q, ll_kv, ll_att, ll_hm, ll_act, part, total;
+};
+size_t pd_align(size_t x) { return (x + 255) & ~(size_t)255; }
+PdLayout pd_layout(const vte_decode_model* m) {
+    PdLayout L;
+    const size_t qd = (size_t)m->n_q * 128, kvd = (size_t)m->n_kv * 128;
+    size_t o = 0;
+    L.ctrl = o; o = pd_align(o + 256);
+    L.layers = o; o = pd_align(o + (size_t)m->n_layers * sizeof(vte_decode_layer));
+    L.ll_h = o; o = pd_align(o + (size_t)m->hidden * 4);
+    L.ll_q = o; o = pd_align(o + qd * 4);
+    L.ll_kv = o; o = pd_align(o + 2 * kvd * 4);
+    L.ll_att = o; o = pd_align(o + qd * 4);
+    L.ll_hm = o; o = pd_align(o + (size_t)m->hidden * 4);
+    L.ll_act = o; o = pd_align(o + (size_t)m->ffn * 4);
+    L.part = o; o = pd_align(o + (size_t)m->n_q * VTE_DECODE_MAX_SPLITS * 130 * 8);
+    L.total = o;
+    return L;
+}
+int pd_check_model(const vte_decode_model* m, bool pointers = true) {
+    REQUIRE(m != nullptr, "decode: null model");
+    REQUIRE(m->n_layers >= 1 && m->n_layers <= 1024, "decode: n_layers %d", m->n_layers);
+    REQUIRE(m->head_dim == 128, "decode: head_dim must be 128");
+    REQUIRE(m->n_kv >= 1 && m->n_q % m->n_kv == 0 && m->n_q / m->n_kv <= 8, "decode: n_q / n_kv must be <= 8");
+    const int qd = m->n_q * 128;
+    REQUIRE(m->hidden % 256 == 0 && m->hidden <= 10240 && m->ffn % 256 == 0 && m->ffn <= 10240 && qd % 256 == 0 &&
+                qd <= 10240, "decode: hidden, ffn and n_q*128 must be multiples of 256 up to 10240");
+    REQUIRE(fmv_ro(m->hidden) == fmv_ro(qd), "decode: hidden %d and q_dim %d need the same unit mapping", m->hidden, qd);
+    REQUIRE(m->vocab >= 1 && m->max_seq >= 1, "decode: vocab / max_seq");
+    if (!pointers) return 0;
+    REQUIRE(m->fmt_lm == 4 || m->fmt_lm == 6, "decode: LM head must be Q4_K or Q6_K");
+    REQUIRE(m->rope_cos && m->rope_sin && m->output_norm && m->lm_head, "decode: null model pointer");
+    REQUIRE(aligned(m->output_norm, 16) && aligned(m->lm_head, 16), "decode: 16-byte alignment");
+    return 0;
+}
+int pd_cap(int K, int upt) {  // rows a tile of K-long rows can hold at `upt` units per thread
+    const int per_row = (K / 256) * 4;
+    return fmv_ro(K) ? (ROWS_THREADS / per_row) * upt : (upt * ROWS_THREADS) / per_row;
+}
+int g_pd_cus[64] = {0};
+}  // namespace
+
+long long vte_decode_workspace_bytes(const vte_decode_model* m) {
+    if (pd_check_model(m, false)) return -1;
+    return (long long)pd_layout(m).total;
+}
+
+int vte_decode_setup(const vte_decode_model* m, const vte_decode_layer* layers, void* ws, long long ws_bytes,
+                     void* stream) {
+    int rc = pd_check_model(m);
+    if (rc) return rc;
+    REQUIRE(layers && ws, "decode_setup: null pointer");
+    REQUIRE(aligned(ws, 256), "decode_setup: workspace must be 256-byte aligned");
+    const PdLayout L = pd_layout(m);
+    REQUIRE(ws_bytes >= (long long)L.total, "decode_setup: workspace %lld < %zu bytes", ws_bytes, L.total);
+    for (int l = 0; l < m->n_layers; ++l) {
+        const vte_decode_layer& y = layers[l];
+        REQUIRE(y.wq && y.wk && y.wv && y.wo && y.w_gate && y.w_up && y.w_down && y.attn_norm && y.ffn_norm &&
+                    y.k_cache && y.v_cache, "decode_setup: layer %d: null pointer", l);
+        REQUIRE(y.fmt_q == 4 && y.fmt_k == 4 && y.fmt_o == 4 && y.fmt_gate_up == 4 &&
+                    (y.fmt_v == 4 || y.fmt_v == 6) && (y.fmt_down == 4 || y.fmt_down == 6),
+                "decode_setup: layer %d: q/k/o/gate/up Q4_K, v and down Q4_K or Q6_K", l);
+        REQUIRE(aligned(y.wq, 16) && aligned(y.wk, 16) && aligned(y.wv, 16) && aligned(y.wo, 16) &&
+                    aligned(y.w_gate, 16) && aligned(y.w_up, 16) && aligned(y.w_down, 16) &&
+                    aligned(y.attn_norm, 16) && aligned(y.ffn_norm, 16) && aligned(y.k_cache, 16) &&
+                    aligned(y.v_cache, 16), "decode_setup: layer %d: 16-byte alignment", l);
+    }
+    hipStream_t st = (hipStream_t)stream;
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    hipError_t e = hipMemsetAsync(base, 0, L.total, st);
+    if (e != hipSuccess) return hip_status(e, "decode_setup memset");
+    const uint32_t ctrl[4] = {1u, 0u, 0u, 0u};  // epoch starts at 1: no tag matches the cleared words
+    e = hipMemcpyAsync(base + L.ctrl, ctrl, sizeof(ctrl), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(base + L.layers, layers, (size_t)m->n_layers * sizeof(vte_decode_layer),
+                           hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return hip_status(e, "decode_setup copy");
+}
+
+int vte_decode_step(const vte_decode_model* m, void* ws, const int* kv_offset, const void* x, float* logits,
+                    void* stream) {
+    int rc = pd_check_model(m);
+    if (rc) return rc;
+    REQUIRE(ws && kv_offset && x && logits, "decode_step: null pointer");
+    REQUIRE(aligned(ws, 256) && aligned(x, 16), "decode_step: alignment");
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    REQUIRE(dev >= 0 && dev < 64, "decode_step: device %d", dev);
+    if (g_pd_cus[dev] == 0) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return hip_status(e, "hipDeviceGetAttribute");
+        g_pd_cus[dev] = n;
+    }
+    const int blocks = g_pd_cus[dev];  // one 256-thread block per CU
+    const PdLayout L = pd_layout(m);
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    VtePdPlan P{};
+    P.layers = reinterpret_cast<const VtePdLayer*>(base + L.layers);
+    P.n_layers = m->n_layers;
+    P.hidden = m->hidden;
+    P.ffn = m->ffn;
+    P.n_q = m->n_q;
+    P.n_kv = m->n_kv;
+    P.vocab = m->vocab;
+    P.eps = m->eps;
+    P.scale = 1.0f / sqrtf(128.0f);
+    P.kv_offset = kv_offset;
+    P.x = static_cast<const __half*>(x);
+    P.rope_cos = static_cast<const __half*>(m->rope_cos);
+    P.rope_sin = static_cast<const __half*>(m->rope_sin);
+    P.output_norm = m->output_norm;
+    P.lm_head = m->lm_head;
+    P.fmt_lm = m->fmt_lm;
+    P.logits = logits;
+    P.ll_h = reinterpret_cast<uint32_t*>(base + L.ll_h);
+    P.ll_q = reinterpret_cast<uint32_t*>(base + L.ll_q);
+    P.ll_kv = reinterpret_cast<uint32_t*>(base + L.ll_kv);
+    P.ll_att = reinterpret_cast<uint32_t*>(base + L.ll_att);
+    P.ll_hm = reinterpret_cast<uint32_t*>(base + L.ll_hm);
+    P.ll_act = reinterpret_cast<uint32_t*>(base + L.ll_act);
+    P.part = reinterpret_cast<uint64_t*>(base + L.part);
+    P.ctrl = reinterpret_cast<uint32_t*>(base + L.ctrl);
+    const int H = m->hidden, F = m->ffn, qd = m->n_q * 128, kvd = m->n_kv * 128;
+    // rows per tile: RoPE tiles a power of two (pairs d, d + 64 of one head);
+    // otherwise about one tile per block, within the stage's units per thread
+    int r = 2;
+    while (r * 2 <= std::min(pd_cap(H, 1), 128)) r *= 2;
+    P.r_qk = r;
+    P.r_v = std::max(1, pd_cap(H, 1));
+    P.r_o = std::max(1, std::min(pd_cap(qd, 1), (H + blocks - 1) / blocks));
+    P.r_gu = std::min(pd_cap(H, 4) & ~1, 2 * ((F + blocks - 1) / blocks));
+    P.r_d = std::min(pd_cap(F, 4), (H + blocks - 1) / blocks);
+    P.r_lm = pd_cap(H, 4);
+    REQUIRE(P.r_qk >= 2 && P.r_gu >= 2 && P.r_d >= 1 && P.r_lm >= 1, "decode_step: tile plan does not fit");
+    REQUIRE(kvd % P.r_qk == 0 && qd % P.r_qk == 0, "decode_step: RoPE tiles");
+    static const int split_env = [] {
+        const char* s = getenv("VTE_PD_SPLIT");  // tuning: smallest attention split (multiple of 32)
+        return s ? atoi(s) : 0;
+    }();
+    P.split_min = split_env >= 32 ? split_env / 32 * 32 : 128;
+    P.timeout_ticks = 20000000ull;  // 0.2 s
+    const size_t lds = vte::decode_persistent_lds(H, F, qd);
+    const int occ = vte::decode_persistent_occupancy(P, lds);
+    REQUIRE(occ >= 1, "decode_step: the kernel does not fit on a CU (occupancy %d)", occ);
+    e = vte::decode_persistent_launch(P, blocks, lds, (hipStream_t)stream);
+    if (e == hipErrorNotSupported) return fail("decode_step: unsupported shape");
+    return hip_status(e, "vte_decode_step launch");
+}
+
+int vte_decode_status(void* ws, int* flags) {
+    REQUIRE(ws && flags, "decode_status: null pointer");
+    uint32_t c[4];
+    hipError_t e = hipMemcpy(c, ws, sizeof(c), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_status(e, "decode_status copy");
+    *flags = (int)c[2];
+    return 0;
+}

@@ -51,9 +51,28 @@ SIGNATURES = {
     "vte_ffn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp],
     "vte_norm_gemv": [_vp, _vp, _f, _vp, _i, _vp, _i, _vp, _vp, _f, _i, _i, _i, _vp],
     "vte_attn_out_gemv": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _f, _i, _vp],
+    "vte_decode_workspace_bytes": [_vp],
+    "vte_decode_setup": [_vp, _vp, _vp, _ll, _vp],
+    "vte_decode_step": [_vp, _vp, _vp, _vp, _vp, _vp],
+    "vte_decode_status": [_vp, _IP],
     "vte_last_error": [],
 }
-RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll, "vte_topk_scratch_bytes": _ll}
+RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll, "vte_topk_scratch_bytes": _ll,
+            "vte_decode_workspace_bytes": _ll}
+
+
+class DecodeLayer(ctypes.Structure):
+    """vte_decode_layer (include/vte_amd.h)."""
+    _fields_ = [(n, _vp) for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down", "q_bias", "k_bias", "v_bias",
+                                   "attn_norm", "ffn_norm", "k_cache", "v_cache")] + \
+               [(n, _i) for n in ("fmt_q", "fmt_k", "fmt_v", "fmt_o", "fmt_gate_up", "fmt_down")]
+
+
+class DecodeModel(ctypes.Structure):
+    """vte_decode_model (include/vte_amd.h)."""
+    _fields_ = [(n, _i) for n in ("n_layers", "hidden", "ffn", "n_q", "n_kv", "head_dim", "vocab", "max_seq")] + \
+               [("eps", _f)] + [(n, _vp) for n in ("rope_cos", "rope_sin", "output_norm", "lm_head")] + \
+               [("fmt_lm", _i)]
 
 
 def _p(x) -> Optional[int]:
@@ -206,6 +225,27 @@ class VTEKernels:
         self._check(self.lib.vte_attn_out_gemv(_p(part_m), _p(part_l), _p(part_o), _p(kv_offset), batch, n_q,
                                                max_splits, split, _p(w), FMT[fmt], _p(out), _p(residual),
                                                residual_scale, N, self._st(stream)), "vte_attn_out_gemv")
+
+    def decode_workspace_bytes(self, model: DecodeModel) -> int:
+        n = int(self.lib.vte_decode_workspace_bytes(ctypes.byref(model)))
+        if n < 0:
+            self._check(-1, "vte_decode_workspace_bytes")
+        return n
+
+    def decode_setup(self, model: DecodeModel, layers, ws, ws_bytes: int, stream=None) -> None:
+        """Copy the layer table (a ctypes array of DecodeLayer) into the workspace and clear it."""
+        self._check(self.lib.vte_decode_setup(ctypes.byref(model), layers, _p(ws), ws_bytes, self._st(stream)),
+                    "vte_decode_setup")
+
+    def decode_step(self, model: DecodeModel, ws, kv_offset, x, logits, stream=None) -> None:
+        """The persistent batch-1 decode step: embedding x -> fp32 logits, one launch."""
+        self._check(self.lib.vte_decode_step(ctypes.byref(model), _p(ws), _p(kv_offset), _p(x), _p(logits),
+                                             self._st(stream)), "vte_decode_step")
+
+    def decode_status(self, ws) -> int:
+        f = ctypes.c_int(0)
+        self._check(self.lib.vte_decode_status(_p(ws), ctypes.byref(f)), "vte_decode_status")
+        return f.value
 
     def fill_normal_f16(self, dst, n, seed, scale=1.0, stream=None):
         self._check(self.lib.vte_fill_normal_f16(_p(dst), n, seed, scale, self._st(stream)), "vte_fill_normal_f16")
