@@ -216,7 +216,8 @@ def attn_bench(hip, K, ctx, split=None, B=1, fused=False, launches=40):
     ms_ = (ctx + split - 1) // split
     pm = DeviceArray(hip, B * n_q * ms_, np.float32, "pm")
     pl = DeviceArray(hip, B * n_q * ms_, np.float32, "pl")
-    po = DeviceArray(hip, B * n_q * ms_ * D, np.float32, "po")
+    po = DeviceArray(hip, B * n_q * ms_ * (2 * (D + 2) if fused else D), np.float32, "po")
+    po.zero()
     out = DeviceArray(hip, B * n_q * D, np.float16, "out")
     ctr = DeviceArray(hip, B * n_kv, np.int32, "ctr")
     ctr.zero()

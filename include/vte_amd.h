@@ -98,8 +98,10 @@ long long vte_attn_scratch_floats(int batch, int n_q, int max_splits);
  * tokens per partial block (multiple of 32), max_splits >= ceil(max_seq/split)
  * (at most 4096).  part_m/part_l [B][n_q][max_splits], part_o
  * [B][n_q][max_splits][128] fp32 scratch.  counters: NULL = separate combine
- * launch; else B*n_kv zeroed ints and the combine runs in the last partial
- * block of each (sequence, KV head) (max_splits <= 512), leaving them zero.
+ * launch; else B*n_kv ints, zeroed before the first call and then owned by the
+ * kernel (per-group epochs), and the combine runs inside the partial kernel
+ * (max_splits <= 512, split > 32): part_o then holds flagged records and must
+ * hold B*n_q*max_splits*260 floats, zeroed before the first call.
  * out NULL (with counters NULL): only the partials are written, for
  * vte_attn_out_gemv to combine.  kv_batch_stride 0 with B > 1: every column
  * reads the same cache (prompt tokens of one sequence, each at its own

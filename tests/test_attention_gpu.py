@@ -16,21 +16,31 @@ NQ, NKV, D = 12, 2, 128
 SCALE = 1.0 / math.sqrt(D)
 
 
-def _run(hip, K, q, kc, vc, offsets, split, dtype="f32", fused=False):
-    """q [B,NQ,D]; caches [B,max_seq,NKV,D] fp16; offsets [B] (position of last token)."""
+def _run(hip, K, q, kc, vc, offsets, split, dtype="f32", fused=False, repeat=1):
+    """q [B,NQ,D]; caches [B,max_seq,NKV,D] fp16; offsets [B] (position of last token).
+    ``fused``: in-kernel combine (flagged records in part_o, per-group epochs in
+    the counters); ``repeat`` calls in a row on the same buffers must agree."""
     B, max_seq = kc.shape[0], kc.shape[1]
     max_splits = (max_seq + split - 1) // split
     part_m = empty(hip, (B, NQ, max_splits), np.float32)
     part_l = empty(hip, (B, NQ, max_splits), np.float32)
-    part_o = empty(hip, (B, NQ, max_splits, D), np.float32)
+    if fused:  # flagged records: 2 x 130 floats per (sequence, head, split), zeroed once
+        part_o = up(hip, np.zeros((B, NQ, max_splits, 2 * (D + 2)), np.float32))
+    else:
+        part_o = empty(hip, (B, NQ, max_splits, D), np.float32)
     out = empty(hip, (B, NQ, D), np.float32 if dtype == "f32" else np.float16)
-    ctr = empty(hip, B * NKV, np.int32) if fused else None
-    K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), part_m, part_l, part_o, out, B, NQ, NKV, D, SCALE,
-                    up(hip, np.asarray(offsets, np.int32)), max_seq * NKV * D, split, max_splits, dtype=dtype,
-                    counters=ctr, stream=hip.stream)
-    if fused:  # the kernel leaves its counters at zero for the next call
-        assert not down(ctr).any()
-    return down(out)
+    ctr = up(hip, np.zeros(B * NKV, np.int32)) if fused else None
+    outs = []
+    for _ in range(repeat):
+        K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), part_m, part_l, part_o, out, B, NQ, NKV, D, SCALE,
+                        up(hip, np.asarray(offsets, np.int32)), max_seq * NKV * D, split, max_splits, dtype=dtype,
+                        counters=ctr, stream=hip.stream)
+        outs.append(down(out))
+    if fused:  # each call advanced every group's epoch by one
+        assert np.array_equal(down(ctr), np.full(B * NKV, repeat, np.int32))
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    return outs[0]
 
 
 def _inputs(rng, B, max_seq):
@@ -52,13 +62,13 @@ def test_config2_single_sequence(hip, K, ctx, split):
 
 @pytest.mark.parametrize("ctx,split", [(4096, 256), (777, 128), (33, 128)])
 def test_in_kernel_combine_matches_separate(hip, K, ctx, split):
-    """The last-block LSE combine agrees with the separate combine kernel (same
+    """The in-kernel LSE combine (three calls in a row on one set of buffers) agrees with the separate combine kernel (same
     terms, different fp32 summation order) and with the float64 oracle."""
     rng = np.random.default_rng(ctx)
     q, kc, vc = _inputs(rng, 3, ctx)
     offs = [ctx - 1, ctx // 2, 0]
     a = _run(hip, K, q, kc, vc, offs, split)
-    b = _run(hip, K, q, kc, vc, offs, split, fused=True)
+    b = _run(hip, K, q, kc, vc, offs, split, fused=True, repeat=3)
     assert rel_l2(b, a) <= 1e-5
     for i, o in enumerate(offs):
         assert rel_l2(b[i], attention_ref(q[i], kc[i], vc[i], o + 1, SCALE)) <= TOL
@@ -66,14 +76,14 @@ def test_in_kernel_combine_matches_separate(hip, K, ctx, split):
 
 @pytest.mark.parametrize("B,split", [(1, 128), (9, 128), (16, 256)])
 def test_in_kernel_combine_ragged_batches(hip, K, B, split):
-    """The in-kernel (last-block) combine on ragged batches: equal to the
+    """The in-kernel combine on ragged batches: equal to the
     separate combine up to summation order, and to the float64 oracle."""
     rng = np.random.default_rng(77 + B)
     lens = rng.integers(1, 2600, B)
     lens[0] = 2049
     q, kc, vc = _inputs(rng, B, 2600)
     a = _run(hip, K, q, kc, vc, lens - 1, split)
-    b = _run(hip, K, q, kc, vc, lens - 1, split, fused=True)
+    b = _run(hip, K, q, kc, vc, lens - 1, split, fused=True, repeat=2)
     assert rel_l2(b, a) <= 1e-5
     for i in range(min(B, 3)):
         assert rel_l2(b[i], attention_ref(q[i], kc[i], vc[i], int(lens[i]), SCALE)) <= TOL

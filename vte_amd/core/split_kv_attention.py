@@ -7,8 +7,8 @@ sequence) and issues the launches of one layer.  MI355X choices:
 
 * a GQA-aware partial kernel (one block serves every query head of a KV head)
   and the LSE combine, either as a second launch or, with ``fuse_combine``,
-  inside the partial kernel's last block per (sequence, KV head); the KV
-  append is a separate tiny launch as in the reference;
+  inside the partial kernel (each group's last splits poll the others'
+  flagged records); the KV append is a separate tiny launch as in the reference;
 * the split is a token count per block (multiple of 32; 128 = one 32-token
   MFMA step per wave of the block's four), kept at 128 while a sequence has
   at most 256 splits (see ``choose_split``; the reference's 1024/num_cus
@@ -48,12 +48,13 @@ class SplitKVAttentionDispatcher:
         self.split = split or choose_split(max_context, batch_size, n_kv, hip.get_num_cus() if hip else 256)
         self.max_splits = math.ceil(max_context / self.split)
         self.scale = 1.0 / math.sqrt(head_dim)
-        # In-kernel (last-block) combine: saves a launch but chains three
-        # device-coherent memory round trips (partial stores complete, count,
-        # read back), about 1 us each on MI355X, so at a 2K context it costs
-        # more than the separate combine launch (attention 282 vs 210 us per
-        # 28-layer step, also with every split of a group on one XCD); opt-in
-        # (VTE_ATT_FUSE=1 or fuse_combine=True).
+        # In-kernel combine: each split stores flagged records, and the group's
+        # last G split blocks poll them and combine one head each (one memory
+        # round trip instead of a kernel boundary).  Measured on MI355X at a
+        # 2049-token context, batch 1: 8.1 us against 7.6 us for the partial
+        # and combine launches (the coherent handoff costs as much as the
+        # kernel boundary it replaces), so it is opt-in (VTE_ATT_FUSE=1 or
+        # fuse_combine=True).
         if fuse_combine is None:
             fuse_combine = os.environ.get("VTE_ATT_FUSE", "0") == "1"
         self.fuse_combine = fuse_combine
@@ -63,14 +64,25 @@ class SplitKVAttentionDispatcher:
         nstat = batch_size * n_q * self.max_splits
         self.part_m = DeviceArray(hip, nstat, np.float32, "attn_part_m", allocator, MemoryRegion.SCRATCH)
         self.part_l = DeviceArray(hip, nstat, np.float32, "attn_part_l", allocator, MemoryRegion.SCRATCH)
-        self.part_o = DeviceArray(hip, nstat * head_dim, np.float32, "attn_part_o", allocator, MemoryRegion.SCRATCH)
-        # split-completion counters of the in-kernel LSE combine: zeroed once here,
-        # returned to zero by the kernel itself after every combine
+        # partial outputs; with the in-kernel combine they hold flagged 64-bit
+        # records (m, l, o[128] per split and head) instead: 2 * 130 floats each
+        per = max(head_dim, 2 * (head_dim + 2)) if fuse_combine else head_dim
+        self.part_o = DeviceArray(hip, nstat * per, np.float32, "attn_part_o", allocator, MemoryRegion.SCRATCH)
+        # per (sequence, KV head) epochs of the in-kernel combine (record tags)
         self.counters = DeviceArray(hip, batch_size * n_kv, np.int32, "attn_counters", allocator, MemoryRegion.SCRATCH)
         self.counters.zero()
+        if fuse_combine:
+            self.part_o.zero()
 
     def scratch_bytes(self) -> int:
         return self.part_m.nbytes + self.part_l.nbytes + self.part_o.nbytes
+
+    def _fused(self, out, kv_batch_stride: int, batch) -> bool:
+        """In-kernel combine, except for prompt columns of one cache (stride 0),
+        where the two-column blocks with a separate combine read each K/V tile
+        once for two columns."""
+        B = batch or self.batch
+        return self.fuse_combine and out is not None and not (kv_batch_stride == 0 and B > 1)
 
     def launch(self, q, k_cache, v_cache, out, kv_offset, kv_batch_stride: int, dtype: str = "f16",
                batch: int | None = None, stream=None) -> None:
@@ -80,5 +92,5 @@ class SplitKVAttentionDispatcher:
         self.K.attn_split_kv(q, k_cache, v_cache, self.part_m, self.part_l, self.part_o, out, batch or self.batch,
                              self.n_q, self.n_kv, self.head_dim, self.scale, kv_offset, kv_batch_stride, self.split,
                              self.max_splits, dtype=dtype,
-                             counters=self.counters if (self.fuse_combine and out is not None) else None,
+                             counters=self.counters if self._fused(out, kv_batch_stride, batch) else None,
                              stream=stream if stream is not None else self.hip.stream)

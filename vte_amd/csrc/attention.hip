@@ -83,6 +83,8 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     const __half* kb = k_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
     const __half* vb = v_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
     const int len_raw = QC == 1 ? kv_offset[b] : max(kv_offset[b], kv_offset[min(b + 1, n_cols - 1)]);
+    // in-kernel combine: this launch's record tag (the group's epoch + 1)
+    const uint32_t tag = counters != nullptr ? (uint32_t)counters[(size_t)b * n_kv + kvh] + 1u : 0u;
     AttTile T, T1;
     int t0 = PW ? t_begin : t_begin + wv * ATT_TILE;
     if (SPEC) {
@@ -193,9 +195,13 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         }
         const int qh = kvh * G + h % G;
         const size_t st = ((size_t)bc * n_q + qh) * max_splits + sp;
-        if (counters != nullptr) {  // read back by another block: write-through stores
-            st_coh(part_o + st * ATT_D + d, O);
-            if (d == 0) { st_coh(part_m + st, M); st_coh(part_l + st, L); }
+        if (counters != nullptr) {  // flagged record, read back by the combining blocks
+            uint64_t* rec = reinterpret_cast<uint64_t*>(part_o) + st * ATT_REC;
+            st_flag32(rec + 2 + d, O, tag);
+            if (d == 0) {
+                st_flag32(rec, M, tag);
+                st_flag32(rec + 1, L, tag);
+            }
         } else {
             part_o[st * ATT_D + d] = O;
             if (d == 0) { part_m[st] = M; part_l[st] = L; }
@@ -203,85 +209,64 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     }
     if (QC > 1 || counters == nullptr) return;  // separate combine launch
 
-    // ---- last block of this (sequence, KV head) performs the LSE combine ----
-    // The partials were written with device-coherent (write-through) stores;
-    // once every wave's stores have completed, thread 0 counts this split, and
-    // the block that completes the count reads every split back with
-    // device-coherent loads and combines.  Only coherent accesses cross blocks,
-    // so no L2 writeback or invalidate is needed (a device-scope release /
-    // acquire fence writes back and invalidates the XCD's whole L2, which per
-    // block costs more than a separate combine launch on this 8-XCD part).
-    // The counter is reset by that block, so a captured graph can be replayed.
-    __shared__ int s_last;
-    wait_stores();
-    __syncthreads();
+    // ---- the last G splits of this (sequence, KV head) combine one head each ----
+    // Every split stored its records as flagged words (value | tag << 32,
+    // device-coherent stores); a combining block polls the records of its head
+    // until each carries this launch's tag: one memory round trip after the
+    // last split, no completion counter, no fence.  The tag is the group's
+    // epoch (counters[b][kvh], read by every block at its start) plus one; the
+    // block combining head 0 advances the epoch once it has seen every split's
+    // records (so every block of the group has read it), which makes the next
+    // replay of a captured graph use a new tag.  Combining blocks are the
+    // group's highest split indices, dispatched after the splits they wait for.
     const int ns = (len + split - 1) / split;
-    if (threadIdx.x == 0) {
-        int* ctr = counters + (size_t)b * n_kv + kvh;
-        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == ns - 1);
-        if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    // per-split weights w[h][c] = exp(m_c - M_h) and L_h in LDS (parallel loads),
-    // then each thread combines its (head, dim) outputs with unrolled loads.
-    auto& wsh = lds.w;  // o_sh is dead once the partials are in global memory
-    __shared__ float Msh[ATT_MAXG], Lsh[ATT_MAXG];
-    for (int i = threadIdx.x; i < G * ns; i += 256) {
-        const int h = i / ns, c = i - h * ns;
-        wsh[h][c] = ld_coh(part_m + ((size_t)b * n_q + kvh * G + h) * max_splits + c);
-    }
-    __syncthreads();
-    if (wv < G) {  // wave h: max and denominator of head h
-        const int h = wv;
-        const size_t base = ((size_t)b * n_q + kvh * G + h) * max_splits;
-        float M = -1e30f;
-        for (int c = lane; c < ns; c += 64) M = fmaxf(M, wsh[h][c]);
-        M = wave_max(M);
-        float L = 0.f;
-        for (int c = lane; c < ns; c += 64) {
-            const float wgt = __expf(wsh[h][c] - M);
-            wsh[h][c] = wgt;
-            L = fmaf(ld_coh(part_l + base + c), wgt, L);
-        }
-        L = wave_sum(L);
-        if (lane == 0) { Msh[h] = M; Lsh[h] = L; }
-    }
-    __syncthreads();
-    if (G > 4) {  // heads 4..G-1 (four waves per block)
-        for (int h = 4 + wv; h < G; h += 4) {
-            const size_t base = ((size_t)b * n_q + kvh * G + h) * max_splits;
-            float M = -1e30f;
-            for (int c = lane; c < ns; c += 64) M = fmaxf(M, wsh[h][c]);
-            M = wave_max(M);
-            float L = 0.f;
-            for (int c = lane; c < ns; c += 64) {
-                const float wgt = __expf(wsh[h][c] - M);
-                wsh[h][c] = wgt;
-                L = fmaf(ld_coh(part_l + base + c), wgt, L);
-            }
-            L = wave_sum(L);
-            if (lane == 0) { Msh[h] = M; Lsh[h] = L; }
+    const int r = ns - 1 - sp;
+    if (r >= G) return;
+    auto& wsh = lds.w;  // o_sh is dead once the records are stored
+    __shared__ float Msh, Lsh;
+    __shared__ float oh[ATT_D];
+    for (int h = r; h < G; h += ns) {
+        const int qh = kvh * G + h;
+        const uint64_t* recs = reinterpret_cast<const uint64_t*>(part_o) + ((size_t)b * n_q + qh) * max_splits * ATT_REC;
+        __syncthreads();  // LDS of the previous head
+        for (int c = threadIdx.x; c < ns; c += 256) {
+            float ml[2];
+            wait_flag32_n<2>(recs + (size_t)c * ATT_REC, 1, tag, ml);
+            wsh[0][c] = ml[0];
+            wsh[1][c] = ml[1];
         }
         __syncthreads();
-    }
-    for (int idx = threadIdx.x; idx < G * ATT_D; idx += 256) {
-        const int h = idx / ATT_D, d = idx % ATT_D;
-        const int qh = kvh * G + h;
-        const float* po = part_o + ((size_t)b * n_q + qh) * max_splits * ATT_D + d;
-        float O = 0.f;
-        int c = 0;
-        for (; c + 8 <= ns; c += 8) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = ld_coh(po + (size_t)(c + j) * ATT_D);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) O = fmaf(v[j], wsh[h][c + j], O);
+        if (wv == 0) {  // maximum, split weights exp(m_c - M) and the denominator
+            float M = -1e30f;
+            for (int c = lane; c < ns; c += 64) M = fmaxf(M, wsh[0][c]);
+            M = wave_max(M);
+            float Ls = 0.f;
+            for (int c = lane; c < ns; c += 64) {
+                const float wgt = __expf(wsh[0][c] - M);
+                wsh[0][c] = wgt;
+                Ls = fmaf(wsh[1][c], wgt, Ls);
+            }
+            Ls = wave_sum(Ls);
+            if (lane == 0) { Msh = M; Lsh = Ls; }
         }
-        for (; c < ns; ++c) O = fmaf(ld_coh(po + (size_t)c * ATT_D), wsh[h][c], O);
-        st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, O / fmaxf(Lsh[h], 1e-20f));
+        __syncthreads();
+        // threads (d, half): half 0 takes the even splits, half 1 the odd ones
+        const int d = threadIdx.x & (ATT_D - 1), hf = threadIdx.x >> 7;
+        const uint64_t* po = recs + 2 + d;
+        float O = 0.f;
+        for (int c = hf; c < ns; c += 16) {  // 8 splits per round, all requested together
+            const int nj = min(8, (ns - c + 1) / 2);  // splits c, c + 2, ... below ns (slots past nj re-read the last)
+            float v[8];
+            wait_flag32_n<8>(po + (size_t)c * ATT_REC, 2 * ATT_REC, tag, v, nj);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) O = j < nj ? fmaf(v[j], wsh[0][c + 2 * j], O) : O;
+        }
+        if (hf) oh[d] = O;
+        __syncthreads();
+        if (!hf) st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, (O + oh[d]) / fmaxf(Lsh, 1e-20f));
     }
+    if (r == 0 && threadIdx.x == 0)
+        __hip_atomic_store(counters + (size_t)b * n_kv + kvh, (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // LSE combine for many splits (> 128): grid (n_q, B, 4 dim quarters), block

@@ -14,6 +14,7 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 #define ATT_MAXG 8   // query heads per KV head served by one block
 #define ATT_MAX_COMBINE 512  // splits per sequence the in-kernel combine handles
 #define ATT_MAX_SPLITS 4096  // splits per sequence the separate combine handles
+#define ATT_REC (ATT_D + 2)  // 64-bit words of a flagged split record: m, l, o[128]
 #define ATT_VT_STRIDE 36     // halves per row of the transposed V tile (32 tokens + pad)
 
 // Device-coherent float store / load (relaxed device-scope atomics: on this
@@ -24,6 +25,46 @@ __device__ __forceinline__ void st_coh(float* p, float v) {
 }
 __device__ __forceinline__ float ld_coh(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Flagged fp32 word (value | tag << 32): one 64-bit device-coherent store or
+// load, so a reader that sees the tag sees the value written with it.
+__device__ __forceinline__ void st_flag32(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+// The value of a flagged word once it carries `tag` (polls; gives up after
+// `limit` polls and returns what it holds, so a kernel never hangs).
+__device__ __forceinline__ float wait_flag32(const uint64_t* p, uint32_t tag, int limit = 1 << 18) {
+    uint64_t w = __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; (uint32_t)(w >> 32) != tag && i < limit; ++i)
+        w = __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __uint_as_float((uint32_t)w);
+}
+// N flagged words p[0], p[stride], ... (slots from `n` on re-read word n - 1)
+// requested together and re-polled until each carries `tag` (one round trip
+// when they are already there).
+template <int N>
+__device__ __forceinline__ void wait_flag32_n(const uint64_t* p, size_t stride, uint32_t tag, float (&v)[N],
+                                              int n = N, int limit = 1 << 18) {
+    uint64_t w[N];
+    const uint64_t* q[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        q[j] = p + (size_t)min(j, n - 1) * stride;
+        w[j] = __hip_atomic_load(const_cast<uint64_t*>(q[j]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    for (int i = 0; i < limit; ++i) {
+        bool all = true;
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const bool ok = (uint32_t)(w[j] >> 32) == tag;
+            all = all && ok;
+            if (!ok) w[j] = __hip_atomic_load(const_cast<uint64_t*>(q[j]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (all) break;
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = __uint_as_float((uint32_t)w[j]);
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // One wave's 32-token tile: K rows (MFMA A operands, two 16-token halves) and
