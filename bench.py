@@ -138,6 +138,15 @@ def fused_mv_roofline(hip, ex, reps=20):
             "avg_launch_us": round(ms * 1e3, 3), "algo_bytes_per_launch": int(per_launch_bytes)}
 
 
+def time_greedy(hip, ex, steps, start_pos):
+    """Greedy decoding with the token fed back on the device (generate_greedy):
+    wall time per step of one call of ``steps`` steps, tokens read at the end."""
+    ex.generate_greedy([1] * ex.B, [start_pos] * ex.B, steps)  # captures its graph
+    t0 = time.perf_counter()
+    ex.generate_greedy([1] * ex.B, [start_pos] * ex.B, steps)
+    return (time.perf_counter() - t0) / steps
+
+
 def time_e2e(hip, ex, steps, start_pos):
     """Per-token loop as a caller runs it: stage token/offset, replay, read top-k, sample."""
     from vte_amd.core.sampler import Sampler
@@ -517,6 +526,7 @@ def main():
         ex._update_staging_buffers([1] * B, [prefix] * B)
         ms, wall = time_graph(hip, ex, args.steps, args.warmup)
         e2e = time_e2e(hip, ex, 20, prefix)
+        greedy = time_greedy(hip, ex, 64, prefix)
         if B == 1:
             ex._update_staging_buffers([1] * B, [prefix] * B)
             roof = fused_mv_roofline(hip, ex)
@@ -524,7 +534,16 @@ def main():
         kv_read = QWEN25_1P5B.n_layers * (prefix + 1) * QWEN25_1P5B.n_kv * QWEN25_1P5B.head_dim * 2 * 2 * B
         step_bytes = wbytes + kv_read
         result[B] = {"ms_per_step": ms, "tok_s": B / (ms * 1e-3), "wall_s": wall, "e2e_ms_per_step": e2e * 1e3,
+                     "greedy_ms_per_step": greedy * 1e3,
                      "step_bytes": step_bytes, "step_GBps": step_bytes / (ms * 1e-3) / 1e9}
+        ex.close()
+    persistent = None
+    if not args.quick:  # the opt-in single-launch form of the batch-1 step, for comparison
+        ex = HIPGraphExecutor(hip, model, batch_size=1, max_seq=prefix + 256, persistent=True)
+        ex.fill_kv_prefix(seed=1)
+        ex._update_staging_buffers([1], [prefix])
+        ms_p, _ = time_graph(hip, ex, max(20, args.steps // 4), args.warmup)
+        persistent = {"ms_per_step": round(ms_p, 4), "tok_s": round(1e3 / ms_p, 2), "status": ex.decode_status()}
         ex.close()
 
     gemv = [] if args.quick else gemv_configs(hip, K)
@@ -550,13 +569,17 @@ def main():
         "step_GBps_b1": round(r1["step_GBps"], 1),
         "step_frac_hbm_b1": round(r1["step_GBps"] / HBM_PEAK_GBPS, 4),
         "e2e_tok_s_b1": round(1e3 / r1["e2e_ms_per_step"], 2),
+        "greedy_tok_s_b1": round(1e3 / r1["greedy_ms_per_step"], 2),
         "weight_gen_s": round(t_gen, 1),
     }
     if 16 in result:
         r16 = result[16]
         line.update({"tok_s_b16": round(r16["tok_s"], 2), "ms_per_step_b16": round(r16["ms_per_step"], 4),
                      "step_GBps_b16": round(r16["step_GBps"], 1),
-                     "e2e_tok_s_b16": round(16e3 / r16["e2e_ms_per_step"], 2)})
+                     "e2e_tok_s_b16": round(16e3 / r16["e2e_ms_per_step"], 2),
+                     "greedy_tok_s_b16": round(16e3 / r16["greedy_ms_per_step"], 2)})
+    if persistent:
+        line["persistent_b1"] = persistent
     if gemv:
         line["gemv"] = gemv
     if attn:

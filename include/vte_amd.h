@@ -184,6 +184,19 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
  * memory (code under HIP graph capture, tight serving loops). */
 int vte_topk_noalloc(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* stream);
 
+/* Greedy decoding on the device (temperature 0, no repetition penalty): for
+ * each row b, tok = top_idx[b*k] (the top-1 candidate of vte_topk: the
+ * largest logit, lowest id among equal ones), tokens[b] = tok, kv_offset[b] =
+ * min(kv_offset[b] + 1, max_pos), history[*step][b] = tok while *step <
+ * history_steps; then *step += 1.  Appended to a captured decode step, the
+ * next replay decodes the next token with no host round trip.
+ * Replaces: the greedy pick of topk_reduce_greedy_kernel
+ *           (topk_reduce_greedy.hip.template:52-83) and the host loop that feeds
+ *           the picked token back (vte/core/model.py:1039-1044 with
+ *           Sampler.pick_greedy_from_gpu_candidates, vte/core/sampler.py:163-233). */
+int vte_greedy_advance(const int* top_idx, int k, int rows, int* tokens, int* kv_offset, int max_pos, int* history,
+                       int history_steps, int* step, void* stream);
+
 /* vte_topk over the tokens NOT in each row's exclusion list, plus the exact
  * logits of the excluded tokens.  excl_ids [rows][max_excl]: sorted token ids
  * (the repetition window of the sampler, max_excl <= 4096; the reference uses

@@ -419,3 +419,33 @@ def test_repetition_window_candidates_reproduce_full_row_sampling(hip, tiny_mode
             assert Sampler.pick_greedy_from_gpu_candidates(vals[b], idx[b], gath[b], ids, counts, 1.1) == want
     finally:
         ex.close()
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_generate_greedy_matches_host_loop(hip, tiny_model, B):
+    """Greedy decoding with the token fed back on the device (vte_greedy_advance
+    captured after the step, replays back to back) yields the token sequence
+    of the host loop: step, read the top-1 candidate, stage it, step again."""
+    cfg = tiny_model.cfg
+    n = 12
+    ex = HIPGraphExecutor(hip, tiny_model, batch_size=B, max_seq=256, top_k=40)
+    try:
+        toks0 = [5 + 7 * b for b in range(B)]
+        pos0 = [60 + 17 * b for b in range(B)]
+        ex.fill_kv_prefix(seed=12)
+        host = []
+        toks, pos = list(toks0), list(pos0)
+        for _ in range(n):
+            ex.execute_decode_batch(toks, pos)
+            logits = ex.read_logits()
+            idx = ex.read_topk()[1][:, 0]
+            assert np.array_equal(idx, np.argmax(logits, axis=1))
+            host.append(idx.copy())
+            toks, pos = [int(t) for t in idx], [p + 1 for p in pos]
+        ex.fill_kv_prefix(seed=12)
+        dev = ex.generate_greedy(toks0, pos0, n)
+        assert np.array_equal(dev, np.stack(host)), (dev, np.stack(host))
+        ex.fill_kv_prefix(seed=12)  # a second run reuses the captured graph
+        assert np.array_equal(ex.generate_greedy(toks0, pos0, n // 2), np.stack(host)[:n // 2])
+    finally:
+        ex.close()

@@ -496,6 +496,54 @@ class HIPGraphExecutor:
         if sync:
             self.hip.synchronize()
 
+    def generate_greedy(self, tokens: Sequence[int], kv_offsets: Sequence[int], n_steps: int) -> np.ndarray:
+        """Greedy decoding of ``n_steps`` tokens per sequence with no host
+        round trip: a second captured graph (the step + ``vte_greedy_advance``)
+        turns each row's top-1 candidate into its next token and advances its
+        position on the device, and is replayed back to back; the generated
+        tokens are read once at the end, [n_steps, B].  Temperature 0 without
+        a repetition penalty: the tokens ``execute_decode_batch`` followed by
+        argmax of the logits would give (vte/core/model.py:1039-1044)."""
+        if self.top_k < 1:
+            raise HIPSafetyError("greedy decoding needs the on-device top-k (top_k >= 1)")
+        offs = np.asarray(kv_offsets, np.int64)
+        if n_steps < 1 or offs.max() + n_steps > self.max_seq:
+            raise HIPSafetyError(f"{n_steps} steps from position {int(offs.max())} exceed max_seq {self.max_seq}")
+        if self._exclude() is not None:
+            self.excl_cnt.zero()  # no repetition window: plain argmax
+        if getattr(self, "_greedy", None) is None or self._greedy[2] < n_steps:
+            self._free_greedy()
+            cap = max(n_steps, 256)
+            hist = DeviceArray(self.hip, (cap, self.B), np.int32, "greedy_history")
+            step = DeviceArray(self.hip, 1, np.int32, "greedy_step")
+            self.hip.stream_synchronize()
+            self.hip.stream_begin_capture()
+            try:
+                self.enqueue_step()
+                self.K.greedy_advance(self.topk_idx, self.top_k, self.B, self.staging_input, self.staging_kv_offset,
+                                      self.max_seq - 1, hist, cap, step, stream=self.hip.stream)
+            finally:
+                g = self.hip.stream_end_capture()
+            self._greedy = (g, self.hip.graph_instantiate(g), cap, hist, step)
+        g, gexec, cap, hist, step = self._greedy
+        self._update_staging_buffers(tokens, kv_offsets)
+        step.zero()
+        for _ in range(n_steps):
+            self.hip.graph_launch(gexec)
+        self.hip.synchronize()
+        out = np.empty((cap, self.B), np.int32)
+        self.hip.safe_memcpy_device_to_host(out, ctypes.c_void_p(hist.ptr), "sampler_greedy_tokens")
+        return out[:n_steps].copy()
+
+    def _free_greedy(self) -> None:
+        gr = getattr(self, "_greedy", None)
+        if gr is not None:
+            self.hip.graph_exec_destroy(gr[1])
+            self.hip.graph_destroy(gr[0])
+            gr[3].free()
+            gr[4].free()
+        self._greedy = None
+
     def execute_decode(self, token_id: int, kv_offset: int, use_graph: bool = True) -> None:
         if self.B != 1:
             raise HIPSafetyError("execute_decode is the batch-1 entry point; use execute_decode_batch")
@@ -552,6 +600,7 @@ class HIPGraphExecutor:
             dep.close()
         self._dependents = []
         self.closed = True
+        self._free_greedy()
         if self.graph_exec is not None:
             self.hip.graph_exec_destroy(self.graph_exec)
             self.hip.graph_destroy(self.graph)

@@ -47,6 +47,8 @@ hipError_t add(const void* r, const void* in, void* out, int n, float scale, hip
 hipError_t embedding(int fmt, const int* tokens, const void* table, void* out, int n_tokens, int hidden,
                      float scale, hipStream_t st);
 size_t topk_scratch_bytes(int rows);
+hipError_t greedy_advance(const int* top_idx, int k, int rows, int* tokens, int* kv_offset, int max_pos,
+                          int* history, int hist_steps, int* step, hipStream_t st);
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* scratch,
                 hipStream_t st, const int* excl_ids, const int* excl_cnt, int max_excl, float* gathered);
 int topk_noalloc_max_rows();
@@ -293,6 +295,16 @@ int vte_topk(const float* logits, int rows, int vocab, int k, float* out_val, in
     return hip_status(vte::topk(logits, rows, vocab, k, out_val, out_idx, scratch, (hipStream_t)stream, nullptr,
                                 nullptr, 0, nullptr),
                       "vte_topk launch");
+}
+
+int vte_greedy_advance(const int* top_idx, int k, int rows, int* tokens, int* kv_offset, int max_pos, int* history,
+                       int history_steps, int* step, void* stream) {
+    REQUIRE(top_idx && tokens && kv_offset && step, "greedy_advance: null pointer");
+    REQUIRE(k >= 1 && rows >= 1 && rows <= 65535 && max_pos >= 0, "greedy_advance: bad shape");
+    REQUIRE(history != nullptr || history_steps == 0, "greedy_advance: history steps without a history buffer");
+    return hip_status(vte::greedy_advance(top_idx, k, rows, tokens, kv_offset, max_pos, history, history_steps, step,
+                                          (hipStream_t)stream),
+                      "vte_greedy_advance launch");
 }
 
 int vte_topk_noalloc(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* stream) {

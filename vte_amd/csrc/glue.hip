@@ -795,6 +795,36 @@ hipError_t embedding(int fmt, const int* tokens, const void* table, void* out, i
     return hipGetLastError();
 }
 
+// Greedy decoding without a host round trip: the next token of row b is its
+// top-1 candidate (out_idx[b][0]: the largest logit, the lowest id among
+// equal ones, as np.argmax picks it); it becomes row b's token of the next
+// step (tokens[b]), its position advances by one (kv_offset[b], held at
+// max_pos), and it is recorded in history[step][b] (while step < hist_steps).
+// One block; every thread reads the step counter before thread 0 advances it.
+__global__ void greedy_advance_kernel(const int* __restrict__ top_idx, int k, int rows, int* __restrict__ tokens,
+                                      int* __restrict__ kv_offset, int max_pos, int* __restrict__ history,
+                                      int hist_steps, int* __restrict__ step) {
+    __shared__ int s_step;
+    if (threadIdx.x == 0) s_step = *step;
+    __syncthreads();
+    const int s = s_step;
+    for (int b = threadIdx.x; b < rows; b += blockDim.x) {
+        const int tok = top_idx[(size_t)b * k];
+        tokens[b] = tok;
+        kv_offset[b] = min(kv_offset[b] + 1, max_pos);
+        if (s < hist_steps) history[(size_t)s * rows + b] = tok;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) *step = s + 1;
+}
+
+hipError_t greedy_advance(const int* top_idx, int k, int rows, int* tokens, int* kv_offset, int max_pos,
+                          int* history, int hist_steps, int* step, hipStream_t st) {
+    hipLaunchKernelGGL(greedy_advance_kernel, dim3(1), dim3(256), 0, st, top_idx, k, rows, tokens, kv_offset, max_pos,
+                       history, hist_steps, step);
+    return hipGetLastError();
+}
+
 size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_P * (TOPK_CAP * 8 + 4); }
 
 hipError_t topk(const float* logits, int rows, int vocab, int k, float* out_val, int* out_idx, void* work,

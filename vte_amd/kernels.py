@@ -51,6 +51,7 @@ SIGNATURES = {
     "vte_ffn_in": [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp],
     "vte_norm_gemv": [_vp, _vp, _f, _vp, _i, _vp, _i, _vp, _vp, _f, _i, _i, _i, _vp],
     "vte_attn_out_gemv": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _f, _i, _vp],
+    "vte_greedy_advance": [_vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _vp],
     "vte_decode_workspace_bytes": [_vp],
     "vte_decode_setup": [_vp, _vp, _vp, _ll, _vp],
     "vte_decode_step": [_vp, _vp, _vp, _vp, _vp, _vp],
@@ -225,6 +226,12 @@ class VTEKernels:
         self._check(self.lib.vte_attn_out_gemv(_p(part_m), _p(part_l), _p(part_o), _p(kv_offset), batch, n_q,
                                                max_splits, split, _p(w), FMT[fmt], _p(out), _p(residual),
                                                residual_scale, N, self._st(stream)), "vte_attn_out_gemv")
+
+    def greedy_advance(self, top_idx, k, rows, tokens, kv_offset, max_pos, history, history_steps, step,
+                       stream=None) -> None:
+        """Top-1 candidates become the next step's tokens (positions + 1), recorded in history."""
+        self._check(self.lib.vte_greedy_advance(_p(top_idx), k, rows, _p(tokens), _p(kv_offset), max_pos, _p(history),
+                                                history_steps, _p(step), self._st(stream)), "vte_greedy_advance")
 
     def decode_workspace_bytes(self, model: DecodeModel) -> int:
         n = int(self.lib.vte_decode_workspace_bytes(ctypes.byref(model)))
