@@ -64,7 +64,7 @@ class HIPGraphExecutor:
         column's logits (the prefill of ``PrefillRunner``).  ``persistent``
         (batch 1; opt-in, or VTE_PERSISTENT=1): the layers and the LM head run
         as one persistent launch instead of six launches per layer (measured
-        slower than the graph of per-node launches on MI355X: 1.18 vs 0.89 ms)."""
+        slower than the graph of per-node launches on MI355X: 1.04 vs 0.89 ms)."""
         if persistent is None:
             persistent = os.environ.get("VTE_PERSISTENT", "0") == "1"
         self.hip = hip
