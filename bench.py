@@ -384,7 +384,7 @@ def hbm_copy_bandwidth(hip, nbytes=1 << 30, reps=10):
     return round(2 * nbytes / (float(np.median(ts)) * 1e-3) / 1e9, 1)
 
 
-def profile_step(B, steps, prefix=2048, classes=None):
+def profile_step(B, steps, prefix=2048, classes=None, persistent=False):
     """Kernel-trace / counter workload: one plain device-to-device copy of
     256 MiB (reads and writes exactly 256 MiB: the scale of FETCH_SIZE and
     WRITE_SIZE), then ``steps`` replays of the batch-B decode-step graph, or
@@ -405,7 +405,8 @@ def profile_step(B, steps, prefix=2048, classes=None):
     hip.synchronize()
     a.free()
     b.free()
-    ex = HIPGraphExecutor(hip, SyntheticQwen2(QWEN25_1P5B, seed=0), batch_size=B, max_seq=prefix + 256)
+    ex = HIPGraphExecutor(hip, SyntheticQwen2(QWEN25_1P5B, seed=0), batch_size=B, max_seq=prefix + 256,
+                          persistent=persistent)
     ex.fill_kv_prefix(seed=B)
     ex._update_staging_buffers([1] * B, [prefix] * B)
     if classes:
@@ -483,6 +484,8 @@ def main():
                     help="profiling run only: a 256 MiB calibration copy, then the quant-GEMV configs 0/1 "
                          "(Q4_K 8960x1536, Q6_K 1536x8960 and 151936x1536, Q8_0 2048x2048) and the batch-16 "
                          "MFMA GEMM over cold rotating pools, and the split-KV attention configs 2/3b")
+    ap.add_argument("--profile-persistent", action="store_true",
+                    help="with --profile-step 1: the opt-in persistent (single-launch) form of the step")
     ap.add_argument("--profile-classes", default="", metavar="C1,C2",
                     help="with --profile-step: replay only these launch classes (e.g. attn_in,ffn_in,lm_head)")
     args = ap.parse_args()
@@ -495,7 +498,8 @@ def main():
         return
     if args.profile_step:
         profile_step(args.profile_step, args.steps,
-                     classes=[c for c in args.profile_classes.split(",") if c] or None)
+                     classes=[c for c in args.profile_classes.split(",") if c] or None,
+                     persistent=args.profile_persistent)
         return
 
     from vte_amd.bridge import HIPRuntime
