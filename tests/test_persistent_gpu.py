@@ -69,8 +69,6 @@ def test_tiny_persistent_matches_oracle(hip, tiny, pos):
 def test_tiny_persistent_consecutive_steps(hip, tiny):
     """Twelve steps in a row through one captured graph (each launch a new
     epoch of the flagged buffers), fed back greedily, against the graph path."""
-    toks = [7]
-    a_out, a_k, a_v = None, None, None
     positions = list(range(40, 52))
     ex = HIPGraphExecutor(hip, tiny, batch_size=1, max_seq=256, persistent=True)
     ref = HIPGraphExecutor(hip, tiny, batch_size=1, max_seq=256, persistent=False)
@@ -134,3 +132,41 @@ def test_full_shape_persistent_vs_graph_path(hip, full_model, pos):
     kth = np.sort(lg)[-40]
     for t in top_p ^ top_g:  # only near-ties at the boundary may differ
         assert abs(lg[t] - kth) <= 1e-2 * np.abs(lg).max()
+
+
+@pytest.mark.parametrize("embd,lm", [("q4_k", "q6_k"), ("q6_k", "q4_k"), ("q4_k", None)])
+def test_persistent_lm_head_formats(hip, embd, lm):
+    """A separate Q6_K output matrix after a Q4_K table (the Qwen2.5-7B layout),
+    a Q4_K output matrix, and a tied Q4_K table as the LM head, against the
+    oracle and the graph path."""
+    model = SyntheticQwen2(TINY, seed=8, embd_fmt=embd, lm_head_fmt=lm)
+    cfg = model.cfg
+    rng = np.random.default_rng(4)
+    ks = [(0.5 * rng.standard_normal((1, 256, cfg.n_kv, cfg.head_dim))).astype(np.float16) for _ in range(cfg.n_layers)]
+    vs = [(0.5 * rng.standard_normal((1, 256, cfg.n_kv, cfg.head_dim))).astype(np.float16) for _ in range(cfg.n_layers)]
+    got = {}
+    for persistent in (True, False):
+        ex = HIPGraphExecutor(hip, model, batch_size=1, max_seq=256, persistent=persistent)
+        try:
+            assert ex.persistent == persistent
+            for L in range(cfg.n_layers):
+                ex.upload_kv(L, ks[L], vs[L])
+            ex.execute_decode_batch([77], [150])
+            got[persistent] = ex.read_logits()[0]
+            assert ex.decode_status() == 0
+        finally:
+            ex.close()
+    ref = ost.decode_step(model, np.array([77]), np.array([150]), [k.copy() for k in ks], [v.copy() for v in vs], {})
+    assert rel_l2(got[True], ref[0]) <= TOL
+    assert rel_l2(got[True], got[False]) <= TOL
+
+
+def test_persistent_falls_back_for_unsupported_formats(hip):
+    """A tied Q8_0 table as the LM head is outside the persistent kernel's
+    formats: the executor keeps the per-node graph (and says so)."""
+    model = SyntheticQwen2(TINY, seed=8, embd_fmt="q8_0", lm_head_fmt=None)
+    ex = HIPGraphExecutor(hip, model, batch_size=1, max_seq=256, persistent=True)
+    try:
+        assert not ex.persistent
+    finally:
+        ex.close()
