@@ -170,3 +170,27 @@ def test_persistent_falls_back_for_unsupported_formats(hip):
         assert not ex.persistent
     finally:
         ex.close()
+
+
+def test_tiny_persistent_long_context(hip):
+    """A 20,000-row cache: the persistent kernel widens its splits (at most 128
+    per KV head; here 160 rows each) and still matches the oracle."""
+    max_seq, pos = 20480, 20000
+    tiny = SyntheticQwen2(TINY.with_(max_seq=max_seq), seed=3)
+    cfg = tiny.cfg
+    rng = np.random.default_rng(20)
+    ks = [(0.5 * rng.standard_normal((1, max_seq, cfg.n_kv, cfg.head_dim))).astype(np.float16)
+          for _ in range(cfg.n_layers)]
+    vs = [(0.5 * rng.standard_normal((1, max_seq, cfg.n_kv, cfg.head_dim))).astype(np.float16)
+          for _ in range(cfg.n_layers)]
+    ex = HIPGraphExecutor(hip, tiny, batch_size=1, max_seq=max_seq, persistent=True)
+    try:
+        for L in range(cfg.n_layers):
+            ex.upload_kv(L, ks[L], vs[L])
+        ex.execute_decode_batch([123], [pos])
+        got = ex.read_logits()[0]
+        assert ex.decode_status() == 0
+    finally:
+        ex.close()
+    ref = ost.decode_step(tiny, np.array([123]), np.array([pos]), ks, vs, {})
+    assert rel_l2(got, ref[0]) <= TOL
