@@ -264,13 +264,14 @@ int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float s
 /* ---- Persistent decode step (batch 1) ----
  * The whole Qwen2-shaped decode step of one sequence (every layer's
  * RMSNorm, q/k/v + bias + RoPE + K/V append, split-KV attention, o-proj +
- * residual, RMSNorm, gate/up + SwiGLU, down + residual; then the output norm
- * and the LM head) as ONE kernel launch of one block per CU, so it can be
- * captured as a single graph node.  Blocks hand activations to each other
- * through flagged words in the workspace instead of kernel boundaries.
+ * residual, RMSNorm, gate/up + SwiGLU, down + residual) as ONE kernel launch
+ * of one block per CU, then the output norm and the LM head as a second
+ * launch (the fused norm + mat-vec of vte_norm_gemv).  Blocks hand
+ * activations to each other through flagged words in the workspace instead
+ * of kernel boundaries.
  * Limits: head_dim 128, n_q / n_kv <= 8, hidden, ffn and n_q * 128 multiples
- * of 256 and <= 10240; q/k/o/gate/up Q4_K, v and down Q4_K or Q6_K, LM head
- * Q4_K or Q6_K; the KV cache of one sequence [max_seq][n_kv][128] fp16 per
+ * of 256 and <= 10240 (hidden <= 8192); q/k/o/gate/up Q4_K, v and down Q4_K
+ * or Q6_K, LM head Q4_K, Q6_K or Q8_0; the KV cache of one sequence [max_seq][n_kv][128] fp16 per
  * layer.  Replaces: the batch-1 capture of vte/core/hip_graph_executor.py:504-738
  * (nodes of vte/compiler/qwen_compute.py:100-282) up to the LM-head logits. */
 typedef struct vte_decode_layer {
@@ -291,7 +292,8 @@ typedef struct vte_decode_model {
 } vte_decode_model;
 
 /* Device workspace bytes the step needs (flagged activation buffers,
- * attention partials, the layer table and a control word block). */
+ * attention partials, down-projection partial sums, the last layer's output,
+ * the layer table and a control word block). */
 long long vte_decode_workspace_bytes(const vte_decode_model* m);
 
 /* Validate the model, copy the layer table into the workspace and clear its

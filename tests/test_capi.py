@@ -83,8 +83,10 @@ def test_decode_workspace_and_rejections_on_host():
     m.eps = 1e-6
     n = K.decode_workspace_bytes(m)
     # control + layer table + flagged buffers + attention records (12 heads x 128 splits x 130 x 8 B)
-    assert 12 * 128 * 130 * 8 < n < 12 * 128 * 130 * 8 + (1 << 20)
-    for field, bad in (("head_dim", 64), ("n_kv", 5), ("hidden", 1000), ("ffn", 12288)):
+    # + down partials (35 slices x 1536 rows x 8 B)
+    rec, dn = 12 * 128 * 130 * 8, 35 * 1536 * 8
+    assert rec + dn < n < rec + dn + (1 << 20)
+    for field, bad in (("head_dim", 64), ("n_kv", 5), ("hidden", 1000), ("ffn", 12288), ("hidden", 8448)):
         mm = DecodeModel.from_buffer_copy(m)
         setattr(mm, field, bad)
         with pytest.raises(HIPSafetyError):
@@ -96,3 +98,25 @@ def test_decode_workspace_and_rejections_on_host():
     # the step itself rejects a model without its pointers before launching
     with pytest.raises(HIPSafetyError):
         K.decode_step(m, 256, 256, 256, 256)
+
+
+def test_persistent_support_follows_the_kernel_formats():
+    """The executor takes the persistent step only for weight formats and
+    shapes the kernel handles (Q4_K q/k/o/gate/up; Q4_K or Q6_K v and down;
+    a Q4_K, Q6_K or Q8_0 LM head; hidden up to 8192)."""
+    from types import SimpleNamespace
+
+    from vte_amd.core.hip_graph_executor import HIPGraphExecutor
+    from vte_amd.core.model_config import QWEN25_1P5B
+
+    def model(cfg=QWEN25_1P5B, lm="q6_k", **fmts):
+        lw = {p + "_fmt": "q4_k" for p in ("q", "k", "v", "o", "gate", "up", "down")}
+        lw.update(fmts)
+        return SimpleNamespace(cfg=cfg, token_embd=object(), token_embd_fmt=lm, layers=[lw])
+
+    ok = HIPGraphExecutor._persistent_supported
+    assert ok(model()) and ok(model(lm="q8_0")) and ok(model(v_fmt="q6_k", down_fmt="q6_k"))
+    assert not ok(model(lm="q5_k"))
+    assert not ok(model(q_fmt="q6_k"))
+    assert not ok(model(down_fmt="q8_0"))
+    assert not ok(model(cfg=QWEN25_1P5B.with_(hidden=8448)))

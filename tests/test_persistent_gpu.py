@@ -134,11 +134,11 @@ def test_full_shape_persistent_vs_graph_path(hip, full_model, pos):
         assert abs(lg[t] - kth) <= 1e-2 * np.abs(lg).max()
 
 
-@pytest.mark.parametrize("embd,lm", [("q4_k", "q6_k"), ("q6_k", "q4_k"), ("q4_k", None)])
+@pytest.mark.parametrize("embd,lm", [("q4_k", "q6_k"), ("q6_k", "q4_k"), ("q4_k", None), ("q8_0", None)])
 def test_persistent_lm_head_formats(hip, embd, lm):
     """A separate Q6_K output matrix after a Q4_K table (the Qwen2.5-7B layout),
-    a Q4_K output matrix, and a tied Q4_K table as the LM head, against the
-    oracle and the graph path."""
+    a Q4_K output matrix, and tied Q4_K and Q8_0 tables as the LM head, against
+    the oracle and the graph path."""
     model = SyntheticQwen2(TINY, seed=8, embd_fmt=embd, lm_head_fmt=lm)
     cfg = model.cfg
     rng = np.random.default_rng(4)
@@ -159,17 +159,6 @@ def test_persistent_lm_head_formats(hip, embd, lm):
     ref = ost.decode_step(model, np.array([77]), np.array([150]), [k.copy() for k in ks], [v.copy() for v in vs], {})
     assert rel_l2(got[True], ref[0]) <= TOL
     assert rel_l2(got[True], got[False]) <= TOL
-
-
-def test_persistent_falls_back_for_unsupported_formats(hip):
-    """A tied Q8_0 table as the LM head is outside the persistent kernel's
-    formats: the executor keeps the per-node graph (and says so)."""
-    model = SyntheticQwen2(TINY, seed=8, embd_fmt="q8_0", lm_head_fmt=None)
-    ex = HIPGraphExecutor(hip, model, batch_size=1, max_seq=256, persistent=True)
-    try:
-        assert not ex.persistent
-    finally:
-        ex.close()
 
 
 def test_tiny_persistent_long_context(hip):

@@ -192,12 +192,12 @@ class HIPGraphExecutor:
         cfg = model.cfg
         if cfg.head_dim != 128 or cfg.n_q % cfg.n_kv or cfg.n_q // cfg.n_kv > 8:
             return False
-        if any(d % 256 or d > 10240 for d in (cfg.hidden, cfg.ffn, cfg.q_dim)):
+        if any(d % 256 or d > 10240 for d in (cfg.hidden, cfg.ffn, cfg.q_dim)) or cfg.hidden > 8192:
             return False
         lm = getattr(model, "lm_head", None)
         lm_fmt = getattr(model, "token_embd_fmt", "q6_k") if lm is None or lm is model.token_embd else \
             getattr(model, "lm_head_fmt", "q6_k")
-        if lm_fmt not in ("q4_k", "q6_k"):
+        if lm_fmt not in ("q4_k", "q6_k", "q8_0"):
             return False
         for lw in model.layers:
             if any(lw[p + "_fmt"] != "q4_k" for p in ("q", "k", "o", "gate", "up")):

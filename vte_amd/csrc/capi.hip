@@ -419,7 +419,7 @@ int vte_fill_normal_f16(void* dst, long long n, unsigned long long seed, float s
 
 namespace {
 struct PdLayout {
-    size_t ctrl, layers, ll_h, ll_q, ll_kv, ll_att, ll_hm, ll_act, part, total;
+    size_t ctrl, layers, ll_h, ll_q, ll_kv, ll_att, ll_hm, ll_act, part, ll_dn, h_out, total;
 };
 size_t pd_align(size_t x) { return (x + 255) & ~(size_t)255; }
 PdLayout pd_layout(const vte_decode_model* m) {
@@ -435,6 +435,8 @@ PdLayout pd_layout(const vte_decode_model* m) {
     L.ll_hm = o; o = pd_align(o + (size_t)m->hidden * 4);
     L.ll_act = o; o = pd_align(o + (size_t)m->ffn * 4);
     L.part = o; o = pd_align(o + (size_t)m->n_q * VTE_DECODE_MAX_SPLITS * 130 * 8);
+    L.ll_dn = o; o = pd_align(o + (size_t)(m->ffn / 256) * m->hidden * 8);
+    L.h_out = o; o = pd_align(o + (size_t)m->hidden * 2);
     L.total = o;
     return L;
 }
@@ -447,9 +449,10 @@ int pd_check_model(const vte_decode_model* m, bool pointers = true) {
     REQUIRE(m->hidden % 256 == 0 && m->hidden <= 10240 && m->ffn % 256 == 0 && m->ffn <= 10240 && qd % 256 == 0 &&
                 qd <= 10240, "decode: hidden, ffn and n_q*128 must be multiples of 256 up to 10240");
     REQUIRE(fmv_ro(m->hidden) == fmv_ro(qd), "decode: hidden %d and q_dim %d need the same unit mapping", m->hidden, qd);
+    REQUIRE(m->hidden <= 8192, "decode: hidden %d above the LM head's 8192", m->hidden);
     REQUIRE(m->vocab >= 1 && m->max_seq >= 1, "decode: vocab / max_seq");
     if (!pointers) return 0;
-    REQUIRE(m->fmt_lm == 4 || m->fmt_lm == 6, "decode: LM head must be Q4_K or Q6_K");
+    REQUIRE(m->fmt_lm == 4 || m->fmt_lm == 6 || m->fmt_lm == 8, "decode: LM head must be Q4_K, Q6_K or Q8_0");
     REQUIRE(m->rope_cos && m->rope_sin && m->output_norm && m->lm_head, "decode: null model pointer");
     REQUIRE(aligned(m->output_norm, 16) && aligned(m->lm_head, 16), "decode: 16-byte alignment");
     return 0;
@@ -525,17 +528,13 @@ int vte_decode_step(const vte_decode_model* m, void* ws, const int* kv_offset, c
     P.ffn = m->ffn;
     P.n_q = m->n_q;
     P.n_kv = m->n_kv;
-    P.vocab = m->vocab;
     P.eps = m->eps;
     P.scale = 1.0f / sqrtf(128.0f);
     P.kv_offset = kv_offset;
     P.x = static_cast<const __half*>(x);
     P.rope_cos = static_cast<const __half*>(m->rope_cos);
     P.rope_sin = static_cast<const __half*>(m->rope_sin);
-    P.output_norm = m->output_norm;
-    P.lm_head = m->lm_head;
-    P.fmt_lm = m->fmt_lm;
-    P.logits = logits;
+    P.h_out = reinterpret_cast<__half*>(base + L.h_out);
     P.ll_h = reinterpret_cast<uint32_t*>(base + L.ll_h);
     P.ll_q = reinterpret_cast<uint32_t*>(base + L.ll_q);
     P.ll_kv = reinterpret_cast<uint32_t*>(base + L.ll_kv);
@@ -543,6 +542,7 @@ int vte_decode_step(const vte_decode_model* m, void* ws, const int* kv_offset, c
     P.ll_hm = reinterpret_cast<uint32_t*>(base + L.ll_hm);
     P.ll_act = reinterpret_cast<uint32_t*>(base + L.ll_act);
     P.part = reinterpret_cast<uint64_t*>(base + L.part);
+    P.ll_dn = reinterpret_cast<uint64_t*>(base + L.ll_dn);
     P.ctrl = reinterpret_cast<uint32_t*>(base + L.ctrl);
     const int H = m->hidden, F = m->ffn, qd = m->n_q * 128, kvd = m->n_kv * 128;
     // rows per tile: RoPE tiles a power of two (pairs d, d + 64 of one head);
@@ -552,10 +552,16 @@ int vte_decode_step(const vte_decode_model* m, void* ws, const int* kv_offset, c
     P.r_qk = r;
     P.r_v = std::max(1, pd_cap(H, 1));
     P.r_o = std::max(1, std::min(pd_cap(qd, 1), (H + blocks - 1) / blocks));
-    P.r_gu = std::min(pd_cap(H, 4) & ~1, 2 * ((F + blocks - 1) / blocks));
-    P.r_d = std::min(pd_cap(F, 4), (H + blocks - 1) / blocks);
-    P.r_lm = pd_cap(H, 4);
-    REQUIRE(P.r_qk >= 2 && P.r_gu >= 2 && P.r_d >= 1 && P.r_lm >= 1, "decode_step: tile plan does not fit");
+    // gate/up: about one tile per block, none on the last n_q blocks (they run
+    // the attention combine, so their o-proj is the stage's critical path)
+    const int gu_blocks = std::max(1, blocks - m->n_q);
+    P.r_gu = std::min(pd_cap(H, VTE_PD_UPT_GU) & ~1, 2 * ((F + gu_blocks - 1) / gu_blocks));
+    // down: F / 256 slices; about blocks / slices row tiles each, of at most
+    // 256 rows (4 units per row, 64 rows per pass of the 256 threads, 4 passes)
+    const int nsl = F / 256;
+    P.r_dn = std::min(256, (H + std::max(1, blocks / nsl) - 1) / std::max(1, blocks / nsl));
+    P.r_red = (H + blocks - 1) / blocks;
+    REQUIRE(P.r_qk >= 2 && P.r_gu >= 2 && P.r_dn >= 1, "decode_step: tile plan does not fit");
     REQUIRE(kvd % P.r_qk == 0 && qd % P.r_qk == 0, "decode_step: RoPE tiles");
     static const int split_env = [] {
         const char* s = getenv("VTE_PD_SPLIT");  // tuning: smallest attention split (multiple of 32)
@@ -563,12 +569,17 @@ int vte_decode_step(const vte_decode_model* m, void* ws, const int* kv_offset, c
     }();
     P.split_min = split_env >= 32 ? split_env / 32 * 32 : 128;
     P.timeout_ticks = 20000000ull;  // 0.2 s
-    const size_t lds = vte::decode_persistent_lds(H, F, qd);
+    const size_t lds = std::max(vte::decode_persistent_lds(H, F, qd), (size_t)P.r_red * nsl * 4);
     const int occ = vte::decode_persistent_occupancy(P, lds);
     REQUIRE(occ >= 1, "decode_step: the kernel does not fit on a CU (occupancy %d)", occ);
     e = vte::decode_persistent_launch(P, blocks, lds, (hipStream_t)stream);
     if (e == hipErrorNotSupported) return fail("decode_step: unsupported shape");
-    return hip_status(e, "vte_decode_step launch");
+    if (e != hipSuccess) return hip_status(e, "vte_decode_step launch");
+    // output norm + LM head over the last layer's output, as the graph path's
+    e = vte::norm_mv(P.h_out, m->output_norm, m->eps, m->lm_head, m->fmt_lm, logits, true, nullptr, nullptr, 1.f, 1, H,
+                     m->vocab, (hipStream_t)stream);
+    if (e == hipErrorNotSupported) return fail("decode_step: the LM head does not fit the fused kernel");
+    return hip_status(e, "vte_decode_step LM head launch");
 }
 
 int vte_decode_status(void* ws, int* flags) {

@@ -8,27 +8,28 @@
 #include "../../include/vte_amd.h"
 
 #define VTE_DECODE_MAX_SPLITS 128  // attention splits per KV head
+#define VTE_PD_UPT_GU 8            // weight units per thread of a gate/up tile
 
 typedef vte_decode_layer VtePdLayer;
 
 struct VtePdPlan {
     const VtePdLayer* layers;  // device copy in the workspace
-    int n_layers, hidden, ffn, n_q, n_kv, vocab;
+    int n_layers, hidden, ffn, n_q, n_kv;
     float eps, scale;
     const int* kv_offset;
     const __half* x;           // the token's embedding (layer 0 input, plain fp16)
     const __half* rope_cos;
     const __half* rope_sin;
-    const void* output_norm;
-    const void* lm_head;
-    int fmt_lm;
-    float* logits;
+    __half* h_out;             // the last layer's output (plain fp16 [hidden], read by the LM head launch)
     // flagged words (fp16 | tag << 16): layer output, q, new K/V row, attention
     // output, post-attention hidden, SwiGLU output
     uint32_t *ll_h, *ll_q, *ll_kv, *ll_att, *ll_hm, *ll_act;
     uint64_t* part;            // attention records (fp32 | tag << 32) [n_q][MAX_SPLITS][130]
+    uint64_t* ll_dn;           // down partial sums (fp32 | tag << 32) [ffn / 256][hidden]
     uint32_t* ctrl;            // [0] epoch, [1] finished blocks, [2] error flags
-    int r_qk, r_v, r_o, r_gu, r_d, r_lm;  // rows per tile of each stage
+    int r_qk, r_v, r_o, r_gu;  // rows per tile of the q/k, v, o-proj and gate/up stages
+    int r_dn;                  // rows per down-partial tile (one 256-wide slice of the ffn activations)
+    int r_red;                 // rows each block reduces over the down partials
     int split_min;             // smallest attention split (rows)
     unsigned long long timeout_ticks;     // per-block wait deadline (100 MHz clock)
 };

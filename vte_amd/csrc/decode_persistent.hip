@@ -2,17 +2,20 @@
 //
 // The whole 28-layer step (vte/compiler/qwen_compute.py:100-282, captured node
 // by node by vte/core/hip_graph_executor.py:504-738) runs as ONE launch of one
-// 256-thread block per CU.  Per layer the blocks pass through six stages:
+// 256-thread block per CU.  Per layer the blocks pass through seven stages:
 //
 //   S1  RMSNorm + q/k/v mat-vec + bias + RoPE + K/V append     (row tiles)
 //   S2  split-KV attention partials over the cached rows        (KV head, split)
 //   S3  log-sum-exp combine + the new token's own row           (query head)
 //   S4  o-proj mat-vec + residual                               (row tiles)
 //   S5  RMSNorm + gate/up mat-vec + SwiGLU                      (row-pair tiles)
-//   S6  down mat-vec + residual                                 (row tiles)
+//   S6a down partial sums over one 256-wide slice of the        (slice, row tiles)
+//       SwiGLU output each
+//   S7  sum of the partials + residual                          (row ranges)
 //
-// then RMSNorm + LM head.  A stage needs the whole output of the one before
-// it, which in a graph costs a kernel boundary (~2 us on this part) plus the
+// The LM head follows as a separate launch (the graph path's norm + mat-vec
+// kernel) over the last layer's output.  Most stages need the whole output of
+// the one before them, which in a graph costs a kernel boundary (~2 us on this part) plus the
 // next kernel's activation fetch before its weights are even requested.  Here
 // every value handed from one block to another is stored as a flagged word
 // (fp16 | tag << 16, or fp32 | tag << 32 for the attention partials) with
@@ -26,18 +29,22 @@
 // makes tag = (epoch << 5 | layer) unique per launch and layer, so the
 // flagged buffers are reused across layers and launches without clearing.
 // A word of a previous layer or launch never carries the current tag.
-// Reuse is safe because every stage waits on all of its predecessor's output,
-// so by the time any block writes a buffer again, every reader of its previous
-// contents has finished (the chain of full dependencies in between).
+// Reuse is safe because between a buffer's readers and its next writer there
+// is always a stage that waits on all of its predecessor's output (S6a reads
+// one slice, but S7 waits on every S6a tile and S1 on every S7 row), so by
+// the time any block writes a buffer again, every reader of its previous
+// contents has finished.
 //
 // All blocks must be resident at once (grid = CU count, one block per CU;
 // the host checks the occupancy).  Every wait is bounded: past a deadline a
 // block records an error flag and proceeds, so the kernel always drains.
 //
 // Arithmetic is the fused mat-vec's (fused_kernels.h: same unit dot products,
-// same row sums, same RMSNorm and epilogue rounding points), so every
-// projection gives the same bits as the graph path; attention splits differ
-// (the new token is folded in by the combine) and agree to fp32 rounding.
+// same row sums, same RMSNorm and epilogue rounding points), so q/k/v, o-proj
+// and gate/up give the same bits as the graph path on the same inputs; the
+// down projection sums per 256-column slice first and the attention splits
+// differ (the new token is folded in by the combine): both agree to fp32
+// rounding.
 #include <cstdio>
 
 #include "fused_kernels.h"
@@ -49,6 +56,7 @@ namespace {
 constexpr int PD_MS = VTE_DECODE_MAX_SPLITS;  // attention splits per KV head
 constexpr int PD_PW = ATT_D + 2;              // words of one (head, split) record: m, l, o[128]
 constexpr int PD_T = ROWS_THREADS;            // threads per block
+constexpr int UPT_QKV = 1, UPT_O = 1, UPT_GU = VTE_PD_UPT_GU, UPT_D = 4;  // weight units per thread of each stage
 
 // ---------------------------------------------------------------- flagged words
 __device__ __forceinline__ uint64_t pd_now() { return __builtin_amdgcn_s_memrealtime(); }
@@ -269,24 +277,44 @@ struct PdOut {
     int pos;
     const __half* cosp;       // RoPE tables at row `pos`
     const __half* sinp;
-    float* logits;
 };
+
+// Epilogue operands of this thread's output (bias of the row and of its RoPE
+// partner, cos / sin of its dimension) as raw fp16 bits, requested together
+// with the tile's weights so the epilogue waits on none of them.
+struct PdPre {
+    uint32_t b1, b2, c, s, r;  // r: the residual word (flagged or plain fp16 bits)
+};
+__device__ __forceinline__ PdPre pd_pre(const TileGeo& T, const PdOut& o) {
+    PdPre p{0u, 0u, 0u, 0u, 0u};
+    const bool paired = fmv_paired(T.mode);
+    const int t = threadIdx.x;
+    if (t >= (paired ? T.hA : T.nr) || T.mode == FMV_SWIGLU) return p;
+    const int row1 = T.j0 + t;
+    if (T.bias != nullptr) {
+        p.b1 = ldg_b16(T.bias, row1);
+        if (paired) p.b2 = ldg_b16(T.bias, row1 + 64);
+    }
+    if (T.mode == FMV_ROPE_Q || T.mode == FMV_ROPE_KCACHE) {
+        p.c = ldg_b16(o.cosp, row1 & 127);
+        p.s = ldg_b16(o.sinp, row1 & 127);
+    }
+    if (T.mode == FMV_STORE_F16)
+        p.r = o.res_ll ? ld_c32(reinterpret_cast<const uint32_t*>(o.res) + row1)
+                       : (uint32_t)reinterpret_cast<const uint16_t*>(o.res)[row1];
+    return p;
+}
 
 // One output per thread, as tile_epilogue (batch 1) with flagged stores.
 __device__ __forceinline__ void pd_epilogue(const TileGeo& T, const float* part, int per_row, const PdOut& o,
-                                            const PdClock& ck) {
+                                            const PdPre& pre, const PdClock& ck) {
     const bool paired = fmv_paired(T.mode);
     const int t = threadIdx.x;
     if (t >= (paired ? T.hA : T.nr)) return;
     const int row1 = T.j0 + t;
     if (!paired) {
-        const uint32_t b1 = T.bias != nullptr ? ldg_b16(T.bias, row1) : 0u;
         float v = row_sum(part + t * per_row, per_row);
-        if (T.mode == FMV_STORE_F32) {
-            o.logits[row1] = (v + 0.f) * 1.f + 0.f;
-            return;
-        }
-        v += h2f_bits(b1);
+        v += h2f_bits(pre.b1);
         if (T.mode == FMV_VCACHE) {
             const uint32_t hb = f16_bits(v);
             reinterpret_cast<uint16_t*>(o.v_cache)[(size_t)o.pos * o.kv_dim + row1] = (uint16_t)hb;
@@ -294,8 +322,13 @@ __device__ __forceinline__ void pd_epilogue(const TileGeo& T, const float* part,
             return;
         }
         // FMV_STORE_F16: fp16((acc + bias) * 1 + residual[row])
-        const uint32_t rb = o.res_ll ? pd_wait16(reinterpret_cast<const uint32_t*>(o.res) + row1, o.res_tag, ck)
-                                     : (uint32_t)reinterpret_cast<const uint16_t*>(o.res)[row1];
+        uint32_t rb = pre.r;
+        if (o.res_ll) {  // requested with the weights; re-polled only if it was not yet written
+            int spins = 0;
+            while ((rb >> 16) != o.res_tag && !pd_expired(ck, spins))
+                rb = ld_c32(reinterpret_cast<const uint32_t*>(o.res) + row1);
+            rb &= 0xFFFFu;
+        }
         v = v * 1.f + h2f_bits(rb);
         st_c32(o.ll + row1, ll16(f16_bits(v), o.tag));
         return;
@@ -309,12 +342,10 @@ __device__ __forceinline__ void pd_epilogue(const TileGeo& T, const float* part,
         st_c32(o.ll + row1, ll16(f16_bits(gg * sig * uu), o.tag));
         return;
     }
-    const uint32_t b1 = T.bias != nullptr ? ldg_b16(T.bias, row1) : 0u;
-    const uint32_t b2 = T.bias != nullptr ? ldg_b16(T.bias, row1 + 64) : 0u;
-    const float x1 = __half2float(__float2half(a + h2f_bits(b1)));
-    const float x2 = __half2float(__float2half(bv + h2f_bits(b2)));
+    const float x1 = __half2float(__float2half(a + h2f_bits(pre.b1)));
+    const float x2 = __half2float(__float2half(bv + h2f_bits(pre.b2)));
     const int d = row1 & 127;
-    const float c = __half2float(o.cosp[d]), sn = __half2float(o.sinp[d]);
+    const float c = h2f_bits(pre.c), sn = h2f_bits(pre.s);
     const uint32_t o1 = f16_bits(x1 * c - x2 * sn), o2 = f16_bits(x1 * sn + x2 * c);
     if (T.mode == FMV_ROPE_Q) {
         st_c32(o.ll + row1, ll16(o1, o.tag));
@@ -333,16 +364,18 @@ __device__ __forceinline__ void pd_epilogue(const TileGeo& T, const float* part,
 // waited on anything; PF: the next tile's weights are requested before the
 // current tile's dot products (stages of several tiles per block).
 template <int UPT, bool RO>
-__device__ __forceinline__ void pd_begin(const PdStage& S, TileW<UPT>& W, TileGeo& T) {
+__device__ __forceinline__ void pd_begin(const PdStage& S, TileW<UPT>& W, TileGeo& T, PdPre& pre, const PdOut& o) {
     if ((int)blockIdx.x < S.total) {
         T = pd_geo(S, blockIdx.x);
         pd_issue<UPT, RO>(W, T, S.K);
+        pre = pd_pre(T, o);
     }
 }
 
 template <int UPT, bool RO, bool PF>
-__device__ __forceinline__ void pd_run(const PdStage& S, TileW<UPT>& W, TileGeo& T, const void* src, bool ll, uint32_t in_tag,
-                       const __half* norm_w, float eps, uint8_t* lds, float* red, const PdOut& o, const PdClock& ck) {
+__device__ __forceinline__ void pd_run(const PdStage& S, TileW<UPT>& W, TileGeo& T, PdPre& pre, const void* src,
+                                       bool ll, uint32_t in_tag, const __half* norm_w, float eps, uint8_t* lds,
+                                       float* red, const PdOut& o, const PdClock& ck) {
     if ((int)blockIdx.x >= S.total) return;
     const int K = S.K, per_row = (K / QK_K) * 4;
     const FmvLDS L = fmv_lds(lds, 1, K, UPT);
@@ -351,21 +384,25 @@ __device__ __forceinline__ void pd_run(const PdStage& S, TileW<UPT>& W, TileGeo&
         const int gn = g + gridDim.x;
         TileW<UPT> Wn;
         TileGeo Tn;
+        PdPre pn;
         if (PF && gn < S.total) {
             Tn = pd_geo(S, gn);
             pd_issue<UPT, RO>(Wn, Tn, K);
+            pn = pd_pre(Tn, o);
         }
         pd_dot<UPT, RO>(W, T, K, L);
         __syncthreads();
-        pd_epilogue(T, L.part, per_row, o, ck);
+        pd_epilogue(T, L.part, per_row, o, pre, ck);
         __syncthreads();
         if (gn < S.total) {
             if (PF) {
                 W = Wn;
                 T = Tn;
+                pre = pn;
             } else {
                 T = pd_geo(S, gn);
                 pd_issue<UPT, RO>(W, T, K);
+                pre = pd_pre(T, o);
             }
         }
     }
@@ -377,11 +414,12 @@ __device__ __forceinline__ void pd_run(const PdStage& S, TileW<UPT>& W, TileGeo&
 // the input is waited for.
 template <int UPT, bool RO, bool PF>
 __device__ __forceinline__ void pd_mv(const PdStage& S, const void* src, bool ll, uint32_t in_tag, const __half* norm_w,
-                                   float eps, uint8_t* lds, float* red, const PdOut& o, const PdClock& ck) {
+                                      float eps, uint8_t* lds, float* red, const PdOut& o, const PdClock& ck) {
     TileW<UPT> W;
     TileGeo T;
-    pd_begin<UPT, RO>(S, W, T);
-    pd_run<UPT, RO, PF>(S, W, T, src, ll, in_tag, norm_w, eps, lds, red, o, ck);
+    PdPre pre;
+    pd_begin<UPT, RO>(S, W, T, pre, o);
+    pd_run<UPT, RO, PF>(S, W, T, pre, src, ll, in_tag, norm_w, eps, lds, red, o, ck);
 }
 
 // ------------------------------------------------------------------ attention
@@ -494,19 +532,52 @@ __device__ __forceinline__ void pd_attn_combine(const VtePdPlan& P, int qh, int 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int G = P.n_q / P.n_kv, kvh = qh / G, kv_dim = P.n_kv * ATT_D;
     const uint64_t* recs = P.part + (size_t)qh * PD_MS * PD_PW;
-    float vnew = 0.f;
-    if (tid < ns) {
-        A.u.c.wm[tid] = pd_wait32(recs + (size_t)tid * PD_PW, tag32, ck);
-        A.u.c.wl[tid] = pd_wait32(recs + (size_t)tid * PD_PW + 1, tag32, ck);
+    const int d = tid & 127, hf = tid >> 7;
+    // every word this thread needs is requested before any is waited for: the
+    // first 16 splits' o[d] (threads (d, half) take every other split), the
+    // split's (m, l), and q[d], k_new[d] (waves 2-3) or v_new[d] (waves 0-1)
+    uint64_t ow[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = hf + 2 * j;
+        ow[j] = c < ns ? ld_c64(recs + (size_t)c * PD_PW + 2 + d) : 0ull;
     }
+    uint64_t wm = 0ull, wl = 0ull;
+    if (tid < ns) {
+        wm = ld_c64(recs + (size_t)tid * PD_PW);
+        wl = ld_c64(recs + (size_t)tid * PD_PW + 1);
+    }
+    const uint32_t* pa = tid >= 128 ? P.ll_q + (size_t)qh * ATT_D + d : P.ll_kv + kv_dim + (size_t)kvh * ATT_D + d;
+    const uint32_t* pb = P.ll_kv + (size_t)kvh * ATT_D + d;
+    uint32_t wa = ld_c32(pa), wb = tid >= 128 ? ld_c32(pb) : (tag << 16);
+    {  // one poll loop over all of them: a single round trip once the last record lands
+        int spins = 0;
+        while (true) {
+            bool ok = (wa >> 16) == tag && (wb >> 16) == tag;
+            if (tid < ns) ok = ok && (uint32_t)(wm >> 32) == tag32 && (uint32_t)(wl >> 32) == tag32;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ok = ok && (hf + 2 * j >= ns || (uint32_t)(ow[j] >> 32) == tag32);
+            if (ok || pd_expired(ck, spins)) break;
+            if (tid < ns && (uint32_t)(wm >> 32) != tag32) wm = ld_c64(recs + (size_t)tid * PD_PW);
+            if (tid < ns && (uint32_t)(wl >> 32) != tag32) wl = ld_c64(recs + (size_t)tid * PD_PW + 1);
+            if ((wa >> 16) != tag) wa = ld_c32(pa);
+            if ((wb >> 16) != tag) wb = ld_c32(pb);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (hf + 2 * j < ns && (uint32_t)(ow[j] >> 32) != tag32)
+                    ow[j] = ld_c64(recs + (size_t)(hf + 2 * j) * PD_PW + 2 + d);
+        }
+    }
+    if (tid < ns) {
+        A.u.c.wm[tid] = __uint_as_float((uint32_t)wm);
+        A.u.c.wl[tid] = __uint_as_float((uint32_t)wl);
+    }
+    float vnew = 0.f;
     if (tid >= 128) {  // waves 2-3: q . k_new
-        const int d = tid - 128;
-        const float qv = h2f_bits(pd_wait16(P.ll_q + (size_t)qh * ATT_D + d, tag, ck));
-        const float kv = h2f_bits(pd_wait16(P.ll_kv + (size_t)kvh * ATT_D + d, tag, ck));
-        const float s = wave_sum(qv * kv);
+        const float s = wave_sum(h2f_bits(wa & 0xFFFFu) * h2f_bits(wb & 0xFFFFu));
         if (lane == 0) A.sc[wv - 2] = s;
     } else {
-        vnew = h2f_bits(pd_wait16(P.ll_kv + kv_dim + (size_t)kvh * ATT_D + tid, tag, ck));
+        vnew = h2f_bits(wa & 0xFFFFu);
     }
     __syncthreads();
     if (wv == 0) {  // maximum, split weights exp(m_c - M) and the denominator
@@ -529,9 +600,13 @@ __device__ __forceinline__ void pd_attn_combine(const VtePdPlan& P, int qh, int 
     }
     __syncthreads();
     // O[d] = sum_c w_c o_c[d] + e_new v_new[d]: threads (d, half) take every other split
-    const int d = tid & 127, hf = tid >> 7;
     float O = 0.f;
-    int c = hf;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = hf + 2 * j;
+        if (c < ns) O = fmaf(__uint_as_float((uint32_t)ow[j]), A.u.c.wm[c], O);
+    }
+    int c = hf + 16;
     for (; c + 14 < ns; c += 16) {
         float v[8];
 #pragma unroll
@@ -550,10 +625,130 @@ __device__ __forceinline__ void pd_attn_combine(const VtePdPlan& P, int qh, int 
     __syncthreads();
 }
 
-// ------------------------------------------------------------------ the kernel
-constexpr int UPT_QKV = 1, UPT_O = 1, UPT_GU = 4, UPT_D = 4, UPT_LM = 4;
+// ------------------------------------------------------------------ down
+// S6a: tile g covers rows j0 .. j0 + r_dn of w_down over the 256 columns of
+// slice s = g / rt (one super-block per row), so a block waits only on the 256
+// SwiGLU words of its slice (written by the few blocks whose gate/up tiles
+// cover it) instead of all ffn of them.  Each row's partial sum (the same
+// per-unit dot products and the row_sum order of the fused mat-vec, over 4
+// units) goes out as a flagged fp32 word.
+template <int FMT>
+__device__ __forceinline__ void pd_down_tile(const VtePdPlan& P, const VtePdLayer& Ly, int g, int rt, uint32_t tag,
+                                             uint32_t tag32, const FmvLDS& L, float* red, const PdClock& ck) {
+    const int H = P.hidden, n_sb = P.ffn / QK_K;
+    const int s = g / rt, rtile = g - s * rt;
+    const int bpb = FMT == 4 ? Q4K_BYTES : Q6K_BYTES;
+    TileGeo T;
+    T.fmt = FMT;
+    T.mode = FMV_STORE_F16;
+    T.rb = n_sb * bpb;
+    T.n_rows = H;
+    T.j0 = rtile * P.r_dn;
+    T.nr = min(P.r_dn, H - T.j0);
+    T.hA = T.nr;
+    T.bA = reinterpret_cast<const uint8_t*>(Ly.w_down) + (size_t)T.j0 * T.rb + (size_t)s * bpb;
+    T.bB = T.bA;
+    T.out = nullptr;
+    T.bias = nullptr;
+    T.residual = nullptr;
+    TileW<UPT_D> W;
+    tile_w_issue<UPT_D, FMT, true>(W, T, 1, 4, threadIdx.x);  // before the wait: the weights do not depend on it
+    pd_stage_x_nj<1>(P.ll_act + (size_t)s * QK_K, true, tag, nullptr, 0.f, QK_K, L, red, ck);
+    tile_dot<1, UPT_D, FMT, true>(W, T.nr, 4, QK_K, L.xs, L.s16, L.part, UPT_D * PD_T, threadIdx.x);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < T.nr) st_c64(P.ll_dn + (size_t)s * H + T.j0 + t, ll32(row_sum(L.part + t * 4, 4), tag32));
+    __syncthreads();
+}
 
-template <bool RO_H, bool RO_F>
+__device__ __forceinline__ void pd_down_part(const VtePdPlan& P, const VtePdLayer& Ly, uint32_t tag, uint32_t tag32,
+                                             uint8_t* lds, float* red, const PdClock& ck) {
+    const int nsl = P.ffn / QK_K, rt = (P.hidden + P.r_dn - 1) / P.r_dn, total = nsl * rt;
+    const FmvLDS L = fmv_lds(lds, 1, QK_K, UPT_D);
+    for (int g = blockIdx.x; g < total; g += gridDim.x) {
+        if (Ly.fmt_down == 4) pd_down_tile<4>(P, Ly, g, rt, tag, tag32, L, red, ck);
+        else pd_down_tile<6>(P, Ly, g, rt, tag, tag32, L, red, ck);
+    }
+}
+
+// S7: rows r0 .. r0 + r_red of the layer output = fp16(sum over the slices,
+// in slice order, + the post-attention residual): flagged for the next
+// layer, plain into h_out after the last layer.
+__device__ __forceinline__ void pd_down_reduce(const VtePdPlan& P, uint32_t tag, uint32_t tag32, bool last,
+                                               uint8_t* lds, const PdClock& ck) {
+    const int H = P.hidden, nsl = P.ffn / QK_K;
+    const int r0 = blockIdx.x * P.r_red, nrw = min(P.r_red, H - r0);
+    if (nrw <= 0) return;
+    float* pp = reinterpret_cast<float*>(lds);  // [nrw][nsl]
+    const int t = threadIdx.x;
+    uint32_t rw = t < nrw ? ld_c32(P.ll_hm + r0 + t) : 0u;  // the residual, requested before the partials
+    for (int i = threadIdx.x; i < nrw * nsl; i += PD_T) {
+        const int row = i / nsl, k = i - row * nsl;
+        pp[i] = pd_wait32(P.ll_dn + (size_t)k * H + r0 + row, tag32, ck);
+    }
+    __syncthreads();
+    if (t < nrw) {
+        float v = 0.f;
+        for (int k = 0; k < nsl; ++k) v += pp[t * nsl + k];
+        int spins = 0;
+        while ((rw >> 16) != tag && !pd_expired(ck, spins)) rw = ld_c32(P.ll_hm + r0 + t);
+        v = v * 1.f + h2f_bits(rw & 0xFFFFu);
+        const uint32_t hb = f16_bits(v);
+        st_c32(P.ll_h + r0 + t, ll16(hb, tag));
+        if (last) reinterpret_cast<uint16_t*>(P.h_out)[r0 + t] = (uint16_t)hb;
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ L2 warm-up
+// While the attention stages run on a few blocks, the HBM stream is idle.  A
+// block then requests one word of every 128-byte line of its gate/up tile and
+// of its down tile (before the o-proj wait), so those weights sit in its XCD's
+// L2 (and the MALL) when their stages request them.  The words are held in
+// registers until the o-proj wait has covered them (loads complete in order),
+// so the warm-up never makes the block wait longer than it waits anyway.
+struct PdTouch {
+    uint32_t v[7];
+};
+__device__ __forceinline__ uint32_t pd_ld_word(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
+}
+// gate rows then up rows of this block's SwiGLU tile: two contiguous ranges
+__device__ __forceinline__ void pd_touch_gu(const PdStage& S5, PdTouch& t) {
+    const int tid = threadIdx.x, b = blockIdx.x;
+    if (b >= S5.total) return;
+    const TileGeo T = pd_geo(S5, b);
+    const int bytes = T.hA * T.rb;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int off = (tid + PD_T * i) * 128;
+        if (off < bytes) {
+            t.v[2 * i] = pd_ld_word(T.bA + off);
+            t.v[2 * i + 1] = pd_ld_word(T.bB + off);
+        }
+    }
+}
+// one super-block of each row of this block's down tile (up to three lines)
+__device__ __forceinline__ void pd_touch_down(const VtePdPlan& P, const VtePdLayer& Ly, PdTouch& t) {
+    const int tid = threadIdx.x, b = blockIdx.x;
+    const int nsl = P.ffn / QK_K, rt = (P.hidden + P.r_dn - 1) / P.r_dn;
+    if (b >= nsl * rt) return;
+    const int s = b / rt, j0 = (b - s * rt) * P.r_dn, nr = min(P.r_dn, P.hidden - j0);
+    const int bpb = Ly.fmt_down == 4 ? Q4K_BYTES : Q6K_BYTES, rb = nsl * bpb;
+    if (tid < nr) {
+        const uint8_t* p = reinterpret_cast<const uint8_t*>(Ly.w_down) + (size_t)(j0 + tid) * rb + (size_t)s * bpb;
+        t.v[4] = pd_ld_word(p);
+        t.v[5] = pd_ld_word(p + bpb / 2);
+        t.v[6] = pd_ld_word(p + bpb - 4);
+    }
+}
+__device__ __forceinline__ void pd_touch_done(const PdTouch& t) {
+    asm volatile("" ::"v"(t.v[0]), "v"(t.v[1]), "v"(t.v[2]), "v"(t.v[3]), "v"(t.v[4]), "v"(t.v[5]), "v"(t.v[6]));
+}
+
+// ------------------------------------------------------------------ the kernel
+
+template <bool RO_H>
 __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P) {
     extern __shared__ uint4 pd_smem[];
     uint8_t* lds = reinterpret_cast<uint8_t*>(pd_smem);
@@ -569,7 +764,6 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
     const int ns = (pos + split - 1) / split;
     const __half* cosp = P.rope_cos + (size_t)pos * ATT_D;
     const __half* sinp = P.rope_sin + (size_t)pos * ATT_D;
-
     for (int l = 0; l < P.n_layers; ++l) {
         const VtePdLayer& Ly = P.layers[l];
         const uint32_t tag32 = (epoch << 5) | (uint32_t)l, tag = tag32 & 0xFFFFu;
@@ -609,51 +803,38 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
         for (int it = b; it < P.n_kv * ns; it += G) pd_attn_item(P, Ly, it / ns, it % ns, split, pos, tag, tag32, A, ck);
         // ---- S3: combine per query head (the last n_q blocks) ----
         for (int qh = G - 1 - b; qh >= 0 && qh < P.n_q; qh += G) pd_attn_combine(P, qh, ns, tag, tag32, A, ck);
-
-        // ---- S4: o-proj + residual ----
+        PdStage S5;
+        S5.K = H;
+        S5.nseg = 1;
+        S5.seg[0] = pd_seg((const uint8_t*)Ly.w_gate, (const uint8_t*)Ly.w_up, nullptr, Ly.fmt_gate_up, F, P.r_gu,
+                           FMV_SWIGLU, H);
+        S5.total = S5.seg[0].tiles;
+        // ---- S4: o-proj + residual; the combine blocks (its critical path) skip the warm-up ----
         o.ll = P.ll_hm;
         o.res = hin;
         o.res_ll = !first;
         o.res_tag = ptag;
-        pd_mv<UPT_O, RO_H, false>(So, P.ll_att, true, tag, nullptr, P.eps, lds, red, o, ck);
-
+        {
+            TileW<UPT_O> W;
+            TileGeo T;
+            PdPre pre;
+            pd_begin<UPT_O, RO_H>(So, W, T, pre, o);
+            PdTouch tw;
+#pragma unroll
+            for (int i = 0; i < 7; ++i) tw.v[i] = 0u;
+            if (G - 1 - b >= P.n_q) {
+                pd_touch_gu(S5, tw);
+                pd_touch_down(P, Ly, tw);
+            }
+            pd_run<UPT_O, RO_H, false>(So, W, T, pre, P.ll_att, true, tag, nullptr, P.eps, lds, red, o, ck);
+            pd_touch_done(tw);
+        }
         // ---- S5: norm + gate/up + SwiGLU ----
-        {
-            PdStage S;
-            S.K = H;
-            S.nseg = 1;
-            S.seg[0] = pd_seg((const uint8_t*)Ly.w_gate, (const uint8_t*)Ly.w_up, nullptr, Ly.fmt_gate_up, F, P.r_gu,
-                              FMV_SWIGLU, H);
-            S.total = S.seg[0].tiles;
-            o.ll = P.ll_act;
-            pd_mv<UPT_GU, RO_H, true>(S, P.ll_hm, true, tag, (const __half*)Ly.ffn_norm, P.eps, lds, red, o,
-                                        ck);
-        }
-        // ---- S6: down + residual ----
-        {
-            PdStage S;
-            S.K = F;
-            S.nseg = 1;
-            S.seg[0] = pd_seg((const uint8_t*)Ly.w_down, nullptr, nullptr, Ly.fmt_down, H, P.r_d, FMV_STORE_F16, F);
-            S.total = S.seg[0].tiles;
-            o.ll = P.ll_h;
-            o.res = P.ll_hm;
-            o.res_ll = true;
-            o.res_tag = tag;
-            pd_mv<UPT_D, RO_F, false>(S, P.ll_act, true, tag, nullptr, P.eps, lds, red, o, ck);
-        }
-    }
-    // ---- output norm + LM head -> fp32 logits ----
-    {
-        const uint32_t ltag = ((epoch << 5) | (uint32_t)(P.n_layers - 1)) & 0xFFFFu;
-        PdStage S;
-        S.K = H;
-        S.nseg = 1;
-        S.seg[0] = pd_seg((const uint8_t*)P.lm_head, nullptr, nullptr, P.fmt_lm, P.vocab, P.r_lm, FMV_STORE_F32, H);
-        S.total = S.seg[0].tiles;
-        PdOut o{};
-        o.logits = P.logits;
-        pd_mv<UPT_LM, RO_H, true>(S, P.ll_h, true, ltag, (const __half*)P.output_norm, P.eps, lds, red, o, ck);
+        o.ll = P.ll_act;
+        pd_mv<UPT_GU, RO_H, false>(S5, P.ll_hm, true, tag, (const __half*)Ly.ffn_norm, P.eps, lds, red, o, ck);
+        // ---- S6a: down partials; S7: their sum + residual -> the layer output ----
+        pd_down_part(P, Ly, tag, tag32, lds, red, ck);
+        pd_down_reduce(P, tag, tag32, l == P.n_layers - 1, lds, ck);
     }
     // ---- the last block to finish advances the epoch (read by every block at its start) ----
     __syncthreads();
@@ -668,6 +849,7 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
 
 }  // namespace
 
+
 namespace vte {
 
 size_t decode_persistent_lds(int hidden, int ffn, int q_dim) {
@@ -679,24 +861,18 @@ size_t decode_persistent_lds(int hidden, int ffn, int q_dim) {
 }
 
 hipError_t decode_persistent_launch(const VtePdPlan& P, int blocks, size_t lds, hipStream_t st) {
-    const bool ro_h = fmv_ro(P.hidden) && fmv_ro(P.n_q * ATT_D);
-    const bool ro_f = fmv_ro(P.ffn);
-    if (fmv_ro(P.hidden) != fmv_ro(P.n_q * ATT_D)) return hipErrorNotSupported;
-    if (ro_h && ro_f) hipLaunchKernelGGL((decode_persistent_kernel<true, true>), dim3(blocks), dim3(PD_T), lds, st, P);
-    else if (ro_h) hipLaunchKernelGGL((decode_persistent_kernel<true, false>), dim3(blocks), dim3(PD_T), lds, st, P);
-    else if (ro_f) hipLaunchKernelGGL((decode_persistent_kernel<false, true>), dim3(blocks), dim3(PD_T), lds, st, P);
-    else hipLaunchKernelGGL((decode_persistent_kernel<false, false>), dim3(blocks), dim3(PD_T), lds, st, P);
+    const bool ro_h = fmv_ro(P.hidden);
+    if (ro_h != fmv_ro(P.n_q * ATT_D)) return hipErrorNotSupported;
+    if (ro_h) hipLaunchKernelGGL((decode_persistent_kernel<true>), dim3(blocks), dim3(PD_T), lds, st, P);
+    else hipLaunchKernelGGL((decode_persistent_kernel<false>), dim3(blocks), dim3(PD_T), lds, st, P);
     return hipGetLastError();
 }
 
 int decode_persistent_occupancy(const VtePdPlan& P, size_t lds) {
-    const bool ro_h = fmv_ro(P.hidden), ro_f = fmv_ro(P.ffn);
     int n = 0;
-    hipError_t e;
-    if (ro_h && ro_f) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_persistent_kernel<true, true>, PD_T, lds);
-    else if (ro_h) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_persistent_kernel<true, false>, PD_T, lds);
-    else if (ro_f) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_persistent_kernel<false, true>, PD_T, lds);
-    else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_persistent_kernel<false, false>, PD_T, lds);
+    const hipError_t e =
+        fmv_ro(P.hidden) ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_persistent_kernel<true>, PD_T, lds)
+                         : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_persistent_kernel<false>, PD_T, lds);
     return e == hipSuccess ? n : -1;
 }
 
