@@ -138,6 +138,27 @@ def fused_mv_roofline(hip, ex, reps=20):
             "avg_launch_us": round(ms * 1e3, 3), "algo_bytes_per_launch": int(per_launch_bytes)}
 
 
+def persistent_roofline(hip, ex_p, layer_bytes, lm_head_ms, reps=20):
+    """Roofline of the default batch-1 step's dominant kernel,
+    decode_persistent_kernel (every layer of the step in one launch):
+    algorithmic bytes of the layers (weights + the KV rows read and appended)
+    over its duration = HIP-event time of the step's ``decode`` node (the
+    persistent launch + the LM-head launch) minus the LM-head launch timed
+    alone on the per-node graph (same kernel, same shapes)."""
+    ms = time_classes(hip, ex_p, ["decode"], reps) - lm_head_ms
+    gbps = layer_bytes / (ms * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_persistent_b1_traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+            "kernel": "decode_persistent_kernel (all %d layers of the batch-1 step, one launch)" % ex_p.cfg.n_layers,
+            "avg_launch_us": round(ms * 1e3, 3), "algo_bytes_per_launch": int(layer_bytes),
+            "timing": "HIP events around graph replays of the decode node, minus the LM-head launch"}
+
+
 def time_greedy(hip, ex, steps, start_pos):
     """Greedy decoding with the token fed back on the device (generate_greedy):
     wall time per step of one call of ``steps`` steps, tokens read at the end."""
@@ -485,7 +506,8 @@ def main():
                          "(Q4_K 8960x1536, Q6_K 1536x8960 and 151936x1536, Q8_0 2048x2048) and the batch-16 "
                          "MFMA GEMM over cold rotating pools, and the split-KV attention configs 2/3b")
     ap.add_argument("--profile-persistent", action="store_true",
-                    help="with --profile-step 1: the opt-in persistent (single-launch) form of the step")
+                    help="with --profile-step 1: the persistent form of the step (the default batch-1 step; "
+                         "without this flag the per-node graph is profiled)")
     ap.add_argument("--profile-classes", default="", metavar="C1,C2",
                     help="with --profile-step: replay only these launch classes (e.g. attn_in,ffn_in,lm_head)")
     args = ap.parse_args()
@@ -523,31 +545,42 @@ def main():
     wbytes = model.weight_bytes()
     prefix = 2048
     result = {}
-    roof, breakdown = None, None
+    cfg = QWEN25_1P5B
+    kv_layer_bytes = cfg.n_layers * (prefix + 1) * cfg.n_kv * cfg.head_dim * 2 * 2  # K and V rows read + appended
+    # the per-node graph of the batch-1 step: its own timing (for comparison),
+    # the per-class breakdown, the fused mat-vec roofline and the LM-head time
+    ex = HIPGraphExecutor(hip, model, batch_size=1, max_seq=prefix + 256, persistent=False)
+    ex.fill_kv_prefix(seed=1)
+    ex._update_staging_buffers([1], [prefix])
+    ms_g, _ = time_graph(hip, ex, max(20, args.steps // 2), args.warmup)
+    ex._update_staging_buffers([1], [prefix])
+    roof_mv = fused_mv_roofline(hip, ex)
+    breakdown = step_breakdown(hip, ex, prefix)
+    algo = ex.class_algorithmic_bytes()
+    layer_bytes = sum(algo[c] for c in ("attn_in", "attn", "o_proj", "ffn_in", "down")) + kv_layer_bytes
+    lm_head_ms = breakdown["lm_head"]["us_per_step"] * 1e-3
+    ex.close()
+    graph_b1 = {"ms_per_step": round(ms_g, 4), "tok_s": round(1e3 / ms_g, 2)}
+    roof = None
     for B in ([1] if args.quick else [1, 16]):
-        ex = HIPGraphExecutor(hip, model, batch_size=B, max_seq=prefix + 256)
+        ex = HIPGraphExecutor(hip, model, batch_size=B, max_seq=prefix + 256)  # batch 1: the persistent step
         ex.fill_kv_prefix(seed=B)
         ex._update_staging_buffers([1] * B, [prefix] * B)
         ms, wall = time_graph(hip, ex, args.steps, args.warmup)
         e2e = time_e2e(hip, ex, 20, prefix)
         greedy = time_greedy(hip, ex, 64, prefix)
         if B == 1:
+            assert ex.persistent, "the batch-1 step of this model runs the persistent kernel"
             ex._update_staging_buffers([1] * B, [prefix] * B)
-            roof = fused_mv_roofline(hip, ex)
-            breakdown = step_breakdown(hip, ex, prefix)
-        kv_read = QWEN25_1P5B.n_layers * (prefix + 1) * QWEN25_1P5B.n_kv * QWEN25_1P5B.head_dim * 2 * 2 * B
+            roof = persistent_roofline(hip, ex, layer_bytes, lm_head_ms)
+            status = ex.decode_status()
+            if status:
+                raise RuntimeError(f"persistent decode step error flags {status:#x}")
+        kv_read = cfg.n_layers * (prefix + 1) * cfg.n_kv * cfg.head_dim * 2 * 2 * B
         step_bytes = wbytes + kv_read
         result[B] = {"ms_per_step": ms, "tok_s": B / (ms * 1e-3), "wall_s": wall, "e2e_ms_per_step": e2e * 1e3,
                      "greedy_ms_per_step": greedy * 1e3,
                      "step_bytes": step_bytes, "step_GBps": step_bytes / (ms * 1e-3) / 1e9}
-        ex.close()
-    persistent = None
-    if not args.quick:  # the opt-in single-launch form of the batch-1 step, for comparison
-        ex = HIPGraphExecutor(hip, model, batch_size=1, max_seq=prefix + 256, persistent=True)
-        ex.fill_kv_prefix(seed=1)
-        ex._update_staging_buffers([1], [prefix])
-        ms_p, _ = time_graph(hip, ex, max(20, args.steps // 4), args.warmup)
-        persistent = {"ms_per_step": round(ms_p, 4), "tok_s": round(1e3 / ms_p, 2), "status": ex.decode_status()}
         ex.close()
 
     gemv = [] if args.quick else gemv_configs(hip, K)
@@ -566,8 +599,9 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(r1["ms_per_step"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "q4_k/q6_k weights, f16 activations, f32 accumulate",
         "data": "synthetic (random-init Q4_K_M-style weights, random fp16 KV prefix)",
-        "config": {"workload": "config4: Qwen2.5-1.5B-shape decode step as one hipGraph, batch 1, "
-                               "2048-token fp16 KV prefix, on-device top-k 40",
+        "config": {"workload": "config4: Qwen2.5-1.5B-shape decode step as one hipGraph (embedding, the "
+                               "persistent 28-layer kernel, norm + LM head, top-k), batch 1, 2048-token fp16 "
+                               "KV prefix, on-device top-k 40",
                    "layers": 28, "hidden": 1536, "ffn": 8960, "heads": "12q/2kv x128", "vocab": 151936,
                    "kv_prefix": prefix, "batch": 1},
         "step_GBps_b1": round(r1["step_GBps"], 1),
@@ -582,8 +616,7 @@ def main():
                      "step_GBps_b16": round(r16["step_GBps"], 1),
                      "e2e_tok_s_b16": round(16e3 / r16["e2e_ms_per_step"], 2),
                      "greedy_tok_s_b16": round(16e3 / r16["greedy_ms_per_step"], 2)})
-    if persistent:
-        line["persistent_b1"] = persistent
+    line["graph_b1"] = graph_b1  # the same step as a graph of per-node launches (VTE_PERSISTENT=0)
     if gemv:
         line["gemv"] = gemv
     if attn:
@@ -593,6 +626,7 @@ def main():
     line["hbm_copy_GBps"] = hbm_copy_bandwidth(hip)
     line["hbm_peak_GBps"] = HBM_PEAK_GBPS
     line["roofline"] = roof
+    line["roofline_graph_fused_mv"] = roof_mv
     line["step_breakdown_b1"] = breakdown
     if cpu:
         line["cpu_baseline"] = cpu

@@ -225,8 +225,9 @@ def test_prefill_matches_token_by_token(hip, request, shape, n1):
 
 
 # ---------------------------------------------------------------- closed-form pins on the GPU
-@pytest.mark.parametrize("B,fused", [(1, True), (1, False), (2, True), (4, True), (16, True)])
-def test_pin_model_closed_form(hip, B, fused):
+@pytest.mark.parametrize("B,fused,persistent", [(1, True, False), (1, True, True), (1, False, False),
+                                                (2, True, False), (4, True, False), (16, True, False)])
+def test_pin_model_closed_form(hip, B, fused, persistent):
     """The sparse exact-integer model of tests/pin_model.py through the HIP
     step (fused mat-vec path at batch 1-2, MFMA path from batch 3, separate
     kernels with fused=False) meets the same closed forms as the oracle:
@@ -236,8 +237,10 @@ def test_pin_model_closed_form(hip, B, fused):
     m = PinModel()
     toks = [TOKENS[b % len(TOKENS)] for b in range(B)]
     ks, vs = prefix_cache(PIN, B)
-    ex = HIPGraphExecutor(hip, m, batch_size=B, max_seq=PIN.max_seq, top_k=40, fused=fused)
+    ex = HIPGraphExecutor(hip, m, batch_size=B, max_seq=PIN.max_seq, top_k=40, fused=fused, persistent=persistent)
     try:
+        if persistent and not ex.persistent:
+            pytest.skip("the pin model's shapes or formats are outside the persistent kernel")
         for L in range(PIN.n_layers):
             ex.upload_kv(L, ks[L], vs[L])
         ex.execute_decode_batch(toks, [POS] * B)
@@ -290,12 +293,14 @@ class _Truncated:
 FLOOR_FACTOR = 2.5
 
 
-@pytest.mark.parametrize("n_layers,B,check", [(2, 1, (0,)), (2, 16, (0, 7, 15)), (28, 1, (0,)),
-                                              (28, 16, (0, 7, 15))])
-def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check):
+@pytest.mark.parametrize("n_layers,B,check,persistent", [(2, 1, (0,), False), (2, 1, (0,), True),
+                                                         (2, 16, (0, 7, 15), False), (28, 1, (0,), False),
+                                                         (28, 1, (0,), True), (28, 16, (0, 7, 15), False)])
+def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check, persistent):
     """Config 4: the Qwen2.5-1.5B-shaped step (all widths; the first 2 or all 28
     layers) with a 2048-token fp16 KV prefix, as one hipGraph at batch 1 (fused
-    mat-vec kernels) and batch 16 (MFMA kernels), against oracle.decode_step on
+    mat-vec kernels per node, or the persistent step) and batch 16 (MFMA
+    kernels), against oracle.decode_step on
     the same caches (weights dequantised per layer on the host, not cached):
     logits within FLOOR_FACTOR x the fp32/f64 oracle drift, the top-40 sets
     equal up to ties inside the measured error, and the appended K rows of the
@@ -307,8 +312,9 @@ def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check):
     toks = rng.integers(0, cfg.vocab, B)
     pos = np.full(B, 2048)
     chk = list(check)
-    ex = HIPGraphExecutor(hip, model, batch_size=B, max_seq=max_seq, top_k=40)
+    ex = HIPGraphExecutor(hip, model, batch_size=B, max_seq=max_seq, top_k=40, persistent=persistent)
     try:
+        assert ex.persistent == persistent
         ex.fill_kv_prefix(seed=11)
         ks = [ex.k_cache[L].numpy()[chk] for L in range(cfg.n_layers)]
         vs = [ex.v_cache[L].numpy()[chk] for L in range(cfg.n_layers)]
@@ -319,7 +325,7 @@ def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check):
         kg = [ex.k_cache[L].numpy()[chk] for L in (0, last)]
     finally:
         ex.close()
-    print(f"oracle step layers={n_layers} B={B} sequences {check}", flush=True)
+    print(f"oracle step layers={n_layers} B={B} persistent={persistent} sequences {check}", flush=True)
     k64 = [k.copy() for k in ks]
     ref = ost.decode_step(model, toks[chk], pos[chk], ks, vs)
     ref64 = ost.decode_step(model, toks[chk], pos[chk], k64, [v.copy() for v in vs], accum="f64")
