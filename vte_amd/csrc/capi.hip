@@ -548,9 +548,9 @@ int vte_decode_step(const vte_decode_model* m, void* ws, const int* kv_offset, c
     // rows per tile: RoPE tiles a power of two (pairs d, d + 64 of one head);
     // otherwise about one tile per block, within the stage's units per thread
     int r = 2;
-    while (r * 2 <= std::min(pd_cap(H, 1), 128)) r *= 2;
+    while (r * 2 <= std::min(pd_cap(H, VTE_PD_UPT_QKV), 128)) r *= 2;
     P.r_qk = r;
-    P.r_v = std::max(1, pd_cap(H, 1));
+    P.r_v = std::max(1, pd_cap(H, VTE_PD_UPT_QKV));
     P.r_o = std::max(1, std::min(pd_cap(qd, 1), (H + blocks - 1) / blocks));
     // gate/up: about one tile per block, none on the last n_q blocks (they run
     // the attention combine, so their o-proj is the stage's critical path)

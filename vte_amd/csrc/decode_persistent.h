@@ -9,6 +9,7 @@
 
 #define VTE_DECODE_MAX_SPLITS 128  // attention splits per KV head
 #define VTE_PD_UPT_GU 8            // weight units per thread of a gate/up tile
+#define VTE_PD_UPT_QKV 2           // weight units per thread of a q/k/v tile
 
 typedef vte_decode_layer VtePdLayer;
 

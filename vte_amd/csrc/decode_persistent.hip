@@ -5,7 +5,8 @@
 // 256-thread block per CU.  Per layer the blocks pass through seven stages:
 //
 //   S1  RMSNorm + q/k/v mat-vec + bias + RoPE + K/V append     (row tiles)
-//   S2  split-KV attention partials over the cached rows        (KV head, split)
+//   S2  split-KV attention partials over the cached rows        (KV head, split;
+//       on the blocks after the S1 tiles)
 //   S3  log-sum-exp combine + the new token's own row           (query head)
 //   S4  o-proj mat-vec + residual                               (row tiles)
 //   S5  RMSNorm + gate/up mat-vec + SwiGLU                      (row-pair tiles)
@@ -56,7 +57,7 @@ namespace {
 constexpr int PD_MS = VTE_DECODE_MAX_SPLITS;  // attention splits per KV head
 constexpr int PD_PW = ATT_D + 2;              // words of one (head, split) record: m, l, o[128]
 constexpr int PD_T = ROWS_THREADS;            // threads per block
-constexpr int UPT_QKV = 1, UPT_O = 1, UPT_GU = VTE_PD_UPT_GU, UPT_D = 4;  // weight units per thread of each stage
+constexpr int UPT_QKV = VTE_PD_UPT_QKV, UPT_O = 1, UPT_GU = VTE_PD_UPT_GU, UPT_D = 4;  // weight units per thread of each stage
 
 // ---------------------------------------------------------------- flagged words
 __device__ __forceinline__ uint64_t pd_now() { return __builtin_amdgcn_s_memrealtime(); }
@@ -436,6 +437,19 @@ struct PdAttLDS {
 };
 
 // S2: partials of split c (rows [c*split, min((c+1)*split, pos))) of KV head kvh.
+// One word of every 128-byte line of the wave's first K/V tile of split c of
+// KV head kvh (cached rows, written by earlier launches): requested while the
+// layer's first stage runs, so the split's tile loads hit the L2.
+__device__ __forceinline__ uint2 pd_attn_touch(const VtePdPlan& P, const VtePdLayer& Ly, int kvh, int c, int split,
+                                               int pos) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int t_begin = c * split, t_end = min(t_begin + split, pos);
+    const int tok = min(t_begin + wv * ATT_TILE + (lane >> 1), t_end - 1);  // 32 rows, two 128-byte lines each
+    const size_t off = ((size_t)tok * P.n_kv + kvh) * ATT_D + (size_t)(lane & 1) * 64;
+    return make_uint2(*reinterpret_cast<const uint32_t*>(reinterpret_cast<const __half*>(Ly.k_cache) + off),
+                      *reinterpret_cast<const uint32_t*>(reinterpret_cast<const __half*>(Ly.v_cache) + off));
+}
+
 __device__ __forceinline__ void pd_attn_item(const VtePdPlan& P, const VtePdLayer& Ly, int kvh, int c, int split, int pos,
                              uint32_t tag, uint32_t tag32, PdAttLDS& A, const PdClock& ck) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, col = lane & 15, grp = lane >> 4;
@@ -781,26 +795,30 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
         o.tag = tag;
 
         // ---- S1: norm + q/k/v + bias + RoPE + K/V append ----
-        {
-            PdStage S;
-            S.K = H;
-            S.nseg = 3;
-            S.seg[0] = pd_seg((const uint8_t*)Ly.wq, nullptr, Ly.q_bias, Ly.fmt_q, qd, P.r_qk, FMV_ROPE_Q, H);
-            S.seg[1] = pd_seg((const uint8_t*)Ly.wk, nullptr, Ly.k_bias, Ly.fmt_k, kvd, P.r_qk, FMV_ROPE_KCACHE, H);
-            S.seg[2] = pd_seg((const uint8_t*)Ly.wv, nullptr, Ly.v_bias, Ly.fmt_v, kvd, P.r_v, FMV_VCACHE, H);
-            S.total = S.seg[0].tiles + S.seg[1].tiles + S.seg[2].tiles;
-            o.ll = P.ll_q;
-            pd_mv<UPT_QKV, RO_H, false>(S, hin, !first, ptag, (const __half*)Ly.attn_norm, P.eps, lds, red, o,
-                                         ck);
-        }
+        PdStage S1;
+        S1.K = H;
+        S1.nseg = 3;
+        S1.seg[0] = pd_seg((const uint8_t*)Ly.wq, nullptr, Ly.q_bias, Ly.fmt_q, qd, P.r_qk, FMV_ROPE_Q, H);
+        S1.seg[1] = pd_seg((const uint8_t*)Ly.wk, nullptr, Ly.k_bias, Ly.fmt_k, kvd, P.r_qk, FMV_ROPE_KCACHE, H);
+        S1.seg[2] = pd_seg((const uint8_t*)Ly.wv, nullptr, Ly.v_bias, Ly.fmt_v, kvd, P.r_v, FMV_VCACHE, H);
+        S1.total = S1.seg[0].tiles + S1.seg[1].tiles + S1.seg[2].tiles;
+        // attention items run on the blocks after the S1 tiles (item it on block
+        // (S1.total + it) mod G), which request their first split's cached K/V
+        // rows toward the L2 now, while the q/k/v stage runs elsewhere
+        const int n_items = P.n_kv * ns, it0 = (b - S1.total % G + G) % G;
+        const uint2 katt = it0 < n_items && b >= S1.total ? pd_attn_touch(P, Ly, it0 / ns, it0 % ns, split, pos)
+                                                          : make_uint2(0u, 0u);
+        o.ll = P.ll_q;
+        pd_mv<UPT_QKV, RO_H, false>(S1, hin, !first, ptag, (const __half*)Ly.attn_norm, P.eps, lds, red, o, ck);
         PdStage So;
         So.K = qd;
         So.nseg = 1;
         So.seg[0] = pd_seg((const uint8_t*)Ly.wo, nullptr, nullptr, Ly.fmt_o, H, P.r_o, FMV_STORE_F16, qd);
         So.total = So.seg[0].tiles;
 
-        // ---- S2: split-KV partials (blocks 0 .. n_kv*ns-1) ----
-        for (int it = b; it < P.n_kv * ns; it += G) pd_attn_item(P, Ly, it / ns, it % ns, split, pos, tag, tag32, A, ck);
+        // ---- S2: split-KV partials ----
+        asm volatile("" ::"v"(katt.x), "v"(katt.y));
+        for (int it = it0; it < n_items; it += G) pd_attn_item(P, Ly, it / ns, it % ns, split, pos, tag, tag32, A, ck);
         // ---- S3: combine per query head (the last n_q blocks) ----
         for (int qh = G - 1 - b; qh >= 0 && qh < P.n_q; qh += G) pd_attn_combine(P, qh, ns, tag, tag32, A, ck);
         PdStage S5;
