@@ -183,3 +183,18 @@ def test_tiny_persistent_long_context(hip):
         ex.close()
     ref = ost.decode_step(tiny, np.array([123]), np.array([pos]), ks, vs, {})
     assert rel_l2(got, ref[0]) <= TOL
+
+
+def test_persistent_more_than_32_layers(hip):
+    """33 layers: the tags of consecutive layers of successive launches stay
+    distinct (tag = epoch * n_layers + layer), three steps in a row against
+    the graph path."""
+    model = SyntheticQwen2(TINY.with_(n_layers=33), seed=5)
+    got = {}
+    for persistent in (True, False):
+        out, _, _ = _run(hip, model, [5, 9, 13], [60, 61, 62], persistent, seed=6)
+        got[persistent] = out
+    # 33 layers of fp16 hand-offs on two summation orders drift ~1e-2 apart; a
+    # stale word taken for a current one would give O(1) differences
+    errs = [rel_l2(a, b) for a, b in zip(got[True], got[False])]
+    assert max(errs) <= 3e-2, errs

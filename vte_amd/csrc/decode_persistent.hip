@@ -27,9 +27,11 @@
 // depend on the activations), so the weight stream overlaps the handoff.
 //
 // Tags: a device-resident epoch, incremented by the last block to finish,
-// makes tag = (epoch << 5 | layer) unique per launch and layer, so the
-// flagged buffers are reused across layers and launches without clearing.
-// A word of a previous layer or launch never carries the current tag.
+// makes tag = epoch * n_layers + layer consecutive over the layers of
+// successive launches, so the flagged buffers are reused across layers and
+// launches without clearing: a word not yet written in this layer still
+// holds the previous layer's tag, one less than the current one (also in the
+// 16 bits of the fp16 words' tags).
 // Reuse is safe because between a buffer's readers and its next writer there
 // is always a stage that waits on all of its predecessor's output (S6a reads
 // one slice, but S7 waits on every S6a tile and S1 on every S7 row), so by
@@ -780,8 +782,8 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
     const __half* sinp = P.rope_sin + (size_t)pos * ATT_D;
     for (int l = 0; l < P.n_layers; ++l) {
         const VtePdLayer& Ly = P.layers[l];
-        const uint32_t tag32 = (epoch << 5) | (uint32_t)l, tag = tag32 & 0xFFFFu;
-        const uint32_t ptag = ((epoch << 5) | (uint32_t)(l - 1)) & 0xFFFFu;  // the previous layer's
+        const uint32_t tag32 = epoch * (uint32_t)P.n_layers + (uint32_t)l, tag = tag32 & 0xFFFFu;
+        const uint32_t ptag = (tag32 - 1u) & 0xFFFFu;  // the previous layer's
         const bool first = l == 0;
         const void* hin = first ? (const void*)P.x : (const void*)P.ll_h;
         PdOut o{};
