@@ -67,7 +67,7 @@ class HIPGraphExecutor:
         column's logits (the prefill of ``PrefillRunner``).  ``persistent``
         (batch 1 with the fused kernels and supported formats; default on,
         VTE_PERSISTENT=0 turns it off): every layer runs as one persistent
-        launch instead of five launches per layer (0.80 against 0.89 ms per
+        launch instead of five launches per layer (0.75 against 0.88 ms per
         step on MI355X); results read back raise if a block of that launch
         waited past its deadline (blocks not all resident)."""
         if persistent is None:
