@@ -543,58 +543,62 @@ __device__ __forceinline__ void pd_attn_item(const VtePdPlan& P, const VtePdLaye
 
 // S3: attention output of query head qh = LSE combine of its ns split records
 // and the new token's row (score q . k_new, value v_new), -> flagged fp16.
-__device__ __forceinline__ void pd_attn_combine(const VtePdPlan& P, int qh, int ns, uint32_t tag, uint32_t tag32, PdAttLDS& A,
-                                const PdClock& ck) {
+// The block takes dims part * 128/np .. of the head (np blocks per head for
+// long caches): threads (dim, group g) sum the splits g, g + TPD, ... and
+// the groups' sums are added in group order.
+__device__ __forceinline__ void pd_attn_combine(const VtePdPlan& P, int qh, int part, int np, int ns, uint32_t tag,
+                                                uint32_t tag32, PdAttLDS& A, const PdClock& ck) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int G = P.n_q / P.n_kv, kvh = qh / G, kv_dim = P.n_kv * ATT_D;
     const uint64_t* recs = P.part + (size_t)qh * PD_MS * PD_PW;
-    const int d = tid & 127, hf = tid >> 7;
-    // every word this thread needs is requested before any is waited for: the
-    // first 16 splits' o[d] (threads (d, half) take every other split), the
-    // split's (m, l), and q[d], k_new[d] (waves 2-3) or v_new[d] (waves 0-1)
+    const int DQ = ATT_D / np, TPD = PD_T / DQ;
+    const int dd = tid % DQ, g = tid / DQ, d = part * DQ + dd;
+    // every word this thread needs is requested before any is waited for: o[d]
+    // of its first 8 splits, the split's (m, l), q and k_new (waves 2-3), v_new
     uint64_t ow[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int c = hf + 2 * j;
-        ow[j] = c < ns ? ld_c64(recs + (size_t)c * PD_PW + 2 + d) : 0ull;
+        const int c = g + TPD * j;
+        ow[j] = c < ns ? ld_c64(recs + (size_t)c * PD_PW + 2 + d) : ((uint64_t)tag32 << 32);
     }
-    uint64_t wm = 0ull, wl = 0ull;
+    uint64_t wm = (uint64_t)tag32 << 32, wl = (uint64_t)tag32 << 32;
     if (tid < ns) {
         wm = ld_c64(recs + (size_t)tid * PD_PW);
         wl = ld_c64(recs + (size_t)tid * PD_PW + 1);
     }
-    const uint32_t* pa = tid >= 128 ? P.ll_q + (size_t)qh * ATT_D + d : P.ll_kv + kv_dim + (size_t)kvh * ATT_D + d;
-    const uint32_t* pb = P.ll_kv + (size_t)kvh * ATT_D + d;
-    uint32_t wa = ld_c32(pa), wb = tid >= 128 ? ld_c32(pb) : (tag << 16);
+    const int dq = tid & 127;
+    const uint32_t* pq = P.ll_q + (size_t)qh * ATT_D + dq;
+    const uint32_t* pk = P.ll_kv + (size_t)kvh * ATT_D + dq;
+    const uint32_t* pv = P.ll_kv + kv_dim + (size_t)kvh * ATT_D + d;
+    uint32_t wq = tid >= 128 ? ld_c32(pq) : (tag << 16), wk = tid >= 128 ? ld_c32(pk) : (tag << 16);
+    uint32_t wvn = tid < DQ ? ld_c32(pv) : (tag << 16);
     {  // one poll loop over all of them: a single round trip once the last record lands
         int spins = 0;
         while (true) {
-            bool ok = (wa >> 16) == tag && (wb >> 16) == tag;
-            if (tid < ns) ok = ok && (uint32_t)(wm >> 32) == tag32 && (uint32_t)(wl >> 32) == tag32;
+            bool ok = (wq >> 16) == tag && (wk >> 16) == tag && (wvn >> 16) == tag &&
+                      (uint32_t)(wm >> 32) == tag32 && (uint32_t)(wl >> 32) == tag32;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ok = ok && (hf + 2 * j >= ns || (uint32_t)(ow[j] >> 32) == tag32);
+            for (int j = 0; j < 8; ++j) ok = ok && (uint32_t)(ow[j] >> 32) == tag32;
             if (ok || pd_expired(ck, spins)) break;
-            if (tid < ns && (uint32_t)(wm >> 32) != tag32) wm = ld_c64(recs + (size_t)tid * PD_PW);
-            if (tid < ns && (uint32_t)(wl >> 32) != tag32) wl = ld_c64(recs + (size_t)tid * PD_PW + 1);
-            if ((wa >> 16) != tag) wa = ld_c32(pa);
-            if ((wb >> 16) != tag) wb = ld_c32(pb);
+            if ((uint32_t)(wm >> 32) != tag32) wm = ld_c64(recs + (size_t)tid * PD_PW);
+            if ((uint32_t)(wl >> 32) != tag32) wl = ld_c64(recs + (size_t)tid * PD_PW + 1);
+            if ((wq >> 16) != tag) wq = ld_c32(pq);
+            if ((wk >> 16) != tag) wk = ld_c32(pk);
+            if ((wvn >> 16) != tag) wvn = ld_c32(pv);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                if (hf + 2 * j < ns && (uint32_t)(ow[j] >> 32) != tag32)
-                    ow[j] = ld_c64(recs + (size_t)(hf + 2 * j) * PD_PW + 2 + d);
+                if ((uint32_t)(ow[j] >> 32) != tag32) ow[j] = ld_c64(recs + (size_t)(g + TPD * j) * PD_PW + 2 + d);
         }
     }
     if (tid < ns) {
         A.u.c.wm[tid] = __uint_as_float((uint32_t)wm);
         A.u.c.wl[tid] = __uint_as_float((uint32_t)wl);
     }
-    float vnew = 0.f;
     if (tid >= 128) {  // waves 2-3: q . k_new
-        const float s = wave_sum(h2f_bits(wa & 0xFFFFu) * h2f_bits(wb & 0xFFFFu));
+        const float s = wave_sum(h2f_bits(wq & 0xFFFFu) * h2f_bits(wk & 0xFFFFu));
         if (lane == 0) A.sc[wv - 2] = s;
-    } else {
-        vnew = h2f_bits(wa & 0xFFFFu);
     }
+    const float vnew = h2f_bits(wvn & 0xFFFFu);
     __syncthreads();
     if (wv == 0) {  // maximum, split weights exp(m_c - M) and the denominator
         const float snew = (A.sc[0] + A.sc[1]) * P.scale;
@@ -615,28 +619,43 @@ __device__ __forceinline__ void pd_attn_combine(const VtePdPlan& P, int qh, int 
         }
     }
     __syncthreads();
-    // O[d] = sum_c w_c o_c[d] + e_new v_new[d]: threads (d, half) take every other split
+    // O[d] = sum_c w_c o_c[d] + e_new v_new[d]
     float O = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int c = hf + 2 * j;
+        const int c = g + TPD * j;
         if (c < ns) O = fmaf(__uint_as_float((uint32_t)ow[j]), A.u.c.wm[c], O);
     }
-    int c = hf + 16;
-    for (; c + 14 < ns; c += 16) {
-        float v[8];
+    // further splits (long caches) in batches of 16 per thread: all 16 words
+    // requested at once and re-polled together, one round trip per batch
+    for (int c = g + 8 * TPD; c < ns; c += 16 * TPD) {
+        uint64_t w[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = pd_wait32(recs + (size_t)(c + 2 * j) * PD_PW + 2 + d, tag32, ck);
+        for (int j = 0; j < 16; ++j) {
+            const int cj = c + TPD * j;
+            w[j] = cj < ns ? ld_c64(recs + (size_t)cj * PD_PW + 2 + d) : ((uint64_t)tag32 << 32);
+        }
+        int spins = 0;
+        while (true) {
+            bool ok = true;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) O = fmaf(v[j], A.u.c.wm[c + 2 * j], O);
+            for (int j = 0; j < 16; ++j) ok = ok && (uint32_t)(w[j] >> 32) == tag32;
+            if (ok || pd_expired(ck, spins)) break;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if ((uint32_t)(w[j] >> 32) != tag32) w[j] = ld_c64(recs + (size_t)(c + TPD * j) * PD_PW + 2 + d);
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (c + TPD * j < ns) O = fmaf(__uint_as_float((uint32_t)w[j]), A.u.c.wm[c + TPD * j], O);
     }
-    for (; c < ns; c += 2) O = fmaf(pd_wait32(recs + (size_t)c * PD_PW + 2 + d, tag32, ck), A.u.c.wm[c], O);
-    if (hf) A.u.c.oh[d] = O;
+    A.u.c.oh[tid] = O;
     __syncthreads();
-    if (!hf) {
-        O = O + A.u.c.oh[d];
-        O = fmaf(A.sc[2], vnew, O);
-        st_c32(P.ll_att + (size_t)qh * ATT_D + d, ll16(f16_bits(O / fmaxf(A.sc[3], 1e-20f)), tag));
+    if (tid < DQ) {
+        float S = 0.f;
+        for (int k = 0; k < TPD; ++k) S += A.u.c.oh[k * DQ + tid];
+        S = fmaf(A.sc[2], vnew, S);
+        st_c32(P.ll_att + (size_t)qh * ATT_D + d, ll16(f16_bits(S / fmaxf(A.sc[3], 1e-20f)), tag));
     }
     __syncthreads();
 }
@@ -778,6 +797,7 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
     // attention geometry: ns splits of the pos cached rows, at most PD_MS per KV head
     const int split = max(P.split_min, ((pos + PD_MS - 1) / PD_MS + ATT_TILE - 1) / ATT_TILE * ATT_TILE);
     const int ns = (pos + split - 1) / split;
+    const int np3 = ns > 16 ? 4 : 1;  // combine blocks per query head
     const __half* cosp = P.rope_cos + (size_t)pos * ATT_D;
     const __half* sinp = P.rope_sin + (size_t)pos * ATT_D;
     for (int l = 0; l < P.n_layers; ++l) {
@@ -821,8 +841,10 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
         // ---- S2: split-KV partials ----
         asm volatile("" ::"v"(katt.x), "v"(katt.y));
         for (int it = it0; it < n_items; it += G) pd_attn_item(P, Ly, it / ns, it % ns, split, pos, tag, tag32, A, ck);
-        // ---- S3: combine per query head (the last n_q blocks) ----
-        for (int qh = G - 1 - b; qh >= 0 && qh < P.n_q; qh += G) pd_attn_combine(P, qh, ns, tag, tag32, A, ck);
+        // ---- S3: combine per query head (the last n_q * np3 blocks) ----
+        // (np3 blocks per head when the splits are many: fewer rounds per thread)
+        for (int i = G - 1 - b; i >= 0 && i < P.n_q * np3; i += G)
+            pd_attn_combine(P, i / np3, i % np3, np3, ns, tag, tag32, A, ck);
         PdStage S5;
         S5.K = H;
         S5.nseg = 1;
@@ -842,7 +864,7 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
             PdTouch tw;
 #pragma unroll
             for (int i = 0; i < 7; ++i) tw.v[i] = 0u;
-            if (G - 1 - b >= P.n_q) {
+            if (G - 1 - b >= P.n_q * np3) {
                 pd_touch_gu(S5, tw);
                 pd_touch_down(P, Ly, tw);
             }
