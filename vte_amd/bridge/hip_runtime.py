@@ -87,6 +87,7 @@ class HIPRuntime:
         self._device_index = 0
         self._stream = ctypes.c_void_p(0)
         self._modules: list[ctypes.c_void_p] = []
+        self._host_allocations: set[int] = set()  # pinned host buffers (hipHostMalloc)
         self._map_hip_functions()
 
     # ------------------------------------------------------------------ setup
@@ -126,6 +127,8 @@ class HIPRuntime:
             "hipEventElapsedTime": ([ctypes.POINTER(ctypes.c_float), vp, vp], i),
             "hipEventDestroy": ([vp], i),
             "hipGetErrorString": ([i], ctypes.c_char_p),
+            "hipHostMalloc": ([ctypes.POINTER(vp), sz, ctypes.c_uint], i),
+            "hipHostFree": ([vp], i),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -257,6 +260,35 @@ class HIPRuntime:
                                               hipMemcpyDeviceToHost), "hipMemcpy (D2H)")
         return True
 
+    def host_alloc(self, nbytes: int) -> int:
+        """Pinned host memory (hipHostMalloc), freed by host_free or cleanup."""
+        self._require_init()
+        p = ctypes.c_void_p(0)
+        self._check_error(self._lib.hipHostMalloc(ctypes.byref(p), max(1, nbytes), 0), "hipHostMalloc")
+        self._host_allocations.add(p.value)
+        return p.value
+
+    def host_free(self, ptr: int) -> None:
+        if ptr in self._host_allocations:
+            self._host_allocations.discard(ptr)
+            self._lib.hipHostFree(ctypes.c_void_p(ptr))
+
+    def memcpy_async_h2d(self, dst, src_host: int, nbytes: int, tag: str = "unnamed") -> None:
+        """Stream-ordered copy from pinned host memory (capturable as a graph node)."""
+        d = self._addr(dst)
+        self._owning_allocation(d, nbytes, "memcpy_h2d_async", tag)
+        self._check_error(self._lib.hipMemcpyAsync(ctypes.c_void_p(d), ctypes.c_void_p(src_host), nbytes,
+                                                   hipMemcpyHostToDevice, self._stream), "hipMemcpyAsync (H2D)")
+
+    def memcpy_async_d2h(self, dst_host: int, src, nbytes: int, tag: str = "unnamed") -> None:
+        """Stream-ordered copy into pinned host memory (capturable), allow-listed by tag."""
+        if self._prevent_host_copies and not any(t in tag.lower() for t in ("logits", "output", "sampler")):
+            raise HIPSafetyError(f"data isolation: device->host copy refused for tag '{tag}'")
+        s_ = self._addr(src)
+        self._owning_allocation(s_, nbytes, "memcpy_d2h_async", tag)
+        self._check_error(self._lib.hipMemcpyAsync(ctypes.c_void_p(dst_host), ctypes.c_void_p(s_), nbytes,
+                                                   hipMemcpyDeviceToHost, self._stream), "hipMemcpyAsync (D2H)")
+
     def memcpy_device_to_device(self, dst, src, nbytes: int) -> None:
         self._check_error(self._lib.hipMemcpyAsync(ctypes.c_void_p(self._addr(dst)), ctypes.c_void_p(self._addr(src)),
                                                    nbytes, hipMemcpyDeviceToDevice, self._stream), "hipMemcpyAsync")
@@ -365,6 +397,9 @@ class HIPRuntime:
                 size, _ = self._active_allocations.pop(base)
                 self._lib.hipFree(ctypes.c_void_p(base))
                 HIPRuntime._process_wide_allocated_bytes = max(0, HIPRuntime._process_wide_allocated_bytes - size)
+            for hp in list(self._host_allocations):
+                self._lib.hipHostFree(ctypes.c_void_p(hp))
+            self._host_allocations.clear()
             for m in self._modules:
                 self._lib.hipModuleUnload(m)
             self._modules.clear()

@@ -165,6 +165,22 @@ class HIPGraphExecutor:
         self.h_final = 0  # index of the hidden buffer holding the layer output
         if self.persistent:
             self._setup_persistent()
+        # pinned host staging and outputs of execute_decode_batch: tokens and
+        # offsets copied in, top-k candidates (and the persistent step's error
+        # flags) copied out by stream-ordered copies around the replay, so a
+        # step costs one synchronisation
+        self._pin, self._pin_fresh = None, False
+        if shared is None and self.top_k > 0:
+            k, R = self.top_k, self.out_rows
+            nbytes = 4 * (2 * B + 2 * R * k + 1)
+            self._pin = hip.host_alloc(nbytes)
+            buf = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(self._pin))
+            cut = np.cumsum([0, 4 * B, 4 * B, 4 * R * k, 4 * R * k, 4])
+            self._pin_tok, self._pin_off = buf[cut[0]:cut[1]].view(np.int32), buf[cut[1]:cut[2]].view(np.int32)
+            self._pin_val = buf[cut[2]:cut[3]].view(np.float32).reshape(R, k)
+            self._pin_idx = buf[cut[3]:cut[4]].view(np.int32).reshape(R, k)
+            self._pin_flags = buf[cut[4]:cut[5]].view(np.int32)
+            self._pin_flags[0] = 0
 
     def _upload_weights(self, model, W, A) -> None:
         cfg, B = self.cfg, self.B
@@ -477,7 +493,7 @@ class HIPGraphExecutor:
         self.graph = self.hip.stream_end_capture()
         self.graph_exec = self.hip.graph_instantiate(self.graph)
 
-    def _update_staging_buffers(self, tokens: Sequence[int], kv_offsets: Sequence[int]) -> None:
+    def _checked_staging(self, tokens: Sequence[int], kv_offsets: Sequence[int]) -> tuple[np.ndarray, np.ndarray]:
         if len(tokens) != self.B or len(kv_offsets) != self.B:
             raise HIPSafetyError(f"expected {self.B} tokens and offsets, got {len(tokens)}/{len(kv_offsets)}")
         offs = np.asarray(kv_offsets, np.int32)
@@ -486,17 +502,39 @@ class HIPGraphExecutor:
         toks = np.asarray(tokens, np.int32)
         if toks.min() < 0 or toks.max() >= self.cfg.vocab:
             raise HIPSafetyError("token id outside the vocabulary")
+        return toks, offs
+
+    def _update_staging_buffers(self, tokens: Sequence[int], kv_offsets: Sequence[int]) -> None:
+        toks, offs = self._checked_staging(tokens, kv_offsets)
         self.staging_input.upload(toks)
         self.staging_kv_offset.upload(offs)
 
     def execute_decode_batch(self, tokens: Sequence[int], kv_offsets: Sequence[int], use_graph: bool = True,
                              sync: bool = True) -> None:
         """One token per sequence, sequence b at position kv_offsets[b]."""
-        self._update_staging_buffers(tokens, kv_offsets)
-        if use_graph:
+        if use_graph and self._pin is not None:
+            # stream-ordered copies through pinned memory around the replay: one
+            # synchronisation per step, none of them inside the graph itself
+            toks, offs = self._checked_staging(tokens, kv_offsets)
+            self.build_decode_graph()
+            self.hip.stream_synchronize()  # the previous step's copies have completed
+            self._pin_tok[:], self._pin_off[:] = toks, offs
+            h = self.hip
+            h.memcpy_async_h2d(self.staging_input.ptr, self._pin_tok.ctypes.data, 4 * self.B, "staging_tokens")
+            h.memcpy_async_h2d(self.staging_kv_offset.ptr, self._pin_off.ctypes.data, 4 * self.B, "staging_kv_offset")
+            h.graph_launch(self.graph_exec)
+            h.memcpy_async_d2h(self._pin_val.ctypes.data, self.topk_val.ptr, self._pin_val.nbytes, "sampler_topk_val")
+            h.memcpy_async_d2h(self._pin_idx.ctypes.data, self.topk_idx.ptr, self._pin_idx.nbytes, "sampler_topk_idx")
+            if self.persistent:  # the workspace's error-flag word (control words: epoch, done, flags)
+                h.memcpy_async_d2h(self._pin_flags.ctypes.data, self.pd_ws.ptr + 8, 4, "sampler_status")
+            self._pin_fresh = True
+        elif use_graph:
+            self._update_staging_buffers(tokens, kv_offsets)
             self.build_decode_graph()
             self.hip.graph_launch(self.graph_exec)
         else:
+            self._update_staging_buffers(tokens, kv_offsets)
+            self._pin_fresh = False
             self.enqueue_step()
         if sync:
             self.hip.synchronize()
@@ -532,6 +570,7 @@ class HIPGraphExecutor:
             self._greedy = (g, self.hip.graph_instantiate(g), cap, hist, step)
         g, gexec, cap, hist, step = self._greedy
         self._update_staging_buffers(tokens, kv_offsets)
+        self._pin_fresh = False
         step.zero()
         for _ in range(n_steps):
             self.hip.graph_launch(gexec)
@@ -560,11 +599,12 @@ class HIPGraphExecutor:
         self.build_decode_graph()
         for _ in range(n):
             self.hip.graph_launch(self.graph_exec)
+        self._pin_fresh = False
 
     # ------------------------------------------------------------------ outputs
     def _check_persistent(self) -> None:
         if self.persistent:
-            flags = self.K.decode_status(self.pd_ws)
+            flags = int(self._pin_flags[0]) if self._pin_fresh else self.K.decode_status(self.pd_ws)
             if flags:
                 raise HIPRuntimeError(f"persistent decode step: error flags {flags:#x} (a block waited past its "
                                       "deadline: were all of its blocks resident?); results are invalid. "
@@ -580,6 +620,8 @@ class HIPGraphExecutor:
     def read_topk(self) -> tuple[np.ndarray, np.ndarray]:
         self.hip.synchronize()
         self._check_persistent()
+        if self._pin_fresh:  # copied out behind the last execute_decode_batch
+            return self._pin_val.copy(), self._pin_idx.copy()
         v = np.empty((self.out_rows, self.top_k), np.float32)
         i = np.empty((self.out_rows, self.top_k), np.int32)
         self.hip.safe_memcpy_device_to_host(v, ctypes.c_void_p(self.topk_val.ptr), "sampler_topk_val")
@@ -621,4 +663,8 @@ class HIPGraphExecutor:
             self.hip.graph_exec_destroy(self.graph_exec)
             self.hip.graph_destroy(self.graph)
             self.graph_exec = self.graph = None
+        if getattr(self, "_pin", None) is not None:
+            self.hip.stream_synchronize()
+            self.hip.host_free(self._pin)
+            self._pin, self._pin_fresh = None, False
         self.slab.cleanup()
