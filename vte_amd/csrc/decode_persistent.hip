@@ -48,7 +48,6 @@
 // down projection sums per 256-column slice first and the attention splits
 // differ (the new token is folded in by the combine): both agree to fp32
 // rounding.
-#include <cstdio>
 
 #include "fused_kernels.h"
 #include "attn_tile.h"
