@@ -455,3 +455,36 @@ def test_generate_greedy_matches_host_loop(hip, tiny_model, B):
         assert np.array_equal(ex.generate_greedy(toks0, pos0, n // 2), np.stack(host)[:n // 2])
     finally:
         ex.close()
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_topk_readback_follows_the_last_launch(hip, tiny_model, B):
+    """read_topk returns the candidates of whatever ran last: the pinned copies
+    behind execute_decode_batch (also with sync=False), and the device buffers
+    after generate_greedy or replay; each equals the top-k of the logits."""
+    ex = HIPGraphExecutor(hip, tiny_model, batch_size=B, max_seq=256, top_k=40)
+
+    def check():
+        logits = ex.read_logits()
+        v, i = ex.read_topk()
+        for b in range(B):
+            assert i[b, 0] == int(np.argmax(logits[b]))
+            assert np.array_equal(v[b], logits[b][i[b]])
+            assert np.allclose(np.sort(v[b])[::-1], np.sort(logits[b])[::-1][:40])
+        return i.copy()
+
+    try:
+        ex.fill_kv_prefix(seed=3)
+        toks, pos = [4 + b for b in range(B)], [30 + b for b in range(B)]
+        ex.execute_decode_batch(toks, pos)
+        first = check()
+        ex.execute_decode_batch([9] * B, [31 + b for b in range(B)], sync=False)
+        second = check()
+        assert not np.array_equal(first, second)
+        ex.generate_greedy(toks, pos, 3)
+        check()
+        ex._update_staging_buffers(toks, pos)
+        ex.replay(1)
+        assert np.array_equal(check(), first)
+    finally:
+        ex.close()
