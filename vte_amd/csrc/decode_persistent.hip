@@ -796,7 +796,8 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
     // attention geometry: ns splits of the pos cached rows, at most PD_MS per KV head
     const int split = max(P.split_min, ((pos + PD_MS - 1) / PD_MS + ATT_TILE - 1) / ATT_TILE * ATT_TILE);
     const int ns = (pos + split - 1) / split;
-    const int np3 = ns > 16 ? 4 : 1;  // combine blocks per query head
+    // combine blocks per query head: enough that a thread's first 8 records cover every split
+    const int np3 = ns <= 16 ? 1 : ns <= 32 ? 2 : ns <= 64 ? 4 : 8;
     const __half* cosp = P.rope_cos + (size_t)pos * ATT_D;
     const __half* sinp = P.rope_sin + (size_t)pos * ATT_D;
     for (int l = 0; l < P.n_layers; ++l) {
