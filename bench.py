@@ -249,7 +249,7 @@ def attn_bench(hip, K, ctx, split=None, B=1, fused=False, launches=40):
     po = DeviceArray(hip, B * n_q * ms_ * (2 * (D + 2) if fused else D), np.float32, "po")
     po.zero()
     out = DeviceArray(hip, B * n_q * D, np.float16, "out")
-    ctr = DeviceArray(hip, B * n_kv, np.int32, "ctr")
+    ctr = DeviceArray(hip, 1 + B * n_kv, np.int32, "ctr")
     ctr.zero()
     hip.synchronize()
     hip.stream_begin_capture()
@@ -306,47 +306,47 @@ def _stats(ts):
 
 def cpu_baseline(trials=5):
     """The NumPy oracle (the reference's CPU arithmetic restated, oracle/) on the
-    host cores, bounded samples of the same workloads, >= 5 trials each:
+    host cores, bounded samples of the same workloads, >= 3 trials each:
 
-    * decode step: 2 of the 28 layers (one Q6_K-down, one Q4_K-down) and the LM
-      head at position 2048, dequantised weights cached outside the timed region
-      (vte/compiler/dequantizer.py), per-layer time x 28 + LM head -> tok/s at
-      batch 1 (``value``) and 16;
+    * decode step: the full 28-layer 1.5B-shaped forward at position 2048,
+      fp32 GEMVs, float32 GQA attention (math_refs.py:30-62), the LM head and
+      a top-40 selection per row, with the dequantised weights of every layer
+      cached once outside the timed region (vte/compiler/dequantizer.py) ->
+      tok/s at batch 1 (``value``, 5 trials) and 16 (3 trials);
     * quant GEMV configs 0/1: dequantisation and the fp32 mat-vec timed
       separately (the pattern of tools/validate_gemv_q6k_header_fix.py:63-64);
-    * split-KV attention config 2: textbook softmax(q K^T / sqrt(128)) V per head.
+    * split-KV attention configs 2 and 3b: float32 softmax(q K^T / sqrt(128)) V
+      per KV head group.
     """
     from oracle import dequant as odq
     from oracle import step as ost
-    from oracle.attention import attention_ref
+    from oracle.attention import attention_gqa_f32
     from vte_amd import synthetic as syn
     from vte_amd.core.model_config import QWEN25_1P5B
     from vte_amd.core.weights import SyntheticQwen2
     info = _host_info()
     t_start = time.perf_counter()
-    cfg = QWEN25_1P5B.with_(n_layers=2, max_seq=2304)
+    cfg = QWEN25_1P5B.with_(max_seq=2304)
     model = SyntheticQwen2(cfg, seed=0)
     rng = np.random.default_rng(0)
     out = {}
-    for B in (1, 16):
-        ks = [(0.5 * rng.standard_normal((B, 2304, 2, 128))).astype(np.float16) for _ in range(2)]
-        vs = [(0.5 * rng.standard_normal((B, 2304, 2, 128))).astype(np.float16) for _ in range(2)]
+    cache = {}
+    # one random KV prefix shared by every layer (the timing does not depend on its values)
+    k16 = (0.5 * rng.standard_normal((16, 2304, 2, 128), np.float32)).astype(np.float16)
+    v16 = (0.5 * rng.standard_normal((16, 2304, 2, 128), np.float32)).astype(np.float16)
+    for B, nt in ((1, trials), (16, max(3, trials - 2))):
+        ks, vs = [k16[:B]] * cfg.n_layers, [v16[:B]] * cfg.n_layers
         toks, pos = list(range(1, B + 1)), [2048] * B
-        cache = {}
-        ost.decode_step(model, toks, pos, ks, vs, cache)  # warm: dequantise once
-        steps, lms = [], []
-        hn = np.ones((B, cfg.hidden), np.float32)
-        for _ in range(trials):
+        # untimed: dequantises every layer and the LM head once (cached), and warms the pages
+        ost.decode_step(model, toks, pos, ks, vs, cache, attn="f32")
+        steps = []
+        for _ in range(nt):
             s = time.perf_counter()
-            ost.decode_step(model, toks, pos, ks, vs, cache)
+            logits = ost.decode_step(model, toks, pos, ks, vs, cache, attn="f32")
+            np.argpartition(logits, -40, axis=1)[:, -40:]
             steps.append(time.perf_counter() - s)
-            s = time.perf_counter()
-            hn @ cache["lm"].T
-            lms.append(time.perf_counter() - s)
-        lm = float(np.median(lms))
-        per_step = [lm + (t - lm) / 2 * 28 for t in steps]  # 2 layers -> 28
-        out[B] = {"tok_s": _stats([B / t for t in per_step]), "step_s": _stats(per_step)}
-        del cache
+        out[B] = {"tok_s": _stats([B / t for t in steps]), "step_s": _stats(steps)}
+    del cache, k16, v16
     gemv = []
     for fmt, n, k, _ in GEMV_CONFIGS[:4]:
         raw = syn.random_matrix(fmt, np.random.default_rng(42), n, k)
@@ -374,13 +374,26 @@ def cpu_baseline(trials=5):
         ts = []
         for _ in range(trials):
             s = time.perf_counter()
-            attention_ref(q, kc, vc, ctx, 1 / np.sqrt(128))
+            attention_gqa_f32(q, kc, vc, ctx, 1 / np.sqrt(128))
             ts.append(time.perf_counter() - s)
         attn.append({"ctx": ctx, "ms": _stats([1e3 * t for t in ts])})
+    # config 3b: 16 sequences of U[128, 8192] cached rows
+    lens = np.random.default_rng(16).integers(128, 8193, 16)
+    qs = rng.standard_normal((16, 12, 128)).astype(np.float32)
+    kcs = [(0.5 * rng.standard_normal((n, 2, 128))).astype(np.float16) for n in lens]
+    vcs = [(0.5 * rng.standard_normal((n, 2, 128))).astype(np.float16) for n in lens]
+    ts = []
+    for _ in range(trials):
+        s = time.perf_counter()
+        for b in range(16):
+            attention_gqa_f32(qs[b], kcs[b], vcs[b], int(lens[b]), 1 / np.sqrt(128))
+        ts.append(time.perf_counter() - s)
+    attn.append({"ctx": "ragged B16 U[128,8192]", "rows": int(lens.sum()), "ms": _stats([1e3 * t for t in ts])})
     return {"value": out[1]["tok_s"]["median"], "unit": "tok/s", "cores": info["blas_threads"], "kind": "port",
-            "sample": "NumPy oracle (oracle/) on the host: decode step = 2 of 28 layers + LM head at position "
-                      f"2048, dequant cached, x28; {trials} trials each (median); GEMV configs 0/1 dequant and "
-                      "mat-vec separately; attention config 2",
+            "sample": "NumPy oracle (oracle/) on the host: decode step = 28 of 28 layers (fp32 GEMVs, float32 "
+                      "GQA attention) + LM head + top-40 at position 2048, dequant cached; batch 1 "
+                      f"{trials} trials, batch 16 {max(3, trials - 2)} (median); GEMV configs 0/1 dequant and "
+                      "mat-vec separately; attention configs 2 and 3b (float32)",
             "tok_s_b1": out[1]["tok_s"], "tok_s_b16": out[16]["tok_s"], "gemv": gemv, "attention": attn,
             "host": info, "wall_s": round(time.perf_counter() - t_start, 1)}
 

@@ -23,7 +23,8 @@
  * gemv_q6k_kernel, gemv_q8_0_kernel, kv_cache_append_kernel,
  * flash_attention_split_kv_partial_kernel, flash_attention_split_kv_reduce_kernel,
  * rmsnorm_kernel, rope_kernel, swiglu_kernel, add_kernel,
- * embedding_lookup_q6k_kernel.
+ * embedding_lookup_q6k_kernel, embedding_lookup_q4k_kernel,
+ * embedding_lookup_q8_0_kernel.
  */
 #ifndef VTE_AMD_H
 #define VTE_AMD_H
@@ -98,8 +99,11 @@ long long vte_attn_scratch_floats(int batch, int n_q, int max_splits);
  * tokens per partial block (multiple of 32), max_splits >= ceil(max_seq/split)
  * (at most 4096).  part_m/part_l [B][n_q][max_splits], part_o
  * [B][n_q][max_splits][128] fp32 scratch.  counters: NULL = separate combine
- * launch; else B*n_kv ints, zeroed before the first call and then owned by the
- * kernel (per-group epochs), and the combine runs inside the partial kernel
+ * launch; else 1 + B*n_kv ints, zeroed before the first call and then owned
+ * by the kernel: counters[0] is a sticky error word (nonzero once a combining
+ * block gave up waiting on a split's records: that launch's outputs are
+ * invalid), counters[1 + b*n_kv + kvh] the per-group epochs; the combine
+ * then runs inside the partial kernel
  * (max_splits <= 512, split > 32): part_o then holds flagged records and must
  * hold B*n_q*max_splits*260 floats, zeroed before the first call.
  * out NULL (with counters NULL): only the partials are written, for
@@ -310,7 +314,9 @@ int vte_decode_step(const vte_decode_model* m, void* workspace, const int* kv_of
                     void* stream);
 
 /* Synchronous read of the workspace's error flags: bit 0 = a block waited
- * past its deadline (a step whose blocks could not all be resident). */
+ * past its deadline (a step whose blocks could not all be resident); bit 1 =
+ * kv_offset[0] was outside [0, max_seq) (the step wrote nothing, its logits
+ * are invalid). */
 int vte_decode_status(void* workspace, int* flags);
 
 #ifdef __cplusplus

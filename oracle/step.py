@@ -13,7 +13,7 @@ from __future__ import annotations
 import numpy as np
 
 from . import dequant as dq
-from .attention import attention_ref
+from .attention import attention_gqa_f32, attention_ref
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
@@ -110,7 +110,7 @@ def _lin(w, x, bias=None, residual=None, accum="f32"):
     return y.astype(np.float16)
 
 
-def decode_step(model, tokens, positions, k_cache, v_cache, cache=None, accum="f32"):
+def decode_step(model, tokens, positions, k_cache, v_cache, cache=None, accum="f32", attn="f64"):
     """One decode step for B sequences.
 
     ``model``: vte_amd.core.weights.SyntheticQwen2 (host copies of the weights).
@@ -123,6 +123,8 @@ def decode_step(model, tokens, positions, k_cache, v_cache, cache=None, accum="f
     -> o-proj + residual -> ffn_norm -> gate, up -> silu(gate) * up -> down +
     residual; then output_norm and the LM head (the tied embedding table unless
     the model has a separate output matrix).
+    ``attn``: "f64" (the checker's textbook attention) or "f32" (the
+    reference's NumPy GQA attention in float32, math_refs.py:30-62).
     """
     cfg = model.cfg
     H, hd, nq, nkv = cfg.hidden, cfg.head_dim, cfg.n_q, cfg.n_kv
@@ -143,8 +145,9 @@ def decode_step(model, tokens, positions, k_cache, v_cache, cache=None, accum="f
             qb = rope_neox(q[b].reshape(nq, hd), pos[b], cos_c, sin_c)
             k_cache[L][b, pos[b]] = rope_neox(k[b].reshape(nkv, hd), pos[b], cos_c, sin_c)
             v_cache[L][b, pos[b]] = v[b].reshape(nkv, hd)
-            att[b] = attention_ref(qb.astype(np.float32), k_cache[L][b], v_cache[L][b], pos[b] + 1,
-                                   scale).astype(np.float16).reshape(-1)
+            fa = attention_gqa_f32 if attn == "f32" else attention_ref
+            att[b] = fa(qb.astype(np.float32), k_cache[L][b], v_cache[L][b], pos[b] + 1,
+                        scale).astype(np.float16).reshape(-1)
         h = _lin(w["o"], att, residual=h, accum=accum)
         xn = rmsnorm(h, lw["ffn_norm"], cfg.eps)
         a = swiglu(_lin(w["gate"], xn, accum=accum), _lin(w["up"], xn, accum=accum))

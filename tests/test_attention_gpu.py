@@ -29,15 +29,17 @@ def _run(hip, K, q, kc, vc, offsets, split, dtype="f32", fused=False, repeat=1):
     else:
         part_o = empty(hip, (B, NQ, max_splits, D), np.float32)
     out = empty(hip, (B, NQ, D), np.float32 if dtype == "f32" else np.float16)
-    ctr = up(hip, np.zeros(B * NKV, np.int32)) if fused else None
+    ctr = up(hip, np.zeros(1 + B * NKV, np.int32)) if fused else None
     outs = []
     for _ in range(repeat):
         K.attn_split_kv(up(hip, q), up(hip, kc), up(hip, vc), part_m, part_l, part_o, out, B, NQ, NKV, D, SCALE,
                         up(hip, np.asarray(offsets, np.int32)), max_seq * NKV * D, split, max_splits, dtype=dtype,
                         counters=ctr, stream=hip.stream)
         outs.append(down(out))
-    if fused:  # each call advanced every group's epoch by one
-        assert np.array_equal(down(ctr), np.full(B * NKV, repeat, np.int32))
+    if fused:  # no wait gave up (word 0), and each call advanced every group's epoch by one
+        c = down(ctr)
+        assert c[0] == 0
+        assert np.array_equal(c[1:], np.full(B * NKV, repeat, np.int32))
     for o in outs[1:]:
         assert np.array_equal(o, outs[0])
     return outs[0]

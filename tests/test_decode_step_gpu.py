@@ -287,10 +287,18 @@ class _Truncated:
 # nodes.  Their distance is the drift between two correct implementations that
 # differ only in summation order (measured 4.1e-3 rel-L2 on the logits after 28
 # layers: fp16 rounding flips compound layer by layer), so no correct kernel
-# can be held much tighter than it.  The GPU must stay within FLOOR_FACTOR times
-# that drift (measured: 1.2x on the batch-1 mat-vec path, 1.4-1.8x on the
-# batched MFMA path and prefill, whose fp32 sums run in another order).
-FLOOR_FACTOR = 2.5
+# can be held much tighter than it.  The GPU must stay within a per-path factor
+# of that drift, set from the measured ratios with some headroom: the batch-1
+# paths (per-node fused mat-vecs and the persistent step) use the oracle's own
+# per-row fp32 sums in another order (measured 1.18-1.25x), the MFMA path and
+# prefill sum in MFMA tile order with exact-integer weight operands and fp32
+# super-block scales (measured 0.8-1.8x).
+FLOOR_B1 = 1.5
+FLOOR_MFMA = 2.0
+
+
+def _floor_factor(B: int) -> float:
+    return FLOOR_B1 if B < 3 else FLOOR_MFMA
 
 
 @pytest.mark.parametrize("n_layers,B,check,persistent", [(2, 1, (0,), False), (2, 1, (0,), True),
@@ -302,9 +310,9 @@ def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check, persiste
     mat-vec kernels per node, or the persistent step) and batch 16 (MFMA
     kernels), against oracle.decode_step on
     the same caches (weights dequantised per layer on the host, not cached):
-    logits within FLOOR_FACTOR x the fp32/f64 oracle drift, the top-40 sets
+    logits within the path's factor (FLOOR_B1 / FLOOR_MFMA) x the fp32/f64 oracle drift, the top-40 sets
     equal up to ties inside the measured error, and the appended K rows of the
-    first and last layer within FLOOR_FACTOR x their own drift (at least 1e-3)."""
+    first and last layer within that factor x their own drift (at least 1e-3)."""
     model = _Truncated(full_model, n_layers)
     cfg = model.cfg
     max_seq = 2304
@@ -332,14 +340,14 @@ def test_full_shape_step_vs_oracle(hip, full_model, n_layers, B, check, persiste
     for i, b in enumerate(check):
         r, floor = rel_l2(got[b], ref[i]), rel_l2(ref64[i], ref[i])
         print(f"  seq {b}: GPU vs oracle {r:.3e}, oracle f32 vs f64 drift {floor:.3e}", flush=True)
-        assert r <= FLOOR_FACTOR * floor, (b, r, floor)
+        assert r <= _floor_factor(B) * floor, (b, r, floor)
         err = 4 * float(np.abs(got[b] - ref[i]).max())
         assert _topk_agrees(got[b], ref[i], 40, err), b
         order = np.lexsort((np.arange(cfg.vocab), -got[b]))[:40]
         assert np.array_equal(idx[b], order)
         for j, L in enumerate((0, last)):        # appended K rows of the first and last layer
             r, floor = rel_l2(kg[j][i, 2048], ks[L][i, 2048]), rel_l2(k64[L][i, 2048], ks[L][i, 2048])
-            assert r <= max(FLOOR_FACTOR * floor, 1e-3), (b, L, r, floor)
+            assert r <= max(_floor_factor(B) * floor, 1e-3), (b, L, r, floor)
 
 
 # ---------------------------------------------------------------- prefill vs the oracle
@@ -349,7 +357,7 @@ def test_prefill_vs_oracle(hip, request, shape, n, chunk):
     """A prompt prefilled in chunks into sequence 1 of a 2-sequence executor
     against oracle.step.prefill (the token-by-token decode of the reference,
     vte/core/model.py:969-973, computed layer by layer) on the same cache: the
-    next-token logits and every layer's written K/V rows within FLOOR_FACTOR x
+    next-token logits and every layer's written K/V rows within FLOOR_MFMA x
     the oracle's fp32/f64 drift (at least 1e-3).
     Widths 33, 36 and 63 are tails that run padded at 64 columns; 600 tokens
     at chunk 512 run the default chunk (weight-stationary launches with
@@ -380,12 +388,12 @@ def test_prefill_vs_oracle(hip, request, shape, n, chunk):
     ref64 = ost.prefill(model, prompt, start, k64, v64, accum="f64")[-1]
     r, floor = rel_l2(got, ref), rel_l2(ref64, ref)
     print(f"  logits: GPU vs oracle {r:.3e}, oracle f32 vs f64 drift {floor:.3e}", flush=True)
-    assert r <= max(FLOOR_FACTOR * floor, 1e-3), (r, floor)
+    assert r <= max(FLOOR_MFMA * floor, 1e-3), (r, floor)
     rows = slice(start, start + n)
     for L in range(cfg.n_layers):
         for g_, o_, o64 in ((kg, kh, k64), (vg, vh, v64)):
             r, floor = rel_l2(g_[L][rows], o_[L][rows]), rel_l2(o64[L][rows], o_[L][rows])
-            assert r <= max(FLOOR_FACTOR * floor, 1e-3), (L, r, floor)
+            assert r <= max(FLOOR_MFMA * floor, 1e-3), (L, r, floor)
 
 
 def test_repetition_window_candidates_reproduce_full_row_sampling(hip, tiny_model):

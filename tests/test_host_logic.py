@@ -44,3 +44,21 @@ def test_choose_split(ctx, split):
     then the smallest power of two (up to 1024) that does."""
     from vte_amd.core.split_kv_attention import choose_split
     assert choose_split(ctx, 1, 2, 256) == split
+
+
+def _fmt_model(cfg):
+    fm = {p + "_fmt": "q4_k" for p in ("q", "k", "v", "o", "gate", "up", "down")}
+    return SimpleNamespace(cfg=cfg, layers=[fm] * cfg.n_layers, token_embd=object(), token_embd_fmt="q6_k")
+
+
+def test_persistent_support_follows_the_library_model_check():
+    """A model whose hidden size and q_dim fall on different unit mappings
+    (hidden 3584: flat, q_dim 2048: range-owned) is refused by the library's
+    own check, so the executor must pick the per-node graph instead of
+    raising at construction; the 1.5B shape is accepted."""
+    from vte_amd.core.hip_graph_executor import HIPGraphExecutor
+    from vte_amd.core.model_config import QWEN25_1P5B, TINY
+    assert HIPGraphExecutor._persistent_supported(_fmt_model(QWEN25_1P5B))
+    assert HIPGraphExecutor._persistent_supported(_fmt_model(TINY))
+    odd = QWEN25_1P5B.with_(n_layers=2, hidden=3584, n_q=16, n_kv=2, ffn=4096)
+    assert not HIPGraphExecutor._persistent_supported(_fmt_model(odd))

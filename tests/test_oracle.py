@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import dequant as dq
-from oracle.attention import attention_ref, split_kv_ref
+from oracle.attention import attention_gqa_f32, attention_ref, split_kv_ref
 from vte_amd import synthetic as syn
 
 
@@ -175,6 +175,13 @@ def test_attention_oracle_invariants():
         assert np.allclose(o2[h], v[:, h // 6].astype(np.float64).mean(0), atol=1e-12)
     # split-KV restatement agrees with the textbook form
     full = attention_ref(q, k, v, ctx, 1 / np.sqrt(d))
+    # the float32 GQA form (the CPU baseline's): same closed forms, and the
+    # head-to-KV-head mapping (a transposed grouping would pair q heads with
+    # the wrong V and miss by O(1))
+    assert np.array_equal(attention_gqa_f32(q, k, v, 1, 1 / np.sqrt(d)), o1.astype(np.float32))
+    assert np.allclose(attention_gqa_f32(q, kk, v, ctx, 1 / np.sqrt(d)), o2, atol=1e-5)
+    g32 = attention_gqa_f32(q, k, v, ctx, 1 / np.sqrt(d))
+    assert np.linalg.norm(g32 - full) / np.linalg.norm(full) < 1e-6
     for chunk in (32, 64, 300):
         sp = split_kv_ref(q, k, v, ctx, 1 / np.sqrt(d), chunk)
         assert np.linalg.norm(sp - full) / np.linalg.norm(full) < 1e-5

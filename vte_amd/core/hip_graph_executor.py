@@ -210,6 +210,9 @@ class HIPGraphExecutor:
 
     @staticmethod
     def _persistent_supported(model) -> bool:
+        """The formats and shapes vte_decode_* accepts (the library's own model
+        check included), so an unsupported model falls back to the per-node
+        graph instead of failing at construction."""
         cfg = model.cfg
         if cfg.head_dim != 128 or cfg.n_q % cfg.n_kv or cfg.n_q // cfg.n_kv > 8:
             return False
@@ -225,7 +228,10 @@ class HIPGraphExecutor:
                 return False
             if lw["v_fmt"] not in ("q4_k", "q6_k") or lw["down_fmt"] not in ("q4_k", "q6_k"):
                 return False
-        return True
+        m = DecodeModel()
+        m.n_layers, m.hidden, m.ffn, m.n_q, m.n_kv = cfg.n_layers, cfg.hidden, cfg.ffn, cfg.n_q, cfg.n_kv
+        m.head_dim, m.vocab, m.max_seq, m.eps = cfg.head_dim, cfg.vocab, max(1, cfg.max_seq), cfg.eps
+        return kernels().decode_workspace_bytes(m, check=False) >= 0
 
     def _decode_model_struct(self, model) -> DecodeModel:
         cfg = self.cfg
@@ -603,6 +609,10 @@ class HIPGraphExecutor:
 
     # ------------------------------------------------------------------ outputs
     def _check_persistent(self) -> None:
+        if self.attn.fuse_combine and self.attn.status():
+            raise HIPRuntimeError("split-KV attention with the in-kernel combine: a combining block gave up waiting "
+                                  "on a split's records; results are invalid (VTE_ATT_FUSE=0 selects the separate "
+                                  "combine launch)")
         if self.persistent:
             flags = int(self._pin_flags[0]) if self._pin_fresh else self.K.decode_status(self.pd_ws)
             if flags:

@@ -68,8 +68,11 @@ class SplitKVAttentionDispatcher:
         # records (m, l, o[128] per split and head) instead: 2 * 130 floats each
         per = max(head_dim, 2 * (head_dim + 2)) if fuse_combine else head_dim
         self.part_o = DeviceArray(hip, nstat * per, np.float32, "attn_part_o", allocator, MemoryRegion.SCRATCH)
-        # per (sequence, KV head) epochs of the in-kernel combine (record tags)
-        self.counters = DeviceArray(hip, batch_size * n_kv, np.int32, "attn_counters", allocator, MemoryRegion.SCRATCH)
+        # in-kernel combine: a sticky error word (a combining block gave up
+        # waiting on a split's records), then per (sequence, KV head) epochs
+        # (record tags)
+        self.counters = DeviceArray(hip, 1 + batch_size * n_kv, np.int32, "attn_counters", allocator,
+                                    MemoryRegion.SCRATCH)
         self.counters.zero()
         if fuse_combine:
             self.part_o.zero()
@@ -94,3 +97,9 @@ class SplitKVAttentionDispatcher:
                              self.max_splits, dtype=dtype,
                              counters=self.counters if self._fused(out, kv_batch_stride, batch) else None,
                              stream=stream if stream is not None else self.hip.stream)
+
+    def status(self) -> int:
+        """Sticky error word of the in-kernel combine (0: every combining block
+        saw every split's records; nonzero: some launch's output is invalid).
+        Synchronous; always 0 without ``fuse_combine``."""
+        return int(self.counters.numpy()[0]) if self.fuse_combine else 0

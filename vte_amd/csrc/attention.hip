@@ -84,7 +84,8 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
     const __half* vb = v_cache + (size_t)b * kv_batch_stride + (size_t)kvh * ATT_D;
     const int len_raw = QC == 1 ? kv_offset[b] : max(kv_offset[b], kv_offset[min(b + 1, n_cols - 1)]);
     // in-kernel combine: this launch's record tag (the group's epoch + 1)
-    const uint32_t tag = counters != nullptr ? (uint32_t)counters[(size_t)b * n_kv + kvh] + 1u : 0u;
+    // (counters[0]: sticky error word; counters[1 + b * n_kv + kvh]: the group's epoch)
+    const uint32_t tag = counters != nullptr ? (uint32_t)counters[1 + (size_t)b * n_kv + kvh] + 1u : 0u;
     AttTile T, T1;
     int t0 = PW ? t_begin : t_begin + wv * ATT_TILE;
     if (SPEC) {
@@ -231,7 +232,8 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         __syncthreads();  // LDS of the previous head
         for (int c = threadIdx.x; c < ns; c += 256) {
             float ml[2];
-            wait_flag32_n<2>(recs + (size_t)c * ATT_REC, 1, tag, ml);
+            if (!wait_flag32_n<2>(recs + (size_t)c * ATT_REC, 1, tag, ml))
+                __hip_atomic_fetch_or(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             wsh[0][c] = ml[0];
             wsh[1][c] = ml[1];
         }
@@ -257,7 +259,8 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         for (int c = hf; c < ns; c += 16) {  // 8 splits per round, all requested together
             const int nj = min(8, (ns - c + 1) / 2);  // splits c, c + 2, ... below ns (slots past nj re-read the last)
             float v[8];
-            wait_flag32_n<8>(po + (size_t)c * ATT_REC, 2 * ATT_REC, tag, v, nj);
+            if (!wait_flag32_n<8>(po + (size_t)c * ATT_REC, 2 * ATT_REC, tag, v, nj))
+                __hip_atomic_fetch_or(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
             for (int j = 0; j < 8; ++j) O = j < nj ? fmaf(v[j], wsh[0][c + 2 * j], O) : O;
         }
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(256, TPW == 2 ? 1 : 3) void attn_partial_gqa(
         if (!hf) st_act<TO>(out + ((size_t)b * n_q + qh) * ATT_D + d, (O + oh[d]) / fmaxf(Lsh, 1e-20f));
     }
     if (r == 0 && threadIdx.x == 0)
-        __hip_atomic_store(counters + (size_t)b * n_kv + kvh, (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(counters + 1 + (size_t)b * n_kv + kvh, (int)tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // LSE combine for many splits (> 128): grid (n_q, B, 4 dim quarters), block

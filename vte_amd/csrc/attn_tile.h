@@ -42,9 +42,10 @@ __device__ __forceinline__ float wait_flag32(const uint64_t* p, uint32_t tag, in
 }
 // N flagged words p[0], p[stride], ... (slots from `n` on re-read word n - 1)
 // requested together and re-polled until each carries `tag` (one round trip
-// when they are already there).
+// when they are already there).  Returns false when it gave up after `limit`
+// polls (the values are then stale).
 template <int N>
-__device__ __forceinline__ void wait_flag32_n(const uint64_t* p, size_t stride, uint32_t tag, float (&v)[N],
+__device__ __forceinline__ bool wait_flag32_n(const uint64_t* p, size_t stride, uint32_t tag, float (&v)[N],
                                               int n = N, int limit = 1 << 18) {
     uint64_t w[N];
     const uint64_t* q[N];
@@ -63,8 +64,13 @@ __device__ __forceinline__ void wait_flag32_n(const uint64_t* p, size_t stride, 
         }
         if (all) break;
     }
+    bool done = true;
 #pragma unroll
-    for (int j = 0; j < N; ++j) v[j] = __uint_as_float((uint32_t)w[j]);
+    for (int j = 0; j < N; ++j) {
+        v[j] = __uint_as_float((uint32_t)w[j]);
+        done = done && (uint32_t)(w[j] >> 32) == tag;
+    }
+    return done;
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // One wave's 32-token tile: K rows (MFMA A operands, two 16-token halves) and

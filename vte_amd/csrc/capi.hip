@@ -531,6 +531,7 @@ int vte_decode_step(const vte_decode_model* m, void* ws, const int* kv_offset, c
     P.eps = m->eps;
     P.scale = 1.0f / sqrtf(128.0f);
     P.kv_offset = kv_offset;
+    P.max_seq = m->max_seq;
     P.x = static_cast<const __half*>(x);
     P.rope_cos = static_cast<const __half*>(m->rope_cos);
     P.rope_sin = static_cast<const __half*>(m->rope_sin);
@@ -562,6 +563,8 @@ int vte_decode_step(const vte_decode_model* m, void* ws, const int* kv_offset, c
     P.r_dn = std::min(256, (H + std::max(1, blocks / nsl) - 1) / std::max(1, blocks / nsl));
     P.r_red = (H + blocks - 1) / blocks;
     REQUIRE(P.r_qk >= 2 && P.r_gu >= 2 && P.r_dn >= 1, "decode_step: tile plan does not fit");
+    REQUIRE(P.r_red <= ROWS_THREADS, "decode_step: %d reduce rows per block exceed %d threads (hidden %d on %d CUs)",
+            P.r_red, ROWS_THREADS, H, blocks);
     REQUIRE(kvd % P.r_qk == 0 && qd % P.r_qk == 0, "decode_step: RoPE tiles");
     static const int split_env = [] {
         const char* s = getenv("VTE_PD_SPLIT");  // tuning: smallest attention split (multiple of 32)

@@ -18,6 +18,7 @@ struct VtePdPlan {
     int n_layers, hidden, ffn, n_q, n_kv;
     float eps, scale;
     const int* kv_offset;
+    int max_seq;               // rows of the K/V caches and RoPE tables: kv_offset[0] must lie in [0, max_seq)
     const __half* x;           // the token's embedding (layer 0 input, plain fp16)
     const __half* rope_cos;
     const __half* rope_sin;
@@ -27,7 +28,7 @@ struct VtePdPlan {
     uint32_t *ll_h, *ll_q, *ll_kv, *ll_att, *ll_hm, *ll_act;
     uint64_t* part;            // attention records (fp32 | tag << 32) [n_q][MAX_SPLITS][130]
     uint64_t* ll_dn;           // down partial sums (fp32 | tag << 32) [ffn / 256][hidden]
-    uint32_t* ctrl;            // [0] epoch, [1] finished blocks, [2] error flags
+    uint32_t* ctrl;            // [0] epoch, [1] finished blocks, [2] error flags (1: a wait timed out, 2: position out of range)
     int r_qk, r_v, r_o, r_gu;  // rows per tile of the q/k, v, o-proj and gate/up stages
     int r_dn;                  // rows per down-partial tile (one 256-wide slice of the ffn activations)
     int r_red;                 // rows each block reduces over the down partials

@@ -790,6 +790,10 @@ __global__ __launch_bounds__(PD_T, 1) void decode_persistent_kernel(VtePdPlan P)
     __shared__ float red[4];
     const uint32_t epoch = ld_c32(P.ctrl);
     const int pos = P.kv_offset[0];
+    if (pos < 0 || pos >= P.max_seq) {  // every block sees the same value: none writes, none waits
+        if (blockIdx.x == 0 && threadIdx.x == 0) __hip_atomic_fetch_or(P.ctrl + 2, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     const PdClock ck{pd_now() + P.timeout_ticks, P.ctrl + 2};
     const int H = P.hidden, F = P.ffn, qd = P.n_q * ATT_D, kvd = P.n_kv * ATT_D;
     const int G = gridDim.x, b = blockIdx.x;

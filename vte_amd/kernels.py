@@ -142,8 +142,9 @@ class VTEKernels:
 
     def attn_split_kv(self, q, k_cache, v_cache, part_m, part_l, part_o, out, batch, n_q, n_kv, head_dim, scale,
                       kv_offset, kv_batch_stride, split, max_splits, dtype="f32", counters=None, stream=None) -> None:
-        """Split-KV decode attention.  With ``counters`` (zeroed int32 [batch * n_kv],
-        kept zero by the kernel) the combine runs inside the partial kernel."""
+        """Split-KV decode attention.  With ``counters`` (zeroed int32 [1 + batch * n_kv]:
+        word 0 a sticky error word, then the per-group epochs the kernel
+        advances) the combine runs inside the partial kernel."""
         self._check(self.lib.vte_attn_split_kv(DT[dtype], _p(q), _p(k_cache), _p(v_cache), _p(part_m), _p(part_l),
                                                _p(part_o), _p(out), batch, n_q, n_kv, head_dim, scale, _p(kv_offset),
                                                kv_batch_stride, split, max_splits, _p(counters), self._st(stream)),
@@ -233,9 +234,11 @@ class VTEKernels:
         self._check(self.lib.vte_greedy_advance(_p(top_idx), k, rows, _p(tokens), _p(kv_offset), max_pos, _p(history),
                                                 history_steps, _p(step), self._st(stream)), "vte_greedy_advance")
 
-    def decode_workspace_bytes(self, model: DecodeModel) -> int:
+    def decode_workspace_bytes(self, model: DecodeModel, check: bool = True) -> int:
+        """Workspace bytes of the persistent step; -1 for a model it does not
+        support (raises instead when ``check``)."""
         n = int(self.lib.vte_decode_workspace_bytes(ctypes.byref(model)))
-        if n < 0:
+        if n < 0 and check:
             self._check(-1, "vte_decode_workspace_bytes")
         return n
 
