@@ -159,6 +159,52 @@ def persistent_roofline(hip, ex_p, layer_bytes, lm_head_ms, reps=20):
             "timing": "HIP events around graph replays of the decode node, minus the LM-head launch"}
 
 
+def mfma_b16_roofline(hip, ex, reps=20):
+    """Roofline of the batch-16 step's dominant kernel, the gate/up + SwiGLU
+    MFMA launch (fused_mm_kernel, 28 per step): algorithmic bytes per launch
+    (gate and up weights + the 16 normalised activation columns read + the 16
+    SwiGLU columns written) over the average launch duration, HIP events on
+    the executor's stream around replays of a graph of the step's 28 launches
+    (same buffers and shapes as the step)."""
+    cfg, B, K = ex.cfg, ex.B, ex.K
+    from vte_amd import synthetic as syn
+    per_launch = [syn.matrix_bytes(lw["gate_fmt"], cfg.ffn, cfg.hidden) + syn.matrix_bytes(lw["up_fmt"], cfg.ffn,
+                  cfg.hidden) + B * 2 * (cfg.hidden + cfg.ffn) for lw in ex.layers]
+    hip.synchronize()
+    hip.stream_begin_capture()
+    try:
+        for lw in ex.layers:
+            K.ffn_in(ex.xn, None, cfg.eps, lw["gate"], lw["up"], lw["gate_fmt"], ex.a, B, cfg.hidden, cfg.ffn,
+                     stream=hip.stream)
+    finally:
+        g = hip.stream_end_capture()
+    ge = hip.graph_instantiate(g)
+    try:
+        hip.graph_launch(ge)
+        hip.synchronize()
+        e0, e1 = _events(hip)
+        hip.event_record(e0)
+        for _ in range(reps):
+            hip.graph_launch(ge)
+        hip.event_record(e1)
+        ms = hip.event_elapsed_ms(e0, e1) / reps / len(ex.layers)
+    finally:
+        hip.graph_exec_destroy(ge)
+        hip.graph_destroy(g)
+    algo = sum(per_launch) / len(per_launch)
+    gbps = algo / (ms * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "fused_mm_gateup_b16_traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+            "kernel": "fused_mm_kernel<2, 1, 6> (gate/up + SwiGLU on MFMA, 28 launches of the batch-16 step)",
+            "avg_launch_us": round(ms * 1e3, 3), "algo_bytes_per_launch": int(algo),
+            "timing": "HIP events around graph replays of the step's 28 gate/up launches"}
+
+
 def time_greedy(hip, ex, steps, start_pos):
     """Greedy decoding with the token fed back on the device (generate_greedy):
     wall time per step of one call of ``steps`` steps, tokens read at the end."""
@@ -574,7 +620,7 @@ def main():
     lm_head_ms = breakdown["lm_head"]["us_per_step"] * 1e-3
     ex.close()
     graph_b1 = {"ms_per_step": round(ms_g, 4), "tok_s": round(1e3 / ms_g, 2)}
-    roof = None
+    roof = roof16 = None
     for B in ([1] if args.quick else [1, 16]):
         ex = HIPGraphExecutor(hip, model, batch_size=B, max_seq=prefix + 256)  # batch 1: the persistent step
         ex.fill_kv_prefix(seed=B)
@@ -589,6 +635,8 @@ def main():
             status = ex.decode_status()
             if status:
                 raise RuntimeError(f"persistent decode step error flags {status:#x}")
+        else:
+            roof16 = mfma_b16_roofline(hip, ex)
         kv_read = cfg.n_layers * (prefix + 1) * cfg.n_kv * cfg.head_dim * 2 * 2 * B
         step_bytes = wbytes + kv_read
         result[B] = {"ms_per_step": ms, "tok_s": B / (ms * 1e-3), "wall_s": wall, "e2e_ms_per_step": e2e * 1e3,
@@ -639,6 +687,8 @@ def main():
     line["hbm_copy_GBps"] = hbm_copy_bandwidth(hip)
     line["hbm_peak_GBps"] = HBM_PEAK_GBPS
     line["roofline"] = roof
+    if roof16:
+        line["roofline_b16"] = roof16
     line["roofline_graph_fused_mv"] = roof_mv
     line["step_breakdown_b1"] = breakdown
     if cpu:
