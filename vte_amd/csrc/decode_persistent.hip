@@ -435,6 +435,7 @@ struct PdAttLDS {
     } u;
     float m_sh[ATT_WAVES][16], l_sh[ATT_WAVES][16];
     float sc[4];
+    alignas(16) uint32_t q[ATT_MAXG * ATT_D / 2];  // the KV group's q as fp16 pairs [head][dim / 2] (S2)
 };
 
 // S2: partials of split c (rows [c*split, min((c+1)*split, pos))) of KV head kvh.
@@ -463,34 +464,34 @@ __device__ __forceinline__ void pd_attn_item(const VtePdPlan& P, const VtePdLaye
     int t0 = t_begin + wv * ATT_TILE;
     att_load_tile(T, kb, vb, row_stride, t0, t_end - 1, col, grp, lane);  // cached rows: written by earlier launches
 
-    // Q^T of the group's heads (B operand, heads past G zero) from the flagged q words
+    // Q^T of the group's heads (B operand, heads past G zero).  The block
+    // polls the group's G * 128 flagged q words together (two 64-bit pairs
+    // per thread at most, G <= 8) and stages them in LDS as fp16 pairs
+    // [head][dim / 2]; each wave then reads its operands from there.
+    {
+        const uint64_t* qg = reinterpret_cast<const uint64_t*>(P.ll_q + (size_t)kvh * G * ATT_D);
+        const int npair = G * ATT_D / 2, t = threadIdx.x;
+        const bool h0 = t < npair, h1 = t + PD_T < npair;
+        const uint64_t dflt = (uint64_t)tag << 48 | (uint64_t)tag << 16;
+        uint64_t w0 = h0 ? ld_c64(qg + t) : dflt, w1 = h1 ? ld_c64(qg + t + PD_T) : dflt;
+        int spins = 0;
+        while (true) {
+            const bool ok0 = ok2(w0, tag), ok1 = ok2(w1, tag);
+            if ((ok0 && ok1) || pd_expired(ck, spins)) break;
+            if (!ok0) w0 = ld_c64(qg + t);
+            if (!ok1) w1 = ld_c64(qg + t + PD_T);
+        }
+        if (h0) A.q[t] = pair2(w0);
+        if (h1) A.q[t + PD_T] = pair2(w1);
+    }
+    __syncthreads();
     half8_t qb[ATT_D / 32];
     {
         const bool slot = col < G;
-        const uint32_t* qp = P.ll_q + (size_t)(kvh * G + (slot ? col : 0)) * ATT_D + 8 * grp;
-        uint64_t w[ATT_D / 32][4];
-#pragma unroll
-        for (int s = 0; s < ATT_D / 32; ++s)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                w[s][i] = slot ? ld_c64(reinterpret_cast<const uint64_t*>(qp + 32 * s) + i)
-                               : ((uint64_t)tag << 48 | (uint64_t)tag << 16);
-        int spins = 0;
-        while (true) {
-            bool all = true;
-#pragma unroll
-            for (int s = 0; s < ATT_D / 32; ++s)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool ok = ok2(w[s][i], tag);
-                    all = all && ok;
-                    if (!ok) w[s][i] = ld_c64(reinterpret_cast<const uint64_t*>(qp + 32 * s) + i);
-                }
-            if (all || pd_expired(ck, spins)) break;
-        }
+        const uint32_t* qs = A.q + (size_t)(slot ? col : 0) * (ATT_D / 2) + 4 * grp;
 #pragma unroll
         for (int s = 0; s < ATT_D / 32; ++s) {
-            const uint4 u = make_uint4(pair2(w[s][0]), pair2(w[s][1]), pair2(w[s][2]), pair2(w[s][3]));
+            const uint4 u = *reinterpret_cast<const uint4*>(qs + 16 * s);
             qb[s] = slot ? __builtin_bit_cast(half8_t, u) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }
