@@ -18,20 +18,24 @@ Pinning (what fixes each function independently of its own formula):
   (tests/integration/test_kernels_numerical.py:59-77 under dequantizer.py
   semantics -> 18.5); independent encoders written from the block layout.
 * ``dequant.gemv`` — linearity in x and one-hot columns (float64).
-* ``attention.attention_ref`` / ``split_kv_ref`` — float64 textbook softmax
-  attention; split equals unsplit; ctx=1 -> v0; identical keys -> mean(V).
+* ``attention.attention_ref`` / ``split_kv_ref`` / ``attention_gqa_f32`` —
+  float64 (float32 for the GQA form) textbook softmax attention; split
+  equals unsplit; ctx=1 -> v0; identical keys -> mean(V); the float32 GQA
+  form within 1e-6 of the float64 one (a wrong head grouping misses by O(1)).
 * ``step.rope_cache`` — golden vectors from the reference's
   RoPECacheBuilder.build_cache (tests/golden/rope.npz, fp16 bit-exact).
 * ``step.rmsnorm`` / ``swiglu`` / ``rope_neox`` — closed forms (unit RMS,
   scale invariance, silu values, rotation by pos*theta^(-i/64) keeping
   pair norms, position 0 identity).
-* ``step.embedding_q6k`` — a row of the pinned Q6_K dequantiser.
-* ``step.decode_step`` — composition of the pinned pieces in the node order
-  of vte/compiler/qwen_compute.py:100-282; its residual wiring, final norm
-  and tied LM head are pinned by the zero-projection reduction (logits =
-  W_embd @ rmsnorm(embedding)); the order of the attention/FFN sub-blocks
-  within a layer is pinned only by that citation (parity of the composed
-  layer beyond the reduction is unpinned).
+* ``step.embedding_row`` — a row of the pinned dequantisers.
+* ``step.decode_step`` / ``prefill`` — composition of the pinned pieces in
+  the node order of vte/compiler/qwen_compute.py:100-282, pinned by an
+  exact-integer model whose every output is a short closed form
+  (tests/pin_model.py, tests/test_step_pins.py): silu(gate)*up, the q/k/v
+  biases, RoPE on q and k only, the K/V row appended before attention, the
+  GQA head map, both residual adds, the FFN norm on the post-attention sum,
+  the final norm and the tied LM head; ten plausible composition mistakes
+  each break it.  ``prefill`` equals ``decode_step`` fed token by token.
 
 The sampler (vte_amd/core/sampler.py, a product module, not oracle) is pinned
 by the reference's own draws under fixed NumPy seeds (tests/golden/sampler.npz).
