@@ -93,3 +93,20 @@ def test_generate_batch_ragged_follows_oracle(hip, tiny):
             _oracle_follows(tiny, p, [s[b] for s in steps], f"seq {b}")
     finally:
         eng.close()
+
+
+def test_generate_full_shape_follows_oracle(hip):
+    """The first 2 layers of the Qwen2.5-1.5B shape: a 40-token prompt
+    prefilled in one chunk, then 6 greedy tokens on the persistent step,
+    each the oracle's argmax up to a near-tie."""
+    from tests.test_decode_step_gpu import _Truncated
+    from vte_amd.core.model_config import QWEN25_1P5B
+    model = _Truncated(SyntheticQwen2(QWEN25_1P5B, seed=0), 2)
+    eng = VTEModel(hip, model, context_length=CTX)
+    try:
+        prompt = [int(t) for t in np.random.default_rng(5).integers(0, model.cfg.vocab, 40)]
+        got = list(eng.generate(prompt, max_tokens=6, temperature=0.0, repetition_penalty=1.0))
+        assert len(got) == 6 and eng.executor(1)[0].persistent
+    finally:
+        eng.close()
+    _oracle_follows(model, prompt, got, "1.5B shape")
