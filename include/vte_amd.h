@@ -24,7 +24,14 @@
  * flash_attention_split_kv_partial_kernel, flash_attention_split_kv_reduce_kernel,
  * rmsnorm_kernel, rope_kernel, swiglu_kernel, add_kernel,
  * embedding_lookup_q6k_kernel, embedding_lookup_q4k_kernel,
- * embedding_lookup_q8_0_kernel.
+ * embedding_lookup_q8_0_kernel.  Beside them the code object holds the
+ * fp32-I/O siblings gemv_q4k_f32_kernel, gemv_q6k_f32_kernel,
+ * gemv_q8_0_f32_kernel (same 10 arguments and geometry, fp32 input, bias,
+ * residual and output) and the batched MFMA GEMMs gemm_q4k_mfma_kernel,
+ * gemm_q6k_mfma_kernel (the same 10 arguments, fp16 I/O; grid
+ * (ceil(out_features/32), ceil(batch*seq_len/16)), block 512) that the
+ * reference's dispatch can select from batch 8 (no reference counterpart:
+ * its batched executor re-runs the GEMV per row, batched_hip_graph_executor.py:231-251).
  */
 #ifndef VTE_AMD_H
 #define VTE_AMD_H

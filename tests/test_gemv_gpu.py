@@ -164,23 +164,52 @@ def test_gemm_mfma_f16_epilogue(hip, K):
 
 
 @pytest.mark.parametrize("name,fmt", [("gemv_q4k_kernel", "q4_k"), ("gemv_q6k_kernel", "q6_k"),
-                                      ("gemv_q8_0_kernel", "q8_0")])
+                                      ("gemv_q8_0_kernel", "q8_0"), ("gemv_q4k_f32_kernel", "q4_k"),
+                                      ("gemv_q6k_f32_kernel", "q6_k"), ("gemv_q8_0_f32_kernel", "q8_0")])
 def test_reference_abi_code_object(hip, name, fmt):
     """Drop-in path: load the code object by kernel name and launch it with the
-    reference's 10-argument ABI and geometry (grid (N, B*S), block 64)."""
+    reference's 10-argument ABI and geometry (grid (N, B*S), block 64); the
+    `_f32` siblings take fp32 input, bias, residual and output."""
     from vte_amd.kernels import HSACO_PATH
     _, fn = hip.load_kernel(str(HSACO_PATH), name)
+    dt = np.float32 if name.endswith("_f32_kernel") else np.float16
     n, k, B = 300, 2048, 2
     rng = np.random.default_rng(9)
     raw = syn.random_matrix(fmt, rng, n, k)
-    x = rng.standard_normal((B, k)).astype(np.float16)
-    bias = (0.1 * rng.standard_normal(n)).astype(np.float16)
-    res = rng.standard_normal((B, n)).astype(np.float16)
+    x = rng.standard_normal((B, k)).astype(dt)
+    bias = (0.1 * rng.standard_normal(n)).astype(dt)
+    res = rng.standard_normal((B, n)).astype(dt)
     dx, dw, db, dr = up(hip, x), up(hip, raw), up(hip, bias), up(hip, res)
-    y = empty(hip, (B, n), np.float16)
+    y = empty(hip, (B, n), dt)
     args = [ctypes.c_void_p(dx.ptr), ctypes.c_void_p(dw.ptr), ctypes.c_void_p(y.ptr), ctypes.c_int(B),
             ctypes.c_int(1), ctypes.c_int(k), ctypes.c_int(n), ctypes.c_void_p(db.ptr), ctypes.c_void_p(dr.ptr),
             ctypes.c_float(1.0)]
     hip.launch_kernel(fn, (n, B, 1), (64, 1, 1), args, expected_args=10)
+    ref = dq.gemv_epilogue(dq.gemv(fmt, raw, n, k, x.astype(np.float32)), bias, res, 1.0)
+    assert rel_l2(down(y), ref) <= TOL
+
+
+@pytest.mark.parametrize("name,fmt", [("gemm_q4k_mfma_kernel", "q4_k"), ("gemm_q6k_mfma_kernel", "q6_k")])
+@pytest.mark.parametrize("k,cols", [(1536, 20), (2048, 16), (1536, 8)])
+def test_reference_abi_mfma_symbol(hip, name, fmt, k, cols):
+    """The batched MFMA GEMM behind the reference GEMV's 10-argument ABI
+    (fp16 I/O, batch * seq_len columns), loaded from the code object by name
+    and launched with its geometry (grid (ceil(N/32), ceil(cols/16)), block
+    512): bias and residual epilogue, a partial row tile (N = 300) and a
+    partial column tile, against the oracle at the GEMV bound."""
+    from vte_amd.kernels import HSACO_PATH
+    _, fn = hip.load_kernel(str(HSACO_PATH), name)
+    n = 300
+    rng = np.random.default_rng(k + cols)
+    raw = syn.random_matrix(fmt, rng, n, k)
+    x = rng.standard_normal((cols, k)).astype(np.float16)
+    bias = (0.1 * rng.standard_normal(n)).astype(np.float16)
+    res = rng.standard_normal((cols, n)).astype(np.float16)
+    dx, dw, db, dr = up(hip, x), up(hip, raw), up(hip, bias), up(hip, res)
+    y = empty(hip, (cols, n), np.float16)
+    args = [ctypes.c_void_p(dx.ptr), ctypes.c_void_p(dw.ptr), ctypes.c_void_p(y.ptr), ctypes.c_int(cols // 2 if cols % 2 == 0 else cols),
+            ctypes.c_int(2 if cols % 2 == 0 else 1), ctypes.c_int(k), ctypes.c_int(n), ctypes.c_void_p(db.ptr),
+            ctypes.c_void_p(dr.ptr), ctypes.c_float(1.0)]
+    hip.launch_kernel(fn, ((n + 31) // 32, (cols + 15) // 16, 1), (512, 1, 1), args, expected_args=10)
     ref = dq.gemv_epilogue(dq.gemv(fmt, raw, n, k, x.astype(np.float32)), bias, res, 1.0)
     assert rel_l2(down(y), ref) <= TOL

@@ -21,15 +21,15 @@
 
 #include "mfma_deq.h"
 
-// NW waves per block split K (6 when K = 1536: one super-block each).
-template <typename TI, typename TO, int FMT, int RT, int NT, int NW = MF_WAVES>
-__global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
-                                                        TO* __restrict__ y, int M, int K, int N,
-                                                        const TO* __restrict__ bias, const TO* __restrict__ residual,
-                                                        float rs, size_t split_stride) {
+// Body of one block: row tile blockIdx.x, split `split` of `nsplit` (split-K
+// partial sums at y + split * split_stride).
+template <typename TI, typename TO, int FMT, int RT, int NT, int NW>
+__device__ __forceinline__ void gemm_mfma_body(const TI* __restrict__ x, const uint8_t* __restrict__ w,
+                                               TO* __restrict__ y, int M, int K, int N, const TO* __restrict__ bias,
+                                               const TO* __restrict__ residual, float rs, size_t split_stride,
+                                               int split, int nsplit, float (*red)[RT][NT][4][64],
+                                               float (*xl)[NT * 128]) {
     constexpr bool XM = NT > 1;  // minimum-term form (q4_xmin)
-    __shared__ float red[NW][RT][NT][4][64];
-    __shared__ float xl[NW][NT * 128];  // minimum-term scratch per wave (q4_xmin)
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -39,9 +39,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
     const int row0 = blockIdx.x * (16 * RT);
     // split-K over blockIdx.y: this block's super-block range, then each
     // wave's contiguous share of it; split s writes its sums at y + s * split_stride
-    const int kb0 = (n_sb * (int)blockIdx.y) / (int)gridDim.y, kb1 = (n_sb * ((int)blockIdx.y + 1)) / (int)gridDim.y;
+    const int kb0 = (n_sb * split) / nsplit, kb1 = (n_sb * (split + 1)) / nsplit;
     const int sb0 = kb0 + ((kb1 - kb0) * wv) / NW, sb1 = kb0 + ((kb1 - kb0) * (wv + 1)) / NW;
-    y += blockIdx.y * split_stride;
+    y += split * split_stride;
 
     floatx4_t acc[RT][NT];
 #pragma unroll
@@ -98,6 +98,53 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict
         const int row = row0 + rr;
         if (row < N && mc < M) gemv_store<TO>(y, bias, residual, rs, row, mc, N, s);
     }
+}
+
+// NW waves per block split K (6 when K = 1536: one super-block each).
+template <typename TI, typename TO, int FMT, int RT, int NT, int NW = MF_WAVES>
+__global__ __launch_bounds__(64 * NW) void gemm_mfma_kernel(const TI* __restrict__ x, const uint8_t* __restrict__ w,
+                                                        TO* __restrict__ y, int M, int K, int N,
+                                                        const TO* __restrict__ bias, const TO* __restrict__ residual,
+                                                        float rs, size_t split_stride) {
+    __shared__ float red[NW][RT][NT][4][64];
+    __shared__ float xl[NW][NT * 128];  // minimum-term scratch per wave (q4_xmin)
+    gemm_mfma_body<TI, TO, FMT, RT, NT, NW>(x, w, y, M, K, N, bias, residual, rs, split_stride, (int)blockIdx.y,
+                                            (int)gridDim.y, red, xl);
+}
+
+// Batched MFMA GEMM behind the reference GEMV's 10-argument ABI (fp16 I/O,
+// argument list of gemv_q4k.hip.template:56-67), for callers that select a
+// batched symbol at batch >= 8: rows = batch * seq_len columns of the input.
+// Launch geometry differs from the GEMV's: grid (ceil(out_features / 32),
+// ceil(batch * seq_len / 16), 1), block (512, 1, 1); blockIdx.y picks 16
+// columns.  in_features must be a multiple of 256.
+template <int FMT>
+__device__ __forceinline__ void gemm_ref_abi(const void* input_ptr, const void* weight_ptr, void* output_ptr, int batch,
+                                             int seq_len, int in_features, int out_features, const void* bias_ptr,
+                                             const void* residual_ptr, float residual_scale) {
+    __shared__ float red[MF_WAVES][2][1][4][64];
+    __shared__ float xl[MF_WAVES][128];
+    const int cols = batch * seq_len, c0 = (int)blockIdx.y * 16;
+    if (c0 >= cols) return;
+    const __half* x = static_cast<const __half*>(input_ptr) + (size_t)c0 * in_features;
+    __half* y = static_cast<__half*>(output_ptr) + (size_t)c0 * out_features;
+    const __half* res = residual_ptr ? static_cast<const __half*>(residual_ptr) + (size_t)c0 * out_features : nullptr;
+    gemm_mfma_body<__half, __half, FMT, 2, 1, MF_WAVES>(x, static_cast<const uint8_t*>(weight_ptr), y,
+                                                        min(16, cols - c0), in_features, out_features,
+                                                        static_cast<const __half*>(bias_ptr), res, residual_scale, 0,
+                                                        0, 1, red, xl);
+}
+extern "C" __global__ __launch_bounds__(64 * MF_WAVES) void gemm_q4k_mfma_kernel(
+    const void* input_ptr, const void* weight_ptr, void* output_ptr, int batch, int seq_len, int in_features,
+    int out_features, const void* bias_ptr, const void* residual_ptr, float residual_scale) {
+    gemm_ref_abi<4>(input_ptr, weight_ptr, output_ptr, batch, seq_len, in_features, out_features, bias_ptr,
+                    residual_ptr, residual_scale);
+}
+extern "C" __global__ __launch_bounds__(64 * MF_WAVES) void gemm_q6k_mfma_kernel(
+    const void* input_ptr, const void* weight_ptr, void* output_ptr, int batch, int seq_len, int in_features,
+    int out_features, const void* bias_ptr, const void* residual_ptr, float residual_scale) {
+    gemm_ref_abi<6>(input_ptr, weight_ptr, output_ptr, batch, seq_len, in_features, out_features, bias_ptr,
+                    residual_ptr, residual_scale);
 }
 
 

@@ -1,6 +1,8 @@
 // Single translation unit for the standalone code object (--genco): the
-// reference-named extern "C" kernels of the GEMV, attention and glue sources,
+// reference-named extern "C" kernels of the GEMV, attention and glue sources
+// (plus their fp32 GEMV siblings and the batched MFMA GEMM symbols),
 // loadable with hipModuleLoad / hipModuleGetFunction.
 #include "gemv.hip"
 #include "attention.hip"
 #include "glue.hip"
+#include "gemm_mfma.hip"
