@@ -80,15 +80,19 @@ def test_generate_sampling_candidates_equal_full_row(hip, tiny):
 
 def test_generate_batch_ragged_follows_oracle(hip, tiny):
     """Three prompts of 3, 9 and 5 tokens decoded together (MFMA batch path,
-    each sequence at its own position): every sequence's tokens follow the
-    oracle loop of that sequence alone."""
+    each sequence at its own position) on an executor that uses the batch-1
+    executor's uploaded weights: every sequence's tokens follow the oracle
+    loop of that sequence alone."""
     eng = VTEModel(hip, tiny, context_length=CTX)
     try:
+        one = list(eng.generate([5, 6], max_tokens=2, temperature=0.0, repetition_penalty=1.0))
         prompts = [[1, 2, 3], [400, 17, 17, 90, 4000, 5, 6, 7, 8], [77, 1000, 2048, 3, 9]]
         stats = {}
         steps = list(eng.generate_batch(prompts, max_tokens=8, temperature=0.0, repetition_penalty=1.0,
                                         stats=stats))
+        assert eng.executor(3)[0].layers is eng.executor(1)[0].layers  # one copy of the weights
         assert len(steps) == 8 and stats["completion_tokens"] == [8, 8, 8]
+        assert list(eng.generate([5, 6], max_tokens=2, temperature=0.0, repetition_penalty=1.0)) == one
         for b, p in enumerate(prompts):
             _oracle_follows(tiny, p, [s[b] for s in steps], f"seq {b}")
     finally:

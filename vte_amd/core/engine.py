@@ -56,7 +56,9 @@ class VTEModel:
 
     ``context_length``: rows of every KV cache (the reference's
     ``_context_length``).  Executors are made per batch size on first use and
-    kept (each holds its own copy of the weights in its slab)."""
+    kept; the first one uploads the weights and the others use them
+    (``weights_of``), each with its own KV cache, as the reference's batched
+    executor shares the loaded model's weights (model.py:1175-1177)."""
 
     def __init__(self, hip: HIPRuntime, model, context_length: int = 4096, top_k_device: int = 40,
                  prefill_chunk: int = 512, stop_ids: Iterable[int] = (), ignore_tokens: Iterable[int] = (),
@@ -77,14 +79,15 @@ class VTEModel:
     # ------------------------------------------------------------------ executors
     def executor(self, batch_size: int) -> tuple[HIPGraphExecutor, PrefillRunner]:
         if batch_size not in self._ex:
+            owner = next(iter(self._ex.values()))[0] if self._ex else None
             ex = HIPGraphExecutor(self.hip, self.model, batch_size=batch_size, max_seq=self.context_length,
-                                  top_k=self.top_k_device, persistent=self.persistent)
+                                  top_k=self.top_k_device, persistent=self.persistent, weights_of=owner)
             chunk = max(self.prefill_chunk, ex.gemm_min_batch)
             self._ex[batch_size] = (ex, PrefillRunner(ex, chunk=chunk))
         return self._ex[batch_size]
 
     def close(self) -> None:
-        for ex, runner in self._ex.values():
+        for ex, runner in reversed(list(self._ex.values())):  # executors that use the weights first
             runner.close()
             ex.close()
         self._ex.clear()

@@ -59,8 +59,12 @@ def splitk_splits(K: int) -> int:
 class HIPGraphExecutor:
     def __init__(self, hip: HIPRuntime, model: SyntheticQwen2, batch_size: int = 1, max_seq: Optional[int] = None,
                  top_k: int = 40, gemm_min_batch: int = 3, split: Optional[int] = None, fused: bool = True,
-                 shared: Optional["HIPGraphExecutor"] = None, kv_seq: int = 0, persistent: Optional[bool] = None):
-        """``shared``: reuse that executor's weights, RoPE tables and the KV
+                 shared: Optional["HIPGraphExecutor"] = None, kv_seq: int = 0, persistent: Optional[bool] = None,
+                 weights_of: Optional["HIPGraphExecutor"] = None):
+        """``weights_of``: use that executor's uploaded weights (same model)
+        instead of uploading another copy; this executor keeps its own KV
+        cache, RoPE tables and activations, and is closed with the owner.
+        ``shared``: reuse that executor's weights, RoPE tables and the KV
         cache of its sequence ``kv_seq`` (columns of this executor are tokens of
         that one sequence: KV rows at each column's own position, stride 0),
         with activation buffers of ``batch_size`` columns and only the last
@@ -111,7 +115,10 @@ class HIPGraphExecutor:
         act_bytes = 4 * B * (2 * H + cfg.q_dim * 2 + cfg.kv_dim * 2 + 3 * cfg.ffn) * 2
         act_bytes += out_rows * (cfg.vocab * 4 + MAX_EXCLUDE * 8 + 1024) + 2 * self._topk_scratch_estimate(out_rows)
         act_bytes += MAX_SPLITK * B * H * 4
-        need = (0 if shared is not None else model.weight_bytes()) + 2 * cfg.n_layers * kv_elems * 2 + act_bytes + \
+        if weights_of is not None and (shared is not None or weights_of.cfg != cfg or weights_of.closed):
+            raise HIPSafetyError("weights_of needs an open executor of the same model and excludes shared")
+        own_w = shared is None and weights_of is None
+        need = (model.weight_bytes() if own_w else 0) + 2 * cfg.n_layers * kv_elems * 2 + act_bytes + \
             (64 << 20)
         need += (cfg.n_layers * len(PROJ) + 16) * 1024  # alignment and slack per tensor
         # split-KV scratch: [B][n_q][splits] stats and [B][n_q][splits][hd] partial outputs
@@ -129,7 +136,7 @@ class HIPGraphExecutor:
         if shared is not None:
             self._share(shared, kv_seq)
         else:
-            self._upload_weights(model, W, A)
+            self._upload_weights(model, W, A, weights_of)
         # ---- activations (fp16 between nodes, fp32 logits) ----
         self.h = [A((B, H), np.float16, "hidden0"), A((B, H), np.float16, "hidden1")]
         self.xn = A((B, H), np.float16, "normed")
@@ -182,8 +189,21 @@ class HIPGraphExecutor:
             self._pin_flags = buf[cut[4]:cut[5]].view(np.int32)
             self._pin_flags[0] = 0
 
-    def _upload_weights(self, model, W, A) -> None:
+    def _upload_weights(self, model, W, A, weights_of=None) -> None:
         cfg, B = self.cfg, self.B
+        if weights_of is not None:  # the owner's device weights; own KV cache below
+            for name in ("token_embd", "token_embd_fmt", "lm_head", "lm_head_fmt", "output_norm", "layers"):
+                setattr(self, name, getattr(weights_of, name))
+            weights_of._dependents.append(self)
+        else:
+            self._upload_own_weights(model, W)
+        # ---- KV cache ----
+        self.kv_batch_stride = self.max_seq * cfg.n_kv * cfg.head_dim
+        kv_shape = (B, self.max_seq, cfg.n_kv, cfg.head_dim)
+        self.k_cache = [A(kv_shape, np.float16, f"blk.{L}.k_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
+        self.v_cache = [A(kv_shape, np.float16, f"blk.{L}.v_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
+
+    def _upload_own_weights(self, model, W) -> None:
         # ---- weights ----
         self.token_embd = W(model.token_embd, "token_embd")
         self.token_embd_fmt = getattr(model, "token_embd_fmt", "q6_k")
@@ -202,11 +222,6 @@ class HIPGraphExecutor:
             for name in ("q_bias", "k_bias", "v_bias", "attn_norm", "ffn_norm"):
                 d[name] = W(lw[name], f"blk.{L}.{name}")
             self.layers.append(d)
-        # ---- KV cache ----
-        self.kv_batch_stride = self.max_seq * cfg.n_kv * cfg.head_dim
-        kv_shape = (B, self.max_seq, cfg.n_kv, cfg.head_dim)
-        self.k_cache = [A(kv_shape, np.float16, f"blk.{L}.k_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
-        self.v_cache = [A(kv_shape, np.float16, f"blk.{L}.v_cache", MemoryRegion.KV_CACHE) for L in range(cfg.n_layers)]
 
     @staticmethod
     def _persistent_supported(model) -> bool:
@@ -663,6 +678,8 @@ class HIPGraphExecutor:
         self.v_cache[layer].upload(v)
 
     def close(self) -> None:
+        if self.closed:
+            return
         # executors and runners that hold pointers into this slab go first
         for dep in list(getattr(self, "_dependents", [])):
             dep.close()
