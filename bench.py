@@ -515,6 +515,101 @@ GEMV_CONFIGS = [("q4_k", 8960, 1536, 0), ("q6_k", 1536, 8960, 0), ("q6_k", 15193
                 ("q8_0", 2048, 2048, 0), ("q4_k", 8960, 1536, 16)]
 
 
+# (fmt, N, K) of the per-launch method: the reference's own shape (Q4_K
+# FFN-down 1536x8960, tools/bench_gemv_q4k_bandwidth.py:66-67) and configs 0/1
+REFMETHOD_SHAPES = [("q4_k", 1536, 8960), ("q4_k", 8960, 1536), ("q6_k", 1536, 8960), ("q6_k", 151936, 1536),
+                    ("q8_0", 2048, 2048)]
+SYMBOL = {"q4_k": "gemv_q4k_kernel", "q6_k": "gemv_q6k_kernel", "q8_0": "gemv_q8_0_kernel"}
+
+
+def gemv_reference_method(hip, K, shapes=REFMETHOD_SHAPES, iters=500, warmup=300, trials=5):
+    """The reference's GEMV bandwidth method (tools/bench_gemv_q4k_bandwidth.py
+    run_trial, :166-200): every launch bracketed by its own pair of events
+    (launches issued one at a time from the host, so none overlaps the next),
+    a 300-launch warm-up, 500 timed launches over a rotating cold pool, the
+    event time of an empty kernel subtracted as the dispatch floor, and the
+    GEMV's corrected bandwidth divided by that of a plain read of the same
+    rows with the GEMV ABI's geometry (one 64-thread block per row,
+    ``vte_read_rows_kernel``); median / min / max over 5 trials.  Timed for
+    the reference-ABI code-object symbol (fp16 I/O, grid (N, 1), block 64) and
+    for the C-ABI mat-vec that the decode step uses (fp16 I/O)."""
+    import ctypes
+    import statistics
+    from vte_amd import synthetic as syn
+    from vte_amd.bridge import DeviceArray
+    from vte_amd.kernels import HSACO_PATH
+    _, f_null = hip.load_kernel(str(HSACO_PATH), "vte_null_kernel")
+    _, f_read = hip.load_kernel(str(HSACO_PATH), "vte_read_rows_kernel")
+    ev = [(hip.event_create(), hip.event_create()) for _ in range(iters)]
+
+    def timed(launch):
+        for i in range(warmup):
+            launch(i)
+        hip.synchronize()
+        for i in range(iters):
+            hip.event_record(ev[i][0])
+            launch(i)
+            hip.event_record(ev[i][1])
+        hip.synchronize()
+        return sum(hip.event_elapsed_ms(a, b) for a, b in ev) / iters
+
+    out = []
+    for fmt, n, k in shapes:
+        raw = syn.random_matrix(fmt, np.random.default_rng(42), n, k)
+        wbytes = raw.nbytes
+        copies = max(2, int(np.ceil((640 << 20) / wbytes)), 40 if wbytes * 40 <= (1 << 30) else 2)
+        pool = DeviceArray(hip, copies * wbytes + 256, np.uint8, "refm_pool")
+        first = DeviceArray.from_numpy(hip, raw, "refm_w0")
+        for c in range(copies):
+            hip.memcpy_device_to_device(pool.ptr + c * wbytes, first.ptr, wbytes)
+        x = DeviceArray.from_numpy(hip, np.random.default_rng(1).standard_normal((1, k)).astype(np.float16), "refm_x")
+        y = DeviceArray(hip, (1, n), np.float16, "refm_y")
+        sink = DeviceArray(hip, (n,), np.uint32, "refm_sink")
+        _, f_gemv = hip.load_kernel(str(HSACO_PATH), SYMBOL[fmt])
+        rb = wbytes // n
+        w = lambda i: pool.ptr + (i % copies) * wbytes
+
+        def l_null(i):
+            hip.launch_kernel(f_null, (1, 1, 1), (1, 1, 1), [], expected_args=0)
+
+        def l_read(i):
+            hip.launch_kernel(f_read, (n, 1, 1), (64, 1, 1),
+                              [ctypes.c_void_p(w(i)), ctypes.c_void_p(sink.ptr), ctypes.c_int(rb)], expected_args=3)
+
+        def l_ref(i):
+            hip.launch_kernel(f_gemv, (n, 1, 1), (64, 1, 1),
+                              [ctypes.c_void_p(x.ptr), ctypes.c_void_p(w(i)), ctypes.c_void_p(y.ptr), ctypes.c_int(1),
+                               ctypes.c_int(1), ctypes.c_int(k), ctypes.c_int(n), ctypes.c_void_p(None),
+                               ctypes.c_void_p(None), ctypes.c_float(1.0)], expected_args=10)
+
+        def l_capi(i):
+            K.gemv(fmt, x, w(i), y, 1, k, n, in_dtype="f16", out_dtype="f16", stream=hip.stream)
+
+        rows = {"null_us": [], "read_us": [], "ref_abi_us": [], "capi_us": []}
+        for _ in range(trials):
+            for key, fn in (("null_us", l_null), ("read_us", l_read), ("ref_abi_us", l_ref), ("capi_us", l_capi)):
+                rows[key].append(timed(fn) * 1e3)
+        r = {"shape": f"{n}x{k}", "fmt": fmt, "weight_bytes": int(wbytes), "cold_copies": copies}
+        for key, v in rows.items():
+            r[key] = round(statistics.median(v), 3)
+        for name in ("read", "ref_abi", "capi"):
+            gb = [wbytes / max(t - z, 1e-3) / 1e3 for t, z in zip(rows[name + "_us"], rows["null_us"])]
+            r[name + "_GBps_corrected"] = round(statistics.median(gb), 1)
+        for name in ("ref_abi", "capi"):
+            ratio = [(rd - z) / max(t - z, 1e-3) for t, rd, z in
+                     zip(rows[name + "_us"], rows["read_us"], rows["null_us"])]
+            r[name + "_vs_read"] = {"median": round(statistics.median(ratio), 4), "min": round(min(ratio), 4),
+                                    "max": round(max(ratio), 4)}
+        r["capi_frac_hbm_peak_corrected"] = round(r["capi_GBps_corrected"] / HBM_PEAK_GBPS, 4)
+        out.append(r)
+        for d in (pool, first, x, y, sink):
+            d.free()
+    for a, b in ev:
+        hip.event_destroy(a)
+        hip.event_destroy(b)
+    return out
+
+
 def gemv_configs(hip, K, launches=200):
     """Quant-GEMV configs 0/1 and the batch-16 MFMA GEMM (config 3a), cold pools."""
     out = []
@@ -645,6 +740,7 @@ def main():
         ex.close()
 
     gemv = [] if args.quick else gemv_configs(hip, K)
+    gemv_refm = [] if args.quick else gemv_reference_method(hip, K)
     attn = []
     if not args.quick:
         for ctx in (512, 4096, 32768):
@@ -680,6 +776,7 @@ def main():
     line["graph_b1"] = graph_b1  # the same step as a graph of per-node launches (VTE_PERSISTENT=0)
     if gemv:
         line["gemv"] = gemv
+        line["gemv_reference_method"] = gemv_refm
     if attn:
         line["attention"] = attn
     if prefill:

@@ -213,3 +213,31 @@ def test_reference_abi_mfma_symbol(hip, name, fmt, k, cols):
     hip.launch_kernel(fn, ((n + 31) // 32, (cols + 15) // 16, 1), (512, 1, 1), args, expected_args=10)
     ref = dq.gemv_epilogue(dq.gemv(fmt, raw, n, k, x.astype(np.float32)), bias, res, 1.0)
     assert rel_l2(down(y), ref) <= TOL
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q4_k", 37, 8960), ("q6_k", 29, 1536), ("q8_0", 11, 2048)])
+def test_measurement_read_kernel(hip, fmt, n, k):
+    """The benchmark's read baseline (vte_read_rows_kernel, one 64-thread
+    block per row, 16-byte loads at any alignment plus a dword tail) touches
+    every byte of every row: its per-row word equals the same fold computed
+    on the host, for Q6_K rows of 1260 bytes (4-byte aligned, a 12-byte
+    tail) included; the empty kernel launches."""
+    from vte_amd.kernels import HSACO_PATH
+    _, f_read = hip.load_kernel(str(HSACO_PATH), "vte_read_rows_kernel")
+    _, f_null = hip.load_kernel(str(HSACO_PATH), "vte_null_kernel")
+    raw = _mat(fmt, n, k, 5)
+    rb = raw.nbytes // n
+    dw = up(hip, raw)
+    sink = empty(hip, n, np.uint32)
+    hip.launch_kernel(f_read, (n, 1, 1), (64, 1, 1), [ctypes.c_void_p(dw.ptr), ctypes.c_void_p(sink.ptr),
+                                                       ctypes.c_int(rb)], expected_args=3)
+    hip.launch_kernel(f_null, (1, 1, 1), (1, 1, 1), [], expected_args=0)
+    rows = np.frombuffer(raw.tobytes(), np.uint8).reshape(n, rb)
+    nv = rb // 16
+    want = []
+    for r in rows:
+        v = r[:16 * nv].view(np.uint32).reshape(nv, 4).astype(np.uint64)
+        f = (v[:, 0] ^ ((v[:, 1] + v[:, 2]) & 0xFFFFFFFF) ^ v[:, 3]).sum()
+        tail = r[16 * nv:16 * nv + (rb - 16 * nv) // 4 * 4].view(np.uint32).astype(np.uint64).sum()
+        want.append((int(f) + int(tail)) & 0xFFFFFFFF)
+    assert down(sink).tolist() == want
