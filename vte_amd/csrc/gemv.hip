@@ -19,6 +19,7 @@
 //    so the inner loop is one int->float convert and one FMA per weight.
 //  * fp32 accumulation; a 64-lane butterfly reduction per row.
 #include "quant.h"
+#include "ref_mv.h"
 
 // ---------------------------------------------------------------------------
 // Q4_K
@@ -240,44 +241,45 @@ __global__ __launch_bounds__(256) void gemv_staged_rows(const TI* __restrict__ x
 // Reference-ABI kernels (drop-in for hipModuleGetFunction by name).
 // grid (out_features, batch*seq_len, 1), block (64,1,1), fp16 in/out
 // (vte/core/fallback_executor.py:140-148, kernel_arg_builder.py:32-43).
-// The staged formats use a static LDS buffer sized for in_features <= 16384.
+// Rows of 64-multiple lengths up to 16384 run on ref_mv.h (several rows per
+// working block); other lengths one row per wave.
 // ---------------------------------------------------------------------------
 
-#define REF_STAGE_BYTES (64 * 272 + 32)  // in_features <= 16384 for Q6_K and Q8_0
-
-template <typename T>
-__device__ __forceinline__ void ref_gemv_q4k(const void* __restrict__ input_ptr, const void* __restrict__ weight_ptr,
+// Rows the batched-row mat-vec (ref_mv.h) does not serve (K not a multiple of
+// 64 or above 16384): one row per wave straight from global memory.
+template <typename T, int FMT>
+__device__ __forceinline__ void ref_gemv_row(const void* __restrict__ input_ptr, const void* __restrict__ weight_ptr,
                                              void* __restrict__ output_ptr, int batch, int seq_len, int in_features,
                                              int out_features, const void* __restrict__ bias_ptr,
                                              const void* __restrict__ residual_ptr, float residual_scale) {
     const int row = blockIdx.x, m = blockIdx.y;
     if (row >= out_features || m >= batch * seq_len) return;
-    const int n_sb = in_features / QK_K;
+    const int n_blk = FMT == 8 ? in_features / QK8_0 : in_features / QK_K;
+    const size_t rb = (size_t)n_blk * (FMT == 4 ? Q4K_BYTES : FMT == 6 ? Q6K_BYTES : Q80_BYTES);
+    const uint8_t* rp = (const uint8_t*)weight_ptr + (size_t)row * rb;
+    const T* xm = (const T*)input_ptr + (size_t)m * in_features;
     float acc[1];
-    q4k_row_dot<T, 1>((const uint8_t*)weight_ptr + (size_t)row * n_sb * Q4K_BYTES,
-                      (const T*)input_ptr + (size_t)m * in_features, in_features, n_sb, threadIdx.x, acc);
+    if constexpr (FMT == 4) q4k_row_dot<T, 1>(rp, xm, in_features, n_blk, threadIdx.x, acc);
+    else if constexpr (FMT == 6) q6k_row_dot<T, 1>(rp, xm, in_features, n_blk, threadIdx.x, acc);
+    else q80_row_dot<T, 1>(rp, xm, in_features, n_blk, threadIdx.x, acc);
     if (threadIdx.x == 0)
         gemv_store<T>((T*)output_ptr, (const T*)bias_ptr, (const T*)residual_ptr, residual_scale, row, m, out_features,
                       acc[0]);
 }
 
 template <typename T, int FMT>
-__device__ __forceinline__ void ref_gemv_staged(const void* __restrict__ input_ptr, const void* __restrict__ weight_ptr,
-                                                void* __restrict__ output_ptr, int batch, int seq_len, int in_features,
-                                                int out_features, const void* __restrict__ bias_ptr,
-                                                const void* __restrict__ residual_ptr, float residual_scale,
-                                                uint8_t* stage) {
-    const int row = blockIdx.x, m = blockIdx.y;
-    if (row >= out_features || m >= batch * seq_len) return;
-    const int n_blk = FMT == 6 ? in_features / QK_K : in_features / QK8_0;
-    const size_t rb = (size_t)n_blk * (FMT == 6 ? Q6K_BYTES : Q80_BYTES);
-    const uint8_t* rl = wave_stage((const uint8_t*)weight_ptr + (size_t)row * rb, rb, stage, threadIdx.x);
-    float acc[1];
-    if constexpr (FMT == 6) q6k_row_dot<T, 1>(rl, (const T*)input_ptr + (size_t)m * in_features, in_features, n_blk, threadIdx.x, acc);
-    else q80_row_dot<T, 1>(rl, (const T*)input_ptr + (size_t)m * in_features, in_features, n_blk, threadIdx.x, acc);
-    if (threadIdx.x == 0)
-        gemv_store<T>((T*)output_ptr, (const T*)bias_ptr, (const T*)residual_ptr, residual_scale, row, m, out_features,
-                      acc[0]);
+__device__ __forceinline__ void ref_gemv(const void* __restrict__ input_ptr, const void* __restrict__ weight_ptr,
+                                         void* __restrict__ output_ptr, int batch, int seq_len, int in_features,
+                                         int out_features, const void* __restrict__ bias_ptr,
+                                         const void* __restrict__ residual_ptr, float residual_scale) {
+    __shared__ float part[64];
+    if (ref_mv_ok(in_features))
+        ref_mv_dispatch<T, FMT>((const T*)input_ptr, (const uint8_t*)weight_ptr, (T*)output_ptr, batch * seq_len,
+                                in_features, out_features, (const T*)bias_ptr, (const T*)residual_ptr, residual_scale,
+                                part);
+    else
+        ref_gemv_row<T, FMT>(input_ptr, weight_ptr, output_ptr, batch, seq_len, in_features, out_features, bias_ptr,
+                             residual_ptr, residual_scale);
 }
 
 #define REF_GEMV_ARGS                                                                                          \
@@ -288,30 +290,14 @@ __device__ __forceinline__ void ref_gemv_staged(const void* __restrict__ input_p
     input_ptr, weight_ptr, output_ptr, batch, seq_len, in_features, out_features, bias_ptr, residual_ptr, residual_scale
 
 // fp16 I/O: the reference's symbols.
-extern "C" __global__ __launch_bounds__(64) void gemv_q4k_kernel(REF_GEMV_ARGS) {
-    ref_gemv_q4k<__half>(REF_GEMV_PASS);
-}
-extern "C" __global__ __launch_bounds__(64) void gemv_q6k_kernel(REF_GEMV_ARGS) {
-    __shared__ uint4 stage_u4[REF_STAGE_BYTES / 16 + 1];
-    ref_gemv_staged<__half, 6>(REF_GEMV_PASS, reinterpret_cast<uint8_t*>(stage_u4));
-}
-extern "C" __global__ __launch_bounds__(64) void gemv_q8_0_kernel(REF_GEMV_ARGS) {
-    __shared__ uint4 stage_u4[REF_STAGE_BYTES / 16 + 1];
-    ref_gemv_staged<__half, 8>(REF_GEMV_PASS, reinterpret_cast<uint8_t*>(stage_u4));
-}
+extern "C" __global__ __launch_bounds__(64) void gemv_q4k_kernel(REF_GEMV_ARGS) { ref_gemv<__half, 4>(REF_GEMV_PASS); }
+extern "C" __global__ __launch_bounds__(64) void gemv_q6k_kernel(REF_GEMV_ARGS) { ref_gemv<__half, 6>(REF_GEMV_PASS); }
+extern "C" __global__ __launch_bounds__(64) void gemv_q8_0_kernel(REF_GEMV_ARGS) { ref_gemv<__half, 8>(REF_GEMV_PASS); }
 // fp32 I/O siblings (same argument list and geometry; input, output, bias and
 // residual fp32): the BASELINE GEMV configs take fp32 activations.
-extern "C" __global__ __launch_bounds__(64) void gemv_q4k_f32_kernel(REF_GEMV_ARGS) {
-    ref_gemv_q4k<float>(REF_GEMV_PASS);
-}
-extern "C" __global__ __launch_bounds__(64) void gemv_q6k_f32_kernel(REF_GEMV_ARGS) {
-    __shared__ uint4 stage_u4[REF_STAGE_BYTES / 16 + 1];
-    ref_gemv_staged<float, 6>(REF_GEMV_PASS, reinterpret_cast<uint8_t*>(stage_u4));
-}
-extern "C" __global__ __launch_bounds__(64) void gemv_q8_0_f32_kernel(REF_GEMV_ARGS) {
-    __shared__ uint4 stage_u4[REF_STAGE_BYTES / 16 + 1];
-    ref_gemv_staged<float, 8>(REF_GEMV_PASS, reinterpret_cast<uint8_t*>(stage_u4));
-}
+extern "C" __global__ __launch_bounds__(64) void gemv_q4k_f32_kernel(REF_GEMV_ARGS) { ref_gemv<float, 4>(REF_GEMV_PASS); }
+extern "C" __global__ __launch_bounds__(64) void gemv_q6k_f32_kernel(REF_GEMV_ARGS) { ref_gemv<float, 6>(REF_GEMV_PASS); }
+extern "C" __global__ __launch_bounds__(64) void gemv_q8_0_f32_kernel(REF_GEMV_ARGS) { ref_gemv<float, 8>(REF_GEMV_PASS); }
 
 // ---------------------------------------------------------------------------
 // Exact dequantisers (bit-exact with the NumPy reference: no FMA contraction).
