@@ -326,6 +326,28 @@ int vte_decode_step(const vte_decode_model* m, void* workspace, const int* kv_of
  * are invalid). */
 int vte_decode_status(void* workspace, int* flags);
 
+/* Batched persistent step (csrc/decode_persistent_mm.hip): the layers of a
+ * decode step for `batch` <= 16 sequences, each at its own position, as one
+ * launch; replaces the per-layer launches of the batched graph
+ * (vte/core/batched_hip_graph_executor.py:231-292, execute_decode_batch at
+ * :287-292) up to the LM head.  Supports hidden and n_q*128 up to 1536, every
+ * projection Q4_K or Q6_K.  Workspace bytes for `batch` sequences (-1: shape
+ * not supported). */
+long long vte_decode_batch_workspace_bytes(const vte_decode_model* m, int batch);
+
+/* As vte_decode_setup, for the batched workspace (synchronous, once). */
+int vte_decode_batch_setup(const vte_decode_model* m, const vte_decode_layer* layers, int batch, void* workspace,
+                           long long workspace_bytes, void* stream);
+
+/* One batched step: x = the embeddings fp16 [batch][hidden]; kv_offset[b]
+ * (device) = sequence b's position, its cache at layer.k_cache + b *
+ * kv_batch_stride (elements); h_out = the last layer's output fp16
+ * [batch][hidden] (the caller runs the output norm and LM head).  Capturable;
+ * error flags through vte_decode_status (bit 1: a position outside
+ * [0, max_seq), nothing written).  Steps on one workspace must not overlap. */
+int vte_decode_batch_step(const vte_decode_model* m, void* workspace, int batch, long long kv_batch_stride,
+                          const int* kv_offset, const void* x, void* h_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

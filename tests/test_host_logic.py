@@ -62,3 +62,20 @@ def test_persistent_support_follows_the_library_model_check():
     assert HIPGraphExecutor._persistent_supported(_fmt_model(TINY))
     odd = QWEN25_1P5B.with_(n_layers=2, hidden=3584, n_q=16, n_kv=2, ffn=4096)
     assert not HIPGraphExecutor._persistent_supported(_fmt_model(odd))
+
+
+def test_batched_persistent_support():
+    """The batched persistent step takes the 1.5B and TINY shapes at 1-16
+    sequences (every projection Q4_K or Q6_K) and refuses, through the
+    library's own check, 17 sequences, a hidden size above its 1536-element
+    staging row, a Q8_0 projection and an FFN of more than 16 slices."""
+    from vte_amd.core.hip_graph_executor import HIPGraphExecutor
+    from vte_amd.core.model_config import QWEN25_1P5B, TINY
+    ok = HIPGraphExecutor._persistent_batch_supported
+    assert ok(_fmt_model(QWEN25_1P5B), 16) and ok(_fmt_model(TINY), 3) and ok(_fmt_model(TINY), 1)
+    assert not ok(_fmt_model(QWEN25_1P5B), 17)
+    assert not ok(_fmt_model(QWEN25_1P5B.with_(hidden=2048, n_q=16)), 16)
+    m = _fmt_model(TINY)
+    m.layers = [dict(m.layers[0], v_fmt="q8_0")] * TINY.n_layers
+    assert not ok(m, 4)
+    assert not ok(_fmt_model(QWEN25_1P5B.with_(ffn=256 * 129)), 16)

@@ -20,7 +20,7 @@ CSRC = HERE / "csrc"
 ARCH = "gfx950"
 LIB = HERE / "libvte_amd.so"
 HSACO = HERE / f"vte_kernels_{ARCH}.hsaco"
-SOURCES = ["gemv.hip", "fused.hip", "fused_f32.hip", "gemm_mfma.hip", "fused_mm.hip", "attention.hip", "glue.hip", "decode_persistent.hip", "capi.hip"]
+SOURCES = ["gemv.hip", "fused.hip", "fused_f32.hip", "gemm_mfma.hip", "fused_mm.hip", "attention.hip", "glue.hip", "decode_persistent.hip", "decode_persistent_mm.hip", "capi.hip"]
 MODULE_SOURCE = "module.hip"
 # Packed FP32 instructions are disabled for every HIP compile: some of their
 # forms have given silently wrong results on the target machines.

@@ -60,7 +60,7 @@ class HIPGraphExecutor:
     def __init__(self, hip: HIPRuntime, model: SyntheticQwen2, batch_size: int = 1, max_seq: Optional[int] = None,
                  top_k: int = 40, gemm_min_batch: int = 3, split: Optional[int] = None, fused: bool = True,
                  shared: Optional["HIPGraphExecutor"] = None, kv_seq: int = 0, persistent: Optional[bool] = None,
-                 weights_of: Optional["HIPGraphExecutor"] = None):
+                 weights_of: Optional["HIPGraphExecutor"] = None, persistent_batch: bool = False):
         """``weights_of``: use that executor's uploaded weights (same model)
         instead of uploading another copy; this executor keeps its own KV
         cache, RoPE tables and activations, and is closed with the owner.
@@ -73,7 +73,11 @@ class HIPGraphExecutor:
         VTE_PERSISTENT=0 turns it off): every layer runs as one persistent
         launch instead of five launches per layer (0.75 against 0.88 ms per
         step on MI355X); results read back raise if a block of that launch
-        waited past its deadline (blocks not all resident)."""
+        waited past its deadline (blocks not all resident).
+        ``persistent_batch``: at 3 to 16 sequences (the MFMA path) run the layers
+        as one persistent launch of the batched step (``vte_decode_batch_step``,
+        csrc/decode_persistent_mm.hip) between the embedding and the output
+        norm + LM head, when the model's shape and formats are supported."""
         if persistent is None:
             persistent = os.environ.get("VTE_PERSISTENT", "1") != "0"
         self.hip = hip
@@ -100,6 +104,8 @@ class HIPGraphExecutor:
         # batch 1: the whole step as one persistent launch (decode_persistent.hip)
         self.persistent = (self.fused and batch_size == 1 and shared is None and persistent
                            and self._persistent_supported(model))
+        self.persistent_batch = (self.mm_fused and 1 < batch_size <= 16 and shared is None and persistent_batch
+                                 and self._persistent_batch_supported(model, batch_size))
         self.graph = None
         self.graph_exec = None
 
@@ -124,9 +130,10 @@ class HIPGraphExecutor:
         # split-KV scratch: [B][n_q][splits] stats and [B][n_q][splits][hd] partial outputs
         sp = split or choose_split(self.max_seq, B, cfg.n_kv, 256)
         need += B * cfg.n_q * (-(-self.max_seq // sp) + 1) * (cfg.head_dim + 2) * 4 + B * cfg.n_kv * 4
-        if self.persistent:
+        if self.persistent or self.persistent_batch:
             self._pd_model = self._decode_model_struct(model)
-            self._pd_ws_bytes = self.K.decode_workspace_bytes(self._pd_model)
+            self._pd_ws_bytes = self.K.decode_workspace_bytes(self._pd_model) if self.persistent else \
+                self.K.decode_batch_workspace_bytes(self._pd_model, batch_size)
             need += self._pd_ws_bytes + 4096
         self.slab = SlabAllocator(hip, 0, requested_pool_size=need + (32 << 20))
         self.slab.initialize()
@@ -170,7 +177,7 @@ class HIPGraphExecutor:
         self.attn = SplitKVAttentionDispatcher(hip, cfg.n_q, cfg.n_kv, cfg.head_dim, self.max_seq, B, split,
                                                allocator=self.slab)
         self.h_final = 0  # index of the hidden buffer holding the layer output
-        if self.persistent:
+        if self.persistent or self.persistent_batch:
             self._setup_persistent()
         # pinned host staging and outputs of execute_decode_batch: tokens and
         # offsets copied in, top-k candidates (and the persistent step's error
@@ -248,6 +255,23 @@ class HIPGraphExecutor:
         m.head_dim, m.vocab, m.max_seq, m.eps = cfg.head_dim, cfg.vocab, max(1, cfg.max_seq), cfg.eps
         return kernels().decode_workspace_bytes(m, check=False) >= 0
 
+    @staticmethod
+    def _persistent_batch_supported(model, B: int) -> bool:
+        """The shapes and formats vte_decode_batch_* accepts (Q4_K / Q6_K
+        projections; hidden and q_dim up to the kernel's staging length)."""
+        cfg = model.cfg
+        if cfg.head_dim != 128 or cfg.n_q % cfg.n_kv or cfg.n_q // cfg.n_kv > 8:
+            return False
+        for lw in model.layers:
+            if any(lw[p + "_fmt"] not in ("q4_k", "q6_k") for p in ("q", "k", "v", "o", "gate", "up", "down")):
+                return False
+            if lw["gate_fmt"] != lw["up_fmt"]:
+                return False
+        m = DecodeModel()
+        m.n_layers, m.hidden, m.ffn, m.n_q, m.n_kv = cfg.n_layers, cfg.hidden, cfg.ffn, cfg.n_q, cfg.n_kv
+        m.head_dim, m.vocab, m.max_seq, m.eps = cfg.head_dim, cfg.vocab, max(1, cfg.max_seq), cfg.eps
+        return kernels().decode_batch_workspace_bytes(m, B, check=False) >= 0
+
     def _decode_model_struct(self, model) -> DecodeModel:
         cfg = self.cfg
         m = DecodeModel()
@@ -273,12 +297,16 @@ class HIPGraphExecutor:
             y.fmt_q, y.fmt_k, y.fmt_v = FMT[lw["q_fmt"]], FMT[lw["k_fmt"]], FMT[lw["v_fmt"]]
             y.fmt_o, y.fmt_gate_up, y.fmt_down = FMT[lw["o_fmt"]], FMT[lw["gate_fmt"]], FMT[lw["down_fmt"]]
         self._pd_layers = arr
-        self.K.decode_setup(m, ctypes.cast(arr, ctypes.c_void_p), self.pd_ws, self._pd_ws_bytes,
-                            stream=self.hip.stream)
+        if self.persistent:
+            self.K.decode_setup(m, ctypes.cast(arr, ctypes.c_void_p), self.pd_ws, self._pd_ws_bytes,
+                                stream=self.hip.stream)
+        else:
+            self.K.decode_batch_setup(m, ctypes.cast(arr, ctypes.c_void_p), self.B, self.pd_ws, self._pd_ws_bytes,
+                                      stream=self.hip.stream)
 
     def decode_status(self) -> int:
         """Error flags of the persistent step (0: every wait completed in time)."""
-        return self.K.decode_status(self.pd_ws) if self.persistent else 0
+        return self.K.decode_status(self.pd_ws) if self.persistent or self.persistent_batch else 0
 
     def _share(self, ex: "HIPGraphExecutor", seq: int) -> None:
         """Weights, RoPE tables and sequence ``seq``'s KV cache of ``ex``."""
@@ -405,8 +433,14 @@ class HIPGraphExecutor:
         offs = self.staging_kv_offset
         cur = 0
         K.embedding(self.token_embd_fmt, self.staging_input, self.token_embd, self.h[cur], B, H, 1.0, stream=st)
-        K.rmsnorm(self.h[cur], self.layers[0]["attn_norm"], self.xn, B, H, cfg.eps, stream=st)
-        for L, lw in enumerate(self.layers):
+        if self.persistent_batch:  # every layer in one launch, then the output norm for the LM head
+            K.decode_batch_step(self._pd_model, self.pd_ws, B, self.kv_batch_stride, offs, self.h[0], self.h[1],
+                                stream=st)
+            K.rmsnorm(self.h[1], self.output_norm, self.xn, B, H, cfg.eps, stream=st)
+            cur = 1
+        else:
+            K.rmsnorm(self.h[cur], self.layers[0]["attn_norm"], self.xn, B, H, cfg.eps, stream=st)
+        for L, lw in enumerate(self.layers if not self.persistent_batch else ()):
             if self.mm_fused:  # q/k/v + bias + RoPE + K/V append in one MFMA launch
                 K.attn_in(self.xn, None, cfg.eps, lw["q"], lw["q_bias"], lw["q_fmt"], lw["k"], lw["k_bias"],
                           lw["k_fmt"], lw["v"], lw["v_bias"], lw["v_fmt"], self.q, self.k_cache[L], self.v_cache[L],
@@ -546,7 +580,7 @@ class HIPGraphExecutor:
             h.graph_launch(self.graph_exec)
             h.memcpy_async_d2h(self._pin_val.ctypes.data, self.topk_val.ptr, self._pin_val.nbytes, "sampler_topk_val")
             h.memcpy_async_d2h(self._pin_idx.ctypes.data, self.topk_idx.ptr, self._pin_idx.nbytes, "sampler_topk_idx")
-            if self.persistent:  # the workspace's error-flag word (control words: epoch, done, flags)
+            if self.persistent or self.persistent_batch:  # the workspace's error-flag word (epoch, done, flags)
                 h.memcpy_async_d2h(self._pin_flags.ctypes.data, self.pd_ws.ptr + 8, 4, "sampler_status")
             self._pin_fresh = True
         elif use_graph:
@@ -628,7 +662,7 @@ class HIPGraphExecutor:
             raise HIPRuntimeError("split-KV attention with the in-kernel combine: a combining block gave up waiting "
                                   "on a split's records; results are invalid (VTE_ATT_FUSE=0 selects the separate "
                                   "combine launch)")
-        if self.persistent:
+        if self.persistent or self.persistent_batch:
             flags = int(self._pin_flags[0]) if self._pin_fresh else self.K.decode_status(self.pd_ws)
             if flags:
                 raise HIPRuntimeError(f"persistent decode step: error flags {flags:#x} (a block waited past its "

@@ -593,3 +593,156 @@ int vte_decode_status(void* ws, int* flags) {
     *flags = (int)c[2];
     return 0;
 }
+
+// ------------------------------------------------------------------ batched persistent decode step
+
+namespace {
+struct PbLayout {
+    size_t ctrl, layers, ll_h, ll_q, ll_kv, ll_att, ll_hm, ll_act, part, ll_dn, trace, total;
+    int sl_sb, nsl;
+};
+PbLayout pb_layout(const vte_decode_model* m, int B) {
+    PbLayout L;
+    const size_t qd = (size_t)m->n_q * 128, kvd = (size_t)m->n_kv * 128, H = m->hidden, F = m->ffn;
+    const int nsb = m->ffn / 256;
+    L.sl_sb = std::max(1, (nsb + 7) / 8);  // about 8 slices of the ffn activations
+    L.nsl = (nsb + L.sl_sb - 1) / L.sl_sb;
+    size_t o = 0;
+    L.ctrl = o; o = pd_align(o + 256);
+    L.layers = o; o = pd_align(o + (size_t)m->n_layers * sizeof(vte_decode_layer));
+    L.ll_h = o; o = pd_align(o + B * H * 4);
+    L.ll_q = o; o = pd_align(o + B * qd * 4);
+    L.ll_kv = o; o = pd_align(o + B * 2 * kvd * 4);
+    L.ll_att = o; o = pd_align(o + B * qd * 4);
+    L.ll_hm = o; o = pd_align(o + B * H * 4);
+    L.ll_act = o; o = pd_align(o + B * F * 4);
+    L.part = o; o = pd_align(o + (size_t)B * m->n_q * VTE_DECODE_MAX_SPLITS * 130 * 8);
+    L.ll_dn = o; o = pd_align(o + (size_t)L.nsl * B * H * 8);
+#ifdef VTE_PB_TRACE
+    L.trace = o; o = pd_align(o + (size_t)1024 * m->n_layers * 16 * 4);
+#else
+    L.trace = 0;
+#endif
+    L.total = o;
+    return L;
+}
+int pb_check_model(const vte_decode_model* m, int B, bool pointers = true) {
+    REQUIRE(m != nullptr, "decode_batch: null model");
+    REQUIRE(B >= 1 && B <= VTE_PB_MAX_B, "decode_batch: batch %d outside [1, %d]", B, VTE_PB_MAX_B);
+    REQUIRE(m->n_layers >= 1 && m->n_layers <= 1024, "decode_batch: n_layers %d", m->n_layers);
+    REQUIRE(m->head_dim == 128, "decode_batch: head_dim must be 128");
+    REQUIRE(m->n_kv >= 1 && m->n_q % m->n_kv == 0 && m->n_q / m->n_kv <= 8, "decode_batch: n_q / n_kv must be <= 8");
+    const int qd = m->n_q * 128;
+    REQUIRE(m->hidden % 256 == 0 && m->hidden <= VTE_PB_MAX_K && qd % 256 == 0 && qd <= VTE_PB_MAX_K &&
+                m->ffn % 256 == 0, "decode_batch: hidden and n_q*128 multiples of 256 up to %d, ffn a multiple of 256",
+            VTE_PB_MAX_K);
+    const PbLayout L = pb_layout(m, B);
+    REQUIRE(L.sl_sb * 256 <= VTE_PB_MAX_K && L.nsl <= VTE_PB_MAX_SLICES, "decode_batch: ffn %d too long", m->ffn);
+    REQUIRE(m->max_seq >= 1, "decode_batch: max_seq");
+    if (!pointers) return 0;
+    REQUIRE(m->rope_cos && m->rope_sin, "decode_batch: null RoPE tables");
+    return 0;
+}
+}  // namespace
+
+long long vte_decode_batch_workspace_bytes(const vte_decode_model* m, int batch) {
+    if (pb_check_model(m, batch, false)) return -1;
+    return (long long)pb_layout(m, batch).total;
+}
+
+int vte_decode_batch_setup(const vte_decode_model* m, const vte_decode_layer* layers, int batch, void* ws,
+                           long long ws_bytes, void* stream) {
+    int rc = pb_check_model(m, batch);
+    if (rc) return rc;
+    REQUIRE(layers && ws, "decode_batch_setup: null pointer");
+    REQUIRE(aligned(ws, 256), "decode_batch_setup: workspace must be 256-byte aligned");
+    const PbLayout L = pb_layout(m, batch);
+    REQUIRE(ws_bytes >= (long long)L.total, "decode_batch_setup: workspace %lld < %zu bytes", ws_bytes, L.total);
+    for (int l = 0; l < m->n_layers; ++l) {
+        const vte_decode_layer& y = layers[l];
+        REQUIRE(y.wq && y.wk && y.wv && y.wo && y.w_gate && y.w_up && y.w_down && y.attn_norm && y.ffn_norm &&
+                    y.k_cache && y.v_cache, "decode_batch_setup: layer %d: null pointer", l);
+        const int f[6] = {y.fmt_q, y.fmt_k, y.fmt_v, y.fmt_o, y.fmt_gate_up, y.fmt_down};
+        for (int i = 0; i < 6; ++i)
+            REQUIRE(f[i] == 4 || f[i] == 6, "decode_batch_setup: layer %d: projections must be Q4_K or Q6_K", l);
+        REQUIRE(aligned(y.wq, 16) && aligned(y.wk, 16) && aligned(y.wv, 16) && aligned(y.wo, 16) &&
+                    aligned(y.w_gate, 16) && aligned(y.w_up, 16) && aligned(y.w_down, 16) &&
+                    aligned(y.attn_norm, 16) && aligned(y.ffn_norm, 16) && aligned(y.k_cache, 16) &&
+                    aligned(y.v_cache, 16), "decode_batch_setup: layer %d: 16-byte alignment", l);
+    }
+    hipStream_t st = (hipStream_t)stream;
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    hipError_t e = hipMemsetAsync(base, 0, L.total, st);
+    if (e != hipSuccess) return hip_status(e, "decode_batch_setup memset");
+    const uint32_t ctrl[4] = {1u, 0u, 0u, 0u};  // epoch starts at 1: no tag matches the cleared words
+    e = hipMemcpyAsync(base + L.ctrl, ctrl, sizeof(ctrl), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(base + L.layers, layers, (size_t)m->n_layers * sizeof(vte_decode_layer),
+                           hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return hip_status(e, "decode_batch_setup copy");
+}
+
+int vte_decode_batch_step(const vte_decode_model* m, void* ws, int batch, long long kv_batch_stride,
+                          const int* kv_offset, const void* x, void* h_out, void* stream) {
+    int rc = pb_check_model(m, batch);
+    if (rc) return rc;
+    REQUIRE(ws && kv_offset && x && h_out, "decode_batch_step: null pointer");
+    REQUIRE(aligned(ws, 256) && aligned(x, 16) && aligned(h_out, 16), "decode_batch_step: alignment");
+    REQUIRE(kv_batch_stride >= (long long)m->max_seq * m->n_kv * 128 || batch == 1,
+            "decode_batch_step: kv_batch_stride %lld below one sequence's cache", kv_batch_stride);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    REQUIRE(dev >= 0 && dev < 64, "decode_batch_step: device %d", dev);
+    if (g_pd_cus[dev] == 0) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return hip_status(e, "hipDeviceGetAttribute");
+        g_pd_cus[dev] = n;
+    }
+    const int blocks = g_pd_cus[dev];  // one 256-thread block per CU
+    const PbLayout L = pb_layout(m, batch);
+    const int H = m->hidden, qd = m->n_q * 128, kvd = m->n_kv * 128;
+    // every q/k/v tile on its own block, the reduce outputs within one pass of the threads
+    REQUIRE(qd / 16 + 2 * (kvd / 16) <= blocks, "decode_batch_step: %d q/k/v tiles exceed %d blocks",
+            qd / 16 + 2 * (kvd / 16), blocks);
+    REQUIRE((batch * H + blocks - 1) / blocks <= 256, "decode_batch_step: %d outputs per block in the reduce",
+            (batch * H + blocks - 1) / blocks);
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    VtePbPlan P{};
+    P.layers = reinterpret_cast<const VtePdLayer*>(base + L.layers);
+    P.n_layers = m->n_layers;
+    P.hidden = H;
+    P.ffn = m->ffn;
+    P.n_q = m->n_q;
+    P.n_kv = m->n_kv;
+    P.B = batch;
+    P.eps = m->eps;
+    P.scale = 1.0f / sqrtf(128.0f);
+    P.kv_offset = kv_offset;
+    P.max_seq = m->max_seq;
+    P.kv_batch_stride = kv_batch_stride;
+    P.x = static_cast<const __half*>(x);
+    P.rope_cos = static_cast<const __half*>(m->rope_cos);
+    P.rope_sin = static_cast<const __half*>(m->rope_sin);
+    P.h_out = static_cast<__half*>(h_out);
+    P.ll_h = reinterpret_cast<uint32_t*>(base + L.ll_h);
+    P.ll_q = reinterpret_cast<uint32_t*>(base + L.ll_q);
+    P.ll_kv = reinterpret_cast<uint32_t*>(base + L.ll_kv);
+    P.ll_att = reinterpret_cast<uint32_t*>(base + L.ll_att);
+    P.ll_hm = reinterpret_cast<uint32_t*>(base + L.ll_hm);
+    P.ll_act = reinterpret_cast<uint32_t*>(base + L.ll_act);
+    P.part = reinterpret_cast<uint64_t*>(base + L.part);
+    P.ll_dn = reinterpret_cast<uint64_t*>(base + L.ll_dn);
+    P.ctrl = reinterpret_cast<uint32_t*>(base + L.ctrl);
+    P.sl_sb = L.sl_sb;
+    P.trace = L.trace ? reinterpret_cast<uint32_t*>(base + L.trace) : nullptr;
+    P.split_min = 128;
+    P.timeout_ticks = 20000000ull;  // 0.2 s
+    const size_t lds = vte::decode_persistent_mm_lds(H, qd, L.sl_sb * 256);
+    const int occ = vte::decode_persistent_mm_occupancy(lds);
+    REQUIRE(occ >= 1, "decode_batch_step: the kernel does not fit on a CU (occupancy %d)", occ);
+    e = vte::decode_persistent_mm_launch(P, blocks, lds, (hipStream_t)stream);
+    return hip_status(e, "vte_decode_batch_step launch");
+}

@@ -56,10 +56,13 @@ SIGNATURES = {
     "vte_decode_setup": [_vp, _vp, _vp, _ll, _vp],
     "vte_decode_step": [_vp, _vp, _vp, _vp, _vp, _vp],
     "vte_decode_status": [_vp, _IP],
+    "vte_decode_batch_workspace_bytes": [_vp, _i],
+    "vte_decode_batch_setup": [_vp, _vp, _i, _vp, _ll, _vp],
+    "vte_decode_batch_step": [_vp, _vp, _i, _ll, _vp, _vp, _vp, _vp],
     "vte_last_error": [],
 }
 RESTYPES = {"vte_last_error": ctypes.c_char_p, "vte_attn_scratch_floats": _ll, "vte_topk_scratch_bytes": _ll,
-            "vte_decode_workspace_bytes": _ll}
+            "vte_decode_workspace_bytes": _ll, "vte_decode_batch_workspace_bytes": _ll}
 
 
 class DecodeLayer(ctypes.Structure):
@@ -251,6 +254,26 @@ class VTEKernels:
         """The persistent batch-1 decode step: embedding x -> fp32 logits, one launch."""
         self._check(self.lib.vte_decode_step(ctypes.byref(model), _p(ws), _p(kv_offset), _p(x), _p(logits),
                                              self._st(stream)), "vte_decode_step")
+
+    def decode_batch_workspace_bytes(self, model: DecodeModel, batch: int, check: bool = True) -> int:
+        """Workspace bytes of the batched persistent step (-1 when the shape is
+        not supported and ``check`` is False)."""
+        n = int(self.lib.vte_decode_batch_workspace_bytes(ctypes.byref(model), batch))
+        if n < 0 and check:
+            self._check(-1, "vte_decode_batch_workspace_bytes")
+        return n
+
+    def decode_batch_setup(self, model: DecodeModel, layers, batch: int, ws, ws_bytes: int, stream=None) -> None:
+        self._check(self.lib.vte_decode_batch_setup(ctypes.byref(model), layers, batch, _p(ws), ws_bytes,
+                                                    self._st(stream)), "vte_decode_batch_setup")
+
+    def decode_batch_step(self, model: DecodeModel, ws, batch: int, kv_batch_stride: int, kv_offset, x, h_out,
+                          stream=None) -> None:
+        """The batched persistent step: embeddings x [batch][hidden] -> the last
+        layer's output h_out [batch][hidden] (fp16), one launch."""
+        self._check(self.lib.vte_decode_batch_step(ctypes.byref(model), _p(ws), batch, kv_batch_stride,
+                                                   _p(kv_offset), _p(x), _p(h_out), self._st(stream)),
+                    "vte_decode_batch_step")
 
     def decode_status(self, ws) -> int:
         f = ctypes.c_int(0)
