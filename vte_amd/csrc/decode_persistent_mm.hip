@@ -42,10 +42,12 @@
 // against 1.54 ms for the batched graph, so the graph stays the default and
 // this step is opt-in.  Per layer ~70 us against ~55 us; stage clocks of a
 // probe build (VTE_PB_TRACE) put most of it in the hand-offs of the 96 KB
-// activation blocks (5-10 us from the producing stage's end to the staged
-// input, against ~1.6 us for a plain read of the same bytes) and in the
-// gate/up and down stages, whose 4 waves per CU (one block per CU) hide less
-// memory latency than the graph kernels' 12.
+// activation blocks: a consumer sees the producing stage's last words within
+// ~0.2 us, but then needs two rounds of device-coherent loads of freshly
+// written lines (~1.8 us each; one round of all 48 pairs per thread does not
+// fit the registers beside their addresses) plus its LDS writes, 5-6 us in
+// all; and in the gate/up and down stages, whose 4 waves per CU (one block
+// per CU) hide less memory latency than the graph kernels' 12.
 
 #include "fused_kernels.h"
 #include "mfma_deq.h"
@@ -114,7 +116,7 @@ __device__ __forceinline__ void pb_stage(const void* src, bool ll, int K, int B,
             // pairs past npair read the workspace buffer that follows this one
             // (every flagged input has one) and count as ready
 #pragma unroll
-            for (int j = 0; j < PB_NR; ++j) w[j] = pb_ld64(s32 + 2 * (tid + PD_T * (r0 + j)));
+            for (int j = 0; j < PB_NR; ++j) w[j] = pb_ld64((s32 + 2 * PD_T * (r0 + j)) + (uint32_t)(2 * tid));
             int spins = 0;
             while (true) {
                 bool all = true;
@@ -122,7 +124,7 @@ __device__ __forceinline__ void pb_stage(const void* src, bool ll, int K, int B,
                 for (int j = 0; j < PB_NR; ++j) {
                     const bool okj = ok2(w[j], tag) || tid + PD_T * (r0 + j) >= npair;
                     all = all && okj;
-                    if (!okj) w[j] = pb_ld64(s32 + 2 * (tid + PD_T * (r0 + j)));
+                    if (!okj) w[j] = pb_ld64((s32 + 2 * PD_T * (r0 + j)) + (uint32_t)(2 * tid));
                 }
                 if (all || pd_expired(ck, spins)) break;
             }
