@@ -166,13 +166,15 @@ def test_gemm_mfma_f16_epilogue(hip, K):
 @pytest.mark.parametrize("name,fmt", [("gemv_q4k_kernel", "q4_k"), ("gemv_q6k_kernel", "q6_k"),
                                       ("gemv_q8_0_kernel", "q8_0"), ("gemv_q4k_f32_kernel", "q4_k"),
                                       ("gemv_q6k_f32_kernel", "q6_k"), ("gemv_q8_0_f32_kernel", "q8_0")])
-@pytest.mark.parametrize("n,k", [(300, 2048), (20003, 1536), (1500, 8960), (300, 2080), (77, 16640)])
+@pytest.mark.parametrize("n,k", [(300, 2048), (20003, 1536), (40001, 512), (1500, 8960), (300, 2080), (77, 16640)])
 def test_reference_abi_code_object(hip, name, fmt, n, k):
     """Drop-in path: load the code object by kernel name and launch it with the
     reference's 10-argument ABI and geometry (grid (N, B*S), block 64); the
     `_f32` siblings take fp32 input, bias, residual and output.  Shapes cover
     the several-rows-per-block form (two 24-lane row groups at K = 1536, four
-    rows per block and a ragged last block at N = 20003), rows of more than 64
+    rows per block and a ragged last block at N = 20003; eight 8-lane groups
+    walking 16 rows per block at N = 40001, K = 512, which Q4_K takes too from
+    32768 rows), rows of more than 64
     units (K = 8960), and the one-row-per-wave form (K = 2080, Q8_0 only; K
     above 16384)."""
     from vte_amd.kernels import HSACO_PATH
