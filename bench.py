@@ -659,6 +659,9 @@ def main():
                     help="profiling run only: a 256 MiB calibration copy, then the quant-GEMV configs 0/1 "
                          "(Q4_K 8960x1536, Q6_K 1536x8960 and 151936x1536, Q8_0 2048x2048) and the batch-16 "
                          "MFMA GEMM over cold rotating pools, and the split-KV attention configs 2/3b")
+    ap.add_argument("--profile-gemv-reference", action="store_true",
+                    help="profiling run only: the reference's per-launch GEMV method (reference-ABI symbols, the "
+                         "C-ABI mat-vec, the read baseline and the empty kernel) over its five shapes, one trial")
     ap.add_argument("--profile-persistent", action="store_true",
                     help="with --profile-step 1: the persistent form of the step (the default batch-1 step; "
                          "without this flag the per-node graph is profiled)")
@@ -671,6 +674,16 @@ def main():
         sys.exit(2)
     if args.profile_gemv:
         profile_configs()
+        return
+    if args.profile_gemv_reference:
+        from vte_amd.bridge import HIPRuntime
+        from vte_amd.kernels import kernels
+        hip = HIPRuntime()
+        if not hip.initialize():
+            raise SystemExit("HIP initialisation failed")
+        for r in gemv_reference_method(hip, kernels(), iters=200, warmup=50, trials=1):
+            print("profile-gemv-reference:", json.dumps(r), flush=True)
+        hip.cleanup()
         return
     if args.profile_step:
         profile_step(args.profile_step, args.steps,

@@ -5,6 +5,7 @@ kept under profiles/.
     python -m vte_amd.profile_summary traffic <fetch counter_collection.csv> <write counter_collection.csv>
                                               <kernel substring> <out.json> <out.md> "<commands>"
     python -m vte_amd.profile_summary mfma    <counter_collection.csv> <out.md> "<command>"
+    python -m vte_amd.profile_summary grid    <kernel_trace.csv> <out.md>   (appends a per-launch-shape table)
 
 ``traffic``: FETCH_SIZE / WRITE_SIZE are averaged per dispatch of the named
 kernel and converted to bytes with the factor that makes the run's 256 MiB
@@ -129,6 +130,25 @@ def mfma(path, out_md, command):
         f.write("\n".join(lines) + "\n")
 
 
+def grid(trace_csv, out_md):
+    """Append to out_md the average kernel time per (kernel, grid, workgroup),
+    which tells apart launches of one symbol over different matrix shapes."""
+    acc = defaultdict(list)
+    for r in _rows(trace_csv):
+        if r.get("Kind") != "KERNEL_DISPATCH":
+            continue
+        key = (r["Kernel_Name"], f'{r["Grid_Size_X"]}x{r["Grid_Size_Y"]}', r["Workgroup_Size_X"])
+        acc[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = ["", "Per launch shape (grid in threads):", "",
+             "| kernel | grid | workgroup | calls | avg us | min us |", "|---|---|---|---|---|---|"]
+    for (k, g, w), ts in sorted(acc.items(), key=lambda kv: (kv[0][0], -len(kv[1]))):
+        if k.startswith("__amd_rocclr"):
+            continue
+        lines.append(f"| `{k[:90]}` | {g} | {w} | {len(ts)} | {sum(ts) / len(ts):.2f} | {min(ts):.2f} |")
+    with open(out_md, "a") as f:
+        f.write("\n".join(lines) + "\n")
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
         stats(sys.argv[2], sys.argv[3], sys.argv[4], sys.argv[5] if len(sys.argv) > 5 else None)
@@ -136,5 +156,7 @@ if __name__ == "__main__":
         traffic(*sys.argv[2:8])
     elif sys.argv[1] == "mfma":
         mfma(sys.argv[2], sys.argv[3], sys.argv[4])
+    elif sys.argv[1] == "grid":
+        grid(sys.argv[2], sys.argv[3])
     else:
         raise SystemExit(__doc__)
