@@ -89,9 +89,8 @@ def test_tiny_ragged_matches_oracle_and_graph(hip, tiny, B):
 
 
 def test_position_out_of_range_raises(hip, tiny):
-    """A position at max_seq sets the step's error flag (nothing written) and
-    reading the results raises; the next valid step clears nothing but runs."""
-    cfg = tiny.cfg
+    """A position at max_seq sets the step's error flag, reading the results
+    raises, and no cache row beyond the earlier valid step's is written."""
     B, max_seq = 4, 256
     ex = HIPGraphExecutor(hip, tiny, batch_size=B, max_seq=max_seq, top_k=40, persistent_batch=True)
     try:
