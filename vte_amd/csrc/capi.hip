@@ -618,6 +618,10 @@ PbLayout pb_layout(const vte_decode_model* m, int B) {
     L.ll_act = o; o = pd_align(o + B * F * 4);
     L.part = o; o = pd_align(o + (size_t)B * m->n_q * VTE_DECODE_MAX_SPLITS * 130 * 8);
     L.ll_dn = o; o = pd_align(o + (size_t)L.nsl * B * H * 8);
+    // The kernel's staging reads whole rounds of 256 x 24 word pairs (48 KB)
+    // past the end of a flagged input without a bounds test: every staged
+    // buffer (ll_h, ll_att, ll_hm, ll_act) is followed by at least that much
+    // workspace (the attention records alone hold >= 133 KB).
 #ifdef VTE_PB_TRACE
     L.trace = o; o = pd_align(o + (size_t)1024 * m->n_layers * 16 * 4);
 #else
@@ -639,6 +643,7 @@ int pb_check_model(const vte_decode_model* m, int B, bool pointers = true) {
     const PbLayout L = pb_layout(m, B);
     REQUIRE(L.sl_sb * 256 <= VTE_PB_MAX_K && L.nsl <= VTE_PB_MAX_SLICES, "decode_batch: ffn %d too long", m->ffn);
     REQUIRE(m->max_seq >= 1, "decode_batch: max_seq");
+    REQUIRE(L.ll_dn - L.ll_act >= (size_t)B * m->ffn * 4 + 48 * 1024, "decode_batch: workspace tail");
     if (!pointers) return 0;
     REQUIRE(m->rope_cos && m->rope_sin, "decode_batch: null RoPE tables");
     return 0;
